@@ -1,0 +1,122 @@
+/*
+ * llmk_sampler.h — C ABI of the MI355X batched token-sampling engine for
+ * llm-rs.  One call samples a whole batch on one GPU, asynchronously on a HIP
+ * stream, and replaces the per-row host loop of
+ *   llm-scheduler/src/scheduler.rs:138-145  (for each row: backend.sample(..))
+ * whose body is
+ *   llm-core/src/backend.rs:23-24           (LlmBackend::sample)
+ *   llm-core/src/backends/candle.rs:2033-2035 (CandleBackend::sample)
+ *   llm-core/src/sampler.rs:25-125          (sample_logits).
+ *
+ * Conventions follow llm-ffi/src/lib.rs: plain `extern "C"` symbols, an opaque
+ * handle with explicit create/destroy (lib.rs:38-84), `#[repr(C)]`-compatible
+ * structs (lib.rs:10-29).  Unlike llm-ffi's null/0 sentinels, every call
+ * returns a status code (0 = success, negative = error) and
+ * llmk_last_error() gives the message for the calling thread.
+ *
+ * Semantics per row (identical to sampler.rs when the extension fields are
+ * at their defaults): repetition penalty (sampler.rs:128-147) -> presence and
+ * frequency penalty -> allow-bitmask -> greedy if temperature <= 1e-5
+ * (sampler.rs:40-50) -> temperature (sampler.rs:150-157) -> softmax
+ * (sampler.rs:56-71) -> order by (probability desc, index asc) (sampler.rs:77)
+ * -> min-p -> top-k (sampler.rs:80-89) -> top-p (sampler.rs:92-110) -> draw
+ * with the caller's uniform (sampler.rs:113-124).
+ *
+ * Memory: every pointer in llmk_sample_batch_args is DEVICE memory owned by
+ * the caller and must stay valid until the stream reaches the call.
+ */
+#ifndef LLMK_SAMPLER_H
+#define LLMK_SAMPLER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LLMK_OK 0
+#define LLMK_ERR_INVALID_ARGUMENT (-1)
+#define LLMK_ERR_EMPTY_LOGITS (-2) /* sampler.rs:30-32 "Empty logits" */
+#define LLMK_ERR_CAPACITY (-3)     /* batch/vocab above the handle's maxima */
+#define LLMK_ERR_HIP (-4)
+#define LLMK_ERR_ALIGNMENT (-5)
+#define LLMK_ERR_UNSUPPORTED (-6)
+
+/* Token written for a row whose parameters are invalid (NaN temperature,
+ * negative top_k, non-finite penalties, ...). */
+#define LLMK_INVALID_TOKEN 0xffffffffu
+
+/* Bits of the device status word (llmk_sampler_status). */
+#define LLMK_STATUS_INVALID_PARAMS 0x1u
+#define LLMK_STATUS_HISTORY_OVERFLOW 0x2u
+
+typedef struct llmk_sampler llmk_sampler; /* opaque; owns device workspace */
+
+typedef enum { LLMK_F32 = 0, LLMK_BF16 = 1 } llmk_dtype;
+
+typedef struct {
+  /* logits[b * row_stride + v], v < vocab; row_stride in elements.  fp32 rows
+   * must be 16-byte aligned, bf16 rows 8-byte aligned. */
+  const void* logits;
+  int32_t dtype; /* llmk_dtype */
+  uint32_t batch;
+  uint32_t vocab;
+  uint64_t row_stride;
+  /* Per-row parameters, [batch] each; NULL = the SampleParams default
+   * (llm-core/src/types.rs:186-195): temperature 1, top_k 0 (off), top_p 1,
+   * repetition 1; extensions: min_p 0, presence 0, frequency 0. */
+  const float* temperature;
+  const int32_t* top_k;
+  const float* top_p;
+  const float* min_p;
+  const float* repetition_penalty;
+  const float* presence_penalty;
+  const float* frequency_penalty;
+  /* Token history as CSR: hist_offsets[batch+1], hist_tokens[...].  NULL =
+   * empty histories.  Ids >= vocab are ignored (sampler.rs:138). */
+  const uint32_t* hist_offsets;
+  const uint32_t* hist_tokens;
+  /* Grammar allow-bitmask, [batch][mask_words_per_row] u32, LSB-first (token
+   * t allowed iff bit t&31 of word t>>5 is set); NULL = everything allowed. */
+  const uint32_t* allow_mask;
+  uint32_t mask_words_per_row;
+  /* One uniform in [0,1) per row; replaces rand::thread_rng (sampler.rs:113). */
+  const float* uniforms;
+  uint32_t* out_tokens; /* [batch] */
+  /* Optional processed distribution: the kept candidates after top-p
+   * renormalisation, in (p desc, idx asc) order, [batch][out_cap] each; and
+   * the kept count per row.  NULL / out_cap 0 = not requested. */
+  uint32_t* out_ids;
+  float* out_probs;
+  uint32_t out_cap;
+  uint32_t* out_count;
+} llmk_sample_batch_args;
+
+/* Create a sampler on `device` able to serve batches up to max_batch rows of
+ * up to max_vocab logits; all device workspace is allocated here.
+ * Replaces nothing in the reference (its sampler keeps no state). */
+int llmk_sampler_create(llmk_sampler** out, int device, uint32_t max_batch,
+                        uint32_t max_vocab);
+
+/* Sample every row of the batch; enqueued on `hip_stream` (a hipStream_t, NULL
+ * = default stream) and returns without waiting.  Allocates nothing.
+ * Replaces the per-row loop scheduler.rs:138-145 over sampler.rs:25-125.
+ * One handle serves one stream at a time (calls on a handle are serialised
+ * by stream order; concurrent calls on two streams race on the workspace). */
+int llmk_sample_batch(llmk_sampler* s, const llmk_sample_batch_args* args,
+                      void* hip_stream);
+
+/* Reads and clears the device status word (OR of LLMK_STATUS_* bits raised by
+ * calls since the last read).  Synchronises `hip_stream`. */
+int llmk_sampler_status(llmk_sampler* s, void* hip_stream, uint32_t* status);
+
+void llmk_sampler_destroy(llmk_sampler* s);
+
+/* Message of the last error on the calling thread ("" if none). */
+const char* llmk_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

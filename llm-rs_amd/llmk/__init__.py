@@ -1,0 +1,12 @@
+"""llmk — MI355X-native batched token sampling for llm-rs (HIP kernels behind a C ABI)."""
+from ._lib import LIB_PATH, EXPORTED_SYMBOLS, load  # noqa: F401
+from .sampler import (  # noqa: F401
+    BatchResult,
+    DeviceBatch,
+    HipSampler,
+    SampleParams,
+    SamplerError,
+    device_batch_from_params,
+    sample,
+    sample_logits,
+)

@@ -1,0 +1,221 @@
+"""Host-side mirror of the reference sampler interface over the HIP engine.
+
+Reference interface (llm-rs, Rust):
+  llm-core/src/types.rs:176-196   SampleParams {temperature, top_p, top_k,
+                                  repetition_penalty, max_new_tokens}
+  llm-core/src/backend.rs:23-24   LlmBackend::sample(logits, params, history)
+                                  -> Result<TokenId>
+  llm-core/src/sampler.rs:25-125  sample_logits(logits, params, history)
+  llm-core/src/sampler.rs:219-228 sample(logits, temperature) -> u32
+Here the same names take torch CUDA tensors (device memory) and an explicit
+uniform per row instead of rand::thread_rng.  `HipSampler.sample_batch` is the
+batched call the scheduler makes once per step instead of scheduler.rs:138-145.
+PyTorch only provides device memory and the stream; every computation runs in
+libllmk_sampler.so.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+from typing import Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import _lib
+
+
+class SamplerError(RuntimeError):
+    """Raised for a non-zero status of the C ABI (the reference's anyhow::Error)."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"llmk error {code}: {msg}")
+        self.code = code
+
+
+@dataclass
+class SampleParams:
+    """llm-core/src/types.rs:176-196, plus the engine's extension fields."""
+
+    temperature: float = 1.0
+    top_p: float = 1.0
+    top_k: int = 0
+    repetition_penalty: float = 1.0
+    max_new_tokens: int = 512
+    presence_penalty: float = 0.0
+    frequency_penalty: float = 0.0
+    min_p: float = 0.0
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+@dataclass
+class BatchResult:
+    tokens: torch.Tensor
+    ids: Optional[torch.Tensor] = None
+    probs: Optional[torch.Tensor] = None
+    count: Optional[torch.Tensor] = None
+
+
+@dataclass
+class DeviceBatch:
+    """Device-resident inputs of one sampling step (all torch CUDA tensors)."""
+
+    logits: torch.Tensor                      # [B, >=V] float32 or bfloat16
+    uniforms: torch.Tensor                    # [B] float32
+    vocab: Optional[int] = None
+    temperature: Optional[torch.Tensor] = None
+    top_k: Optional[torch.Tensor] = None      # int32
+    top_p: Optional[torch.Tensor] = None
+    min_p: Optional[torch.Tensor] = None
+    repetition_penalty: Optional[torch.Tensor] = None
+    presence_penalty: Optional[torch.Tensor] = None
+    frequency_penalty: Optional[torch.Tensor] = None
+    hist_offsets: Optional[torch.Tensor] = None  # int32/uint32 [B+1]
+    hist_tokens: Optional[torch.Tensor] = None   # int32/uint32
+    allow_mask: Optional[torch.Tensor] = None    # int32/uint32 [B, words]
+
+
+class HipSampler:
+    """Owns an llmk_sampler handle (device workspace) on one GPU."""
+
+    def __init__(self, max_batch: int, max_vocab: int, device: int = 0):
+        self._lib = _lib.load()
+        self.device = device
+        self.max_batch = max_batch
+        self.max_vocab = max_vocab
+        h = ctypes.c_void_p()
+        rc = self._lib.llmk_sampler_create(ctypes.byref(h), device, max_batch, max_vocab)
+        if rc != 0:
+            raise SamplerError(rc, _lib.last_error())
+        self._h = h
+
+    def close(self):
+        if getattr(self, "_h", None) is not None and self._h.value:
+            self._lib.llmk_sampler_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ---- the batched call -------------------------------------------------
+    def launch(self, db: DeviceBatch, out_tokens: torch.Tensor,
+               out_ids: Optional[torch.Tensor] = None,
+               out_probs: Optional[torch.Tensor] = None,
+               out_count: Optional[torch.Tensor] = None,
+               stream: Optional[torch.cuda.Stream] = None) -> None:
+        """Enqueue one batched sampling call; no allocation, no sync."""
+        lg = db.logits
+        if lg.dtype == torch.float32:
+            dt = _lib.LLMK_F32
+        elif lg.dtype == torch.bfloat16:
+            dt = _lib.LLMK_BF16
+        else:
+            raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT, "logits must be float32 or bfloat16")
+        B = lg.shape[0]
+        V = db.vocab if db.vocab is not None else lg.shape[1]
+        a = _lib.SampleBatchArgs()
+        a.logits = lg.data_ptr()
+        a.dtype = dt
+        a.batch = B
+        a.vocab = V
+        a.row_stride = lg.stride(0)
+        a.temperature = _ptr(db.temperature)
+        a.top_k = _ptr(db.top_k)
+        a.top_p = _ptr(db.top_p)
+        a.min_p = _ptr(db.min_p)
+        a.repetition_penalty = _ptr(db.repetition_penalty)
+        a.presence_penalty = _ptr(db.presence_penalty)
+        a.frequency_penalty = _ptr(db.frequency_penalty)
+        a.hist_offsets = _ptr(db.hist_offsets)
+        a.hist_tokens = _ptr(db.hist_tokens)
+        a.allow_mask = _ptr(db.allow_mask)
+        a.mask_words_per_row = 0 if db.allow_mask is None else db.allow_mask.shape[1]
+        a.uniforms = _ptr(db.uniforms)
+        a.out_tokens = _ptr(out_tokens)
+        a.out_ids = _ptr(out_ids)
+        a.out_probs = _ptr(out_probs)
+        cap = 0
+        if out_ids is not None:
+            cap = out_ids.shape[1]
+        elif out_probs is not None:
+            cap = out_probs.shape[1]
+        a.out_cap = cap
+        a.out_count = _ptr(out_count)
+        st = stream if stream is not None else torch.cuda.current_stream()
+        rc = self._lib.llmk_sample_batch(self._h, ctypes.byref(a), ctypes.c_void_p(st.cuda_stream))
+        if rc != 0:
+            raise SamplerError(rc, _lib.last_error())
+
+    def sample_batch(self, db: DeviceBatch, out_cap: int = 0) -> BatchResult:
+        B = db.logits.shape[0]
+        dev = db.logits.device
+        tok = torch.empty(B, dtype=torch.int32, device=dev)
+        ids = probs = None
+        if out_cap:
+            ids = torch.empty(B, out_cap, dtype=torch.int32, device=dev)
+            probs = torch.empty(B, out_cap, dtype=torch.float32, device=dev)
+        cnt = torch.empty(B, dtype=torch.int32, device=dev)
+        self.launch(db, tok, ids, probs, cnt)
+        return BatchResult(tok, ids, probs, cnt)
+
+    def status(self) -> int:
+        v = ctypes.c_uint32()
+        rc = self._lib.llmk_sampler_status(self._h, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream), ctypes.byref(v))
+        if rc != 0:
+            raise SamplerError(rc, _lib.last_error())
+        return v.value
+
+    # ---- the per-row reference call (LlmBackend::sample) ------------------
+    def sample(self, logits: torch.Tensor, params: SampleParams,
+               token_history: Sequence[int], u: float) -> int:
+        """sampler.rs:25-125 for one row; raises SamplerError on empty logits."""
+        if logits.numel() == 0:
+            raise SamplerError(_lib.LLMK_ERR_EMPTY_LOGITS, "Empty logits passed to sampler")
+        db = device_batch_from_params(logits.reshape(1, -1), [params], [list(token_history)], [u])
+        return int(self.sample_batch(db).tokens[0].item())
+
+
+def device_batch_from_params(logits: torch.Tensor, params: Sequence[SampleParams],
+                             histories: Sequence[Sequence[int]], uniforms: Sequence[float],
+                             allow_mask: Optional[np.ndarray] = None) -> DeviceBatch:
+    """Pack per-row SampleParams / histories into device arrays."""
+    dev = logits.device
+    f = lambda xs: torch.tensor(np.asarray(xs, dtype=np.float32), device=dev)
+    offs = np.zeros(len(histories) + 1, dtype=np.int64)
+    for i, h in enumerate(histories):
+        offs[i + 1] = offs[i] + len(h)
+    toks = np.concatenate([np.asarray(h, dtype=np.uint32) for h in histories]) if offs[-1] else np.zeros(1, np.uint32)
+    return DeviceBatch(
+        logits=logits,
+        uniforms=f(uniforms),
+        temperature=f([p.temperature for p in params]),
+        top_k=torch.tensor(np.asarray([p.top_k for p in params], dtype=np.int32), device=dev),
+        top_p=f([p.top_p for p in params]),
+        min_p=f([p.min_p for p in params]),
+        repetition_penalty=f([p.repetition_penalty for p in params]),
+        presence_penalty=f([p.presence_penalty for p in params]),
+        frequency_penalty=f([p.frequency_penalty for p in params]),
+        hist_offsets=torch.tensor(offs.astype(np.int32), device=dev),
+        hist_tokens=torch.tensor(toks.view(np.int32), device=dev),
+        allow_mask=None if allow_mask is None else torch.tensor(allow_mask.view(np.int32), device=dev),
+    )
+
+
+def sample_logits(sampler: HipSampler, logits: torch.Tensor, params: SampleParams,
+                  token_history: Sequence[int], u: float) -> int:
+    """Free-function form of sampler.rs:25 sample_logits."""
+    return sampler.sample(logits, params, token_history, u)
+
+
+def sample(sampler: HipSampler, logits: torch.Tensor, temperature: float, u: float) -> int:
+    """sampler.rs:219-228: temperature only, unwrap_or(0) on error."""
+    try:
+        return sampler.sample(logits, SampleParams(temperature=temperature), [], u)
+    except SamplerError:
+        return 0

@@ -1,0 +1,674 @@
+/*
+ * llmk_oracle.c — CPU oracle for the llm-rs token-sampling path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see llmk_oracle.h).  Built with
+ * -ffp-contract=off so every multiply and add rounds on its own, as Rust does
+ * (Rust never contracts a*b+c into an FMA).
+ *
+ * Reference being restated: /root/reference/llm-core/src/sampler.rs
+ *   sample_logits            :25-125   -> sample_row()
+ *   apply_repetition_penalty :128-147  -> apply_repetition()
+ *   apply_temperature        :150-157  -> apply_temperature()
+ *   apply_top_k              :160-173  -> llmk_oracle_apply_top_k()
+ *   apply_top_p              :176-216  -> llmk_oracle_apply_top_p()
+ *   sample                   :219-228  -> llmk_oracle_sample_simple()
+ * Presence/frequency formula: llm-tests/tests/mlc_parity.rs:1074-1089.
+ */
+#define _GNU_SOURCE
+#include "llmk_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define TILE 1024u
+
+/* ------------------------------------------------------------------------ */
+/* Numerics                                                                  */
+/* ------------------------------------------------------------------------ */
+
+/* ln 2 split for Cody–Waite reduction (hi has 32 significant bits), 1/ln 2,
+ * and 1/n! for the degree-13 Taylor polynomial of e^r on |r| <= ln2/2
+ * (truncation error < 5e-18 relative).  Derived in oracle/gen_constants.py. */
+static const double LN2_HI = 0x1.62e42fee00000p-1;
+static const double LN2_LO = 0x1.a39ef35793c76p-33;
+static const double INV_LN2 = 0x1.71547652b82fep+0;
+static const double INV_FACT[14] = {
+    0x1.0000000000000p+0, 0x1.0000000000000p+0, 0x1.0000000000000p-1,
+    0x1.5555555555555p-3, 0x1.5555555555555p-5, 0x1.1111111111111p-7,
+    0x1.6c16c16c16c17p-10, 0x1.a01a01a01a01ap-13, 0x1.a01a01a01a01ap-16,
+    0x1.71de3a556c734p-19, 0x1.27e4fb7789f5cp-22, 0x1.ae64567f544e4p-26,
+    0x1.1eed8eff8d898p-29, 0x1.6124613a86d09p-33};
+
+/* 2^f on [-1/2, 1/2], constant term 1, degree 5, minimax relative error
+ * 1.7e-7 after fp32 rounding of the coefficients (gen_constants.py). */
+static const float E2C1 = 0x1.62e42ap-1f;
+static const float E2C2 = 0x1.ebf9bcp-3f;
+static const float E2C3 = 0x1.c6b752p-5f;
+static const float E2C4 = 0x1.3cea88p-7f;
+static const float E2C5 = 0x1.5bba14p-10f;
+static const float LOG2E_F = 0x1.715476p+0f;
+
+float llmk_oracle_exp_m(float y) {
+  /* e^y evaluated in double, rounded once to float.  Below -110 the result
+   * is far under the smallest subnormal (2^-149 ~ e^-103.3). */
+  if (!(y >= -110.0f)) return 0.0f;
+  double yd = (double)y;
+  double kd = rint(yd * INV_LN2);
+  double r = fma(-kd, LN2_HI, yd);
+  r = fma(-kd, LN2_LO, r);
+  double p = INV_FACT[13];
+  for (int n = 12; n >= 0; --n) p = fma(p, r, INV_FACT[n]);
+  return (float)ldexp(p, (int)kd);
+}
+
+float llmk_oracle_exp2_f(float d) {
+  /* Terms of the softmax normaliser: 2^d for d <= 0.  Below -125 (and for
+   * -inf / NaN) the term is 0; otherwise the result is a normal float and the
+   * final scaling by 2^k is exact. */
+  if (!(d >= -125.0f)) return 0.0f;
+  float k = rintf(d);
+  float f = d - k;
+  float p = fmaf(E2C5, f, E2C4);
+  p = fmaf(p, f, E2C3);
+  p = fmaf(p, f, E2C2);
+  p = fmaf(p, f, E2C1);
+  p = fmaf(p, f, 1.0f);
+  return ldexpf(p, (int)k);
+}
+
+float llmk_oracle_libm_expf(float y) { return expf(y); }
+
+static void tree_sum_inplace(float* buf, uint32_t len) {
+  /* Balanced pairwise tree over contiguous indices: node = left + right. */
+  for (; len > 1; len >>= 1)
+    for (uint32_t i = 0; i < len / 2; ++i) buf[i] = buf[2 * i] + buf[2 * i + 1];
+}
+
+float llmk_oracle_normalizer(const float* lp, uint32_t V, float temperature) {
+  /* Two-level log-sum-exp over 1024-wide vocabulary tiles.
+   *   c2 = fl(log2(e) / T)
+   *   tile c: lc = max lp (NaN ignored); s_c = tree_sum(2^((lp_i - lc)*c2))
+   *   row:    L = max lc; S = tree_sum over next_pow2(#tiles) of
+   *           s_c * 2^((lc - L)*c2)      (padding entries are 0)
+   * Mathematically S = sum_i e^{(lp_i - L)/T}, the reference's softmax
+   * denominator (sampler.rs:57-66); the order of operations is fixed. */
+  const float c2 = LOG2E_F / temperature;
+  const uint32_t nt = (V + TILE - 1) / TILE;
+  uint32_t ntp = 1;
+  while (ntp < nt) ntp <<= 1;
+  float* lc = (float*)malloc(sizeof(float) * nt);
+  float* w = (float*)calloc(ntp, sizeof(float));
+  float buf[TILE];
+  for (uint32_t c = 0; c < nt; ++c) {
+    const uint32_t base = c * TILE;
+    const uint32_t n = (V - base < TILE) ? V - base : TILE;
+    float m = -INFINITY;
+    for (uint32_t i = 0; i < n; ++i)
+      if (lp[base + i] > m) m = lp[base + i];
+    lc[c] = m;
+    if (m == -INFINITY) {
+      w[c] = 0.0f;
+      continue;
+    }
+    for (uint32_t i = 0; i < TILE; ++i)
+      buf[i] = (i < n) ? llmk_oracle_exp2_f((lp[base + i] - m) * c2) : 0.0f;
+    tree_sum_inplace(buf, TILE);
+    w[c] = buf[0];
+  }
+  float L = -INFINITY;
+  for (uint32_t c = 0; c < nt; ++c)
+    if (lc[c] > L) L = lc[c];
+  float S = 0.0f;
+  if (L != -INFINITY) {
+    for (uint32_t c = 0; c < nt; ++c)
+      w[c] = w[c] * llmk_oracle_exp2_f((lc[c] - L) * c2);
+    tree_sum_inplace(w, ntp);
+    S = w[0];
+  }
+  free(lc);
+  free(w);
+  return S;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Sorting helpers (in-place introsort on u64 / u32 keys, ascending)         */
+/* ------------------------------------------------------------------------ */
+
+#define DEFINE_SORT(NAME, T)                                                  \
+  static void NAME##_insertion(T* a, int64_t n) {                             \
+    for (int64_t i = 1; i < n; ++i) {                                         \
+      T v = a[i];                                                             \
+      int64_t j = i - 1;                                                      \
+      while (j >= 0 && a[j] > v) {                                            \
+        a[j + 1] = a[j];                                                      \
+        --j;                                                                  \
+      }                                                                       \
+      a[j + 1] = v;                                                           \
+    }                                                                         \
+  }                                                                           \
+  static void NAME##_sift(T* a, int64_t start, int64_t n) {                   \
+    int64_t r = start;                                                        \
+    for (;;) {                                                                \
+      int64_t c = 2 * r + 1;                                                  \
+      if (c >= n) return;                                                     \
+      if (c + 1 < n && a[c + 1] > a[c]) ++c;                                  \
+      if (a[r] >= a[c]) return;                                               \
+      T t = a[r];                                                             \
+      a[r] = a[c];                                                            \
+      a[c] = t;                                                               \
+      r = c;                                                                  \
+    }                                                                         \
+  }                                                                           \
+  static void NAME##_heap(T* a, int64_t n) {                                  \
+    for (int64_t s = n / 2 - 1; s >= 0; --s) NAME##_sift(a, s, n);            \
+    for (int64_t e = n - 1; e > 0; --e) {                                     \
+      T t = a[0];                                                             \
+      a[0] = a[e];                                                            \
+      a[e] = t;                                                               \
+      NAME##_sift(a, 0, e);                                                   \
+    }                                                                         \
+  }                                                                           \
+  static void NAME##_intro(T* a, int64_t n, int depth) {                      \
+    while (n > 24) {                                                          \
+      if (depth-- == 0) {                                                     \
+        NAME##_heap(a, n);                                                    \
+        return;                                                               \
+      }                                                                       \
+      T x = a[0], y = a[n / 2], z = a[n - 1], piv;                            \
+      if (x < y) piv = (y < z) ? y : ((x < z) ? z : x);                       \
+      else piv = (x < z) ? x : ((y < z) ? z : y);                             \
+      int64_t i = 0, j = n - 1;                                               \
+      for (;;) {                                                              \
+        while (a[i] < piv) ++i;                                               \
+        while (a[j] > piv) --j;                                               \
+        if (i >= j) break;                                                    \
+        T t = a[i];                                                           \
+        a[i] = a[j];                                                          \
+        a[j] = t;                                                             \
+        ++i;                                                                  \
+        --j;                                                                  \
+      }                                                                       \
+      NAME##_intro(a + j + 1, n - j - 1, depth);                              \
+      n = j + 1;                                                              \
+    }                                                                         \
+    NAME##_insertion(a, n);                                                   \
+  }                                                                           \
+  static void NAME(T* a, int64_t n) {                                         \
+    int depth = 0;                                                            \
+    for (int64_t m = n; m > 1; m >>= 1) depth += 2;                           \
+    NAME##_intro(a, n, depth);                                                \
+  }
+
+DEFINE_SORT(sort_u64, uint64_t)
+DEFINE_SORT(sort_u32, uint32_t)
+
+static inline uint32_t f2u(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return u;
+}
+static inline float u2f(uint32_t u) {
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+/* (p desc, idx asc) order as one ascending u64 key.  p >= 0 here (NaN rows
+ * are outside the parity contract; in ref mode a NaN p lands wherever its bit
+ * pattern puts it, deterministically). */
+static inline uint64_t pkey(float p, uint32_t idx) {
+  return ((uint64_t)(~f2u(p)) << 32) | idx;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Steps                                                                     */
+/* ------------------------------------------------------------------------ */
+
+static uint32_t* sorted_history(const uint32_t* hist, uint32_t H) {
+  uint32_t* h = (uint32_t*)malloc(sizeof(uint32_t) * (H ? H : 1));
+  if (H) memcpy(h, hist, sizeof(uint32_t) * H);
+  sort_u32(h, H);
+  return h;
+}
+
+/* sampler.rs:128-147 */
+static void apply_repetition(float* l, uint32_t V, const uint32_t* hist,
+                             uint32_t H, float penalty) {
+  if (penalty == 1.0f || H == 0) return;
+  uint32_t* h = sorted_history(hist, H);
+  for (uint32_t i = 0; i < H; ++i) {
+    if (i > 0 && h[i] == h[i - 1]) continue; /* dedup */
+    uint32_t t = h[i];
+    if (t < V) {
+      float v = l[t];
+      l[t] = (v > 0.0f) ? v / penalty : v * penalty;
+    }
+  }
+  free(h);
+}
+
+/* Extension: l -= presence + count*frequency for tokens seen count > 0 times
+ * (formula of llm-tests/tests/mlc_parity.rs:1083, evaluated without FMA). */
+static void apply_presence_frequency(float* l, uint32_t V, const uint32_t* hist,
+                                     uint32_t H, float presence,
+                                     float frequency) {
+  if ((presence == 0.0f && frequency == 0.0f) || H == 0) return;
+  uint32_t* h = sorted_history(hist, H);
+  uint32_t i = 0;
+  while (i < H) {
+    uint32_t j = i;
+    while (j < H && h[j] == h[i]) ++j;
+    uint32_t t = h[i], count = j - i;
+    if (t < V) {
+      float cf = (float)count * frequency;
+      l[t] = l[t] - (presence + cf);
+    }
+    i = j;
+  }
+  free(h);
+}
+
+/* sampler.rs:150-157 */
+static void apply_temperature(float* l, uint32_t V, float t) {
+  if (t <= 1e-5f || t == 1.0f) return;
+  for (uint32_t i = 0; i < V; ++i) l[i] = l[i] / t;
+}
+
+typedef struct {
+  float* p;
+  uint32_t* idx;
+  uint32_t n;
+} plist;
+
+static void renormalize(plist* L) {
+  float s = 0.0f;
+  for (uint32_t j = 0; j < L->n; ++j) s += L->p[j];
+  if (s > 0.0f)
+    for (uint32_t j = 0; j < L->n; ++j) L->p[j] = L->p[j] / s;
+}
+
+static int params_invalid(const llmk_oracle_params* p) {
+  if (isnan(p->temperature) || isinf(p->temperature)) return 1;
+  if (p->top_k < 0) return 1;
+  if (!isfinite(p->top_p) || !isfinite(p->min_p) || p->min_p < 0.0f) return 1;
+  if (!isfinite(p->repetition_penalty) || !isfinite(p->presence_penalty) ||
+      !isfinite(p->frequency_penalty))
+    return 1;
+  return 0;
+}
+
+int llmk_oracle_sample_row(int mode, const float* logits, uint32_t V,
+                           const llmk_oracle_params* prm, const uint32_t* hist,
+                           uint32_t H, const uint32_t* mask, float u,
+                           uint32_t* out_token, uint32_t* out_ids,
+                           float* out_probs, uint32_t out_cap,
+                           uint32_t* out_count) {
+  if (V == 0) return -1; /* sampler.rs:30-32 */
+  if (params_invalid(prm)) return -2;
+  float* l = (float*)malloc(sizeof(float) * V);
+  memcpy(l, logits, sizeof(float) * V); /* sampler.rs:34 */
+  if (mode == LLMK_ORACLE_MIRROR)
+    for (uint32_t i = 0; i < V; ++i)
+      if (isnan(l[i])) l[i] = -INFINITY;
+
+  apply_repetition(l, V, hist, H, prm->repetition_penalty); /* :37 */
+  apply_presence_frequency(l, V, hist, H, prm->presence_penalty,
+                           prm->frequency_penalty);
+  if (mask)
+    for (uint32_t i = 0; i < V; ++i)
+      if (!((mask[i >> 5] >> (i & 31)) & 1u)) l[i] = -INFINITY;
+
+  if (prm->temperature <= 1e-5f) { /* greedy, :40-50 */
+    uint32_t best = 0;
+    float bv = l[0];
+    for (uint32_t i = 0; i < V; ++i)
+      if (l[i] > bv) {
+        bv = l[i];
+        best = i;
+      }
+    *out_token = best;
+    if (out_count) *out_count = 1;
+    if (out_cap > 0) {
+      if (out_ids) out_ids[0] = best;
+      if (out_probs) out_probs[0] = 1.0f;
+    }
+    free(l);
+    return 0;
+  }
+
+  /* The mirror normaliser works on the penalised, masked, unscaled logits. */
+  float S_mirror = 0.0f;
+  if (mode == LLMK_ORACLE_MIRROR)
+    S_mirror = llmk_oracle_normalizer(l, V, prm->temperature);
+
+  apply_temperature(l, V, prm->temperature); /* :53 */
+
+  /* Softmax, :56-71 */
+  float m = -INFINITY;
+  for (uint32_t i = 0; i < V; ++i) m = fmaxf(m, l[i]);
+  float* e = (float*)malloc(sizeof(float) * V);
+  for (uint32_t i = 0; i < V; ++i) {
+    if (l[i] == -INFINITY) e[i] = 0.0f;
+    else
+      e[i] = (mode == LLMK_ORACLE_MIRROR) ? llmk_oracle_exp_m(l[i] - m)
+                                          : expf(l[i] - m);
+  }
+  float S;
+  if (mode == LLMK_ORACLE_MIRROR) S = S_mirror;
+  else {
+    S = 0.0f;
+    for (uint32_t i = 0; i < V; ++i) S += e[i];
+  }
+  if (S > 0.0f)
+    for (uint32_t i = 0; i < V; ++i) e[i] = e[i] / S;
+
+  /* Sort (p desc, idx asc), :77 */
+  uint64_t* keys = (uint64_t*)malloc(sizeof(uint64_t) * V);
+  for (uint32_t i = 0; i < V; ++i) keys[i] = pkey(e[i], i);
+  sort_u64(keys, V);
+  plist L;
+  L.n = V;
+  L.p = (float*)malloc(sizeof(float) * V);
+  L.idx = (uint32_t*)malloc(sizeof(uint32_t) * V);
+  for (uint32_t j = 0; j < V; ++j) {
+    L.idx[j] = (uint32_t)(keys[j] & 0xffffffffu);
+    L.p[j] = u2f(~(uint32_t)(keys[j] >> 32));
+  }
+  free(keys);
+
+  /* min-p (extension): keep p >= min_p * p_max; renormalise if it cut. */
+  if (prm->min_p > 0.0f && L.n > 0) {
+    float thr = prm->min_p * L.p[0];
+    uint32_t cut = L.n;
+    for (uint32_t j = 0; j < L.n; ++j)
+      if (L.p[j] < thr) {
+        cut = j;
+        break;
+      }
+    if (cut < L.n) {
+      L.n = cut;
+      renormalize(&L);
+    }
+  }
+  /* top-k, :80-89 */
+  if (prm->top_k > 0 && (uint32_t)prm->top_k < L.n) {
+    L.n = (uint32_t)prm->top_k;
+    renormalize(&L);
+  }
+  /* top-p, :92-110 */
+  if (prm->top_p < 1.0f) {
+    float cum = 0.0f;
+    uint32_t cut = L.n;
+    for (uint32_t j = 0; j < L.n; ++j) {
+      cum += L.p[j];
+      if (cum >= prm->top_p) {
+        cut = j + 1;
+        break;
+      }
+    }
+    L.n = cut;
+    renormalize(&L);
+  }
+  /* draw, :113-124 */
+  uint32_t tok = (L.n > 0) ? L.idx[L.n - 1] : 0;
+  {
+    float cum = 0.0f;
+    for (uint32_t j = 0; j < L.n; ++j) {
+      cum += L.p[j];
+      if (u <= cum) {
+        tok = L.idx[j];
+        break;
+      }
+    }
+  }
+  *out_token = tok;
+  if (out_count) *out_count = L.n;
+  for (uint32_t j = 0; j < L.n && j < out_cap; ++j) {
+    if (out_ids) out_ids[j] = L.idx[j];
+    if (out_probs) out_probs[j] = L.p[j];
+  }
+  free(L.p);
+  free(L.idx);
+  free(e);
+  free(l);
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Batch driver                                                              */
+/* ------------------------------------------------------------------------ */
+
+typedef struct {
+  int mode;
+  const float* logits;
+  uint32_t B, V;
+  uint64_t stride;
+  const float *T, *tp, *mp, *rp, *pp, *fp;
+  const int32_t* tk;
+  const uint32_t *ho, *ht, *mask;
+  uint32_t mw;
+  const float* u;
+  uint32_t *out_tokens, *out_ids, *out_count;
+  float* out_probs;
+  uint32_t out_cap;
+  uint32_t r0, r1;
+  int status;
+} batch_job;
+
+static void* batch_worker(void* arg) {
+  batch_job* j = (batch_job*)arg;
+  j->status = 0;
+  for (uint32_t r = j->r0; r < j->r1; ++r) {
+    llmk_oracle_params p;
+    p.temperature = j->T ? j->T[r] : 1.0f;
+    p.top_k = j->tk ? j->tk[r] : 0;
+    p.top_p = j->tp ? j->tp[r] : 1.0f;
+    p.min_p = j->mp ? j->mp[r] : 0.0f;
+    p.repetition_penalty = j->rp ? j->rp[r] : 1.0f;
+    p.presence_penalty = j->pp ? j->pp[r] : 0.0f;
+    p.frequency_penalty = j->fp ? j->fp[r] : 0.0f;
+    const uint32_t* h = NULL;
+    uint32_t H = 0;
+    if (j->ho && j->ht) {
+      h = j->ht + j->ho[r];
+      H = j->ho[r + 1] - j->ho[r];
+    }
+    uint32_t cnt = 0;
+    int s = llmk_oracle_sample_row(
+        j->mode, j->logits + (uint64_t)r * j->stride, j->V, &p, h, H,
+        j->mask ? j->mask + (uint64_t)r * j->mw : NULL, j->u ? j->u[r] : 0.0f,
+        &j->out_tokens[r],
+        j->out_ids ? j->out_ids + (uint64_t)r * j->out_cap : NULL,
+        j->out_probs ? j->out_probs + (uint64_t)r * j->out_cap : NULL,
+        j->out_cap, &cnt);
+    if (j->out_count) j->out_count[r] = cnt;
+    if (s != 0) {
+      j->out_tokens[r] = 0xffffffffu;
+      if (j->status == 0) j->status = s;
+    }
+  }
+  return NULL;
+}
+
+int llmk_oracle_sample_batch(int mode, const float* logits, uint32_t B,
+                             uint32_t V, uint64_t row_stride,
+                             const float* temperature, const int32_t* top_k,
+                             const float* top_p, const float* min_p,
+                             const float* repetition, const float* presence,
+                             const float* frequency,
+                             const uint32_t* hist_offsets,
+                             const uint32_t* hist_tokens,
+                             const uint32_t* mask, uint32_t mask_words,
+                             const float* uniforms, uint32_t* out_tokens,
+                             uint32_t* out_ids, float* out_probs,
+                             uint32_t out_cap, uint32_t* out_count,
+                             int nthreads) {
+  if (V == 0 || B == 0) return -1;
+  if (nthreads < 1) nthreads = 1;
+  if ((uint32_t)nthreads > B) nthreads = (int)B;
+  batch_job* jobs = (batch_job*)calloc((size_t)nthreads, sizeof(batch_job));
+  pthread_t* th = (pthread_t*)calloc((size_t)nthreads, sizeof(pthread_t));
+  for (int t = 0; t < nthreads; ++t) {
+    batch_job* j = &jobs[t];
+    j->mode = mode;
+    j->logits = logits;
+    j->B = B;
+    j->V = V;
+    j->stride = row_stride;
+    j->T = temperature;
+    j->tk = top_k;
+    j->tp = top_p;
+    j->mp = min_p;
+    j->rp = repetition;
+    j->pp = presence;
+    j->fp = frequency;
+    j->ho = hist_offsets;
+    j->ht = hist_tokens;
+    j->mask = mask;
+    j->mw = mask_words;
+    j->u = uniforms;
+    j->out_tokens = out_tokens;
+    j->out_ids = out_ids;
+    j->out_probs = out_probs;
+    j->out_cap = out_cap;
+    j->out_count = out_count;
+    j->r0 = (uint32_t)(((uint64_t)B * t) / nthreads);
+    j->r1 = (uint32_t)(((uint64_t)B * (t + 1)) / nthreads);
+  }
+  if (nthreads == 1) batch_worker(&jobs[0]);
+  else {
+    for (int t = 0; t < nthreads; ++t)
+      pthread_create(&th[t], NULL, batch_worker, &jobs[t]);
+    for (int t = 0; t < nthreads; ++t) pthread_join(th[t], NULL);
+  }
+  int status = 0;
+  for (int t = 0; t < nthreads; ++t)
+    if (jobs[t].status && !status) status = jobs[t].status;
+  free(jobs);
+  free(th);
+  return status;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Mask-form helpers                                                         */
+/* ------------------------------------------------------------------------ */
+
+void llmk_oracle_apply_repetition_penalty(float* logits, uint32_t V,
+                                          const uint32_t* hist, uint32_t H,
+                                          float penalty) {
+  apply_repetition(logits, V, hist, H, penalty);
+}
+
+void llmk_oracle_apply_temperature(float* logits, uint32_t V, float t) {
+  apply_temperature(logits, V, t);
+}
+
+/* sampler.rs:160-173: threshold = k-th largest value; values below it are
+ * masked, so ties at the threshold survive (more than k can remain). */
+void llmk_oracle_apply_top_k(float* logits, uint32_t V, int64_t k) {
+  if (k <= 0 || (uint64_t)k >= V) return;
+  uint32_t* keys = (uint32_t*)malloc(sizeof(uint32_t) * V);
+  for (uint32_t i = 0; i < V; ++i) {
+    uint32_t b = f2u(logits[i]);
+    keys[i] = (b & 0x80000000u) ? ~b : (b | 0x80000000u); /* ascending order key */
+  }
+  sort_u32(keys, V);
+  uint32_t tk = keys[V - (uint32_t)k];
+  uint32_t tb = (tk & 0x80000000u) ? (tk & 0x7fffffffu) : ~tk;
+  float thr = u2f(tb);
+  for (uint32_t i = 0; i < V; ++i)
+    if (logits[i] < thr) logits[i] = -INFINITY;
+  free(keys);
+}
+
+/* sampler.rs:176-216 */
+void llmk_oracle_apply_top_p(int mode, float* logits, uint32_t V, float top_p) {
+  if (top_p >= 1.0f || V == 0) return;
+  float m = -INFINITY;
+  for (uint32_t i = 0; i < V; ++i) m = fmaxf(m, logits[i]);
+  float* e = (float*)malloc(sizeof(float) * V);
+  for (uint32_t i = 0; i < V; ++i) {
+    if (logits[i] == -INFINITY) e[i] = 0.0f;
+    else
+      e[i] = (mode == LLMK_ORACLE_MIRROR) ? llmk_oracle_exp_m(logits[i] - m)
+                                          : expf(logits[i] - m);
+  }
+  float S;
+  if (mode == LLMK_ORACLE_MIRROR) {
+    float* lp = (float*)malloc(sizeof(float) * V);
+    for (uint32_t i = 0; i < V; ++i) lp[i] = isnan(logits[i]) ? -INFINITY : logits[i];
+    S = llmk_oracle_normalizer(lp, V, 1.0f);
+    free(lp);
+  } else {
+    S = 0.0f;
+    for (uint32_t i = 0; i < V; ++i) S += e[i];
+  }
+  if (!(S > 0.0f)) {
+    free(e);
+    return;
+  }
+  for (uint32_t i = 0; i < V; ++i) e[i] = e[i] / S;
+  uint64_t* keys = (uint64_t*)malloc(sizeof(uint64_t) * V);
+  for (uint32_t i = 0; i < V; ++i) keys[i] = pkey(e[i], i);
+  sort_u64(keys, V);
+  float cum = 0.0f;
+  uint32_t cut = V;
+  for (uint32_t j = 0; j < V; ++j) {
+    cum += u2f(~(uint32_t)(keys[j] >> 32));
+    if (cum >= top_p) {
+      cut = j + 1;
+      break;
+    }
+  }
+  unsigned char* keep = (unsigned char*)calloc(V, 1);
+  for (uint32_t j = 0; j < cut; ++j) keep[keys[j] & 0xffffffffu] = 1;
+  for (uint32_t i = 0; i < V; ++i)
+    if (!keep[i]) logits[i] = -INFINITY;
+  free(keep);
+  free(keys);
+  free(e);
+}
+
+uint32_t llmk_oracle_sample_simple(int mode, const float* logits, uint32_t V,
+                                   float temperature, float u) {
+  llmk_oracle_params p = {temperature, 0, 1.0f, 0.0f, 1.0f, 0.0f, 0.0f};
+  uint32_t tok = 0, cnt = 0;
+  if (llmk_oracle_sample_row(mode, logits, V, &p, NULL, 0, NULL, u, &tok, NULL,
+                             NULL, 0, &cnt) != 0)
+    return 0; /* sampler.rs:227 unwrap_or(0) */
+  return tok;
+}
+
+/* ------------------------------------------------------------------------ */
+/* exp_m exhaustive scan                                                     */
+/* ------------------------------------------------------------------------ */
+
+void llmk_oracle_exp_scan(uint32_t lo_bits, uint32_t hi_bits,
+                          uint64_t* n_checked, uint64_t* n_mismatch,
+                          uint64_t* n_nonmono, uint32_t* max_ulp) {
+  uint64_t chk = 0, mis = 0, nm = 0;
+  uint32_t mu = 0;
+  float prev = 0.0f;
+  int have_prev = 0;
+  for (uint64_t b = lo_bits; b <= hi_bits; ++b) {
+    float y = u2f((uint32_t)b);
+    float a = llmk_oracle_exp_m(y);
+    float r = expf(y);
+    ++chk;
+    if (f2u(a) != f2u(r)) {
+      ++mis;
+      uint32_t d = f2u(a) > f2u(r) ? f2u(a) - f2u(r) : f2u(r) - f2u(a);
+      if (d > mu) mu = d;
+    }
+    /* bit patterns ascend in magnitude for negative floats: e^y must not grow */
+    if (have_prev && a > prev) ++nm;
+    prev = a;
+    have_prev = 1;
+  }
+  *n_checked = chk;
+  *n_mismatch = mis;
+  *n_nonmono = nm;
+  *max_ulp = mu;
+}

@@ -1,0 +1,160 @@
+"""ctypes binding of the CPU oracle (oracle/_build/libllmk_oracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, as the checker / CPU baseline.  The product path
+(llm-rs_amd) never imports it.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "_build", "libllmk_oracle.so")
+REF, MIRROR = 0, 1
+
+_lib = None
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def load():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB):
+        build()
+    lib = ctypes.CDLL(LIB)
+    P = ctypes.c_void_p
+    u32, i32, f32 = ctypes.c_uint32, ctypes.c_int32, ctypes.c_float
+    lib.llmk_oracle_sample_batch.argtypes = [
+        ctypes.c_int, P, u32, u32, ctypes.c_uint64, P, P, P, P, P, P, P, P, P, P, u32,
+        P, P, P, P, u32, P, ctypes.c_int]
+    lib.llmk_oracle_sample_batch.restype = ctypes.c_int
+    lib.llmk_oracle_exp_m.argtypes = [f32]
+    lib.llmk_oracle_exp_m.restype = f32
+    lib.llmk_oracle_exp2_f.argtypes = [f32]
+    lib.llmk_oracle_exp2_f.restype = f32
+    lib.llmk_oracle_libm_expf.argtypes = [f32]
+    lib.llmk_oracle_libm_expf.restype = f32
+    lib.llmk_oracle_normalizer.argtypes = [P, u32, f32]
+    lib.llmk_oracle_normalizer.restype = f32
+    lib.llmk_oracle_apply_repetition_penalty.argtypes = [P, u32, P, u32, f32]
+    lib.llmk_oracle_apply_temperature.argtypes = [P, u32, f32]
+    lib.llmk_oracle_apply_top_k.argtypes = [P, u32, ctypes.c_int64]
+    lib.llmk_oracle_apply_top_p.argtypes = [ctypes.c_int, P, u32, f32]
+    lib.llmk_oracle_sample_simple.argtypes = [ctypes.c_int, P, u32, f32, f32]
+    lib.llmk_oracle_sample_simple.restype = u32
+    u64p = ctypes.POINTER(ctypes.c_uint64)
+    lib.llmk_oracle_exp_scan.argtypes = [u32, u32, u64p, u64p, u64p, ctypes.POINTER(u32)]
+    _lib = lib
+    return lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def sample_batch(mode, logits, temperature=None, top_k=None, top_p=None, min_p=None,
+                 repetition=None, presence=None, frequency=None, hist_offsets=None,
+                 hist_tokens=None, mask=None, uniforms=None, out_cap=0, nthreads=1, V=None):
+    """Returns (tokens, ids, probs, counts) as numpy arrays.  logits: float32 [B, stride]."""
+    lib = load()
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    B, stride = logits.shape
+    V = stride if V is None else V
+    c = lambda a, dt: None if a is None else np.ascontiguousarray(a, dtype=dt)
+    T, K, TP, MP = c(temperature, np.float32), c(top_k, np.int32), c(top_p, np.float32), c(min_p, np.float32)
+    R, PR, FR = c(repetition, np.float32), c(presence, np.float32), c(frequency, np.float32)
+    HO, HT = c(hist_offsets, np.uint32), c(hist_tokens, np.uint32)
+    if HT is not None and HT.size == 0:
+        HT = np.zeros(1, np.uint32)
+    M = c(mask, np.uint32)
+    U = c(uniforms if uniforms is not None else np.zeros(B), np.float32)
+    tok = np.zeros(B, np.uint32)
+    cnt = np.zeros(B, np.uint32)
+    ids = np.zeros((B, max(out_cap, 1)), np.uint32)
+    probs = np.zeros((B, max(out_cap, 1)), np.float32)
+    rc = lib.llmk_oracle_sample_batch(
+        mode, _p(logits), B, V, stride, _p(T), _p(K), _p(TP), _p(MP), _p(R), _p(PR), _p(FR),
+        _p(HO), _p(HT), _p(M), 0 if M is None else M.shape[1], _p(U), _p(tok),
+        _p(ids) if out_cap else None, _p(probs) if out_cap else None, out_cap, _p(cnt), nthreads)
+    return rc, tok, ids[:, :out_cap], probs[:, :out_cap], cnt
+
+
+def sample_workload(mode, w, out_cap=0, nthreads=1, rows=None):
+    """Run the oracle on an llmk.synth.Workload (optionally a subset of rows)."""
+    sel = slice(None) if rows is None else rows
+    lg = w.logits[sel]
+    ho, ht = w.hist_offsets, w.hist_tokens
+    if rows is not None:
+        idx = np.arange(w.B)[sel]
+        hs = [ht[ho[i]:ho[i + 1]] for i in idx]
+        ho = np.zeros(len(hs) + 1, np.uint32)
+        for i, h in enumerate(hs):
+            ho[i + 1] = ho[i] + len(h)
+        ht = np.concatenate(hs).astype(np.uint32) if ho[-1] else np.zeros(0, np.uint32)
+    return sample_batch(mode, lg, w.temperature[sel], w.top_k[sel], w.top_p[sel], w.min_p[sel],
+                        w.repetition[sel], w.presence[sel], w.frequency[sel], ho, ht,
+                        None if w.mask is None else w.mask[sel], w.uniforms[sel], out_cap, nthreads)
+
+
+def _f32p(x):
+    return np.ascontiguousarray(x, dtype=np.float32)
+
+
+def apply_repetition_penalty(logits, hist, penalty):
+    l = _f32p(logits).copy()
+    h = np.ascontiguousarray(hist, dtype=np.uint32)
+    load().llmk_oracle_apply_repetition_penalty(_p(l), l.size, _p(h) if h.size else None, h.size, penalty)
+    return l
+
+
+def apply_temperature(logits, t):
+    l = _f32p(logits).copy()
+    load().llmk_oracle_apply_temperature(_p(l), l.size, t)
+    return l
+
+
+def apply_top_k(logits, k):
+    l = _f32p(logits).copy()
+    load().llmk_oracle_apply_top_k(_p(l), l.size, k)
+    return l
+
+
+def apply_top_p(mode, logits, top_p):
+    l = _f32p(logits).copy()
+    load().llmk_oracle_apply_top_p(mode, _p(l), l.size, top_p)
+    return l
+
+
+def sample_simple(mode, logits, t, u):
+    l = _f32p(logits)
+    return int(load().llmk_oracle_sample_simple(mode, _p(l), l.size, t, u))
+
+
+def normalizer(lp, temperature):
+    l = _f32p(lp)
+    return float(load().llmk_oracle_normalizer(_p(l), l.size, temperature))
+
+
+def exp_m(y):
+    return np.float32(load().llmk_oracle_exp_m(float(y)))
+
+
+def exp2_f(d):
+    return np.float32(load().llmk_oracle_exp2_f(float(d)))
+
+
+def libm_expf(y):
+    return np.float32(load().llmk_oracle_libm_expf(float(y)))
+
+
+def exp_scan(lo_bits, hi_bits):
+    a, b, c = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
+    d = ctypes.c_uint32()
+    load().llmk_oracle_exp_scan(lo_bits, hi_bits, ctypes.byref(a), ctypes.byref(b), ctypes.byref(c), ctypes.byref(d))
+    return a.value, b.value, c.value, d.value
