@@ -1,0 +1,182 @@
+"""Benchmark of the batched sampling step on one MI355X.
+
+Workload (default): config C3 of the contract — B=256 rows, V=151936 fp32 logits
+~N(0,3^2) with 0.1% of entries from N(8,2^2), top-k 50, top-p 0.95, T 0.7,
+repetition 1.1 / presence 0.5 / frequency 0.3 over 2048-token Zipf(1.1)
+histories, one caller uniform per row.  A step = one llmk_sample_batch call
+over the whole batch with every input already resident in HBM.  Several
+copies of the logits are rotated so that consecutive steps do not re-read the
+previous step's logits from the 256 MB Infinity Cache.
+
+Prints ONE JSON line on stdout.  Extra diagnostics go to stderr.
+"""
+import argparse
+import json
+import os
+import subprocess
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "llm-rs_amd"))
+sys.path.insert(0, ROOT)
+
+METRIC = "sampled tokens/sec and µs/step at B=256, V=151936 fp32; % HBM roofline"
+HBM_PEAK_GBPS = 8000.0
+MALL_BYTES = 256 << 20
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(w, budget_s=12.0):
+    """The oracle's `ref` mode (a C restatement of llm-core/src/sampler.rs
+    sample_logits, full-vocabulary sort per row) timed on this host: rows
+    serial on one core, as Scheduler::step calls it (scheduler.rs:138-145)."""
+    import numpy as np
+    from oracle import llmk_oracle as O
+    O.load()
+    rows_done, t_total = 0, 0.0
+    order = np.arange(w.B)
+    while t_total < budget_s and rows_done < 4 * w.B:
+        sel = order[rows_done % w.B: rows_done % w.B + 32]
+        t0 = time.perf_counter()
+        O.sample_workload(O.REF, w, nthreads=1, rows=sel)
+        t_total += time.perf_counter() - t0
+        rows_done += len(sel)
+    us_per_row = t_total / rows_done * 1e6
+    # all host cores, rows spread over threads (reported beside it)
+    nth = os.cpu_count() or 1
+    nth = min(nth, 16)
+    t0 = time.perf_counter()
+    O.sample_workload(O.REF, w, nthreads=nth)
+    t_all = time.perf_counter() - t0
+    return {
+        "value": 1e6 / us_per_row,
+        "unit": "tokens/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{rows_done} rows of the {w.name} workload (oracle ref mode, 1 thread, "
+                  f"{t_total:.1f} s); us/row {us_per_row:.0f}",
+        "all_cores": {"threads": nth, "tokens_per_s": w.B / t_all, "step_ms": t_all * 1e3},
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="C3")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--sets", type=int, default=0, help="logit copies rotated (0 = auto)")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build measures one GPU only (rows shard with no communication; "
+              "see DESIGN.md); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    import llmk
+    from llmk import synth
+    w = synth.make(args.config)
+    dev = torch.device("cuda:0")
+    db0 = w.to_device(dev)
+    step_bytes = w.algorithmic_bytes()
+    logit_bytes = db0.logits.numel() * db0.logits.element_size()
+    nsets = args.sets or max(1, int(np.ceil(2 * MALL_BYTES / logit_bytes)) + 1)
+    dbs = [db0]
+    for _ in range(nsets - 1):
+        d = llmk.DeviceBatch(**{k: getattr(db0, k) for k in db0.__dataclass_fields__})
+        d.logits = db0.logits.clone()
+        dbs.append(d)
+    s = llmk.HipSampler(max_batch=w.B, max_vocab=w.V)
+    B = w.B
+    tok = torch.empty(B, dtype=torch.int32, device=dev)
+    cnt = torch.empty(B, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream()
+
+    for i in range(args.warmup):
+        s.launch(dbs[i % nsets], tok, out_count=cnt, stream=stream)
+    torch.cuda.synchronize()
+
+    K = args.steps
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_start.record(stream)
+    for i in range(K):
+        ev[i][0].record(stream)
+        s.launch(dbs[i % nsets], tok, out_count=cnt, stream=stream)
+        ev[i][1].record(stream)
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    total_ms = t_start.elapsed_time(t_end)
+    kern_ms = [a.elapsed_time(b) for a, b in ev]
+    ms_per_step = total_ms / K
+    kern_avg_ms = float(np.mean(kern_ms))
+    value = B / (ms_per_step * 1e-3)
+    achieved = step_bytes / (kern_avg_ms * 1e-3) / 1e9
+
+    # same-buffer (Infinity-Cache-warm) rate, for reference only
+    torch.cuda.synchronize()
+    a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a0.record(stream)
+    for i in range(K):
+        s.launch(db0, tok, out_count=cnt, stream=stream)
+    a1.record(stream)
+    torch.cuda.synchronize()
+    warm_ms = a0.elapsed_time(a1) / K
+
+    log(f"[bench] {w.name}: {ms_per_step*1e3:.2f} us/step (kernel avg {kern_avg_ms*1e3:.2f} us, "
+        f"min {min(kern_ms)*1e3:.2f}, max {max(kern_ms)*1e3:.2f}), warm {warm_ms*1e3:.2f} us, "
+        f"{achieved:.0f} GB/s algorithmic, sets {nsets}")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(w)
+        log(f"[bench] cpu baseline: {cpu}")
+
+    esz = "f32" if w.dtype == "f32" else "bf16"
+    out = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "us_per_step": ms_per_step * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": esz,
+        "data": f"synthetic (seeded, {w.name} distributions); {nsets} logit copies rotated",
+        "config": {
+            "workload": f"{w.name}: B={w.B} V={w.V} {esz} logits, top-k 50, top-p 0.95, T 0.7, "
+                        "repetition 1.1 / presence 0.5 / frequency 0.3, histories 2048 Zipf(1.1)"
+                        if w.name == "C3" else w.name,
+            "batch": w.B, "vocab": w.V, "algorithmic_bytes_per_step": step_bytes,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBPS,
+            "traffic": None,
+            "kernel": "llmk::stream_kernel",
+            "kernel_avg_us": kern_avg_ms * 1e3,
+        },
+        "warm_us_per_step": warm_ms * 1e3,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -50,6 +50,7 @@ extern "C" {
 /* Bits of the device status word (llmk_sampler_status). */
 #define LLMK_STATUS_INVALID_PARAMS 0x1u
 #define LLMK_STATUS_HISTORY_OVERFLOW 0x2u
+#define LLMK_STATUS_SLOT_TIMEOUT 0x4u /* slow-path scratch slot not acquired */
 
 typedef struct llmk_sampler llmk_sampler; /* opaque; owns device workspace */
 

@@ -4,26 +4,31 @@
 // llm-core/src/sampler.rs:25-125 (sample_logits) once per row, with one
 // stream-ordered call that samples the whole batch on the GPU.
 //
-// Kernels
-//   stream_kernel   one workgroup per (row, vocabulary segment).  Reads the
-//                   logits of its segment once from HBM (128-bit / 64-bit
-//                   non-temporal loads), applies the penalties (from an LDS
-//                   bitmap + hash of the row's history), the allow-mask, and
-//                   per 1024-token tile computes the tile max and
-//                   sum 2^((l - max) log2(e)/T) (the softmax normaliser's
-//                   partial) — or the tile argmax for greedy rows — and
-//                   collects top-candidates above a rising threshold kept
-//                   in an LDS histogram over the logits' order-preserving
-//                   keys.  The last workgroup of a row to finish (arrival
-//                   counter) runs `finalize`: merges the tile partials into
-//                   the normaliser S, computes exact probabilities of the
-//                   candidates, sorts them by (p desc, idx asc), proves that
-//                   no non-candidate can precede the ones it uses, and runs
-//                   min-p / top-k / top-p / the draw exactly as sampler.rs.
-//   slow_kernel     rows the fast path cannot prove exact (top-k = 0 with a
-//                   large nucleus, candidate overflow, fully masked rows):
-//                   exact probabilities of the whole row, stable LSD radix
-//                   sort in global memory, the same sequential semantics.
+// One kernel, `stream_kernel`, one workgroup per (row, vocabulary segment):
+//   * history  the row's token history restricted to the segment becomes an
+//              LDS bitmap + popcount prefix (rank of a token among the
+//              history's distinct tokens) and a table of the penalised logits
+//              of those tokens (repetition, presence, frequency).
+//   * stream   the segment's logits are read once from HBM with 128-bit (fp32)
+//              / 64-bit (bf16) non-temporal loads, 1024-token tiles, each lane
+//              owning 4 runs of 4 consecutive tokens.  Per tile: history
+//              tokens take their penalised value, the allow-mask applies, and
+//              the wave computes the tile max and the tile's share of the
+//              softmax normaliser sum 2^((l - max) log2(e)/T) with a DPP
+//              balanced-tree sum — or the tile argmax for greedy rows — and
+//              appends top candidates above a rising threshold kept in an LDS
+//              histogram of the logits' order-preserving keys.
+//   * finalize the last workgroup of the row (arrival counter when a row spans
+//              several workgroups) merges the tile partials into the
+//              normaliser S, computes exact probabilities of the candidates,
+//              ranks them by (p desc, idx asc), proves no other token can
+//              precede the ones used, and runs min-p / top-k / top-p / the
+//              draw exactly as sampler.rs:77-124.
+//   * slow     rows the candidate path cannot prove exact (top-k = 0 with a
+//              large nucleus, candidate overflow, fully masked rows) are done
+//              by the same workgroup: exact probabilities of the whole row,
+//              a stable LSD radix sort in a global scratch slot, and the same
+//              sequential semantics.
 //
 // Numerics are fixed (llmk_numerics.h); the CPU mirror oracle restates them.
 #include <hip/hip_runtime.h>
@@ -38,23 +43,39 @@
 
 namespace llmk {
 
+// Explicit address spaces: LDS (3) and global (1).  Pointers that pass
+// through structs or function parameters would otherwise become generic
+// (flat) pointers, whose loads wait on both the vector-memory and the LDS
+// counters.
+#define LDS __attribute__((address_space(3)))
+#define GLB __attribute__((address_space(1)))
+template <class T>
+__device__ __forceinline__ GLB T* G(T* p) { return (GLB T*)p; }
+template <class T>
+__device__ __forceinline__ const GLB T* G(const T* p) { return (const GLB T*)p; }
+
+typedef float f2v __attribute__((ext_vector_type(2)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+
 constexpr uint32_t TILE = 1024;      // canonical vocabulary tile
 constexpr int WAVE = 64;
-constexpr int NW = 8;                // waves per stream workgroup
-constexpr int NT = NW * WAVE;        // 512 threads
+constexpr int NW = 16;               // waves per workgroup
+constexpr int NT = NW * WAVE;        // 1024 threads
 constexpr uint32_t NBINS = 4096;     // fine histogram bins: key >> 20
 constexpr uint32_t BIN_SHIFT = 20;
 constexpr uint32_t CBIN_SHIFT = 26;  // coarse bins: key >> 26 (64 bins)
-constexpr uint32_t HASH_SLOTS = 8192;
-constexpr uint32_t HASH_MAX_PROBE = 1024;
+constexpr uint32_t U_MAX = 8192;     // distinct history tokens per segment
 constexpr uint32_t CAND_CAP = 8192;  // candidate entries per workgroup
 constexpr uint32_t SORT_CAP = 4096;  // candidates sorted in finalize
-constexpr uint32_t KMAX = 2048;      // largest top-k served by the fast path
-constexpr uint32_t KCAND_NOK = 512;  // candidate target when top-k is off
+constexpr uint32_t KMAX = 1024;      // largest top-k served by the fast path
+constexpr uint32_t KCAND_NOK = 1024; // candidate target when top-k is off
 constexpr uint32_t MAX_TILES = 1024; // max_vocab <= 2^20
+constexpr uint32_t MAX_SEG = 64;     // segments per row
 constexpr uint32_t MAX_WGS = 4096;   // candidate-buffer pool entries
-constexpr int SLOW_NT = 1024;        // slow-path workgroup
-constexpr uint32_t SLOW_WGS = 64;    // concurrent slow rows
+constexpr uint32_t SLOW_SLOTS = 64;  // global scratch slots of the slow path
+constexpr uint32_t STAGE = 2048;     // slow path: LDS window of the sorted list
 constexpr uint32_t EMPTY = 0xffffffffu;
 constexpr float NEG_INF = -__builtin_huge_valf();
 
@@ -75,19 +96,18 @@ struct Args {
   float* out_probs;
   uint32_t out_cap;
   uint32_t G, tps, ntiles;
-  uint32_t xcd_map;  // 1: segments of a row share an XCD
+  uint32_t xcd_map;  // 1: the segments of a row share an XCD
 };
 
 struct Ws {
   uint32_t* row_arrive;  // [max_batch]
-  float2* tile_part;     // [max_batch][MAX_TILES]
-  uint4* seg_meta;       // [pool]: count, beta, flags, -
-  uint2* cand;           // [pool][CAND_CAP]: value bits, index
-  uint32_t* row_flags;   // [max_batch]: 1 = needs slow path
-  float4* row_stats;     // [max_batch]: S, m, L, -
-  uint64_t* slow_keys;   // [SLOW_WGS][3][max_vocab]
-  float* slow_p;         // [SLOW_WGS][max_vocab]
-  uint32_t* slow_idx;    // [SLOW_WGS][max_vocab]
+  f2v* tile_part;        // [max_batch][MAX_TILES]: tile max, tile sum
+  u4v* seg_meta;         // [pool]: count, beta, flags, -
+  u2v* cand;             // [pool][CAND_CAP]: value bits, index
+  uint32_t* slow_lock;   // [SLOW_SLOTS]
+  uint64_t* slow_keys;   // [SLOW_SLOTS][3][max_vocab]
+  float* slow_p;         // [SLOW_SLOTS][max_vocab]
+  uint32_t* slow_idx;    // [SLOW_SLOTS][max_vocab]
   uint32_t* status;      // [1]
   uint32_t max_vocab;
 };
@@ -96,12 +116,12 @@ struct RowP {
   float T, top_p, min_p, rp, pp, fp;
   int32_t K;
   uint32_t mode;
-  uint32_t Kc;  // candidate target; 0 = fast path impossible
+  uint32_t Kc;  // candidate target; 0 = candidate path impossible
 };
 
 __device__ __forceinline__ bool finitef(float x) { return __builtin_isfinite(x); }
 
-__device__ RowP row_params(const Args& a, uint32_t b) {
+__device__ __forceinline__ RowP row_params(const Args& a, uint32_t b) {
   RowP r;
   r.T = a.T ? a.T[b] : 1.0f;
   r.top_p = a.top_p ? a.top_p[b] : 1.0f;
@@ -120,98 +140,115 @@ __device__ RowP row_params(const Args& a, uint32_t b) {
 }
 
 // ---------------------------------------------------------------------------
-// Wave helpers (wave64)
+// Wave64 helpers on DPP (row_shr within 16-lane rows, row_bcast across rows)
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) x = fmaxf(x, __shfl_xor(x, o));
-  return x;
+template <int CTRL, int RM, bool BC>
+__device__ __forceinline__ float dppf(float old, float src) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(
+      __float_as_int(old), __float_as_int(src), CTRL, RM, 0xf, BC));
 }
-__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t y = __shfl_xor(x, o);
-    x = y < x ? y : x;
-  }
-  return x;
+template <int CTRL, int RM, bool BC>
+__device__ __forceinline__ uint32_t dppu(uint32_t old, uint32_t src) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)src, CTRL, RM, 0xf, BC);
 }
-// Balanced-tree sum over lanes 0..63 (lane pairs (2i,2i+1), then pairs of
-// pairs, ...): every lane ends with the same value.
+__device__ __forceinline__ float bcast63f(float x) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+}
+__device__ __forceinline__ uint32_t bcast63u(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
+}
+
+// Sum of lanes 0..63 as a balanced binary tree over contiguous lanes
+// ((x0+x1)+(x2+x3))+...; the root forms in lane 63 and is broadcast.
 __device__ __forceinline__ float wave_tree_sum(float x) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) x = x + __shfl_xor(x, o);
+  x = x + dppf<0x111, 0xf, true>(0.0f, x);
+  x = x + dppf<0x112, 0xf, true>(0.0f, x);
+  x = x + dppf<0x114, 0xf, true>(0.0f, x);
+  x = x + dppf<0x118, 0xf, true>(0.0f, x);
+  x = x + dppf<0x142, 0xa, false>(0.0f, x);
+  x = x + dppf<0x143, 0xc, false>(0.0f, x);
+  return bcast63f(x);
+}
+__device__ __forceinline__ float wave_max(float x) {
+  x = fmaxf(x, dppf<0x111, 0xf, false>(x, x));
+  x = fmaxf(x, dppf<0x112, 0xf, false>(x, x));
+  x = fmaxf(x, dppf<0x114, 0xf, false>(x, x));
+  x = fmaxf(x, dppf<0x118, 0xf, false>(x, x));
+  x = fmaxf(x, dppf<0x142, 0xa, false>(x, x));
+  x = fmaxf(x, dppf<0x143, 0xc, false>(x, x));
+  return bcast63f(x);
+}
+__device__ __forceinline__ uint32_t umin(uint32_t a, uint32_t b) { return a < b ? a : b; }
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
+  x = umin(x, dppu<0x111, 0xf, false>(x, x));
+  x = umin(x, dppu<0x112, 0xf, false>(x, x));
+  x = umin(x, dppu<0x114, 0xf, false>(x, x));
+  x = umin(x, dppu<0x118, 0xf, false>(x, x));
+  x = umin(x, dppu<0x142, 0xa, false>(x, x));
+  x = umin(x, dppu<0x143, 0xc, false>(x, x));
+  return bcast63u(x);
+}
+// Inclusive prefix sum over lanes.
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
+  x += dppu<0x111, 0xf, true>(0u, x);
+  x += dppu<0x112, 0xf, true>(0u, x);
+  x += dppu<0x114, 0xf, true>(0u, x);
+  x += dppu<0x118, 0xf, true>(0u, x);
+  x += dppu<0x142, 0xa, false>(0u, x);
+  x += dppu<0x143, 0xc, false>(0u, x);
   return x;
 }
-__device__ __forceinline__ uint32_t wave_incl_prefix(uint32_t x, int lane) {
+__device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                   __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// Block-wide exclusive scan of one value per thread (NT threads).
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t x, LDS uint32_t* red, uint32_t& total) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const uint32_t incl = wave_incl_scan(x);
+  if (lane == 63) red[wv] = incl;
+  __syncthreads();
+  uint32_t off = 0, tot = 0;
 #pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t y = __shfl_up(x, o);
-    if (lane >= o) x += y;
-  }
-  return x;
-}
-
-// ---------------------------------------------------------------------------
-// History: LDS bitmap over a vocabulary range + hash of counts
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t hslot(uint32_t t) {
-  return (t * 2654435761u) >> (32 - 13);  // HASH_SLOTS = 2^13
-}
-
-__device__ bool hash_insert(uint32_t* hk, uint32_t* hc, uint32_t t) {
-  uint32_t s = hslot(t);
-  for (uint32_t n = 0; n < HASH_MAX_PROBE; ++n) {
-    const uint32_t old = atomicCAS(&hk[s], EMPTY, t);
-    if (old == EMPTY || old == t) {
-      atomicAdd(&hc[s], 1u);
-      return true;
-    }
-    s = (s + 1) & (HASH_SLOTS - 1);
-  }
-  return false;
-}
-
-__device__ uint32_t hash_count(const uint32_t* hk, const uint32_t* hc,
-                               uint32_t t) {
-  uint32_t s = hslot(t);
-  for (uint32_t n = 0; n < HASH_MAX_PROBE; ++n) {
-    const uint32_t k = hk[s];
-    if (k == t) return hc[s];
-    if (k == EMPTY) return 0;
-    s = (s + 1) & (HASH_SLOTS - 1);
-  }
-  return 0;
-}
-
-// Fill bitmap[(t-lo)>>5] and the hash for history tokens t in [lo, hi).
-template <int NTH>
-__device__ void build_history(const Args& a, const RowP& P, uint32_t b,
-                              uint32_t lo, uint32_t hi, uint32_t nwords,
-                              uint32_t* bitmap, uint32_t* hk, uint32_t* hc,
-                              uint32_t* flags) {
-  const uint32_t tid = threadIdx.x;
-  for (uint32_t i = tid; i < nwords; i += NTH) bitmap[i] = 0;
-  const bool need_cnt = P.fp != 0.0f;
-  if (need_cnt)
-    for (uint32_t i = tid; i < HASH_SLOTS; i += NTH) {
-      hk[i] = EMPTY;
-      hc[i] = 0;
-    }
-  __syncthreads();
-  const bool need_pen = P.rp != 1.0f || P.pp != 0.0f || P.fp != 0.0f;
-  if (need_pen && a.hoff && a.htok) {
-    const uint32_t h0 = a.hoff[b], h1 = a.hoff[b + 1];
-    for (uint32_t i = h0 + tid; i < h1; i += NTH) {
-      const uint32_t t = a.htok[i];
-      if (t >= lo && t < hi) {
-        atomicOr(&bitmap[(t - lo) >> 5], 1u << (t & 31));
-        if (need_cnt && !hash_insert(hk, hc, t)) atomicOr(flags, FLAG_HIST_OVERFLOW);
-      }
-    }
+  for (int i = 0; i < NW; ++i) {
+    const uint32_t c = red[i];
+    off += (i < wv) ? c : 0u;
+    tot += c;
   }
   __syncthreads();
+  total = tot;
+  return off + incl - x;
+}
+__device__ __forceinline__ float block_max(float x, LDS float* red) {
+  x = wave_max(x);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  if (lane == 0) red[wv] = x;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) r = fmaxf(r, red[i]);
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ uint32_t block_min_u32(uint32_t x, LDS uint32_t* red) {
+  x = wave_min_u32(x);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  if (lane == 0) red[wv] = x;
+  __syncthreads();
+  uint32_t r = red[0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) r = umin(r, red[i]);
+  __syncthreads();
+  return r;
 }
 
+// Wait until this wave's global stores have reached L2 (vmcnt(0)).
+__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+
+// ---------------------------------------------------------------------------
+// History: bitmap over a vocabulary range, popcount prefix, penalised values
+// ---------------------------------------------------------------------------
 // Penalties on one logit of a history token (sampler.rs:139-143, then the
 // presence/frequency formula of llm-tests/tests/mlc_parity.rs:1083).
 __device__ __forceinline__ float penalize(float x, const RowP& P,
@@ -224,16 +261,141 @@ __device__ __forceinline__ float penalize(float x, const RowP& P,
   return x;
 }
 
+template <int DT>
+__device__ __forceinline__ float load_logit(const void* row, uint32_t e) {
+  if (DT == LLMK_F32) return G((const float*)row)[e];
+  return __uint_as_float((uint32_t)G((const uint16_t*)row)[e] << 16);
+}
+
+struct Hist {
+  LDS uint32_t* bitmap;  // nwords
+  LDS uint16_t* pre;     // nwords: distinct history tokens in words before
+  LDS float* pen;        // U_MAX: penalised logit by rank (counts while building)
+  LDS uint32_t* tokr;    // U_MAX: token of each rank
+  uint32_t lo;
+  __device__ __forceinline__ uint32_t rank(uint32_t t) const {
+    const uint32_t o = t - lo, w = o >> 5;
+    return pre[w] + __popc(bitmap[w] & ((1u << (o & 31)) - 1u));
+  }
+};
+
+__host__ __device__ inline size_t hist_lds_words(uint32_t nwords) {
+  return (size_t)((nwords + 3) & ~3u) + (size_t)(((nwords + 1) / 2 + 3) & ~3u) + 2 * U_MAX;
+}
+__device__ __forceinline__ void hist_carve(Hist& h, LDS uint32_t* base, uint32_t nwords) {
+  h.bitmap = base;
+  h.pre = (LDS uint16_t*)(base + ((nwords + 3) & ~3u));
+  h.pen = (LDS float*)(base + ((nwords + 3) & ~3u) + (((nwords + 1) / 2 + 3) & ~3u));
+  h.tokr = (LDS uint32_t*)(h.pen + U_MAX);
+}
+
+// Builds the history tables for tokens in [lo, hi) of row b.  All threads.
+// Global round trips: the row's history (held in registers, HTPT tokens per
+// thread per pass) and one gather of the logits of the distinct tokens.
+constexpr int HTPT = 8;
+template <int DT>
+__device__ __forceinline__ void build_history(const Args& a, const RowP& P, uint32_t b,
+                              const void* row, uint32_t lo, uint32_t hi,
+                              uint32_t nwords, Hist& h, LDS uint32_t* red,
+                              LDS uint32_t* flags) {
+  const uint32_t tid = threadIdx.x;
+  const bool need_pen = P.rp != 1.0f || P.pp != 0.0f || P.fp != 0.0f;
+  const bool have = need_pen && a.hoff;
+  const uint32_t h0 = have ? G(a.hoff)[b] : 0u, h1 = have ? G(a.hoff)[b + 1] : 0u;
+  uint32_t tk[HTPT];
+#pragma unroll
+  for (int q = 0; q < HTPT; ++q) {
+    const uint32_t i = h0 + q * NT + tid;
+    tk[q] = (i < h1) ? G(a.htok)[i] : EMPTY;
+  }
+  for (uint32_t i = tid; i < nwords; i += NT) h.bitmap[i] = 0;
+  __syncthreads();
+  if (!have) {  // uniform; the tables stay empty
+    for (uint32_t i = tid; i < nwords; i += NT) h.pre[i] = 0;
+    __syncthreads();
+    return;
+  }
+  const bool need_cnt = P.fp != 0.0f;
+  const bool one_pass = h1 - h0 <= (uint32_t)(HTPT * NT);
+  for (uint32_t c0 = h0; c0 < h1; c0 += HTPT * NT) {
+#pragma unroll
+    for (int q = 0; q < HTPT; ++q) {
+      uint32_t t = tk[q];
+      if (c0 != h0) {
+        const uint32_t i = c0 + q * NT + tid;
+        t = (i < h1) ? G(a.htok)[i] : EMPTY;
+      }
+      if (t >= lo && t < hi) __atomic_fetch_or(&h.bitmap[(t - lo) >> 5], 1u << (t & 31), __ATOMIC_RELAXED);
+    }
+  }
+  __syncthreads();
+  // exclusive popcount prefix over the words, each thread a contiguous run;
+  // the token of every rank is recorded
+  const uint32_t wpt = (nwords + NT - 1) / NT;
+  const uint32_t w0 = tid * wpt, w1 = (w0 + wpt < nwords) ? w0 + wpt : nwords;
+  uint32_t local = 0;
+  for (uint32_t wi = w0; wi < w1; ++wi) local += __popc(h.bitmap[wi]);
+  uint32_t U;
+  uint32_t run = block_excl_scan(local, red, U);
+  for (uint32_t wi = w0; wi < w1; ++wi) {
+    h.pre[wi] = (uint16_t)(run < 0xffffu ? run : 0xffffu);
+    uint32_t bits = h.bitmap[wi];
+    while (bits) {
+      const uint32_t bit = __builtin_ctz(bits);
+      bits &= bits - 1;
+      if (run < U_MAX) h.tokr[run] = lo + 32 * wi + bit;
+      ++run;
+    }
+  }
+  if (U > U_MAX && tid == 0) __atomic_fetch_or(flags, FLAG_HIST_OVERFLOW, __ATOMIC_RELAXED);
+  const uint32_t Uc = U < U_MAX ? U : U_MAX;
+  LDS uint32_t* cnt = (LDS uint32_t*)h.pen;
+  if (need_cnt) {
+    for (uint32_t i = tid; i < Uc; i += NT) cnt[i] = 0;
+    __syncthreads();
+    for (uint32_t c0 = h0; c0 < h1; c0 += HTPT * NT) {
+#pragma unroll
+      for (int q = 0; q < HTPT; ++q) {
+        uint32_t t = tk[q];
+        if (!one_pass) {
+          const uint32_t i = c0 + q * NT + tid;
+          t = (i < h1) ? G(a.htok)[i] : EMPTY;
+        }
+        if (t >= lo && t < hi) {
+          const uint32_t r = h.rank(t);
+          if (r < U_MAX) __atomic_fetch_add(&cnt[r], 1u, __ATOMIC_RELAXED);
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // penalised logit of every distinct history token: loads first, then math
+  for (uint32_t r0 = 0; r0 < Uc; r0 += HTPT * NT) {
+    float x[HTPT];
+#pragma unroll
+    for (int q = 0; q < HTPT; ++q) {
+      const uint32_t r = r0 + q * NT + tid;
+      x[q] = (r < Uc) ? load_logit<DT>(row, h.tokr[r]) : 0.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < HTPT; ++q) {
+      const uint32_t r = r0 + q * NT + tid;
+      if (r < Uc) h.pen[r] = penalize(x[q], P, need_cnt ? cnt[r] : 1u);
+    }
+  }
+  __syncthreads();
+}
+
 // ---------------------------------------------------------------------------
 // Candidate-threshold histogram
 // ---------------------------------------------------------------------------
 // Largest fine bin beta such that at least Kc counted elements have bin >=
-// beta (0 if fewer than Kc are counted).  Counts are lower bounds of the true
-// counts, so the result never exceeds the bin of the true Kc-th largest.
-__device__ uint32_t compute_beta(const uint32_t* hc, const uint32_t* hf,
+// beta (0 if fewer are counted).  Counts are lower bounds of the true counts,
+// so beta never exceeds the bin of the true Kc-th largest logit.
+__device__ __forceinline__ uint32_t compute_beta(LDS const uint32_t* hc, LDS const uint32_t* hf,
                                  uint32_t Kc, int lane) {
   const uint32_t c = hc[63 - lane];
-  const uint32_t incl = wave_incl_prefix(c, lane);
+  const uint32_t incl = wave_incl_scan(c);
   const uint64_t m = __ballot(incl >= Kc);
   if (m == 0) return 0;
   const int l = __ffsll((unsigned long long)m) - 1;
@@ -241,15 +403,23 @@ __device__ uint32_t compute_beta(const uint32_t* hc, const uint32_t* hf,
   const uint32_t before = __shfl(incl - c, l);
   const uint32_t need = Kc - before;
   const uint32_t f = hf[cb * 64 + 63 - lane];
-  const uint32_t fincl = wave_incl_prefix(f, lane);
+  const uint32_t fincl = wave_incl_scan(f);
   const uint64_t m2 = __ballot(fincl >= need);
   if (m2 == 0) return 0;
   const int l2 = __ffsll((unsigned long long)m2) - 1;
   return cb * 64u + 63u - (uint32_t)l2;
 }
 
+// Smallest float whose key lies in bin `beta` (all finite values for the
+// bins below that of -FLT_MAX, which hold only NaN and -inf keys).  For
+// finite v: v >= theta_of(beta) exactly when bin(v) >= beta, except that
+// -0.0 also passes at beta = bin(+0.0), which only adds a candidate.
+__device__ __forceinline__ float theta_of(uint32_t beta) {
+  return beta <= 8u ? -3.402823466e+38f : funkey(beta << BIN_SHIFT);
+}
+
 // ---------------------------------------------------------------------------
-// Geometry helpers
+// Geometry
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void wg_to_row_seg(const Args& a, uint32_t i,
                                               uint32_t& b, uint32_t& g) {
@@ -271,23 +441,22 @@ __device__ __forceinline__ uint32_t row_seg_to_wg(const Args& a, uint32_t b,
 // ---------------------------------------------------------------------------
 // Tile loads
 // ---------------------------------------------------------------------------
-typedef float f4v __attribute__((ext_vector_type(4)));
-typedef uint32_t u2v __attribute__((ext_vector_type(2)));
 
 struct Raw {
-  uint32_t d[16];   // fp32 bits (or 8 dwords of bf16 pairs)
-  uint32_t mw[4];   // allow-mask words for the lane's 4 groups
+  uint32_t d[16];  // fp32 bits (bf16: 8 dwords of pairs)
+  uint32_t mw[4];  // allow-mask words of the lane's 4 runs
 };
 
 // Lane `lane` owns tile offsets 256r + 4*lane + q (r, q in 0..3).
 template <int DT>
 __device__ __forceinline__ void load_tile(const Args& a, const void* row,
-                                          const uint32_t* mrow, uint32_t t,
-                                          int lane, Raw& raw) {
+                                          const uint32_t* mrow, const Hist& h,
+                                          uint32_t t, int lane, Raw& raw) {
   const uint32_t tb = t * TILE;
+  (void)h;
   if (tb + TILE <= a.V) {
     if (DT == LLMK_F32) {
-      const f4v* p = (const f4v*)((const float*)row + tb) + lane;
+      const GLB f4v* p = (const GLB f4v*)G((const float*)row + tb) + lane;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const f4v x = __builtin_nontemporal_load(p + 64 * r);
@@ -297,7 +466,7 @@ __device__ __forceinline__ void load_tile(const Args& a, const void* row,
         raw.d[4 * r + 3] = __float_as_uint(x.w);
       }
     } else {
-      const u2v* p = (const u2v*)((const uint16_t*)row + tb) + lane;
+      const GLB u2v* p = (const GLB u2v*)G((const uint16_t*)row + tb) + lane;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const u2v x = __builtin_nontemporal_load(p + 64 * r);
@@ -312,17 +481,13 @@ __device__ __forceinline__ void load_tile(const Args& a, const void* row,
       for (int q = 0; q < 4; ++q) {
         const uint32_t e = tb + 256u * r + 4u * lane + q;
         uint32_t bits = 0xff800000u;  // -inf beyond the vocabulary
-        if (e < a.V) {
-          if (DT == LLMK_F32) bits = ((const uint32_t*)row)[e];
-          else bits = (uint32_t)((const uint16_t*)row)[e] << 16;
-        }
+        if (e < a.V) bits = __float_as_uint(load_logit<DT>(row, e));
         if (DT == LLMK_F32) raw.d[4 * r + q] = bits;
         else {
-          // repack into the bf16 pair layout used by the full-tile path
-          const uint32_t h = bits >> 16;
+          const uint32_t hv = bits >> 16;
           const int w = 2 * r + (q >> 1);
-          if ((q & 1) == 0) raw.d[w] = h;
-          else raw.d[w] |= h << 16;
+          if ((q & 1) == 0) raw.d[w] = hv;
+          else raw.d[w] |= hv << 16;
         }
       }
   }
@@ -330,7 +495,7 @@ __device__ __forceinline__ void load_tile(const Args& a, const void* row,
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const uint32_t wi = (tb >> 5) + 8u * r + ((uint32_t)lane >> 3);
-      raw.mw[r] = (wi < a.mask_words) ? mrow[wi] : 0u;
+      raw.mw[r] = (wi < a.mask_words) ? G(mrow)[wi] : 0u;
     }
   }
 }
@@ -352,55 +517,10 @@ __device__ __forceinline__ void unpack(const Raw& raw, float v[16]) {
 }
 
 // ---------------------------------------------------------------------------
-// Shared-memory layout of the stream kernel
+// Probabilities and the sequential semantics
 // ---------------------------------------------------------------------------
-enum : uint32_t { M_BETA = 0, M_CCOUNT = 1, M_FLAGS = 2, M_LAST = 3, M_NMISC = 16 };
-
-struct StreamLds {
-  uint32_t* bitmap;  // tps*32
-  uint32_t* hk;      // HASH_SLOTS
-  uint32_t* hc;      // HASH_SLOTS
-  uint32_t* hf;      // NBINS
-  uint32_t* hcoarse; // 64
-  uint32_t* misc;    // M_NMISC
-};
-
-__host__ __device__ inline size_t stream_lds_words(uint32_t tps) {
-  return (size_t)tps * 32 + 2 * HASH_SLOTS + NBINS + 64 + M_NMISC;
-}
-// finalize: tile arrays 2*MAX_TILES floats, keys SORT_CAP u64, p/idx SORT_CAP
-__host__ __device__ inline size_t finalize_lds_words() {
-  return 2 * MAX_TILES + 2 * SORT_CAP + 2 * SORT_CAP + 64;
-}
-
-// ---------------------------------------------------------------------------
-// Finalize one row (one workgroup of NT threads)
-// ---------------------------------------------------------------------------
-__device__ float block_max(float x, float* red) {
-  x = wave_max(x);
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  __syncthreads();
-  if (lane == 0) red[wv] = x;
-  __syncthreads();
-  float r = red[0];
-  for (int i = 1; i < NT / WAVE; ++i) r = fmaxf(r, red[i]);
-  __syncthreads();
-  return r;
-}
-__device__ uint32_t block_min_u32(uint32_t x, uint32_t* red) {
-  x = wave_min_u32(x);
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  __syncthreads();
-  if (lane == 0) red[wv] = x;
-  __syncthreads();
-  uint32_t r = red[0];
-  for (int i = 1; i < NT / WAVE; ++i) r = red[i] < r ? red[i] : r;
-  __syncthreads();
-  return r;
-}
-
-// p of a (penalised, masked) logit v given the row's temperature, x_max = m
-// and normaliser S: exactly sampler.rs:53-70 with exp_m.
+// p of a (penalised, masked) logit v given the temperature, x_max = m and
+// the normaliser S: sampler.rs:53-70 with exp_m.
 __device__ __forceinline__ float prob_of(float v, float T, float m, float S) {
   const float x = (T != 1.0f) ? v / T : v;
   const float e = (x == NEG_INF) ? 0.0f : exp_m(x - m);
@@ -411,333 +531,667 @@ __device__ __forceinline__ uint64_t pkey(float p, uint32_t idx) {
   return ((uint64_t)(~__float_as_uint(p)) << 32) | idx;
 }
 
-// Sequential semantics of sampler.rs:77-124 (+ min-p) over a list sorted by
-// (p desc, idx asc) of which the first E entries are known exactly and the
-// list has `len` entries in total.  Executed by all threads of the block;
-// thread 0 does the order-dependent sums, all threads the divisions.
-// Returns false if the semantics need an entry beyond E.
-template <typename PAcc, typename IAcc, int NTH>
-__device__ bool run_semantics(const RowP& P, float u, uint32_t E,
-                              uint32_t full_len, PAcc pget, IAcc iget,
-                              uint32_t* sh, uint32_t& tok_out,
-                              uint32_t& len_out) {
-  // sh[0]=ok, sh[1]=len, sh[2]=trunc, sh[3]=sum bits, sh[4]=tok
-  const uint32_t tid = threadIdx.x;
-  if (tid == 0) {
-    sh[0] = 1;
-    sh[1] = full_len;
-    sh[2] = (E < full_len) ? 1u : 0u;
+// A list sorted by (p desc, idx asc) holding the probabilities as first
+// computed; renormalisations (sampler.rs:84-87, :104-109) are recorded as a
+// chain of divisors and applied on every read, fl(fl(p/s1)/s2), exactly as
+// the reference's in-place divisions, so the list itself is never rewritten.
+// `win(j0, n)` returns an LDS pointer to the current values of
+// p[j0 .. j0+n) (n <= wmax()); all threads call it.
+struct Chain {
+  float d0, d1, d2;
+  int n;
+  __device__ __forceinline__ float apply(float x) const {
+    if (n > 0) x = x / d0;
+    if (n > 1) x = x / d1;
+    if (n > 2) x = x / d2;
+    return x;
   }
-  __syncthreads();
-  // ---- min-p (extension): keep p >= min_p * p_max, renormalise if cut
-  if (P.min_p > 0.0f) {
-    if (tid == 0) {
-      uint32_t len = sh[1], ok = 1, cut = len;
-      float s = 0.0f;
-      bool do_norm = false;
-      if (E == 0) ok = 0;
-      else {
-        const float thr = P.min_p * pget(0);
-        uint32_t j = 0;
-        bool found = false;
-        for (; j < E && j < len; ++j)
-          if (pget(j) < thr) {
-            found = true;
-            break;
-          }
-        if (found) cut = j;
-        else if (sh[2] && E < len) ok = 0;
-        if (ok && cut < len) {
-          for (uint32_t i = 0; i < cut; ++i) s += pget(i);
-          do_norm = true;
-          sh[1] = cut;
-          sh[2] = 0;
+  __device__ __forceinline__ void push(float s) {
+    if (n == 0) d0 = s;
+    else if (n == 1) d1 = s;
+    else d2 = s;
+    ++n;
+  }
+};
+struct LdsList {
+  LDS const float* p;
+  LDS const uint32_t* idx;
+  LDS float* stage;  // SORT_CAP floats
+  Chain c;
+  __device__ uint32_t wmax() const { return SORT_CAP; }
+  __device__ LDS const float* win(uint32_t j0, uint32_t n) const {
+    if (c.n == 0) return p + j0;
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < n; i += NT) stage[i] = c.apply(p[j0 + i]);
+    __syncthreads();
+    return stage;
+  }
+  __device__ float get(uint32_t i) const { return c.apply(p[i]); }
+  __device__ uint32_t id(uint32_t i) const { return idx[i]; }
+};
+struct GlobList {
+  const GLB float* p;
+  const GLB uint32_t* idx;
+  LDS float* stage;  // STAGE floats
+  Chain c;
+  __device__ uint32_t wmax() const { return STAGE; }
+  __device__ LDS const float* win(uint32_t j0, uint32_t n) const {
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < n; i += NT) stage[i] = c.apply(p[j0 + i]);
+    __syncthreads();
+    return stage;
+  }
+  __device__ float get(uint32_t i) const { return c.apply(p[i]); }
+  __device__ uint32_t id(uint32_t i) const { return idx[i]; }
+};
+
+// Sequential f32 scan of p[0..n) in order (all threads call; thread 0 adds).
+// mode 0: sum of all n.  mode 1: stop at the first j with cum >= thr.
+// mode 2: stop at the first j with thr <= cum (the draw's `r <= cumulative`).
+// Returns the stop index (n if none) and the cumulative including it.
+template <class L>
+__device__ __forceinline__ uint32_t seq_scan(const L& list, uint32_t n, int mode, float thr,
+                             float& cum_out, LDS uint32_t* sh) {
+  float cum = 0.0f;
+  uint32_t stop = n;
+  const uint32_t W = list.wmax();
+  for (uint32_t j0 = 0; j0 < n; j0 += W) {
+    const uint32_t cnt = (n - j0 < W) ? n - j0 : W;
+    LDS const float* pw = list.win(j0, cnt);
+    if (threadIdx.x == 0) {
+      uint32_t j = 0, hit = EMPTY;
+      for (; j + 8 <= cnt && hit == EMPTY; j += 8) {
+        const f4v lo4 = *(LDS const f4v*)(pw + j);
+        const f4v hi4 = *(LDS const f4v*)(pw + j + 4);
+        const float t[8] = {lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          if (hit != EMPTY) break;
+          cum += t[q];
+          if ((mode == 1 && cum >= thr) || (mode == 2 && thr <= cum)) hit = j + q;
         }
       }
-      sh[0] = ok;
-      sh[3] = do_norm ? __float_as_uint(s) : 0u;
-      sh[5] = do_norm ? 1u : 0u;
+      for (; j < cnt && hit == EMPTY; ++j) {
+        cum += pw[j];
+        if ((mode == 1 && cum >= thr) || (mode == 2 && thr <= cum)) hit = j;
+      }
+      sh[0] = __float_as_uint(cum);
+      sh[1] = hit;
     }
     __syncthreads();
-    if (!sh[0]) return false;
-    if (sh[5]) {
-      const float s = __uint_as_float(sh[3]);
-      if (s > 0.0f)
-        for (uint32_t i = tid; i < sh[1]; i += NTH) pget.set(i, pget(i) / s);
-    }
+    cum = __uint_as_float(sh[0]);
+    const uint32_t hit = sh[1];
     __syncthreads();
+    if (hit != EMPTY) {
+      stop = j0 + hit;
+      break;
+    }
+  }
+  cum_out = cum;
+  return stop;
+}
+
+template <class L>
+__device__ __forceinline__ void div_all(L& list, float s) {
+  if (s > 0.0f) list.c.push(s);
+}
+
+// min-p / top-k / top-p / draw (sampler.rs:77-124 + min-p) over a sorted list
+// whose first E entries are exact and which has full_len entries.  All
+// threads.  Returns false if an entry beyond E would be needed.
+template <class L>
+__device__ __forceinline__ bool run_semantics(const RowP& P, float u, uint32_t E,
+                              uint32_t full_len, L& list, LDS uint32_t* sh,
+                              uint32_t& tok_out, uint32_t& len_out) {
+  uint32_t len = full_len;
+  bool trunc = E < full_len;
+  float s;
+  // ---- min-p (extension): keep p >= min_p * p_max, renormalise if it cuts
+  if (P.min_p > 0.0f) {
+    if (E == 0) return false;
+    const float thr = P.min_p * list.get(0);
+    if (threadIdx.x == 0) sh[2] = EMPTY;
+    __syncthreads();
+    const uint32_t lim = E < len ? E : len;
+    for (uint32_t i = threadIdx.x; i < lim; i += NT)
+      if (list.get(i) < thr) __atomic_fetch_min(&sh[2], i, __ATOMIC_RELAXED);
+    __syncthreads();
+    const uint32_t cut = sh[2];
+    __syncthreads();
+    if (cut == EMPTY) {
+      if (trunc) return false;
+    } else if (cut < len) {
+      len = cut;
+      trunc = false;
+      seq_scan(list, len, 0, 0.0f, s, sh);
+      div_all(list, s);
+    }
   }
   // ---- top-k, sampler.rs:80-89
-  if (P.K > 0 && (uint32_t)P.K < sh[1]) {
-    if (tid == 0) {
-      const uint32_t K = (uint32_t)P.K;
-      if (K > E) sh[0] = 0;
-      else {
-        float s = 0.0f;
-        for (uint32_t i = 0; i < K; ++i) s += pget(i);
-        sh[1] = K;
-        sh[2] = 0;
-        sh[3] = __float_as_uint(s);
-      }
-    }
-    __syncthreads();
-    if (!sh[0]) return false;
-    const float s = __uint_as_float(sh[3]);
-    if (s > 0.0f)
-      for (uint32_t i = tid; i < sh[1]; i += NTH) pget.set(i, pget(i) / s);
-    __syncthreads();
+  if (P.K > 0 && (uint32_t)P.K < len) {
+    if ((uint32_t)P.K > E) return false;
+    len = (uint32_t)P.K;
+    trunc = false;
+    seq_scan(list, len, 0, 0.0f, s, sh);
+    div_all(list, s);
   }
   // ---- top-p, sampler.rs:92-110
   if (P.top_p < 1.0f) {
-    if (tid == 0) {
-      const uint32_t len = sh[1];
-      float cum = 0.0f;
-      uint32_t cut = len, j = 0;
-      uint32_t ok = 1;
-      for (; j < len; ++j) {
-        if (j >= E) {
-          ok = 0;
-          break;
-        }
-        cum += pget(j);
-        if (cum >= P.top_p) {
-          cut = j + 1;
-          break;
-        }
-      }
-      sh[0] = ok;
-      if (ok) {
-        // the renormalisation sum over the kept prefix is the same
-        // sequential sum as the cumulative at the cut
-        sh[1] = cut;
-        sh[2] = 0;
-        sh[3] = __float_as_uint(cum);
-      }
-    }
-    __syncthreads();
-    if (!sh[0]) return false;
-    const float s = __uint_as_float(sh[3]);
-    if (s > 0.0f)
-      for (uint32_t i = tid; i < sh[1]; i += NTH) pget.set(i, pget(i) / s);
-    __syncthreads();
+    const uint32_t lim = (trunc && E < len) ? E : len;
+    const uint32_t j = seq_scan(list, lim, 1, P.top_p, s, sh);
+    if (j == lim && trunc) return false;
+    // the renormalisation sum over the kept prefix is the same sequential
+    // sum as the cumulative at the cut
+    len = (j < lim) ? j + 1 : len;
+    trunc = false;
+    div_all(list, s);
   }
   // ---- draw, sampler.rs:113-124
-  if (tid == 0) {
-    const uint32_t len = sh[1];
-    uint32_t ok = 1, tok = 0;
-    if (len > 0) {
-      if (len - 1 < E) tok = iget(len - 1);
-      else tok = EMPTY;  // fallback index unknown unless reached below
-    }
-    float cum = 0.0f;
-    bool hit = false;
-    for (uint32_t j = 0; j < len; ++j) {
-      if (j >= E) {
-        ok = 0;
-        break;
-      }
-      cum += pget(j);
-      if (u <= cum) {
-        tok = iget(j);
-        hit = true;
-        break;
-      }
-    }
-    if (!hit && tok == EMPTY) ok = 0;
-    sh[0] = ok;
-    sh[4] = tok;
+  const uint32_t lim = (trunc && E < len) ? E : len;
+  const uint32_t j = seq_scan(list, lim, 2, u, s, sh);
+  uint32_t tok;
+  if (j < lim) tok = list.id(j);
+  else {
+    if (trunc) return false;
+    tok = len > 0 ? list.id(len - 1) : 0u;
   }
-  __syncthreads();
-  if (!sh[0]) return false;
-  tok_out = sh[4];
-  len_out = sh[1];
+  tok_out = tok;
+  len_out = len;
   return true;
 }
 
-struct LdsP {
-  float* p;
-  __device__ float operator()(uint32_t i) const { return p[i]; }
-  __device__ void set(uint32_t i, float x) const { p[i] = x; }
-};
-struct LdsI {
-  const uint32_t* p;
-  __device__ uint32_t operator()(uint32_t i) const { return p[i]; }
-};
-
-__device__ void write_outputs(const Args& a, uint32_t b, uint32_t tok,
-                              uint32_t len, const float* pp,
-                              const uint32_t* pidx, uint32_t E, int nth) {
+template <class L>
+__device__ __forceinline__ void write_outputs(const Args& a, uint32_t b, uint32_t tok,
+                              uint32_t len, const L& list) {
   const uint32_t tid = threadIdx.x;
   if (tid == 0) {
-    a.out_tok[b] = tok;
-    if (a.out_cnt) a.out_cnt[b] = len;
+    G(a.out_tok)[b] = tok;
+    if (a.out_cnt) G(a.out_cnt)[b] = len;
   }
   if (a.out_cap) {
     const uint32_t n = len < a.out_cap ? len : a.out_cap;
-    for (uint32_t j = tid; j < n; j += nth) {
-      if (a.out_ids) a.out_ids[(uint64_t)b * a.out_cap + j] = pidx[j];
-      if (a.out_probs) a.out_probs[(uint64_t)b * a.out_cap + j] = pp[j];
+    for (uint32_t j = tid; j < n; j += NT) {
+      if (a.out_ids) G(a.out_ids)[(uint64_t)b * a.out_cap + j] = list.id(j);
+      if (a.out_probs) G(a.out_probs)[(uint64_t)b * a.out_cap + j] = list.get(j);
     }
   }
 }
 
-__device__ void finalize_row(const Args& a, const Ws& w, uint32_t b,
-                             const RowP& P, uint32_t* smem) {
+// ---------------------------------------------------------------------------
+// Shared-memory layouts (in 32-bit words)
+// ---------------------------------------------------------------------------
+enum : uint32_t { M_BETA = 0, M_CCOUNT = 1, M_FLAGS = 2, M_LAST = 3, M_NMISC = 16 };
+
+__host__ __device__ inline size_t stream_lds_words(uint32_t tps) {
+  return 64 + M_NMISC + NBINS + 64 + hist_lds_words(tps * 32);
+}
+__host__ __device__ inline size_t finalize_lds_words() {
+  // tiles (2 x MAX_TILES) + keys + sorted keys (2 x SORT_CAP u64) + p + idx
+  // + segment tables + scratch
+  return 2 * MAX_TILES + 4 * SORT_CAP + 2 * SORT_CAP + 4 * (MAX_SEG + 1) + 128;
+}
+__host__ __device__ inline size_t slow_lds_words(uint32_t V) {
+  return 128 + 256 + NW * 256 + 256 + STAGE + hist_lds_words((V + 31) / 32);
+}
+
+// ---------------------------------------------------------------------------
+// Slow path (one workgroup, one row)
+// ---------------------------------------------------------------------------
+template <int DT>
+__device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b, const RowP& P,
+                         float S, float m, LDS uint32_t* smem) {
   const uint32_t tid = threadIdx.x;
-  float* tl = (float*)smem;                         // MAX_TILES
-  float* ts = tl + MAX_TILES;                       // MAX_TILES
-  uint64_t* keys = (uint64_t*)(smem + 2 * MAX_TILES);  // SORT_CAP
-  float* pp = (float*)(keys + SORT_CAP);            // SORT_CAP
-  uint32_t* pidx = (uint32_t*)(pp + SORT_CAP);      // SORT_CAP
-  uint32_t* fm = pidx + SORT_CAP;                   // 64 words
+  const int lane = (int)(tid & 63), wv = (int)(tid >> 6);
+  const uint32_t V = a.V;
+  __syncthreads();
+  LDS uint32_t* sh = smem;                   // 64
+  LDS uint32_t* red = sh + 64;               // 64
+  LDS uint32_t* digit_off = red + 64;        // 256
+  LDS uint32_t* wcnt = digit_off + 256;      // NW*256
+  LDS uint32_t* ttot = wcnt + NW * 256;      // 256
+  LDS float* stage = (LDS float*)(ttot + 256);   // STAGE
+  LDS uint32_t* hb = (LDS uint32_t*)(stage + STAGE);
+  const uint32_t nwords = (V + 31) / 32;
+  Hist h;
+  hist_carve(h, hb, nwords);
+  h.lo = 0;
+  // Acquire scratch slot b % SLOW_SLOTS.  A holder waits on nothing, so the
+  // wait ends; the spin is bounded all the same.
+  const uint32_t slot = b % SLOW_SLOTS;
+  if (tid == 0) {
+    uint32_t got = 0;
+    for (uint32_t n = 0; n < (1u << 26); ++n) {
+      if (atomicCAS(&w.slow_lock[slot], 0u, 1u) == 0u) {
+        got = 1;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(8);
+    }
+    if (got) __threadfence();
+    sh[63] = got;
+  }
+  __syncthreads();
+  if (!sh[63]) {
+    if (tid == 0) {
+      a.out_tok[b] = LLMK_INVALID_TOKEN;
+      if (a.out_cnt) a.out_cnt[b] = 0;
+      atomicOr(w.status, LLMK_STATUS_SLOT_TIMEOUT);
+    }
+    return;
+  }
+  const void* row = (const char*)a.logits +
+                    (uint64_t)b * a.stride * (DT == LLMK_F32 ? 4u : 2u);
+  if (tid == 0) sh[10] = 0;
+  build_history<DT>(a, P, b, row, 0, V, nwords, h, red, &sh[10]);
+  if (tid == 0 && (sh[10] & FLAG_HIST_OVERFLOW))
+    atomicOr(w.status, LLMK_STATUS_HISTORY_OVERFLOW);
+  GLB uint64_t* kA = G(w.slow_keys) + (uint64_t)slot * 3 * (uint64_t)w.max_vocab;
+  GLB uint64_t* kB = kA + w.max_vocab;
+  GLB uint32_t* zl = (GLB uint32_t*)(kB + w.max_vocab);  // zero-probability indices
+  GLB float* plist = G(w.slow_p) + (uint64_t)slot * w.max_vocab;
+  GLB uint32_t* ilist = G(w.slow_idx) + (uint64_t)slot * w.max_vocab;
+  const GLB uint32_t* mrow = a.mask ? G(a.mask) + (uint64_t)b * a.mask_words : nullptr;
+  // pass 1: exact p of every element, stable split into p>0 / p==0 lists
+  uint32_t npos = 0, nzero = 0;
+  for (uint32_t base = 0; base < V; base += NT) {
+    const uint32_t e = base + tid;
+    float p = 0.0f;
+    const bool valid = e < V;
+    if (valid) {
+      float x = load_logit<DT>(row, e);
+      if ((h.bitmap[e >> 5] >> (e & 31)) & 1u) {
+        const uint32_t r = h.rank(e);
+        if (r < U_MAX) x = h.pen[r];
+      }
+      if (mrow && !((mrow[e >> 5] >> (e & 31)) & 1u)) x = NEG_INF;
+      if (!(x > NEG_INF)) x = NEG_INF;  // NaN acts as -inf
+      p = prob_of(x, P.T, m, S);
+    }
+    uint32_t tot;
+    const bool pos_f = valid && p > 0.0f;
+    const uint32_t pos = block_excl_scan(pos_f ? 1u : 0u, red, tot);
+    if (pos_f) kA[npos + pos] = pkey(p, e);
+    npos += tot;
+    const bool zero_f = valid && !(p > 0.0f);
+    const uint32_t zpos = block_excl_scan(zero_f ? 1u : 0u, red, tot);
+    if (zero_f) zl[nzero + zpos] = e;
+    nzero += tot;
+  }
+  wait_stores();
+  __syncthreads();
+  if (tid == 0) __threadfence();  // drop stale vector-L1 lines before re-reads
+  __syncthreads();
+  // stable LSD radix sort of kA[0..npos) on bits 32..63, 4 passes of 8 bits
+  GLB uint64_t* src = kA;
+  GLB uint64_t* dst = kB;
+  for (int pass = 0; pass < 4; ++pass) {
+    const int sh_bits = 32 + 8 * pass;
+    if (tid < 256) digit_off[tid] = 0;
+    __syncthreads();
+    for (uint32_t i = tid; i < npos; i += NT)
+      __atomic_fetch_add(&digit_off[(uint32_t)(src[i] >> sh_bits) & 255u], 1u, __ATOMIC_RELAXED);
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t acc = 0;
+      for (int d = 0; d < 256; ++d) {
+        const uint32_t c = digit_off[d];
+        digit_off[d] = acc;
+        acc += c;
+      }
+    }
+    __syncthreads();
+    for (uint32_t base = 0; base < npos; base += NT) {
+      const uint32_t i = base + tid;
+      const bool valid = i < npos;
+      const uint64_t key = valid ? src[i] : 0ull;
+      const uint32_t d = (uint32_t)(key >> sh_bits) & 255u;
+      uint64_t peers = __ballot(valid);
+#pragma unroll
+      for (int bit = 0; bit < 8; ++bit) {
+        const uint64_t bb = __ballot(((d >> bit) & 1u) != 0);
+        peers &= ((d >> bit) & 1u) ? bb : ~bb;
+      }
+      const uint32_t rank = lanes_below(peers);
+      for (uint32_t j = tid; j < NW * 256; j += NT) wcnt[j] = 0;
+      __syncthreads();
+      if (valid && rank == 0) wcnt[wv * 256 + d] = __popcll(peers);
+      __syncthreads();
+      if (tid < 256) {
+        uint32_t acc = 0;
+        for (int q = 0; q < NW; ++q) {
+          const uint32_t c = wcnt[q * 256 + tid];
+          wcnt[q * 256 + tid] = acc;
+          acc += c;
+        }
+        ttot[tid] = acc;
+      }
+      __syncthreads();
+      if (valid) dst[digit_off[d] + wcnt[wv * 256 + d] + rank] = key;
+      __syncthreads();
+      if (tid < 256) digit_off[tid] += ttot[tid];
+      __syncthreads();
+    }
+    wait_stores();
+    __syncthreads();
+    if (tid == 0) __threadfence();
+    __syncthreads();
+    GLB uint64_t* tmp = src;
+    src = dst;
+    dst = tmp;
+  }
+  // unpack into p / idx lists (sorted positives, then zeros by index)
+  for (uint32_t i = tid; i < npos; i += NT) {
+    const uint64_t k = src[i];
+    plist[i] = __uint_as_float(~(uint32_t)(k >> 32));
+    ilist[i] = (uint32_t)k;
+  }
+  for (uint32_t i = tid; i < nzero; i += NT) {
+    plist[npos + i] = 0.0f;
+    ilist[npos + i] = zl[i];
+  }
+  wait_stores();
+  __syncthreads();
+  if (tid == 0) __threadfence();
+  __syncthreads();
+  (void)lane;
+  GlobList L{plist, ilist, stage, Chain{0.f, 0.f, 0.f, 0}};
+  uint32_t tok = 0, len = 0;
+  run_semantics(P, a.u[b], V, V, L, sh + 20, tok, len);
+  wait_stores();
+  __syncthreads();
+  write_outputs(a, b, tok, len, L);
+  wait_stores();
+  __syncthreads();
+  if (tid == 0) {
+    __threadfence();
+    atomicExch(&w.slow_lock[slot], 0u);
+  }
+}
+
+// Key (fkey) of the K-th largest of cval[0..n) (K <= n), by a four-round
+// radix select on 8-bit digits.  All threads.  hist: 256 words, sh: 2 words.
+__device__ __forceinline__ uint32_t block_kth_largest_key(LDS const float* cval, uint32_t n,
+                                          uint32_t K, LDS uint32_t* hist,
+                                          LDS uint32_t* sh) {
+  const uint32_t tid = threadIdx.x;
+  const int lane = (int)(tid & 63), wv = (int)(tid >> 6);
+  uint32_t prefix = 0, need = K;
+  for (int round = 0; round < 4; ++round) {
+    const int shift = 24 - 8 * round;
+    const uint32_t hmask = round == 0 ? 0u : (0xffffffffu << (shift + 8));
+    if (tid < 256) hist[tid] = 0;
+    __syncthreads();
+    for (uint32_t i = tid; i < n; i += NT) {
+      const uint32_t k = fkey(cval[i]);
+      if ((k & hmask) == prefix) __atomic_fetch_add(&hist[(k >> shift) & 255u], 1u, __ATOMIC_RELAXED);
+    }
+    __syncthreads();
+    if (wv == 0) {
+      // lane l covers digits 255-4l .. 252-4l (descending)
+      uint32_t c[4], local = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        c[j] = hist[255 - 4 * lane - j];
+        local += c[j];
+      }
+      const uint32_t incl = wave_incl_scan(local);
+      const uint64_t ms = __ballot(incl >= need);
+      const int l = __ffsll((unsigned long long)ms) - 1;
+      if (lane == l) {
+        uint32_t acc = incl - local;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (acc + c[j] >= need) {
+            sh[0] = 255u - 4u * (uint32_t)lane - (uint32_t)j;
+            sh[1] = need - acc;
+            break;
+          }
+          acc += c[j];
+        }
+      }
+    }
+    __syncthreads();
+    prefix |= sh[0] << shift;
+    need = sh[1];
+    __syncthreads();
+  }
+  return prefix;
+}
+
+// ---------------------------------------------------------------------------
+// Finalize one row
+// ---------------------------------------------------------------------------
+template <int DT>
+__device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_t b,
+                             const RowP& P, LDS uint32_t* smem) {
+  const uint32_t tid = threadIdx.x;
+  const int lane = (int)(tid & 63), wv = (int)(tid >> 6);
+  LDS float* tl = (LDS float*)smem;                          // MAX_TILES
+  LDS float* ts = tl + MAX_TILES;                            // MAX_TILES
+  LDS uint64_t* keys = (LDS uint64_t*)(smem + 2 * MAX_TILES);  // SORT_CAP
+  LDS uint64_t* skeys = keys + SORT_CAP;                     // SORT_CAP (sorted)
+  LDS float* pp = (LDS float*)(skeys + SORT_CAP);            // SORT_CAP
+  LDS uint32_t* pidx = (LDS uint32_t*)(pp + SORT_CAP);       // SORT_CAP
+  LDS uint32_t* seg_cnt = pidx + SORT_CAP;                   // MAX_SEG+1
+  LDS uint32_t* seg_off = seg_cnt + MAX_SEG + 1;             // MAX_SEG+1
+  LDS uint32_t* seg_beta = seg_off + MAX_SEG + 1;            // MAX_SEG+1
+  LDS uint32_t* seg_flag = seg_beta + MAX_SEG + 1;           // MAX_SEG+1
+  LDS uint32_t* fm = seg_flag + MAX_SEG + 1;                 // 128
   const uint32_t nt = a.ntiles;
-  const float2* part = w.tile_part + (uint64_t)b * MAX_TILES;
+  const GLB f2v* part = G(w.tile_part) + (uint64_t)b * MAX_TILES;
   for (uint32_t c = tid; c < nt; c += NT) {
-    const float2 q = part[c];
+    const f2v q = part[c];
     tl[c] = q.x;
     ts[c] = q.y;
+  }
+  if (tid < a.G) {
+    const u4v sm = G(w.seg_meta)[row_seg_to_wg(a, b, tid)];
+    seg_cnt[tid] = sm.x < CAND_CAP ? sm.x : CAND_CAP;
+    seg_beta[tid] = sm.y;
+    seg_flag[tid] = sm.z;
   }
   __syncthreads();
 
   if (P.mode == MODE_GREEDY) {
     // sampler.rs:40-50: the first index holding the maximum.
-    float m = NEG_INF;
-    for (uint32_t c = tid; c < nt; c += NT) m = fmaxf(m, tl[c]);
-    m = block_max(m, (float*)fm);
+    float mx = NEG_INF;
+    for (uint32_t c = tid; c < nt; c += NT) mx = fmaxf(mx, tl[c]);
+    mx = block_max(mx, (LDS float*)fm);
     uint32_t bi = EMPTY;
     for (uint32_t c = tid; c < nt; c += NT)
-      if (tl[c] == m) {
-        const uint32_t ci = __float_as_uint(ts[c]);
-        bi = ci < bi ? ci : bi;
-      }
+      if (tl[c] == mx) bi = umin(bi, __float_as_uint(ts[c]));
     bi = block_min_u32(bi, fm + 16);
     if (bi == EMPTY) bi = 0;
     if (tid == 0) {
-      a.out_tok[b] = bi;
-      if (a.out_cnt) a.out_cnt[b] = 1;
+      G(a.out_tok)[b] = bi;
+      if (a.out_cnt) G(a.out_cnt)[b] = 1;
       if (a.out_cap) {
-        if (a.out_ids) a.out_ids[(uint64_t)b * a.out_cap] = bi;
-        if (a.out_probs) a.out_probs[(uint64_t)b * a.out_cap] = 1.0f;
+        if (a.out_ids) G(a.out_ids)[(uint64_t)b * a.out_cap] = bi;
+        if (a.out_probs) G(a.out_probs)[(uint64_t)b * a.out_cap] = 1.0f;
       }
     }
     return;
   }
 
-  // ---- normaliser S
+  // ---- normaliser S: tree over next_pow2(#tiles), 64-tile blocks per wave
   float L = NEG_INF;
   for (uint32_t c = tid; c < nt; c += NT) L = fmaxf(L, tl[c]);
-  L = block_max(L, (float*)fm);
+  L = block_max(L, (LDS float*)fm);
   const float c2 = LOG2E_F / P.T;
   uint32_t ntp = 1;
   while (ntp < nt) ntp <<= 1;
-  for (uint32_t c = tid; c < ntp; c += NT) {
+  const uint32_t nblk = (ntp + 63) / 64;
+  LDS float* blk = (LDS float*)(fm + 32);  // up to 16 block sums
+  for (uint32_t k = (uint32_t)wv; k < nblk; k += NW) {
+    const uint32_t c = 64 * k + (uint32_t)lane;
     float x = 0.0f;
     if (c < nt && L != NEG_INF) x = ts[c] * exp2_f((tl[c] - L) * c2);
-    ts[c] = x;
+    x = wave_tree_sum(x);
+    if (lane == 0) blk[k] = x;
   }
   __syncthreads();
-  for (uint32_t len = ntp; len > 1; len >>= 1) {
-    float x[MAX_TILES / NT];
-    uint32_t k = 0;
-    for (uint32_t i = tid; i < len / 2; i += NT) x[k++] = ts[2 * i] + ts[2 * i + 1];
-    __syncthreads();
-    k = 0;
-    for (uint32_t i = tid; i < len / 2; i += NT) ts[i] = x[k++];
-    __syncthreads();
-  }
-  const float S = (L != NEG_INF) ? ts[0] : 0.0f;
-  const float m = (P.T != 1.0f) ? L / P.T : L;
-  if (tid == 0) w.row_stats[b] = make_float4(S, m, L, 0.0f);
-
-  // ---- candidates
   if (tid == 0) {
-    uint32_t lam = 0, flags = 0, total = 0;
-    for (uint32_t g = 0; g < a.G; ++g) {
-      const uint4 sm = w.seg_meta[row_seg_to_wg(a, b, g)];
-      const uint32_t lk = sm.y << BIN_SHIFT;
-      lam = lk > lam ? lk : lam;
-      flags |= sm.z;
-      total += sm.x;
-    }
-    fm[32] = lam;
-    fm[33] = flags;
-    fm[34] = 0;  // gathered count
-    fm[35] = (L == NEG_INF || P.Kc == 0 || (flags & FLAG_OVERFLOW)) ? 1u : 0u;
+    for (uint32_t len = nblk; len > 1; len >>= 1)
+      for (uint32_t i = 0; i < len / 2; ++i) blk[i] = blk[2 * i] + blk[2 * i + 1];
   }
   __syncthreads();
-  bool slow = fm[35] != 0;
-  const uint32_t lam = fm[32];
-  if (!slow) {
+  const float S = (L != NEG_INF) ? blk[0] : 0.0f;
+  const float m = (P.T != 1.0f) ? L / P.T : L;
+
+  // ---- candidate bound: every element outside the candidate buffers has a
+  // key below lam, hence probability at most plim
+  if (tid == 0) {
+    uint32_t lam = 0, flags = 0, acc = 0;
     for (uint32_t g = 0; g < a.G; ++g) {
-      const uint32_t wg = row_seg_to_wg(a, b, g);
-      const uint32_t cnt = min(w.seg_meta[wg].x, CAND_CAP);
-      const uint2* cb = w.cand + (uint64_t)wg * CAND_CAP;
-      for (uint32_t i = tid; i < cnt; i += NT) {
-        const uint2 e = cb[i];
-        if (fkey(__uint_as_float(e.x)) >= lam) {
-          const uint32_t pos = atomicAdd(&fm[34], 1u);
-          if (pos < SORT_CAP)
-            keys[pos] = pkey(prob_of(__uint_as_float(e.x), P.T, m, S), e.y);
+      const uint32_t lk = seg_beta[g] << BIN_SHIFT;
+      lam = lk > lam ? lk : lam;
+      flags |= seg_flag[g];
+      seg_off[g] = acc;
+      acc += seg_cnt[g];
+    }
+    seg_off[a.G] = acc;
+    float plim = 0.0f;
+    if (lam > 0x007fffffu) plim = prob_of(funkey(lam - 1), P.T, m, S);
+    fm[0] = lam;
+    fm[1] = __float_as_uint(plim);
+    fm[2] = 0;  // gathered
+    fm[3] = (L == NEG_INF || P.Kc == 0 || (flags & FLAG_OVERFLOW)) ? 1u : 0u;
+  }
+  __syncthreads();
+  bool slow = fm[3] != 0;
+  if (!slow) {
+    // ---- gather the candidates at or above lam (values and indices)
+    const uint32_t lam = fm[0];
+    LDS float* cval = pp;
+    LDS uint32_t* cidx = pidx;
+    const uint32_t total = seg_off[a.G];
+    for (uint32_t i0 = 0; i0 < total; i0 += 4 * NT) {
+      u2v e[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t i = i0 + q * NT + tid;
+        e[q] = u2v{0xff800000u, 0u};
+        if (i < total) {
+          uint32_t g = 0;
+          while (g + 1 < a.G && seg_off[g + 1] <= i) ++g;
+          e[q] = G(w.cand)[(uint64_t)row_seg_to_wg(a, b, g) * CAND_CAP + (i - seg_off[g])];
         }
       }
-    }
-    __syncthreads();
-    if (fm[34] > SORT_CAP) slow = true;
-  }
-  if (!slow) {
-    const uint32_t n = fm[34];
-    uint32_t npad = 1;
-    while (npad < n) npad <<= 1;
-    for (uint32_t i = n + tid; i < npad; i += NT) keys[i] = ~0ull;
-    __syncthreads();
-    for (uint32_t k = 2; k <= npad; k <<= 1)
-      for (uint32_t j = k >> 1; j > 0; j >>= 1) {
-        for (uint32_t i = tid; i < npad; i += NT) {
-          const uint32_t ixj = i ^ j;
-          if (ixj > i) {
-            const uint64_t x = keys[i], y = keys[ixj];
-            const bool up = (i & k) == 0;
-            if ((x > y) == up) {
-              keys[i] = y;
-              keys[ixj] = x;
-            }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float v = __uint_as_float(e[q].x);
+        const bool keep = v > NEG_INF && fkey(v) >= lam;
+        const uint64_t mk = __ballot(keep);
+        uint32_t base = 0;
+        if (lane == 0 && mk) base = __atomic_fetch_add(&fm[2], (uint32_t)__popcll(mk), __ATOMIC_RELAXED);
+        base = __shfl(base, 0);
+        if (keep) {
+          const uint32_t pos = base + lanes_below(mk);
+          if (pos < SORT_CAP) {
+            cval[pos] = v;
+            cidx[pos] = e[q].y;
           }
         }
+      }
+    }
+    __syncthreads();
+    const uint32_t n0 = fm[2];
+    if (n0 > SORT_CAP) slow = true;
+    if (!slow) {
+      // ---- top-k rows: the exact K-th largest candidate logit tightens
+      // the bound (every element below it has p <= plim of that bound)
+      const bool topk = P.K > 0 && (uint32_t)P.K < a.V;
+      uint32_t lam_e = lam;
+      float plim_e = __uint_as_float(fm[1]);
+      if (topk && n0 > 2u * (uint32_t)P.K) {
+        const uint32_t tau = block_kth_largest_key(cval, n0, (uint32_t)P.K,
+                                                   (LDS uint32_t*)keys, fm + 8);
+        lam_e = tau;
+        plim_e = tau > 0x007fffffu ? prob_of(funkey(tau - 1), P.T, m, S) : 0.0f;
+      }
+      for (int attempt = 0; attempt < 2; ++attempt) {
+        if (tid == 0) fm[4] = 0;
+        __syncthreads();
+        for (uint32_t i = tid; i < n0; i += NT) {
+          const float v = cval[i];
+          bool keep = false;
+          uint64_t key = 0;
+          if (fkey(v) >= lam_e) {
+            const float p = prob_of(v, P.T, m, S);
+            if (p > plim_e) {
+              keep = true;
+              key = pkey(p, cidx[i]);
+            }
+          }
+          const uint64_t mk = __ballot(keep);
+          uint32_t base = 0;
+          if (lane == 0 && mk) base = __atomic_fetch_add(&fm[4], (uint32_t)__popcll(mk), __ATOMIC_RELAXED);
+          base = __shfl(base, 0);
+          if (keep) keys[base + lanes_below(mk)] = key;
+        }
+        __syncthreads();
+        // a tightened bound that keeps fewer than K (ties in p across it)
+        // falls back to the gather bound
+        if (!(topk && fm[4] < (uint32_t)P.K && lam_e != lam)) break;
+        lam_e = lam;
+        plim_e = __uint_as_float(fm[1]);
         __syncthreads();
       }
-    // P_lim: largest probability any non-candidate can have.
-    if (tid == 0) {
-      float plim = 0.0f;
-      if (lam > 0x007fffffu) plim = prob_of(funkey(lam - 1), P.T, m, S);
-      fm[36] = __float_as_uint(plim);
-      fm[37] = n;  // E
+    }
+  }
+  if (!slow) {
+    // ---- sort ascending; keys are distinct (indices differ)
+    const uint32_t n = fm[4];
+    if (n <= 128) {
+      for (uint32_t i = tid; i < n; i += NT) {
+        const uint64_t k = keys[i];
+        uint32_t r = 0;
+        for (uint32_t j = 0; j < n; ++j) r += (keys[j] < k) ? 1u : 0u;
+        skeys[r] = k;
+      }
+    } else {
+      uint32_t npad = 1;
+      while (npad < n) npad <<= 1;
+      for (uint32_t i = tid; i < npad; i += NT) skeys[i] = i < n ? keys[i] : ~0ull;
+      __syncthreads();
+      for (uint32_t k = 2; k <= npad; k <<= 1)
+        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+          for (uint32_t i = tid; i < npad / 2; i += NT) {
+            // i-th compare-exchange pair of this stage
+            const uint32_t lo = ((i & ~(j - 1)) << 1) | (i & (j - 1));
+            const uint32_t hi = lo | j;
+            const uint64_t x = skeys[lo], y = skeys[hi];
+            const bool up = (lo & k) == 0;
+            if ((x > y) == up) {
+              skeys[lo] = y;
+              skeys[hi] = x;
+            }
+          }
+          __syncthreads();
+        }
     }
     __syncthreads();
-    const float plim = __uint_as_float(fm[36]);
     for (uint32_t i = tid; i < n; i += NT) {
-      const float p = __uint_as_float(~(uint32_t)(keys[i] >> 32));
-      pp[i] = p;
-      pidx[i] = (uint32_t)keys[i];
-      if (!(p > plim)) atomicMin(&fm[37], i);
+      const uint64_t k = skeys[i];
+      pp[i] = __uint_as_float(~(uint32_t)(k >> 32));
+      pidx[i] = (uint32_t)k;
     }
     __syncthreads();
-    const uint32_t E = fm[37];
-    const float u = a.u[b];
+    LdsList Ls{pp, pidx, (LDS float*)keys, Chain{0.f, 0.f, 0.f, 0}};
     uint32_t tok = 0, len = 0;
-    const bool ok = run_semantics<LdsP, LdsI, NT>(P, u, E, a.V, LdsP{pp},
-                                                  LdsI{pidx}, fm + 40, tok, len);
-    if (ok && a.out_cap && len > E && a.out_cap > E) slow = true;
+    const bool ok = run_semantics(P, a.u[b], n, a.V, Ls, fm + 64, tok, len);
+    if (ok && a.out_cap && len > n && a.out_cap > n) slow = true;
     if (!ok) slow = true;
     if (!slow) {
-      write_outputs(a, b, tok, len, pp, pidx, E, NT);
+      write_outputs(a, b, tok, len, Ls);
       return;
     }
   }
-  if (tid == 0) w.row_flags[b] = 1u;
+  slow_row<DT>(a, w, b, P, S, m, smem);
 }
 
 // ---------------------------------------------------------------------------
-// Stream kernel
+// The kernel
 // ---------------------------------------------------------------------------
 template <int DT>
 __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
@@ -757,56 +1211,58 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   }
   const uint32_t t0 = g * a.tps;
   const uint32_t t1 = min(t0 + a.tps, a.ntiles);
-  StreamLds S;
-  S.bitmap = smem;
-  S.hk = S.bitmap + (size_t)a.tps * 32;
-  S.hc = S.hk + HASH_SLOTS;
-  S.hf = S.hc + HASH_SLOTS;
-  S.hcoarse = S.hf + NBINS;
-  S.misc = S.hcoarse + 64;
+  LDS uint32_t* sm = (LDS uint32_t*)smem;
+  LDS uint32_t* red = sm;                    // 64
+  LDS uint32_t* misc = red + 64;             // M_NMISC
+  LDS uint32_t* hf = misc + M_NMISC;         // NBINS
+  LDS uint32_t* hcoarse = hf + NBINS;        // 64
+  LDS uint32_t* hb = hcoarse + 64;           // history tables
+  const uint32_t nwords = (t1 - t0) * 32;
+  Hist h;
+  hist_carve(h, hb, nwords);
+  h.lo = t0 * TILE;
   const bool collect = P.mode == MODE_SAMPLE && P.Kc > 0;
   if (collect) {
-    for (uint32_t i = tid; i < NBINS; i += NT) S.hf[i] = 0;
-    if (tid < 64) S.hcoarse[tid] = 0;
+    for (uint32_t i = tid; i < NBINS; i += NT) hf[i] = 0;
+    if (tid < 64) hcoarse[tid] = 0;
   }
-  if (tid < M_NMISC) S.misc[tid] = 0;
-  const uint32_t lo = t0 * TILE;
-  const uint32_t hi = min(a.V, t1 * TILE);
-  build_history<NT>(a, P, b, lo, hi, (t1 - t0) * 32, S.bitmap, S.hk, S.hc,
-                    &S.misc[M_FLAGS]);
-  const bool need_pen = P.rp != 1.0f || P.pp != 0.0f || P.fp != 0.0f;
-  const bool need_cnt = P.fp != 0.0f;
+  if (tid < M_NMISC) misc[tid] = 0;
   const void* row = (const char*)a.logits +
                     (uint64_t)b * a.stride * (DT == LLMK_F32 ? 4u : 2u);
+  build_history<DT>(a, P, b, row, h.lo, min(a.V, t1 * TILE), nwords, h, red,
+                    &misc[M_FLAGS]);
   const uint32_t* mrow = a.mask ? a.mask + (uint64_t)b * a.mask_words : nullptr;
-  float2* part = w.tile_part + (uint64_t)b * MAX_TILES;
-  uint2* cbuf = w.cand + (uint64_t)blockIdx.x * CAND_CAP;
+  GLB f2v* part = G(w.tile_part) + (uint64_t)b * MAX_TILES;
+  GLB u2v* cbuf = G(w.cand) + (uint64_t)blockIdx.x * CAND_CAP;
   const float c2 = LOG2E_F / P.T;
   const float NINF = NEG_INF;
+  const uint32_t recompute_at = P.Kc / 2 > 16 ? P.Kc / 2 : 16;
+  uint32_t since = EMPTY;  // candidates counted since the last beta update
 
-  auto process = [&](const Raw& raw, uint32_t t) {
+  auto process = [&](const Raw& raw, uint32_t t) __attribute__((always_inline)) {
     float v[16];
     unpack<DT>(raw, v);
     const uint32_t tb = t * TILE;
-    if (need_pen) {
-      uint32_t nib[4];
-      bool anyf = false;
+    // history tokens take their penalised value
+    const uint32_t sh4 = (4u * (uint32_t)lane) & 31u;
+    uint32_t bw[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const uint32_t o = (t - t0) * TILE + 256u * r + 4u * lane;
-        nib[r] = (S.bitmap[o >> 5] >> (o & 31)) & 0xfu;
-        anyf |= nib[r] != 0;
-      }
-      if (anyf) {
+    for (int r = 0; r < 4; ++r)
+      bw[r] = h.bitmap[((tb - h.lo) >> 5) + 8u * r + ((uint32_t)lane >> 3)];
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t nib = (bw[r] >> sh4) & 0xfu;
+      if (nib) {
+        const uint32_t wi = ((tb - h.lo) >> 5) + 8u * r + ((uint32_t)lane >> 3);
+        const uint32_t base = h.pre[wi] + __popc(bw[r] & ((1u << sh4) - 1u));
+        uint32_t k = 0;
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            if ((nib[r] >> q) & 1u) {
-              const uint32_t tok = tb + 256u * r + 4u * lane + q;
-              const uint32_t cnt = need_cnt ? hash_count(S.hk, S.hc, tok) : 1u;
-              v[4 * r + q] = penalize(v[4 * r + q], P, cnt);
-            }
+        for (int q = 0; q < 4; ++q)
+          if ((nib >> q) & 1u) {
+            const uint32_t rr = base + k;
+            if (rr < U_MAX) v[4 * r + q] = h.pen[rr];
+            ++k;
+          }
       }
     }
     if (mrow) {
@@ -831,10 +1287,10 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
           const float x = v[4 * r + q];
           const uint32_t e = tb + 256u * r + 4u * lane + q;
           const bool hit = (x == lm) || (lm == NINF && !(x > NINF));
-          if (hit && e < a.V && e < bi) bi = e;
+          if (hit && e < a.V) bi = umin(bi, e);
         }
       bi = wave_min_u32(bi);
-      if (lane == 0) part[t] = make_float2(lm, __uint_as_float(bi));
+      if (lane == 0) part[t] = f2v{lm, __uint_as_float(bi)};
       return;
     }
     float s = 0.0f;
@@ -850,264 +1306,109 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
       }
       s = (sr[0] + sr[1]) + (sr[2] + sr[3]);
     }
-    if (lane == 0) part[t] = make_float2(lm, s);
+    if (lane == 0) part[t] = f2v{lm, s};
     if (!collect) return;
     // ---- candidates above the rising histogram threshold
-    uint32_t beta = __atomic_load_n(&S.misc[M_BETA], __ATOMIC_RELAXED);
-    uint32_t k[16];
-    bool pass[16];
-    bool anyp = false;
+    uint32_t beta = __atomic_load_n(&misc[M_BETA], __ATOMIC_RELAXED);
+    float th = theta_of(beta);
+    if (!(lm >= th)) return;  // no element of this tile can pass
+    bool counted = false;
+    if (since == EMPTY) {
+      // a wave's first tile: count it, raise the threshold, then append
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      k[j] = fkey(v[j]);
-      pass[j] = (v[j] > NINF) && ((k[j] >> BIN_SHIFT) >= beta);
-      anyp |= pass[j];
-    }
-    if (!__any(anyp)) return;
-#pragma unroll
-    for (int j = 0; j < 16; ++j)
-      if (pass[j]) {
-        atomicAdd(&S.hf[k[j] >> BIN_SHIFT], 1u);
-        atomicAdd(&S.hcoarse[k[j] >> CBIN_SHIFT], 1u);
+      for (int j = 0; j < 16; ++j)
+        if (v[j] >= th) {
+          const uint32_t bin = fkey(v[j]) >> BIN_SHIFT;
+          __atomic_fetch_add(&hf[bin], 1u, __ATOMIC_RELAXED);
+          __atomic_fetch_add(&hcoarse[bin >> (CBIN_SHIFT - BIN_SHIFT)], 1u, __ATOMIC_RELAXED);
+        }
+      const uint32_t nb = compute_beta(hcoarse, hf, P.Kc, lane);
+      if (nb > beta) {
+        if (lane == 0) __atomic_fetch_max(&misc[M_BETA], nb, __ATOMIC_RELAXED);
+        beta = nb;
+        th = theta_of(beta);
       }
-    const uint32_t nb = compute_beta(S.hcoarse, S.hf, P.Kc, lane);
-    if (nb > beta) {
-      if (lane == 0) atomicMax(&S.misc[M_BETA], nb);
-      beta = nb;
+      since = 0;
+      counted = true;
     }
-    uint32_t cnt = 0;
+    uint32_t npass = 0;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      pass[j] = pass[j] && ((k[j] >> BIN_SHIFT) >= beta);
-      cnt += pass[j] ? 1u : 0u;
-    }
-    const uint32_t incl = wave_incl_prefix(cnt, lane);
-    const uint32_t tot = __shfl(incl, 63);
-    if (tot == 0) return;
+    for (int j = 0; j < 16; ++j) npass += (uint32_t)__popcll(__ballot(v[j] >= th));
+    if (npass == 0) return;
     uint32_t base = 0;
-    if (lane == 0) base = atomicAdd(&S.misc[M_CCOUNT], tot);
+    if (lane == 0) base = __atomic_fetch_add(&misc[M_CCOUNT], npass, __ATOMIC_RELAXED);
     base = __shfl(base, 0);
-    if (base + tot > CAND_CAP) {
-      if (lane == 0) atomicOr(&S.misc[M_FLAGS], FLAG_OVERFLOW);
+    if (base + npass > CAND_CAP) {
+      if (lane == 0) __atomic_fetch_or(&misc[M_FLAGS], FLAG_OVERFLOW, __ATOMIC_RELAXED);
       return;
     }
-    uint32_t pos = base + incl - cnt;
+    // append, and count what was appended in the histogram
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (pass[4 * r + q])
-          cbuf[pos++] = make_uint2(__float_as_uint(v[4 * r + q]),
-                                   tb + 256u * r + 4u * lane + q);
+    for (int j = 0; j < 16; ++j) {
+      const uint64_t mk = __ballot(v[j] >= th);
+      if (mk) {
+        if ((mk >> lane) & 1ull) {
+          if (!counted) {
+            const uint32_t bin = fkey(v[j]) >> BIN_SHIFT;
+            __atomic_fetch_add(&hf[bin], 1u, __ATOMIC_RELAXED);
+            __atomic_fetch_add(&hcoarse[bin >> (CBIN_SHIFT - BIN_SHIFT)], 1u, __ATOMIC_RELAXED);
+          }
+          cbuf[base + lanes_below(mk)] =
+              u2v{__float_as_uint(v[j]), tb + 256u * (j >> 2) + 4u * lane + (j & 3)};
+        }
+        base += (uint32_t)__popcll(mk);
+      }
+    }
+    if (counted) return;
+    since += npass;
+    if (since >= recompute_at) {
+      since = 0;
+      const uint32_t nb = compute_beta(hcoarse, hf, P.Kc, lane);
+      if (nb > beta && lane == 0) __atomic_fetch_max(&misc[M_BETA], nb, __ATOMIC_RELAXED);
+    }
   };
 
   Raw ra, rb;
   uint32_t t = t0 + (uint32_t)wv;
-  if (t < t1) load_tile<DT>(a, row, mrow, t, lane, ra);
+  if (t < t1) load_tile<DT>(a, row, mrow, h, t, lane, ra);
   for (;;) {
     if (t >= t1) break;
-    if (t + NW < t1) load_tile<DT>(a, row, mrow, t + NW, lane, rb);
+    if (t + NW < t1) load_tile<DT>(a, row, mrow, h, t + NW, lane, rb);
     process(ra, t);
     t += NW;
     if (t >= t1) break;
-    if (t + NW < t1) load_tile<DT>(a, row, mrow, t + NW, lane, ra);
+    if (t + NW < t1) load_tile<DT>(a, row, mrow, h, t + NW, lane, ra);
     process(rb, t);
     t += NW;
   }
 
-  // ---- publish the segment, find the row's last workgroup
-  __threadfence();
+  // ---- publish the segment; the row's last workgroup finalizes
+  wait_stores();
   __syncthreads();
   if (tid == 0) {
-    const uint32_t fl = S.misc[M_FLAGS];
-    w.seg_meta[blockIdx.x] = make_uint4(S.misc[M_CCOUNT], S.misc[M_BETA], fl, 0u);
+    const uint32_t fl = misc[M_FLAGS];
     if (fl & FLAG_HIST_OVERFLOW) atomicOr(w.status, LLMK_STATUS_HISTORY_OVERFLOW);
     uint32_t last = 1;
     if (a.G > 1) {
-      __threadfence();
+      G(w.seg_meta)[blockIdx.x] = u4v{misc[M_CCOUNT], misc[M_BETA], fl, 0u};
+      __threadfence();  // release this workgroup's stores (all waves waited above)
       const uint32_t old = atomicAdd(&w.row_arrive[b], 1u);
       last = (old == a.G - 1) ? 1u : 0u;
+      if (last) {
+        __threadfence();  // acquire the other segments' stores
+        w.row_arrive[b] = 0;
+      }
+    } else {
+      G(w.seg_meta)[blockIdx.x] = u4v{misc[M_CCOUNT], misc[M_BETA], fl, 0u};
+      wait_stores();
     }
-    S.misc[M_LAST] = last;
+    misc[M_LAST] = last;
   }
   __syncthreads();
-  if (!S.misc[M_LAST]) return;
-  __threadfence();
-  if (tid == 0 && a.G > 1) w.row_arrive[b] = 0;
-  finalize_row(a, w, b, P, smem);
-}
-
-// ---------------------------------------------------------------------------
-// Slow path: exact probabilities of the whole row, stable radix sort
-// ---------------------------------------------------------------------------
-struct GlobP {
-  float* p;
-  __device__ float operator()(uint32_t i) const { return p[i]; }
-  __device__ void set(uint32_t i, float x) const { p[i] = x; }
-};
-struct GlobI {
-  const uint32_t* p;
-  __device__ uint32_t operator()(uint32_t i) const { return p[i]; }
-};
-
-// Block-wide exclusive scan of one flag per thread (SLOW_NT threads).
-__device__ uint32_t block_excl_scan_flag(bool f, uint32_t* red,
-                                         uint32_t& total) {
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const uint64_t m = __ballot(f);
-  const uint32_t below = __popcll(m & ((1ull << lane) - 1ull));
-  if (lane == 0) red[wv] = __popcll(m);
-  __syncthreads();
-  uint32_t off = 0, tot = 0;
-  for (int i = 0; i < SLOW_NT / WAVE; ++i) {
-    const uint32_t c = red[i];
-    if (i < wv) off += c;
-    tot += c;
-  }
-  __syncthreads();
-  total = tot;
-  return off + below;
-}
-
-template <int DT>
-__global__ __launch_bounds__(SLOW_NT) void slow_kernel(Args a, Ws w) {
-  extern __shared__ __align__(16) uint32_t smem[];
-  const uint32_t tid = threadIdx.x;
-  const int lane = (int)(tid & 63), wv = (int)(tid >> 6);
-  const uint32_t V = a.V;
-  uint32_t* bitmap = smem;                       // ceil(V/32)
-  const uint32_t nwords = (V + 31) / 32;
-  uint32_t* hk = bitmap + ((nwords + 3) & ~3u);  // HASH_SLOTS
-  uint32_t* hc = hk + HASH_SLOTS;                // HASH_SLOTS
-  uint32_t* red = hc + HASH_SLOTS;               // 64
-  uint32_t* sh = red + 64;                       // 64
-  uint32_t* digit_off = sh + 64;                 // 256
-  uint32_t* wcnt = digit_off + 256;              // 16*256
-  uint32_t* ttot = wcnt + 16 * 256;              // 256
-  for (uint32_t b = blockIdx.x; b < a.B; b += gridDim.x) {
-    if (__atomic_load_n(&w.row_flags[b], __ATOMIC_RELAXED) == 0) continue;
-    const RowP P = row_params(a, b);
-    if (tid < 64) sh[tid] = 0;
-    build_history<SLOW_NT>(a, P, b, 0, V, nwords, bitmap, hk, hc, &sh[10]);
-    const bool need_pen = P.rp != 1.0f || P.pp != 0.0f || P.fp != 0.0f;
-    const bool need_cnt = P.fp != 0.0f;
-    const float4 st = w.row_stats[b];
-    const float S = st.x, m = st.y;
-    const uint64_t slot = blockIdx.x;
-    uint64_t* kA = w.slow_keys + slot * 3 * (uint64_t)w.max_vocab;
-    uint64_t* kB = kA + w.max_vocab;
-    uint32_t* zl = (uint32_t*)(kB + w.max_vocab);  // zero-probability indices
-    float* plist = w.slow_p + slot * (uint64_t)w.max_vocab;
-    uint32_t* ilist = w.slow_idx + slot * (uint64_t)w.max_vocab;
-    const void* row = (const char*)a.logits +
-                      (uint64_t)b * a.stride * (DT == LLMK_F32 ? 4u : 2u);
-    const uint32_t* mrow = a.mask ? a.mask + (uint64_t)b * a.mask_words : nullptr;
-    // pass 1: exact p of every element, stable split into p>0 / p==0 lists
-    uint32_t npos = 0, nzero = 0;
-    for (uint32_t base = 0; base < V; base += SLOW_NT) {
-      const uint32_t e = base + tid;
-      float p = 0.0f;
-      bool valid = e < V;
-      if (valid) {
-        float x;
-        if (DT == LLMK_F32) x = ((const float*)row)[e];
-        else x = __uint_as_float((uint32_t)((const uint16_t*)row)[e] << 16);
-        if (need_pen && ((bitmap[e >> 5] >> (e & 31)) & 1u))
-          x = penalize(x, P, need_cnt ? hash_count(hk, hc, e) : 1u);
-        if (mrow && !((mrow[e >> 5] >> (e & 31)) & 1u)) x = NEG_INF;
-        if (!(x > NEG_INF)) x = NEG_INF;  // NaN acts as -inf
-        p = prob_of(x, P.T, m, S);
-      }
-      uint32_t tot;
-      const uint32_t pos = block_excl_scan_flag(valid && p > 0.0f, red, tot);
-      if (valid && p > 0.0f) kA[npos + pos] = pkey(p, e);
-      npos += tot;
-      const uint32_t zpos = block_excl_scan_flag(valid && !(p > 0.0f), red, tot);
-      if (valid && !(p > 0.0f)) zl[nzero + zpos] = e;
-      nzero += tot;
-    }
-    // stable LSD radix sort of kA[0..npos) on bits 32..63, 4 passes of 8 bits
-    uint64_t* src = kA;
-    uint64_t* dst = kB;
-    for (int pass = 0; pass < 4; ++pass) {
-      const int sh_bits = 32 + 8 * pass;
-      if (tid < 256) digit_off[tid] = 0;
-      __syncthreads();
-      for (uint32_t i = tid; i < npos; i += SLOW_NT)
-        atomicAdd(&digit_off[(uint32_t)(src[i] >> sh_bits) & 255u], 1u);
-      __syncthreads();
-      if (tid == 0) {
-        uint32_t acc = 0;
-        for (int d = 0; d < 256; ++d) {
-          const uint32_t c = digit_off[d];
-          digit_off[d] = acc;
-          acc += c;
-        }
-      }
-      __syncthreads();
-      for (uint32_t base = 0; base < npos; base += SLOW_NT) {
-        const uint32_t i = base + tid;
-        const bool valid = i < npos;
-        const uint64_t key = valid ? src[i] : 0ull;
-        const uint32_t d = (uint32_t)(key >> sh_bits) & 255u;
-        uint64_t peers = __ballot(valid);
-#pragma unroll
-        for (int bit = 0; bit < 8; ++bit) {
-          const uint64_t bb = __ballot(((d >> bit) & 1u) != 0);
-          peers &= ((d >> bit) & 1u) ? bb : ~bb;
-        }
-        const uint32_t rank = __popcll(peers & ((1ull << lane) - 1ull));
-        for (uint32_t j = tid; j < 16 * 256; j += SLOW_NT) wcnt[j] = 0;
-        __syncthreads();
-        if (valid && rank == 0) wcnt[wv * 256 + d] = __popcll(peers);
-        __syncthreads();
-        if (tid < 256) {
-          uint32_t acc = 0;
-          for (int q = 0; q < SLOW_NT / WAVE; ++q) {
-            const uint32_t c = wcnt[q * 256 + tid];
-            wcnt[q * 256 + tid] = acc;
-            acc += c;
-          }
-          ttot[tid] = acc;
-        }
-        __syncthreads();
-        if (valid) dst[digit_off[d] + wcnt[wv * 256 + d] + rank] = key;
-        __syncthreads();
-        if (tid < 256) digit_off[tid] += ttot[tid];
-        __syncthreads();
-      }
-      uint64_t* tmp = src;
-      src = dst;
-      dst = tmp;
-    }
-    // unpack into p / idx lists (sorted positives, then zeros by index)
-    for (uint32_t i = tid; i < npos; i += SLOW_NT) {
-      const uint64_t k = src[i];
-      plist[i] = __uint_as_float(~(uint32_t)(k >> 32));
-      ilist[i] = (uint32_t)k;
-    }
-    for (uint32_t i = tid; i < nzero; i += SLOW_NT) {
-      plist[npos + i] = 0.0f;
-      ilist[npos + i] = zl[i];
-    }
-    __threadfence_block();
-    __syncthreads();
-    uint32_t tok = 0, len = 0;
-    const float u = a.u[b];
-    run_semantics<GlobP, GlobI, SLOW_NT>(P, u, V, V, GlobP{plist},
-                                         GlobI{ilist}, sh + 20, tok, len);
-    __threadfence_block();
-    __syncthreads();
-    write_outputs(a, b, tok, len, plist, ilist, V, SLOW_NT);
-    if (tid == 0) w.row_flags[b] = 0;
-    __syncthreads();
-  }
-}
-
-size_t slow_lds_bytes(uint32_t V) {
-  const uint32_t nwords = (V + 31) / 32;
-  return 4 * ((size_t)((nwords + 3) & ~3u) + 2 * HASH_SLOTS + 64 + 64 + 256 +
-              16 * 256 + 256);
+  const uint32_t last = misc[M_LAST];
+  __syncthreads();  // finalize reuses this shared memory
+  if (!last) return;
+  finalize_row<DT>(a, w, b, P, sm);
 }
 
 }  // namespace llmk
@@ -1152,15 +1453,13 @@ extern "C" int llmk_sampler_create(llmk_sampler** out, int device,
     return fail(LLMK_ERR_INVALID_ARGUMENT, "max_batch and max_vocab must be > 0");
   if (max_vocab > MAX_TILES * TILE)
     return fail(LLMK_ERR_CAPACITY, "max_vocab above 2^20");
+  if (4 * slow_lds_words(max_vocab) > 160 * 1024)
+    return fail(LLMK_ERR_CAPACITY, "max_vocab too large for the slow path's LDS tables");
   HIPCHK(hipSetDevice(device));
   // Dynamic LDS above 64 KiB must be allowed explicitly.
   HIPCHK(hipFuncSetAttribute((const void*)stream_kernel<LLMK_F32>,
                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
   HIPCHK(hipFuncSetAttribute((const void*)stream_kernel<LLMK_BF16>,
-                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-  HIPCHK(hipFuncSetAttribute((const void*)slow_kernel<LLMK_F32>,
-                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-  HIPCHK(hipFuncSetAttribute((const void*)slow_kernel<LLMK_BF16>,
                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
   const uint32_t pool = max_batch > MAX_WGS ? max_batch : MAX_WGS;
   size_t off = 0;
@@ -1173,23 +1472,18 @@ extern "C" int llmk_sampler_create(llmk_sampler** out, int device,
   const size_t o_part = take(8ull * max_batch * MAX_TILES);
   const size_t o_meta = take(16ull * pool);
   const size_t o_cand = take(8ull * pool * CAND_CAP);
-  const size_t o_flags = take(4ull * max_batch);
-  const size_t o_stats = take(16ull * max_batch);
-  const size_t o_skeys = take(8ull * SLOW_WGS * 3 * max_vocab);
-  const size_t o_sp = take(4ull * SLOW_WGS * max_vocab);
-  const size_t o_si = take(4ull * SLOW_WGS * max_vocab);
+  const size_t o_lock = take(4ull * SLOW_SLOTS);
+  const size_t o_skeys = take(8ull * SLOW_SLOTS * 3 * max_vocab);
+  const size_t o_sp = take(4ull * SLOW_SLOTS * max_vocab);
+  const size_t o_si = take(4ull * SLOW_SLOTS * max_vocab);
   const size_t o_status = take(256);
   void* mem = nullptr;
   HIPCHK(hipMalloc(&mem, off));
   hipError_t e = hipMemset(mem, 0, off);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) {
     (void)hipFree(mem);
-    return fail(LLMK_ERR_HIP, std::string("hipMemset failed: ") + hipGetErrorString(e));
-  }
-  e = hipDeviceSynchronize();
-  if (e != hipSuccess) {
-    (void)hipFree(mem);
-    return fail(LLMK_ERR_HIP, std::string("hipDeviceSynchronize failed: ") + hipGetErrorString(e));
+    return fail(LLMK_ERR_HIP, std::string("workspace init failed: ") + hipGetErrorString(e));
   }
   char* base = (char*)mem;
   llmk_sampler* s = new llmk_sampler();
@@ -1199,11 +1493,10 @@ extern "C" int llmk_sampler_create(llmk_sampler** out, int device,
   s->mem = mem;
   s->mem_bytes = off;
   s->ws.row_arrive = (uint32_t*)(base + o_arrive);
-  s->ws.tile_part = (float2*)(base + o_part);
-  s->ws.seg_meta = (uint4*)(base + o_meta);
-  s->ws.cand = (uint2*)(base + o_cand);
-  s->ws.row_flags = (uint32_t*)(base + o_flags);
-  s->ws.row_stats = (float4*)(base + o_stats);
+  s->ws.tile_part = (f2v*)(base + o_part);
+  s->ws.seg_meta = (u4v*)(base + o_meta);
+  s->ws.cand = (u2v*)(base + o_cand);
+  s->ws.slow_lock = (uint32_t*)(base + o_lock);
   s->ws.slow_keys = (uint64_t*)(base + o_skeys);
   s->ws.slow_p = (float*)(base + o_sp);
   s->ws.slow_idx = (uint32_t*)(base + o_si);
@@ -1229,7 +1522,9 @@ extern "C" int llmk_sampler_status(llmk_sampler* s, void* stream,
   hipStream_t st = (hipStream_t)stream;
   uint32_t v = 0;
   HIPCHK(hipMemcpyAsync(&v, s->ws.status, 4, hipMemcpyDeviceToHost, st));
-  HIPCHK(hipMemsetAsync(s->ws.status, 0, 4, st));
+  HIPCHK(hipStreamSynchronize(st));
+  const uint32_t zero = 0;
+  HIPCHK(hipMemcpyAsync(s->ws.status, &zero, 4, hipMemcpyHostToDevice, st));
   HIPCHK(hipStreamSynchronize(st));
   *status = v;
   return LLMK_OK;
@@ -1285,34 +1580,30 @@ extern "C" int llmk_sample_batch(llmk_sampler* s,
   a.out_probs = in->out_probs;
   a.out_cap = in->out_cap;
   a.ntiles = (a.V + TILE - 1) / TILE;
-  // Segments per row: enough workgroups to cover the 256 CUs, at least 4
-  // tiles per segment.
+  // Segments per row: enough workgroups to cover the 256 CUs, at least 16
+  // tiles per segment, at most MAX_SEG segments.
+  const uint32_t pool = s->max_batch > MAX_WGS ? s->max_batch : MAX_WGS;
   uint32_t G = (256 + a.B - 1) / a.B;
-  const uint32_t gmax = (a.ntiles + 3) / 4;
+  const uint32_t gmax = (a.ntiles + 15) / 16;
   if (G > gmax) G = gmax;
+  if (G > MAX_SEG) G = MAX_SEG;
   if (G < 1) G = 1;
-  while ((uint64_t)a.B * G > (s->max_batch > MAX_WGS ? s->max_batch : MAX_WGS)) --G;
+  while (G > 1 && (uint64_t)a.B * G > pool) --G;
   a.tps = (a.ntiles + G - 1) / G;
   a.G = (a.ntiles + a.tps - 1) / a.tps;
   a.xcd_map = (a.G > 1 && (a.B % 8) == 0) ? 1u : 0u;
 
   HIPCHK(hipSetDevice(s->device));
   hipStream_t st = (hipStream_t)stream;
-  const size_t lds_stream =
-      4 * (stream_lds_words(a.tps) > finalize_lds_words() ? stream_lds_words(a.tps)
-                                                          : finalize_lds_words());
+  size_t words = stream_lds_words(a.tps);
+  if (finalize_lds_words() > words) words = finalize_lds_words();
+  if (slow_lds_words(a.V) > words) words = slow_lds_words(a.V);
+  const size_t lds = 4 * words;
   const dim3 grid(a.B * a.G), block(NT);
   if (a.dtype == LLMK_F32)
-    hipLaunchKernelGGL(stream_kernel<LLMK_F32>, grid, block, lds_stream, st, a, s->ws);
+    hipLaunchKernelGGL(stream_kernel<LLMK_F32>, grid, block, lds, st, a, s->ws);
   else
-    hipLaunchKernelGGL(stream_kernel<LLMK_BF16>, grid, block, lds_stream, st, a, s->ws);
-  HIPCHK(hipGetLastError());
-  const uint32_t nslow = a.B < SLOW_WGS ? a.B : SLOW_WGS;
-  const size_t lds_slow = slow_lds_bytes(a.V);
-  if (a.dtype == LLMK_F32)
-    hipLaunchKernelGGL(slow_kernel<LLMK_F32>, dim3(nslow), dim3(SLOW_NT), lds_slow, st, a, s->ws);
-  else
-    hipLaunchKernelGGL(slow_kernel<LLMK_BF16>, dim3(nslow), dim3(SLOW_NT), lds_slow, st, a, s->ws);
+    hipLaunchKernelGGL(stream_kernel<LLMK_BF16>, grid, block, lds, st, a, s->ws);
   HIPCHK(hipGetLastError());
   return LLMK_OK;
 }

@@ -20,6 +20,7 @@ LLMK_ERR_UNSUPPORTED = -6
 LLMK_INVALID_TOKEN = 0xFFFFFFFF
 LLMK_STATUS_INVALID_PARAMS = 0x1
 LLMK_STATUS_HISTORY_OVERFLOW = 0x2
+LLMK_STATUS_SLOT_TIMEOUT = 0x4
 LLMK_F32 = 0
 LLMK_BF16 = 1
 

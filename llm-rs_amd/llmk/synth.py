@@ -43,6 +43,25 @@ class Workload:
     def mask_words(self) -> int:
         return 0 if self.mask is None else self.mask.shape[1]
 
+    def to_device(self, dev="cuda:0"):
+        """The workload as an llmk.DeviceBatch of torch CUDA tensors."""
+        import torch
+        from .sampler import DeviceBatch
+        T = lambda a, dt=None: torch.from_numpy(
+            np.ascontiguousarray(a) if dt is None else np.ascontiguousarray(a).view(dt)).to(dev)
+        if self.dtype == "bf16":
+            lg = T(self.bf16_bits, np.int16).view(torch.bfloat16)
+        else:
+            lg = T(self.logits)
+        ht = self.hist_tokens if self.hist_tokens.size else np.zeros(1, np.uint32)
+        return DeviceBatch(
+            logits=lg, uniforms=T(self.uniforms), vocab=self.V, temperature=T(self.temperature),
+            top_k=T(self.top_k), top_p=T(self.top_p), min_p=T(self.min_p),
+            repetition_penalty=T(self.repetition), presence_penalty=T(self.presence),
+            frequency_penalty=T(self.frequency), hist_offsets=T(self.hist_offsets, np.int32),
+            hist_tokens=T(ht, np.int32),
+            allow_mask=None if self.mask is None else T(self.mask, np.int32))
+
     def algorithmic_bytes(self) -> int:
         """HBM bytes one step must move at minimum (logits once, histories,
         mask, per-row params/uniform/output)."""

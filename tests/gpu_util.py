@@ -8,20 +8,7 @@ from oracle import llmk_oracle as O
 
 
 def to_device(w, dev="cuda:0"):
-    T = lambda a, dt=None: torch.from_numpy(
-        np.ascontiguousarray(a) if dt is None else np.ascontiguousarray(a).view(dt)).to(dev)
-    if w.dtype == "bf16":
-        lg = T(w.bf16_bits, np.int16).view(torch.bfloat16)
-    else:
-        lg = T(w.logits)
-    ht = w.hist_tokens if w.hist_tokens.size else np.zeros(1, np.uint32)
-    return llmk.DeviceBatch(
-        logits=lg, uniforms=T(w.uniforms), vocab=w.V, temperature=T(w.temperature),
-        top_k=T(w.top_k), top_p=T(w.top_p), min_p=T(w.min_p),
-        repetition_penalty=T(w.repetition), presence_penalty=T(w.presence),
-        frequency_penalty=T(w.frequency), hist_offsets=T(w.hist_offsets, np.int32),
-        hist_tokens=T(ht, np.int32),
-        allow_mask=None if w.mask is None else T(w.mask, np.int32))
+    return w.to_device(dev)
 
 
 def run_gpu(sampler, w, out_cap=64):
