@@ -39,21 +39,23 @@ __device__ __forceinline__ float exp_m(float y) {
   return ok ? res : 0.0f;
 }
 
-// 2^d for d <= 0: the terms of the softmax normaliser.  Integer/fraction
-// split d = k + f (|f| <= 1/2), degree-5 minimax polynomial for 2^f
-// (relative error 1.7e-7), exact scaling by 2^k.  d < -125, -inf and NaN give 0.
+// 2^d for d <= 0: the terms of the softmax normaliser.  d is clamped to
+// [-125, ...] (NaN and -inf give the clamp), rounded to k = rint(d) by adding
+// and subtracting 1.5*2^23, f = d - k in [-1/2, 1/2], 2^f by a degree-5
+// minimax polynomial (relative error 1.7e-7), and the scaling by 2^k is an
+// integer add of k to the exponent field (exact: the result stays normal).
+// Elements at or below the clamp contribute 2^-125 * 2^f.
 __device__ __forceinline__ float exp2_f(float d) {
-  const bool ok = d >= -125.0f;
-  const float dd = ok ? d : 0.0f;
-  const float k = __builtin_rintf(dd);
-  const float f = dd - k;
+  const float dc = __builtin_fmaxf(d, -125.0f);
+  const float t = dc + 12582912.0f;
+  const float k = t - 12582912.0f;
+  const float f = dc - k;
   float p = __builtin_fmaf(0x1.5bba14p-10f, f, 0x1.3cea88p-7f);
   p = __builtin_fmaf(p, f, 0x1.c6b752p-5f);
   p = __builtin_fmaf(p, f, 0x1.ebf9bcp-3f);
   p = __builtin_fmaf(p, f, 0x1.62e42ap-1f);
   p = __builtin_fmaf(p, f, 1.0f);
-  const float res = __builtin_amdgcn_ldexpf(p, (int)k);
-  return ok ? res : 0.0f;
+  return __uint_as_float(__float_as_uint(p) + (__float_as_uint(t) << 23));
 }
 
 constexpr float LOG2E_F = 0x1.715476p+0f;

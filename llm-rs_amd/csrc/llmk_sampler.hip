@@ -188,6 +188,16 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
   x = umin(x, dppu<0x143, 0xc, false>(x, x));
   return bcast63u(x);
 }
+__device__ __forceinline__ uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+  x = umax(x, dppu<0x111, 0xf, false>(x, x));
+  x = umax(x, dppu<0x112, 0xf, false>(x, x));
+  x = umax(x, dppu<0x114, 0xf, false>(x, x));
+  x = umax(x, dppu<0x118, 0xf, false>(x, x));
+  x = umax(x, dppu<0x142, 0xa, false>(x, x));
+  x = umax(x, dppu<0x143, 0xc, false>(x, x));
+  return bcast63u(x);
+}
 // Inclusive prefix sum over lanes.
 __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
   x += dppu<0x111, 0xf, true>(0u, x);
@@ -531,12 +541,30 @@ __device__ __forceinline__ uint64_t pkey(float p, uint32_t idx) {
   return ((uint64_t)(~__float_as_uint(p)) << 32) | idx;
 }
 
+// Synchronisation policies: a whole workgroup (barriers) or one wave (LDS
+// traffic of a single wave completes in order; waiting for it suffices).
+struct BlockSync {
+  static constexpr uint32_t N = NT;
+  __device__ static __forceinline__ uint32_t id() { return threadIdx.x; }
+  __device__ static __forceinline__ void sync() { __syncthreads(); }
+};
+struct WaveSync {
+  static constexpr uint32_t N = WAVE;
+  __device__ static __forceinline__ uint32_t id() { return threadIdx.x & 63u; }
+  __device__ static __forceinline__ void sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS ops done
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+};
+
 // A list sorted by (p desc, idx asc) holding the probabilities as first
 // computed; renormalisations (sampler.rs:84-87, :104-109) are recorded as a
 // chain of divisors and applied on every read, fl(fl(p/s1)/s2), exactly as
 // the reference's in-place divisions, so the list itself is never rewritten.
 // `win(j0, n)` returns an LDS pointer to the current values of
-// p[j0 .. j0+n) (n <= wmax()); all threads call it.
+// p[j0 .. j0+n) (n <= wmax()); every thread of the policy calls it.
 struct Chain {
   float d0, d1, d2;
   int n;
@@ -553,6 +581,7 @@ struct Chain {
     ++n;
   }
 };
+template <class SY>
 struct LdsList {
   LDS const float* p;
   LDS const uint32_t* idx;
@@ -561,14 +590,15 @@ struct LdsList {
   __device__ uint32_t wmax() const { return SORT_CAP; }
   __device__ LDS const float* win(uint32_t j0, uint32_t n) const {
     if (c.n == 0) return p + j0;
-    __syncthreads();
-    for (uint32_t i = threadIdx.x; i < n; i += NT) stage[i] = c.apply(p[j0 + i]);
-    __syncthreads();
+    SY::sync();
+    for (uint32_t i = SY::id(); i < n; i += SY::N) stage[i] = c.apply(p[j0 + i]);
+    SY::sync();
     return stage;
   }
   __device__ float get(uint32_t i) const { return c.apply(p[i]); }
   __device__ uint32_t id(uint32_t i) const { return idx[i]; }
 };
+template <class SY>
 struct GlobList {
   const GLB float* p;
   const GLB uint32_t* idx;
@@ -576,29 +606,30 @@ struct GlobList {
   Chain c;
   __device__ uint32_t wmax() const { return STAGE; }
   __device__ LDS const float* win(uint32_t j0, uint32_t n) const {
-    __syncthreads();
-    for (uint32_t i = threadIdx.x; i < n; i += NT) stage[i] = c.apply(p[j0 + i]);
-    __syncthreads();
+    SY::sync();
+    for (uint32_t i = SY::id(); i < n; i += SY::N) stage[i] = c.apply(p[j0 + i]);
+    SY::sync();
     return stage;
   }
   __device__ float get(uint32_t i) const { return c.apply(p[i]); }
   __device__ uint32_t id(uint32_t i) const { return idx[i]; }
 };
 
-// Sequential f32 scan of p[0..n) in order (all threads call; thread 0 adds).
+// Sequential f32 scan of p[0..n) in order (the policy's thread 0 adds).
 // mode 0: sum of all n.  mode 1: stop at the first j with cum >= thr.
 // mode 2: stop at the first j with thr <= cum (the draw's `r <= cumulative`).
 // Returns the stop index (n if none) and the cumulative including it.
-template <class L>
-__device__ __forceinline__ uint32_t seq_scan(const L& list, uint32_t n, int mode, float thr,
-                             float& cum_out, LDS uint32_t* sh) {
+template <class SY, class L>
+__device__ __forceinline__ uint32_t seq_scan(const L& list, uint32_t n, int mode,
+                                             float thr, float& cum_out,
+                                             LDS uint32_t* sh) {
   float cum = 0.0f;
   uint32_t stop = n;
   const uint32_t W = list.wmax();
   for (uint32_t j0 = 0; j0 < n; j0 += W) {
     const uint32_t cnt = (n - j0 < W) ? n - j0 : W;
     LDS const float* pw = list.win(j0, cnt);
-    if (threadIdx.x == 0) {
+    if (SY::id() == 0) {
       uint32_t j = 0, hit = EMPTY;
       for (; j + 8 <= cnt && hit == EMPTY; j += 8) {
         const f4v lo4 = *(LDS const f4v*)(pw + j);
@@ -618,10 +649,10 @@ __device__ __forceinline__ uint32_t seq_scan(const L& list, uint32_t n, int mode
       sh[0] = __float_as_uint(cum);
       sh[1] = hit;
     }
-    __syncthreads();
+    SY::sync();
     cum = __uint_as_float(sh[0]);
     const uint32_t hit = sh[1];
-    __syncthreads();
+    SY::sync();
     if (hit != EMPTY) {
       stop = j0 + hit;
       break;
@@ -637,12 +668,13 @@ __device__ __forceinline__ void div_all(L& list, float s) {
 }
 
 // min-p / top-k / top-p / draw (sampler.rs:77-124 + min-p) over a sorted list
-// whose first E entries are exact and which has full_len entries.  All
-// threads.  Returns false if an entry beyond E would be needed.
-template <class L>
+// whose first E entries are exact and which has full_len entries.  Every
+// thread of the policy.  Returns false if an entry beyond E would be needed.
+template <class SY, class L>
 __device__ __forceinline__ bool run_semantics(const RowP& P, float u, uint32_t E,
-                              uint32_t full_len, L& list, LDS uint32_t* sh,
-                              uint32_t& tok_out, uint32_t& len_out) {
+                                              uint32_t full_len, L& list,
+                                              LDS uint32_t* sh, uint32_t& tok_out,
+                                              uint32_t& len_out) {
   uint32_t len = full_len;
   bool trunc = E < full_len;
   float s;
@@ -650,20 +682,20 @@ __device__ __forceinline__ bool run_semantics(const RowP& P, float u, uint32_t E
   if (P.min_p > 0.0f) {
     if (E == 0) return false;
     const float thr = P.min_p * list.get(0);
-    if (threadIdx.x == 0) sh[2] = EMPTY;
-    __syncthreads();
+    if (SY::id() == 0) sh[2] = EMPTY;
+    SY::sync();
     const uint32_t lim = E < len ? E : len;
-    for (uint32_t i = threadIdx.x; i < lim; i += NT)
+    for (uint32_t i = SY::id(); i < lim; i += SY::N)
       if (list.get(i) < thr) __atomic_fetch_min(&sh[2], i, __ATOMIC_RELAXED);
-    __syncthreads();
+    SY::sync();
     const uint32_t cut = sh[2];
-    __syncthreads();
+    SY::sync();
     if (cut == EMPTY) {
       if (trunc) return false;
     } else if (cut < len) {
       len = cut;
       trunc = false;
-      seq_scan(list, len, 0, 0.0f, s, sh);
+      seq_scan<SY>(list, len, 0, 0.0f, s, sh);
       div_all(list, s);
     }
   }
@@ -672,13 +704,13 @@ __device__ __forceinline__ bool run_semantics(const RowP& P, float u, uint32_t E
     if ((uint32_t)P.K > E) return false;
     len = (uint32_t)P.K;
     trunc = false;
-    seq_scan(list, len, 0, 0.0f, s, sh);
+    seq_scan<SY>(list, len, 0, 0.0f, s, sh);
     div_all(list, s);
   }
   // ---- top-p, sampler.rs:92-110
   if (P.top_p < 1.0f) {
     const uint32_t lim = (trunc && E < len) ? E : len;
-    const uint32_t j = seq_scan(list, lim, 1, P.top_p, s, sh);
+    const uint32_t j = seq_scan<SY>(list, lim, 1, P.top_p, s, sh);
     if (j == lim && trunc) return false;
     // the renormalisation sum over the kept prefix is the same sequential
     // sum as the cumulative at the cut
@@ -688,7 +720,7 @@ __device__ __forceinline__ bool run_semantics(const RowP& P, float u, uint32_t E
   }
   // ---- draw, sampler.rs:113-124
   const uint32_t lim = (trunc && E < len) ? E : len;
-  const uint32_t j = seq_scan(list, lim, 2, u, s, sh);
+  const uint32_t j = seq_scan<SY>(list, lim, 2, u, s, sh);
   uint32_t tok;
   if (j < lim) tok = list.id(j);
   else {
@@ -700,17 +732,16 @@ __device__ __forceinline__ bool run_semantics(const RowP& P, float u, uint32_t E
   return true;
 }
 
-template <class L>
+template <class SY, class L>
 __device__ __forceinline__ void write_outputs(const Args& a, uint32_t b, uint32_t tok,
-                              uint32_t len, const L& list) {
-  const uint32_t tid = threadIdx.x;
-  if (tid == 0) {
+                                              uint32_t len, const L& list) {
+  if (SY::id() == 0) {
     G(a.out_tok)[b] = tok;
     if (a.out_cnt) G(a.out_cnt)[b] = len;
   }
   if (a.out_cap) {
     const uint32_t n = len < a.out_cap ? len : a.out_cap;
-    for (uint32_t j = tid; j < n; j += NT) {
+    for (uint32_t j = SY::id(); j < n; j += SY::N) {
       if (a.out_ids) G(a.out_ids)[(uint64_t)b * a.out_cap + j] = list.id(j);
       if (a.out_probs) G(a.out_probs)[(uint64_t)b * a.out_cap + j] = list.get(j);
     }
@@ -720,7 +751,7 @@ __device__ __forceinline__ void write_outputs(const Args& a, uint32_t b, uint32_
 // ---------------------------------------------------------------------------
 // Shared-memory layouts (in 32-bit words)
 // ---------------------------------------------------------------------------
-enum : uint32_t { M_BETA = 0, M_CCOUNT = 1, M_FLAGS = 2, M_LAST = 3, M_NMISC = 16 };
+enum : uint32_t { M_BETA = 0, M_CCOUNT = 1, M_FLAGS = 2, M_LAST = 3, M_NEXT = 4, M_NMISC = 16 };
 
 __host__ __device__ inline size_t stream_lds_words(uint32_t tps) {
   return 64 + M_NMISC + NBINS + 64 + hist_lds_words(tps * 32);
@@ -728,7 +759,7 @@ __host__ __device__ inline size_t stream_lds_words(uint32_t tps) {
 __host__ __device__ inline size_t finalize_lds_words() {
   // tiles (2 x MAX_TILES) + keys + sorted keys (2 x SORT_CAP u64) + p + idx
   // + segment tables + scratch
-  return 2 * MAX_TILES + 4 * SORT_CAP + 2 * SORT_CAP + 4 * (MAX_SEG + 1) + 128;
+  return 2 * MAX_TILES + 4 * SORT_CAP + 2 * SORT_CAP + 128 + MAX_SEG + 1;
 }
 __host__ __device__ inline size_t slow_lds_words(uint32_t V) {
   return 128 + 256 + NW * 256 + 256 + STAGE + hist_lds_words((V + 31) / 32);
@@ -894,12 +925,12 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
   if (tid == 0) __threadfence();
   __syncthreads();
   (void)lane;
-  GlobList L{plist, ilist, stage, Chain{0.f, 0.f, 0.f, 0}};
+  GlobList<BlockSync> L{plist, ilist, stage, Chain{0.f, 0.f, 0.f, 0}};
   uint32_t tok = 0, len = 0;
-  run_semantics(P, a.u[b], V, V, L, sh + 20, tok, len);
+  run_semantics<BlockSync>(P, G(a.u)[b], V, V, L, sh + 20, tok, len);
   wait_stores();
   __syncthreads();
-  write_outputs(a, b, tok, len, L);
+  write_outputs<BlockSync>(a, b, tok, len, L);
   wait_stores();
   __syncthreads();
   if (tid == 0) {
@@ -909,24 +940,27 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
 }
 
 // Key (fkey) of the K-th largest of cval[0..n) (K <= n), by a four-round
-// radix select on 8-bit digits.  All threads.  hist: 256 words, sh: 2 words.
-__device__ __forceinline__ uint32_t block_kth_largest_key(LDS const float* cval, uint32_t n,
-                                          uint32_t K, LDS uint32_t* hist,
-                                          LDS uint32_t* sh) {
-  const uint32_t tid = threadIdx.x;
-  const int lane = (int)(tid & 63), wv = (int)(tid >> 6);
+// radix select on 8-bit digits.  Every thread of the policy; the digit
+// search runs in the policy's first wave.  hist: 256 words, sh: 2 words.
+template <class SY>
+__device__ __forceinline__ uint32_t kth_largest_key(LDS const float* cval, uint32_t n,
+                                                    uint32_t K, LDS uint32_t* hist,
+                                                    LDS uint32_t* sh) {
+  const uint32_t id = SY::id();
+  const int lane = (int)(threadIdx.x & 63);
   uint32_t prefix = 0, need = K;
   for (int round = 0; round < 4; ++round) {
     const int shift = 24 - 8 * round;
     const uint32_t hmask = round == 0 ? 0u : (0xffffffffu << (shift + 8));
-    if (tid < 256) hist[tid] = 0;
-    __syncthreads();
-    for (uint32_t i = tid; i < n; i += NT) {
+    for (uint32_t i = id; i < 256; i += SY::N) hist[i] = 0;
+    SY::sync();
+    for (uint32_t i = id; i < n; i += SY::N) {
       const uint32_t k = fkey(cval[i]);
-      if ((k & hmask) == prefix) __atomic_fetch_add(&hist[(k >> shift) & 255u], 1u, __ATOMIC_RELAXED);
+      if ((k & hmask) == prefix)
+        __atomic_fetch_add(&hist[(k >> shift) & 255u], 1u, __ATOMIC_RELAXED);
     }
-    __syncthreads();
-    if (wv == 0) {
+    SY::sync();
+    if (id < WAVE) {
       // lane l covers digits 255-4l .. 252-4l (descending)
       uint32_t c[4], local = 0;
 #pragma unroll
@@ -950,20 +984,24 @@ __device__ __forceinline__ uint32_t block_kth_largest_key(LDS const float* cval,
         }
       }
     }
-    __syncthreads();
+    SY::sync();
     prefix |= sh[0] << shift;
     need = sh[1];
-    __syncthreads();
+    SY::sync();
   }
   return prefix;
 }
 
 // ---------------------------------------------------------------------------
-// Finalize one row
+// Finalize one row.  The candidate path runs in wave 0 alone (no workgroup
+// barriers); if it cannot prove its result exact, the whole workgroup runs
+// the slow path.
 // ---------------------------------------------------------------------------
+enum : uint32_t { F_DONE = 0, F_S = 1, F_M = 2, F_N = 3, F_CNT = 4, F_SCR = 8 };
+
 template <int DT>
 __device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_t b,
-                             const RowP& P, LDS uint32_t* smem) {
+                                             const RowP& P, LDS uint32_t* smem) {
   const uint32_t tid = threadIdx.x;
   const int lane = (int)(tid & 63), wv = (int)(tid >> 6);
   LDS float* tl = (LDS float*)smem;                          // MAX_TILES
@@ -972,222 +1010,207 @@ __device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_
   LDS uint64_t* skeys = keys + SORT_CAP;                     // SORT_CAP (sorted)
   LDS float* pp = (LDS float*)(skeys + SORT_CAP);            // SORT_CAP
   LDS uint32_t* pidx = (LDS uint32_t*)(pp + SORT_CAP);       // SORT_CAP
-  LDS uint32_t* seg_cnt = pidx + SORT_CAP;                   // MAX_SEG+1
-  LDS uint32_t* seg_off = seg_cnt + MAX_SEG + 1;             // MAX_SEG+1
-  LDS uint32_t* seg_beta = seg_off + MAX_SEG + 1;            // MAX_SEG+1
-  LDS uint32_t* seg_flag = seg_beta + MAX_SEG + 1;           // MAX_SEG+1
-  LDS uint32_t* fm = seg_flag + MAX_SEG + 1;                 // 128
-  const uint32_t nt = a.ntiles;
-  const GLB f2v* part = G(w.tile_part) + (uint64_t)b * MAX_TILES;
-  for (uint32_t c = tid; c < nt; c += NT) {
-    const f2v q = part[c];
-    tl[c] = q.x;
-    ts[c] = q.y;
-  }
-  if (tid < a.G) {
-    const u4v sm = G(w.seg_meta)[row_seg_to_wg(a, b, tid)];
-    seg_cnt[tid] = sm.x < CAND_CAP ? sm.x : CAND_CAP;
-    seg_beta[tid] = sm.y;
-    seg_flag[tid] = sm.z;
-  }
-  __syncthreads();
-
-  if (P.mode == MODE_GREEDY) {
-    // sampler.rs:40-50: the first index holding the maximum.
-    float mx = NEG_INF;
-    for (uint32_t c = tid; c < nt; c += NT) mx = fmaxf(mx, tl[c]);
-    mx = block_max(mx, (LDS float*)fm);
-    uint32_t bi = EMPTY;
-    for (uint32_t c = tid; c < nt; c += NT)
-      if (tl[c] == mx) bi = umin(bi, __float_as_uint(ts[c]));
-    bi = block_min_u32(bi, fm + 16);
-    if (bi == EMPTY) bi = 0;
-    if (tid == 0) {
-      G(a.out_tok)[b] = bi;
-      if (a.out_cnt) G(a.out_cnt)[b] = 1;
-      if (a.out_cap) {
-        if (a.out_ids) G(a.out_ids)[(uint64_t)b * a.out_cap] = bi;
-        if (a.out_probs) G(a.out_probs)[(uint64_t)b * a.out_cap] = 1.0f;
-      }
+  LDS uint32_t* fm = pidx + SORT_CAP;                        // 128
+  LDS uint32_t* soff = fm + 128;                             // MAX_SEG+1
+  using SY = WaveSync;
+  if (wv == 0) {
+    uint32_t done = 0;
+    const uint32_t nt = a.ntiles;
+    const GLB f2v* part = G(w.tile_part) + (uint64_t)b * MAX_TILES;
+    float L = NEG_INF;
+    for (uint32_t c = (uint32_t)lane; c < nt; c += WAVE) {
+      const f2v q = part[c];
+      tl[c] = q.x;
+      ts[c] = q.y;
+      L = fmaxf(L, q.x);
     }
-    return;
-  }
-
-  // ---- normaliser S: tree over next_pow2(#tiles), 64-tile blocks per wave
-  float L = NEG_INF;
-  for (uint32_t c = tid; c < nt; c += NT) L = fmaxf(L, tl[c]);
-  L = block_max(L, (LDS float*)fm);
-  const float c2 = LOG2E_F / P.T;
-  uint32_t ntp = 1;
-  while (ntp < nt) ntp <<= 1;
-  const uint32_t nblk = (ntp + 63) / 64;
-  LDS float* blk = (LDS float*)(fm + 32);  // up to 16 block sums
-  for (uint32_t k = (uint32_t)wv; k < nblk; k += NW) {
-    const uint32_t c = 64 * k + (uint32_t)lane;
-    float x = 0.0f;
-    if (c < nt && L != NEG_INF) x = ts[c] * exp2_f((tl[c] - L) * c2);
-    x = wave_tree_sum(x);
-    if (lane == 0) blk[k] = x;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    for (uint32_t len = nblk; len > 1; len >>= 1)
-      for (uint32_t i = 0; i < len / 2; ++i) blk[i] = blk[2 * i] + blk[2 * i + 1];
-  }
-  __syncthreads();
-  const float S = (L != NEG_INF) ? blk[0] : 0.0f;
-  const float m = (P.T != 1.0f) ? L / P.T : L;
-
-  // ---- candidate bound: every element outside the candidate buffers has a
-  // key below lam, hence probability at most plim
-  if (tid == 0) {
-    uint32_t lam = 0, flags = 0, acc = 0;
-    for (uint32_t g = 0; g < a.G; ++g) {
-      const uint32_t lk = seg_beta[g] << BIN_SHIFT;
-      lam = lk > lam ? lk : lam;
-      flags |= seg_flag[g];
-      seg_off[g] = acc;
-      acc += seg_cnt[g];
-    }
-    seg_off[a.G] = acc;
-    float plim = 0.0f;
-    if (lam > 0x007fffffu) plim = prob_of(funkey(lam - 1), P.T, m, S);
-    fm[0] = lam;
-    fm[1] = __float_as_uint(plim);
-    fm[2] = 0;  // gathered
-    fm[3] = (L == NEG_INF || P.Kc == 0 || (flags & FLAG_OVERFLOW)) ? 1u : 0u;
-  }
-  __syncthreads();
-  bool slow = fm[3] != 0;
-  if (!slow) {
-    // ---- gather the candidates at or above lam (values and indices)
-    const uint32_t lam = fm[0];
-    LDS float* cval = pp;
-    LDS uint32_t* cidx = pidx;
-    const uint32_t total = seg_off[a.G];
-    for (uint32_t i0 = 0; i0 < total; i0 += 4 * NT) {
-      u2v e[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t i = i0 + q * NT + tid;
-        e[q] = u2v{0xff800000u, 0u};
-        if (i < total) {
-          uint32_t g = 0;
-          while (g + 1 < a.G && seg_off[g + 1] <= i) ++g;
-          e[q] = G(w.cand)[(uint64_t)row_seg_to_wg(a, b, g) * CAND_CAP + (i - seg_off[g])];
+    L = wave_max(L);
+    SY::sync();
+    float S = 0.0f, m = L;
+    if (P.mode == MODE_GREEDY) {
+      // sampler.rs:40-50: the first index holding the maximum.
+      uint32_t bi = EMPTY;
+      for (uint32_t c = (uint32_t)lane; c < nt; c += WAVE)
+        if (tl[c] == L) bi = umin(bi, __float_as_uint(ts[c]));
+      bi = wave_min_u32(bi);
+      if (bi == EMPTY) bi = 0;
+      if (lane == 0) {
+        G(a.out_tok)[b] = bi;
+        if (a.out_cnt) G(a.out_cnt)[b] = 1;
+        if (a.out_cap) {
+          if (a.out_ids) G(a.out_ids)[(uint64_t)b * a.out_cap] = bi;
+          if (a.out_probs) G(a.out_probs)[(uint64_t)b * a.out_cap] = 1.0f;
         }
       }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float v = __uint_as_float(e[q].x);
-        const bool keep = v > NEG_INF && fkey(v) >= lam;
-        const uint64_t mk = __ballot(keep);
-        uint32_t base = 0;
-        if (lane == 0 && mk) base = __atomic_fetch_add(&fm[2], (uint32_t)__popcll(mk), __ATOMIC_RELAXED);
-        base = __shfl(base, 0);
-        if (keep) {
-          const uint32_t pos = base + lanes_below(mk);
-          if (pos < SORT_CAP) {
-            cval[pos] = v;
-            cidx[pos] = e[q].y;
-          }
-        }
-      }
-    }
-    __syncthreads();
-    const uint32_t n0 = fm[2];
-    if (n0 > SORT_CAP) slow = true;
-    if (!slow) {
-      // ---- top-k rows: the exact K-th largest candidate logit tightens
-      // the bound (every element below it has p <= plim of that bound)
-      const bool topk = P.K > 0 && (uint32_t)P.K < a.V;
-      uint32_t lam_e = lam;
-      float plim_e = __uint_as_float(fm[1]);
-      if (topk && n0 > 2u * (uint32_t)P.K) {
-        const uint32_t tau = block_kth_largest_key(cval, n0, (uint32_t)P.K,
-                                                   (LDS uint32_t*)keys, fm + 8);
-        lam_e = tau;
-        plim_e = tau > 0x007fffffu ? prob_of(funkey(tau - 1), P.T, m, S) : 0.0f;
-      }
-      for (int attempt = 0; attempt < 2; ++attempt) {
-        if (tid == 0) fm[4] = 0;
-        __syncthreads();
-        for (uint32_t i = tid; i < n0; i += NT) {
-          const float v = cval[i];
-          bool keep = false;
-          uint64_t key = 0;
-          if (fkey(v) >= lam_e) {
-            const float p = prob_of(v, P.T, m, S);
-            if (p > plim_e) {
-              keep = true;
-              key = pkey(p, cidx[i]);
-            }
-          }
-          const uint64_t mk = __ballot(keep);
-          uint32_t base = 0;
-          if (lane == 0 && mk) base = __atomic_fetch_add(&fm[4], (uint32_t)__popcll(mk), __ATOMIC_RELAXED);
-          base = __shfl(base, 0);
-          if (keep) keys[base + lanes_below(mk)] = key;
-        }
-        __syncthreads();
-        // a tightened bound that keeps fewer than K (ties in p across it)
-        // falls back to the gather bound
-        if (!(topk && fm[4] < (uint32_t)P.K && lam_e != lam)) break;
-        lam_e = lam;
-        plim_e = __uint_as_float(fm[1]);
-        __syncthreads();
-      }
-    }
-  }
-  if (!slow) {
-    // ---- sort ascending; keys are distinct (indices differ)
-    const uint32_t n = fm[4];
-    if (n <= 128) {
-      for (uint32_t i = tid; i < n; i += NT) {
-        const uint64_t k = keys[i];
-        uint32_t r = 0;
-        for (uint32_t j = 0; j < n; ++j) r += (keys[j] < k) ? 1u : 0u;
-        skeys[r] = k;
-      }
+      done = 1;
     } else {
-      uint32_t npad = 1;
-      while (npad < n) npad <<= 1;
-      for (uint32_t i = tid; i < npad; i += NT) skeys[i] = i < n ? keys[i] : ~0ull;
-      __syncthreads();
-      for (uint32_t k = 2; k <= npad; k <<= 1)
-        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
-          for (uint32_t i = tid; i < npad / 2; i += NT) {
-            // i-th compare-exchange pair of this stage
-            const uint32_t lo = ((i & ~(j - 1)) << 1) | (i & (j - 1));
-            const uint32_t hi = lo | j;
-            const uint64_t x = skeys[lo], y = skeys[hi];
-            const bool up = (lo & k) == 0;
-            if ((x > y) == up) {
-              skeys[lo] = y;
-              skeys[hi] = x;
+      // ---- normaliser S: tree over next_pow2(#tiles) in blocks of 64 tiles
+      const float c2 = LOG2E_F / P.T;
+      uint32_t ntp = 1;
+      while (ntp < nt) ntp <<= 1;
+      const uint32_t nblk = (ntp + 63) / 64;
+      float blk[MAX_TILES / 64];
+#pragma unroll
+      for (uint32_t k = 0; k < MAX_TILES / 64; ++k) {
+        blk[k] = 0.0f;
+        if (k < nblk) {
+          const uint32_t c = 64 * k + (uint32_t)lane;
+          float x = 0.0f;
+          if (c < nt && L != NEG_INF) x = ts[c] * exp2_f((tl[c] - L) * c2);
+          blk[k] = wave_tree_sum(x);
+        }
+      }
+      for (uint32_t len = nblk; len > 1; len >>= 1)
+#pragma unroll
+        for (uint32_t i = 0; i < MAX_TILES / 128; ++i)
+          if (i < len / 2) blk[i] = blk[2 * i] + blk[2 * i + 1];
+      S = (L != NEG_INF) ? blk[0] : 0.0f;
+      m = (P.T != 1.0f) ? L / P.T : L;
+      // ---- candidate bound: every element outside the candidate buffers
+      // has a key below lam, hence probability at most plim
+      uint32_t cnt = 0, beta = 0, flg = 0;
+      if ((uint32_t)lane < a.G) {
+        const u4v sm = G(w.seg_meta)[row_seg_to_wg(a, b, (uint32_t)lane)];
+        cnt = sm.x < CAND_CAP ? sm.x : CAND_CAP;
+        beta = sm.y;
+        flg = sm.z;
+      }
+      uint32_t lam = wave_max_u32(beta << BIN_SHIFT);
+      const bool ovf = __ballot((flg & FLAG_OVERFLOW) != 0) != 0;
+      // segment g holds candidates [soff[g], soff[g+1]); written with the
+      // whole wave active, looked up from LDS in the divergent gather below
+      const uint32_t off_incl = wave_incl_scan(cnt);
+      const uint32_t total = bcast63u(off_incl);
+      if ((uint32_t)lane <= a.G) soff[lane] = off_incl - cnt;  // lane G: total
+      SY::sync();
+      bool ok = !(L == NEG_INF || P.Kc == 0 || ovf);
+      // ---- gather the candidates at or above lam (values and indices)
+      LDS float* cval = pp;
+      LDS uint32_t* cidx = pidx;
+      uint32_t n0 = 0;
+      if (ok) {
+        for (uint32_t i0 = 0; i0 < total; i0 += WAVE) {
+          const uint32_t i = i0 + (uint32_t)lane;
+          float v = NEG_INF;
+          uint32_t ix = 0;
+          if (i < total) {
+            uint32_t g = 0;
+            while (g + 1 < a.G && soff[g + 1] <= i) ++g;
+            const u2v e = G(w.cand)[(uint64_t)row_seg_to_wg(a, b, g) * CAND_CAP + (i - soff[g])];
+            v = __uint_as_float(e.x);
+            ix = e.y;
+          }
+          const bool keep = v > NEG_INF && fkey(v) >= lam;
+          const uint64_t mk = __ballot(keep);
+          if (keep) {
+            const uint32_t pos = n0 + lanes_below(mk);
+            if (pos < SORT_CAP) {
+              cval[pos] = v;
+              cidx[pos] = ix;
             }
           }
-          __syncthreads();
+          n0 += (uint32_t)__popcll(mk);
         }
+        if (n0 > SORT_CAP) ok = false;
+      }
+      SY::sync();
+      uint32_t n = 0;
+      if (ok) {
+        // ---- top-k rows: the exact K-th largest candidate logit tightens
+        // the bound (every element below it has p <= plim of that bound)
+        const bool topk = P.K > 0 && (uint32_t)P.K < a.V;
+        float plim = lam > 0x007fffffu ? prob_of(funkey(lam - 1), P.T, m, S) : 0.0f;
+        uint32_t lam_e = lam;
+        float plim_e = plim;
+        if (topk && n0 > 2u * (uint32_t)P.K && n0 >= (uint32_t)P.K) {
+          const uint32_t tau = kth_largest_key<SY>(cval, n0, (uint32_t)P.K,
+                                                   (LDS uint32_t*)keys, fm + F_SCR);
+          lam_e = tau;
+          plim_e = tau > 0x007fffffu ? prob_of(funkey(tau - 1), P.T, m, S) : 0.0f;
+        }
+        for (int attempt = 0; attempt < 2; ++attempt) {
+          n = 0;
+          for (uint32_t i0 = 0; i0 < n0; i0 += WAVE) {
+            const uint32_t i = i0 + (uint32_t)lane;
+            bool keep = false;
+            uint64_t key = 0;
+            if (i < n0) {
+              const float v = cval[i];
+              if (fkey(v) >= lam_e) {
+                const float pv = prob_of(v, P.T, m, S);
+                if (pv > plim_e) {
+                  keep = true;
+                  key = pkey(pv, cidx[i]);
+                }
+              }
+            }
+            const uint64_t mk = __ballot(keep);
+            if (keep) keys[n + lanes_below(mk)] = key;
+            n += (uint32_t)__popcll(mk);
+          }
+          // a tightened bound that keeps fewer than K (ties in p across it)
+          // falls back to the gather bound
+          if (!(topk && n < (uint32_t)P.K && lam_e != lam)) break;
+          lam_e = lam;
+          plim_e = plim;
+        }
+        SY::sync();
+        // ---- sort ascending; keys are distinct (indices differ)
+        if (n <= 512) {
+          for (uint32_t i = (uint32_t)lane; i < n; i += WAVE) {
+            const uint64_t k = keys[i];
+            uint32_t r = 0;
+            for (uint32_t j = 0; j < n; ++j) r += (keys[j] < k) ? 1u : 0u;
+            skeys[r] = k;
+          }
+        } else {
+          uint32_t npad = 1;
+          while (npad < n) npad <<= 1;
+          for (uint32_t i = (uint32_t)lane; i < npad; i += WAVE) skeys[i] = i < n ? keys[i] : ~0ull;
+          SY::sync();
+          for (uint32_t k = 2; k <= npad; k <<= 1)
+            for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+              for (uint32_t i = (uint32_t)lane; i < npad / 2; i += WAVE) {
+                const uint32_t lo = ((i & ~(j - 1)) << 1) | (i & (j - 1));
+                const uint32_t hi = lo | j;
+                const uint64_t x = skeys[lo], y = skeys[hi];
+                const bool up = (lo & k) == 0;
+                if ((x > y) == up) {
+                  skeys[lo] = y;
+                  skeys[hi] = x;
+                }
+              }
+              SY::sync();
+            }
+        }
+        SY::sync();
+        for (uint32_t i = (uint32_t)lane; i < n; i += WAVE) {
+          const uint64_t k = skeys[i];
+          pp[i] = __uint_as_float(~(uint32_t)(k >> 32));
+          pidx[i] = (uint32_t)k;
+        }
+        SY::sync();
+        LdsList<SY> Ls{pp, pidx, (LDS float*)keys, Chain{0.f, 0.f, 0.f, 0}};
+        uint32_t tok = 0, len = 0;
+        ok = run_semantics<SY>(P, G(a.u)[b], n, a.V, Ls, fm + F_SCR, tok, len);
+        if (ok && a.out_cap && len > n && a.out_cap > n) ok = false;
+        if (ok) {
+          write_outputs<SY>(a, b, tok, len, Ls);
+          done = 1;
+        }
+      }
     }
-    __syncthreads();
-    for (uint32_t i = tid; i < n; i += NT) {
-      const uint64_t k = skeys[i];
-      pp[i] = __uint_as_float(~(uint32_t)(k >> 32));
-      pidx[i] = (uint32_t)k;
-    }
-    __syncthreads();
-    LdsList Ls{pp, pidx, (LDS float*)keys, Chain{0.f, 0.f, 0.f, 0}};
-    uint32_t tok = 0, len = 0;
-    const bool ok = run_semantics(P, a.u[b], n, a.V, Ls, fm + 64, tok, len);
-    if (ok && a.out_cap && len > n && a.out_cap > n) slow = true;
-    if (!ok) slow = true;
-    if (!slow) {
-      write_outputs(a, b, tok, len, Ls);
-      return;
+    if (lane == 0) {
+      fm[F_DONE] = done;
+      fm[F_S] = __float_as_uint(S);
+      fm[F_M] = __float_as_uint(m);
     }
   }
-  slow_row<DT>(a, w, b, P, S, m, smem);
+  __syncthreads();
+  const uint32_t done = fm[F_DONE];
+  const float S = __uint_as_float(fm[F_S]), m = __uint_as_float(fm[F_M]);
+  __syncthreads();
+  if (!done) slow_row<DT>(a, w, b, P, S, m, smem);
 }
 
 // ---------------------------------------------------------------------------
@@ -1229,6 +1252,15 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   if (tid < M_NMISC) misc[tid] = 0;
   const void* row = (const char*)a.logits +
                     (uint64_t)b * a.stride * (DT == LLMK_F32 ? 4u : 2u);
+  const uint32_t* mrow0 = a.mask ? a.mask + (uint64_t)b * a.mask_words : nullptr;
+  // The first two tiles of every wave are requested before the history
+  // tables are built, so HBM works while the workgroup waits on them.
+  Raw ra, rb;
+  uint32_t ta = t0 + (uint32_t)wv, tb2 = t0 + (uint32_t)wv + NW;
+  ta = ta < t1 ? ta : EMPTY;
+  tb2 = tb2 < t1 ? tb2 : EMPTY;
+  if (ta != EMPTY) load_tile<DT>(a, row, mrow0, h, ta, lane, ra);
+  if (tb2 != EMPTY) load_tile<DT>(a, row, mrow0, h, tb2, lane, rb);
   build_history<DT>(a, P, b, row, h.lo, min(a.V, t1 * TILE), nwords, h, red,
                     &misc[M_FLAGS]);
   const uint32_t* mrow = a.mask ? a.mask + (uint64_t)b * a.mask_words : nullptr;
@@ -1295,16 +1327,19 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
     }
     float s = 0.0f;
     if (lm != NINF) {
+      // per lane: ((run0 + run1) + (run2 + run3)), each run ((e0+e1)+(e2+e3));
+      // then a balanced tree over the 64 lanes
+      const float nb = -(lm * c2);
       float sr[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float e0 = exp2_f((v[4 * r + 0] - lm) * c2);
-        const float e1 = exp2_f((v[4 * r + 1] - lm) * c2);
-        const float e2 = exp2_f((v[4 * r + 2] - lm) * c2);
-        const float e3 = exp2_f((v[4 * r + 3] - lm) * c2);
-        sr[r] = wave_tree_sum((e0 + e1) + (e2 + e3));
+        const float e0 = exp2_f(__builtin_fmaf(v[4 * r + 0], c2, nb));
+        const float e1 = exp2_f(__builtin_fmaf(v[4 * r + 1], c2, nb));
+        const float e2 = exp2_f(__builtin_fmaf(v[4 * r + 2], c2, nb));
+        const float e3 = exp2_f(__builtin_fmaf(v[4 * r + 3], c2, nb));
+        sr[r] = (e0 + e1) + (e2 + e3);
       }
-      s = (sr[0] + sr[1]) + (sr[2] + sr[3]);
+      s = wave_tree_sum((sr[0] + sr[1]) + (sr[2] + sr[3]));
     }
     if (lane == 0) part[t] = f2v{lm, s};
     if (!collect) return;
@@ -1368,18 +1403,26 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
     }
   };
 
-  Raw ra, rb;
-  uint32_t t = t0 + (uint32_t)wv;
-  if (t < t1) load_tile<DT>(a, row, mrow, h, t, lane, ra);
+  // Later tiles are claimed dynamically, so the waves finish together.
+  auto grab = [&]() -> uint32_t {
+    uint32_t k = 0;
+    if (lane == 0) k = __atomic_fetch_add(&misc[M_NEXT], 1u, __ATOMIC_RELAXED);
+    k = (uint32_t)__builtin_amdgcn_readfirstlane((int)k);
+    const uint32_t t = t0 + 2u * NW + k;
+    return t < t1 ? t : EMPTY;
+  };
   for (;;) {
-    if (t >= t1) break;
-    if (t + NW < t1) load_tile<DT>(a, row, mrow, h, t + NW, lane, rb);
-    process(ra, t);
-    t += NW;
-    if (t >= t1) break;
-    if (t + NW < t1) load_tile<DT>(a, row, mrow, h, t + NW, lane, ra);
-    process(rb, t);
-    t += NW;
+    if (ta == EMPTY && tb2 == EMPTY) break;
+    if (ta != EMPTY) {
+      process(ra, ta);
+      ta = grab();
+      if (ta != EMPTY) load_tile<DT>(a, row, mrow, h, ta, lane, ra);
+    }
+    if (tb2 != EMPTY) {
+      process(rb, tb2);
+      tb2 = grab();
+      if (tb2 != EMPTY) load_tile<DT>(a, row, mrow, h, tb2, lane, rb);
+    }
   }
 
   // ---- publish the segment; the row's last workgroup finalizes

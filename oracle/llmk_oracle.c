@@ -64,18 +64,26 @@ float llmk_oracle_exp_m(float y) {
 }
 
 float llmk_oracle_exp2_f(float d) {
-  /* Terms of the softmax normaliser: 2^d for d <= 0.  Below -125 (and for
-   * -inf / NaN) the term is 0; otherwise the result is a normal float and the
-   * final scaling by 2^k is exact. */
-  if (!(d >= -125.0f)) return 0.0f;
-  float k = rintf(d);
-  float f = d - k;
+  /* Terms of the softmax normaliser: 2^d for d <= 0.  d is clamped at -125
+   * (fmaxf also maps NaN there), k = rint(d) through +/- 1.5*2^23, f = d - k,
+   * degree-5 polynomial for 2^f, exact scaling by adding k to the exponent
+   * bits. */
+  const float dc = fmaxf(d, -125.0f);
+  const float t = dc + 12582912.0f;
+  const float k = t - 12582912.0f;
+  const float f = dc - k;
   float p = fmaf(E2C5, f, E2C4);
   p = fmaf(p, f, E2C3);
   p = fmaf(p, f, E2C2);
   p = fmaf(p, f, E2C1);
   p = fmaf(p, f, 1.0f);
-  return ldexpf(p, (int)k);
+  uint32_t pb, tb;
+  memcpy(&pb, &p, 4);
+  memcpy(&tb, &t, 4);
+  const uint32_t rb = pb + (tb << 23);
+  float r;
+  memcpy(&r, &rb, 4);
+  return r;
 }
 
 float llmk_oracle_libm_expf(float y) { return expf(y); }
@@ -89,9 +97,14 @@ static void tree_sum_inplace(float* buf, uint32_t len) {
 float llmk_oracle_normalizer(const float* lp, uint32_t V, float temperature) {
   /* Two-level log-sum-exp over 1024-wide vocabulary tiles.
    *   c2 = fl(log2(e) / T)
-   *   tile c: lc = max lp (NaN ignored); s_c = tree_sum(2^((lp_i - lc)*c2))
-   *   row:    L = max lc; S = tree_sum over next_pow2(#tiles) of
-   *           s_c * 2^((lc - L)*c2)      (padding entries are 0)
+   *   tile c (positions past V count as -inf): lc = max lp (NaN ignored);
+   *     if lc = -inf the tile sum is 0, else with nb = -fl(lc*c2) each
+   *     element gives e = exp2_f(fma(lp, c2, nb)); position 256r + 4L + q
+   *     belongs to lane L, run r; a run sums ((e0+e1)+(e2+e3)), a lane
+   *     ((run0+run1)+(run2+run3)), the tile is the balanced tree over the
+   *     64 lanes.
+   *   row: L = max lc; S = balanced tree over next_pow2(#tiles) of
+   *     s_c * exp2_f((lc - L)*c2)  (padding entries are 0).
    * Mathematically S = sum_i e^{(lp_i - L)/T}, the reference's softmax
    * denominator (sampler.rs:57-66); the order of operations is fixed. */
   const float c2 = LOG2E_F / temperature;
@@ -100,7 +113,7 @@ float llmk_oracle_normalizer(const float* lp, uint32_t V, float temperature) {
   while (ntp < nt) ntp <<= 1;
   float* lc = (float*)malloc(sizeof(float) * nt);
   float* w = (float*)calloc(ntp, sizeof(float));
-  float buf[TILE];
+  float lanes[64];
   for (uint32_t c = 0; c < nt; ++c) {
     const uint32_t base = c * TILE;
     const uint32_t n = (V - base < TILE) ? V - base : TILE;
@@ -112,10 +125,22 @@ float llmk_oracle_normalizer(const float* lp, uint32_t V, float temperature) {
       w[c] = 0.0f;
       continue;
     }
-    for (uint32_t i = 0; i < TILE; ++i)
-      buf[i] = (i < n) ? llmk_oracle_exp2_f((lp[base + i] - m) * c2) : 0.0f;
-    tree_sum_inplace(buf, TILE);
-    w[c] = buf[0];
+    const float nb = -(m * c2);
+    for (uint32_t L = 0; L < 64; ++L) {
+      float run[4];
+      for (uint32_t r = 0; r < 4; ++r) {
+        float e[4];
+        for (uint32_t q = 0; q < 4; ++q) {
+          const uint32_t i = 256 * r + 4 * L + q;
+          const float x = (i < n) ? lp[base + i] : -INFINITY;
+          e[q] = llmk_oracle_exp2_f(fmaf(x, c2, nb));
+        }
+        run[r] = (e[0] + e[1]) + (e[2] + e[3]);
+      }
+      lanes[L] = (run[0] + run[1]) + (run[2] + run[3]);
+    }
+    tree_sum_inplace(lanes, 64);
+    w[c] = lanes[0];
   }
   float L = -INFINITY;
   for (uint32_t c = 0; c < nt; ++c)
