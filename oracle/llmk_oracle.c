@@ -324,6 +324,87 @@ static int params_invalid(const llmk_oracle_params* p) {
   return 0;
 }
 
+/* min-p, top-k (sampler.rs:80-89), top-p (:92-110) and the draw (:113-124)
+ * on a list sorted by (p desc, idx asc); L is truncated in place. */
+static void semantics(plist* Lp, const llmk_oracle_params* prm, float u,
+                      uint32_t* out_token, uint32_t* out_ids, float* out_probs,
+                      uint32_t out_cap, uint32_t* out_count) {
+  plist L = *Lp;
+  /* min-p (extension): keep p >= min_p * p_max; renormalise if it cut. */
+  if (prm->min_p > 0.0f && L.n > 0) {
+    float thr = prm->min_p * L.p[0];
+    uint32_t cut = L.n;
+    for (uint32_t j = 0; j < L.n; ++j)
+      if (L.p[j] < thr) {
+        cut = j;
+        break;
+      }
+    if (cut < L.n) {
+      L.n = cut;
+      renormalize(&L);
+    }
+  }
+  /* top-k, :80-89 */
+  if (prm->top_k > 0 && (uint32_t)prm->top_k < L.n) {
+    L.n = (uint32_t)prm->top_k;
+    renormalize(&L);
+  }
+  /* top-p, :92-110 */
+  if (prm->top_p < 1.0f) {
+    float cum = 0.0f;
+    uint32_t cut = L.n;
+    for (uint32_t j = 0; j < L.n; ++j) {
+      cum += L.p[j];
+      if (cum >= prm->top_p) {
+        cut = j + 1;
+        break;
+      }
+    }
+    L.n = cut;
+    renormalize(&L);
+  }
+  /* draw, :113-124 */
+  uint32_t tok = (L.n > 0) ? L.idx[L.n - 1] : 0;
+  {
+    float cum = 0.0f;
+    for (uint32_t j = 0; j < L.n; ++j) {
+      cum += L.p[j];
+      if (u <= cum) {
+        tok = L.idx[j];
+        break;
+      }
+    }
+  }
+  *out_token = tok;
+  if (out_count) *out_count = L.n;
+  for (uint32_t j = 0; j < L.n && j < out_cap; ++j) {
+    if (out_ids) out_ids[j] = L.idx[j];
+    if (out_probs) out_probs[j] = L.p[j];
+  }
+  *Lp = L;
+}
+
+/* The penalised, masked logits before the greedy check (sampler.rs:34-37
+ * plus the extensions in their order); NaN becomes -inf in mirror mode. */
+int llmk_oracle_process_logits(int mode, const float* logits, uint32_t V,
+                               const llmk_oracle_params* prm,
+                               const uint32_t* hist, uint32_t H,
+                               const uint32_t* mask, float* out) {
+  if (V == 0) return -1;
+  if (params_invalid(prm)) return -2;
+  memcpy(out, logits, sizeof(float) * V);
+  if (mode == LLMK_ORACLE_MIRROR)
+    for (uint32_t i = 0; i < V; ++i)
+      if (isnan(out[i])) out[i] = -INFINITY;
+  apply_repetition(out, V, hist, H, prm->repetition_penalty);
+  apply_presence_frequency(out, V, hist, H, prm->presence_penalty,
+                           prm->frequency_penalty);
+  if (mask)
+    for (uint32_t i = 0; i < V; ++i)
+      if (!((mask[i >> 5] >> (i & 31)) & 1u)) out[i] = -INFINITY;
+  return 0;
+}
+
 int llmk_oracle_sample_row(int mode, const float* logits, uint32_t V,
                            const llmk_oracle_params* prm, const uint32_t* hist,
                            uint32_t H, const uint32_t* mask, float u,
@@ -403,61 +484,32 @@ int llmk_oracle_sample_row(int mode, const float* logits, uint32_t V,
   }
   free(keys);
 
-  /* min-p (extension): keep p >= min_p * p_max; renormalise if it cut. */
-  if (prm->min_p > 0.0f && L.n > 0) {
-    float thr = prm->min_p * L.p[0];
-    uint32_t cut = L.n;
-    for (uint32_t j = 0; j < L.n; ++j)
-      if (L.p[j] < thr) {
-        cut = j;
-        break;
-      }
-    if (cut < L.n) {
-      L.n = cut;
-      renormalize(&L);
-    }
-  }
-  /* top-k, :80-89 */
-  if (prm->top_k > 0 && (uint32_t)prm->top_k < L.n) {
-    L.n = (uint32_t)prm->top_k;
-    renormalize(&L);
-  }
-  /* top-p, :92-110 */
-  if (prm->top_p < 1.0f) {
-    float cum = 0.0f;
-    uint32_t cut = L.n;
-    for (uint32_t j = 0; j < L.n; ++j) {
-      cum += L.p[j];
-      if (cum >= prm->top_p) {
-        cut = j + 1;
-        break;
-      }
-    }
-    L.n = cut;
-    renormalize(&L);
-  }
-  /* draw, :113-124 */
-  uint32_t tok = (L.n > 0) ? L.idx[L.n - 1] : 0;
-  {
-    float cum = 0.0f;
-    for (uint32_t j = 0; j < L.n; ++j) {
-      cum += L.p[j];
-      if (u <= cum) {
-        tok = L.idx[j];
-        break;
-      }
-    }
-  }
-  *out_token = tok;
-  if (out_count) *out_count = L.n;
-  for (uint32_t j = 0; j < L.n && j < out_cap; ++j) {
-    if (out_ids) out_ids[j] = L.idx[j];
-    if (out_probs) out_probs[j] = L.p[j];
-  }
+  semantics(&L, prm, u, out_token, out_ids, out_probs, out_cap, out_count);
   free(L.p);
   free(L.idx);
   free(e);
   free(l);
+  return 0;
+}
+
+/* The steps after the sort on a caller-supplied sorted list. */
+int llmk_oracle_semantics(const float* p_sorted, const uint32_t* idx, uint32_t n,
+                          const llmk_oracle_params* prm, float u,
+                          uint32_t* out_token, uint32_t* out_ids,
+                          float* out_probs, uint32_t out_cap,
+                          uint32_t* out_count) {
+  if (params_invalid(prm)) return -2;
+  plist L;
+  L.n = n;
+  L.p = (float*)malloc(sizeof(float) * (n ? n : 1));
+  L.idx = (uint32_t*)malloc(sizeof(uint32_t) * (n ? n : 1));
+  if (n) {
+    memcpy(L.p, p_sorted, sizeof(float) * n);
+    memcpy(L.idx, idx, sizeof(uint32_t) * n);
+  }
+  semantics(&L, prm, u, out_token, out_ids, out_probs, out_cap, out_count);
+  free(L.p);
+  free(L.idx);
   return 0;
 }
 

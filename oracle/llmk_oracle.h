@@ -68,6 +68,21 @@ int llmk_oracle_sample_row(int mode, const float* logits, uint32_t V,
                            float* out_probs, uint32_t out_cap,
                            uint32_t* out_count);
 
+/* The penalised (repetition, presence/frequency) and masked logits of one
+ * row, before the greedy check and temperature.  Returns 0, -1, -2 as above. */
+int llmk_oracle_process_logits(int mode, const float* logits, uint32_t V,
+                               const llmk_oracle_params* p,
+                               const uint32_t* hist, uint32_t H,
+                               const uint32_t* mask, float* out);
+
+/* The steps after the sort — min-p, top-k, top-p, draw — on a list already
+ * in (p desc, idx asc) order (p_sorted[n], idx[n]).  Outputs as above. */
+int llmk_oracle_semantics(const float* p_sorted, const uint32_t* idx, uint32_t n,
+                          const llmk_oracle_params* p, float u,
+                          uint32_t* out_token, uint32_t* out_ids,
+                          float* out_probs, uint32_t out_cap,
+                          uint32_t* out_count);
+
 /* Batch over rows with nthreads host threads (rows split in contiguous
  * blocks).  Array arguments follow the device ABI layout: params as [B]
  * arrays (NULL = default), history as CSR (offsets[B+1], tokens), mask as

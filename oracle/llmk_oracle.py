@@ -34,6 +34,12 @@ def load():
         ctypes.c_int, P, u32, u32, ctypes.c_uint64, P, P, P, P, P, P, P, P, P, P, u32,
         P, P, P, P, u32, P, ctypes.c_int]
     lib.llmk_oracle_sample_batch.restype = ctypes.c_int
+    lib.llmk_oracle_sample_row.argtypes = [ctypes.c_int, P, u32, P, P, u32, P, f32, P, P, P, u32, P]
+    lib.llmk_oracle_sample_row.restype = ctypes.c_int
+    lib.llmk_oracle_process_logits.argtypes = [ctypes.c_int, P, u32, P, P, u32, P, P]
+    lib.llmk_oracle_process_logits.restype = ctypes.c_int
+    lib.llmk_oracle_semantics.argtypes = [P, P, u32, P, f32, P, P, P, u32, P]
+    lib.llmk_oracle_semantics.restype = ctypes.c_int
     lib.llmk_oracle_exp_m.argtypes = [f32]
     lib.llmk_oracle_exp_m.restype = f32
     lib.llmk_oracle_exp2_f.argtypes = [f32]
@@ -100,6 +106,67 @@ def sample_workload(mode, w, out_cap=0, nthreads=1, rows=None):
     return sample_batch(mode, lg, w.temperature[sel], w.top_k[sel], w.top_p[sel], w.min_p[sel],
                         w.repetition[sel], w.presence[sel], w.frequency[sel], ho, ht,
                         None if w.mask is None else w.mask[sel], w.uniforms[sel], out_cap, nthreads)
+
+
+class Params(ctypes.Structure):
+    """llmk_oracle_params (oracle/llmk_oracle.h)."""
+    _fields_ = [("temperature", ctypes.c_float), ("top_k", ctypes.c_int32),
+                ("top_p", ctypes.c_float), ("min_p", ctypes.c_float),
+                ("repetition_penalty", ctypes.c_float), ("presence_penalty", ctypes.c_float),
+                ("frequency_penalty", ctypes.c_float)]
+
+
+def params(temperature=1.0, top_k=0, top_p=1.0, min_p=0.0, repetition=1.0, presence=0.0,
+           frequency=0.0):
+    return Params(temperature, top_k, top_p, min_p, repetition, presence, frequency)
+
+
+def sample_row(mode, logits, prm, hist=(), mask=None, u=0.0, out_cap=None):
+    """One row.  Returns (rc, token, ids, probs, count); out_cap defaults to V."""
+    lib = load()
+    l = _f32p(logits)
+    V = l.size
+    cap = V if out_cap is None else out_cap
+    h = np.ascontiguousarray(hist, dtype=np.uint32)
+    m = None if mask is None else np.ascontiguousarray(mask, dtype=np.uint32)
+    tok, cnt = ctypes.c_uint32(), ctypes.c_uint32()
+    ids = np.zeros(max(cap, 1), np.uint32)
+    probs = np.zeros(max(cap, 1), np.float32)
+    rc = lib.llmk_oracle_sample_row(mode, _p(l) if V else None, V, ctypes.byref(prm),
+                                    _p(h) if h.size else None, h.size, _p(m), u,
+                                    ctypes.byref(tok), _p(ids), _p(probs), cap, ctypes.byref(cnt))
+    n = min(cnt.value, cap)
+    return rc, tok.value, ids[:n], probs[:n], cnt.value
+
+
+def semantics(p_sorted, idx, prm, u=0.0, out_cap=None):
+    """min-p / top-k / top-p / draw on a sorted list.  Returns (rc, token, ids, probs, count)."""
+    lib = load()
+    p = _f32p(p_sorted)
+    ix = np.ascontiguousarray(idx, dtype=np.uint32)
+    n = p.size
+    cap = n if out_cap is None else out_cap
+    tok, cnt = ctypes.c_uint32(), ctypes.c_uint32()
+    ids = np.zeros(max(cap, 1), np.uint32)
+    probs = np.zeros(max(cap, 1), np.float32)
+    rc = lib.llmk_oracle_semantics(_p(p), _p(ix), n, ctypes.byref(prm), u, ctypes.byref(tok),
+                                   _p(ids), _p(probs), cap, ctypes.byref(cnt))
+    k = min(cnt.value, cap)
+    return rc, tok.value, ids[:k], probs[:k], cnt.value
+
+
+def process_logits(mode, logits, prm, hist=(), mask=None):
+    """Penalised + masked logits of one row (before greedy / temperature)."""
+    lib = load()
+    l = _f32p(logits)
+    out = np.zeros_like(l)
+    h = np.ascontiguousarray(hist, dtype=np.uint32)
+    m = None if mask is None else np.ascontiguousarray(mask, dtype=np.uint32)
+    rc = lib.llmk_oracle_process_logits(mode, _p(l), l.size, ctypes.byref(prm),
+                                        _p(h) if h.size else None, h.size, _p(m), _p(out))
+    if rc != 0:
+        raise ValueError(f"oracle rc {rc}")
+    return out
 
 
 def _f32p(x):

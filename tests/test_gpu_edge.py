@@ -1,0 +1,217 @@
+"""GPU edge cases through the C ABI, each compared bit for bit with the CPU
+mirror oracle (tokens, kept counts, kept ids and probabilities): the
+reference's known-answer vectors, tiny and ragged vocabularies, padded rows,
+fully masked rows, top-k at and beyond its limits, extreme top-p and
+uniforms, bf16 ties, history ids outside the vocabulary, invalid parameters
+and the device status word.  Marked gpu."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import llmk
+from llmk import _lib, synth
+from oracle import llmk_oracle as O
+
+from gpu_util import assert_bit_exact, run_gpu, run_gpu_strided, workload
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CAP = 64
+
+
+@pytest.fixture(scope="module")
+def sampler():
+    s = llmk.HipSampler(max_batch=512, max_vocab=256000)
+    yield s
+    s.close()
+
+
+def check(sampler, w, cap=CAP, strided=False, label=""):
+    print(f"[case] {label or w.name} B={w.B} V={w.V} dtype={w.dtype} strided={strided}", flush=True)
+    gpu = (run_gpu_strided if strided else run_gpu)(sampler, w, cap)
+    orc = O.sample_workload(O.MIRROR, w, out_cap=cap, nthreads=16)
+    assert_bit_exact(w, gpu, orc, cap, label or w.name)
+    return gpu, orc
+
+
+def test_reference_kats_through_the_abi(sampler):
+    with open(os.path.join(HERE, "golden", "reference_kats.json")) as f:
+        kats = [k for k in json.load(f)["kats"] if k["op"] in ("sample_simple", "softmax")]
+    for k in kats:
+        lg = np.asarray(k["logits"], np.float32)
+        T = k.get("temperature", 1.0)
+        for u in (0.0, 0.37, 0.999):
+            gpu, orc = check(sampler, workload(lg, T=T, u=u), cap=8, strided=True, label=k["name"])
+            if "expect_token" in k:
+                assert gpu[0][0] == k["expect_token"]
+            if "sum_tol" in k:
+                assert abs(float(np.sum(gpu[2][0, :gpu[3][0]], dtype=np.float32)) - 1) < k["sum_tol"]
+
+
+@pytest.mark.parametrize("V", [1, 2, 3, 5, 63, 1023, 1024, 1025, 4097, 16385, 151937])
+def test_ragged_vocabularies(sampler, V):
+    rng = np.random.default_rng(V)
+    B = 6
+    lg = rng.normal(0, 3, (B, V)).astype(np.float32)
+    T = np.array([0.0, 0.7, 1.0, 1.3, 0.7, 0.9], np.float32)
+    K = np.array([0, 50, 0, 3, 1, 0], np.int32)
+    P = np.array([1.0, 0.95, 0.9, 1.0, 0.5, 1.0], np.float32)
+    hists = [rng.integers(0, V + 5, 40) for _ in range(B)]
+    w = workload(lg, T=T, K=K, P=P, R=1.1, PR=0.2, FR=0.1, hists=hists,
+                 u=rng.random(B).astype(np.float32))
+    check(sampler, w, strided=True, label=f"ragged V={V}")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_fully_masked_rows(sampler, dtype):
+    V = 5000
+    lg = np.random.default_rng(1).normal(0, 2, (5, V)).astype(np.float32)
+    mask = np.zeros((5, (V + 31) // 32), np.uint32)
+    mask[4] = 0xFFFFFFFF  # one ordinary row beside them
+    w = workload(lg, T=[0.0, 0.8, 0.8, 0.8, 0.8], K=[0, 0, 7, 0, 20], P=[1.0, 0.9, 1.0, 1.0, 0.9],
+                 u=[0.3, 0.0, 0.3, 0.3, 0.3], mask=mask, dtype=dtype)
+    gpu, _ = check(sampler, w, label=f"masked {dtype}")
+    assert gpu[0][:4].tolist() == [0, 0, 6, V - 1]
+
+
+def test_top_k_limits(sampler):
+    V = 20000
+    rng = np.random.default_rng(2)
+    lg = rng.normal(0, 3, (8, V)).astype(np.float32)
+    K = np.array([1, 2, 1023, 1024, 1025, V - 1, V, V + 7], np.int32)
+    w = workload(lg, T=0.8, K=K, P=1.0, u=rng.random(8).astype(np.float32))
+    check(sampler, w, cap=1100, label="top-k limits")
+
+
+def test_extreme_top_p_and_uniforms(sampler):
+    V = 30000
+    rng = np.random.default_rng(3)
+    lg = rng.normal(0, 3, (8, V)).astype(np.float32)
+    one_minus = np.float32(1.0 - 2.0 ** -24)
+    w = workload(lg, T=0.9, K=[40, 40, 0, 0, 40, 40, 0, 0],
+                 P=[1e-30, 1.0, 1e-30, 0.3, 0.95, 0.95, 0.95, 0.999],
+                 u=[0.5, 0.5, 0.0, one_minus, 0.0, one_minus, one_minus, 0.999])
+    check(sampler, w, label="extreme top-p / u")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_ties(sampler, dtype):
+    """Quantised logits make many equal probabilities: (p desc, idx asc)."""
+    V = 40000
+    rng = np.random.default_rng(4)
+    lg = np.round(rng.normal(0, 2, (6, V)) * 2) / 2
+    lg[:, :: 97] = 6.0  # a plateau of equal maxima
+    lg[5] = 1.25  # all equal
+    w = workload(lg.astype(np.float32), T=[0.7, 0.7, 1.0, 1.0, 0.0, 0.9], K=[50, 0, 200, 1, 0, 30],
+                 P=[0.95, 0.9, 1.0, 1.0, 1.0, 1.0], MP=[0.0, 0.05, 0.0, 0.0, 0.0, 0.0],
+                 u=rng.random(6).astype(np.float32), dtype=dtype)
+    check(sampler, w, cap=256, label=f"ties {dtype}")
+
+
+def test_min_p_rows(sampler):
+    V = 50000
+    rng = np.random.default_rng(5)
+    lg = rng.normal(0, 3, (6, V)).astype(np.float32)
+    lg[:, 7] = 12.0
+    w = workload(lg, T=0.9, K=[0, 200, 0, 50, 0, 0], P=[1.0, 0.98, 0.9, 1.0, 1.0, 0.95],
+                 MP=[0.02, 0.02, 0.1, 0.5, 1.0, 1e-4], u=rng.random(6).astype(np.float32))
+    check(sampler, w, cap=256, label="min-p")
+
+
+def test_empty_and_out_of_vocab_histories(sampler):
+    V = 30000
+    rng = np.random.default_rng(6)
+    lg = rng.normal(0, 3, (4, V)).astype(np.float32)
+    hists = [[], [V, V + 1, 2 ** 31, 0xFFFFFFFE], rng.integers(0, V, 3000), [5] * 500]
+    w = workload(lg, T=0.8, K=30, P=0.9, R=1.3, PR=0.4, FR=0.2, hists=hists,
+                 u=rng.random(4).astype(np.float32))
+    check(sampler, w, label="histories")
+    # no history arrays at all
+    db = w.to_device()
+    db.hist_offsets = db.hist_tokens = None
+    r = sampler.sample_batch(db, out_cap=0)
+    w2 = workload(lg, T=0.8, K=30, P=0.9, R=1.3, PR=0.4, FR=0.2, u=w.uniforms)
+    orc = O.sample_workload(O.MIRROR, w2, out_cap=0)
+    assert np.array_equal(r.tokens.cpu().numpy().view(np.uint32), orc[1])
+
+
+def test_invalid_parameters_and_status(sampler):
+    V = 9000
+    rng = np.random.default_rng(7)
+    lg = rng.normal(0, 3, (6, V)).astype(np.float32)
+    T = np.array([np.nan, 0.8, 0.8, np.inf, 0.8, 0.8], np.float32)
+    K = np.array([0, -1, 10, 0, 10, 10], np.int32)
+    P = np.array([1.0, 1.0, np.nan, 1.0, 1.0, 0.9], np.float32)
+    R = np.array([1.0, 1.0, 1.0, 1.0, np.inf, 1.1], np.float32)
+    w = workload(lg, T=T, K=K, P=P, R=R, u=0.4)
+    sampler.status()  # clear what earlier calls raised
+    print("[case] invalid params", flush=True)
+    tok, ids, probs, cnt = run_gpu(sampler, w, 8)
+    assert np.all(tok[:5] == _lib.LLMK_INVALID_TOKEN) and np.all(cnt[:5] == 0)
+    ok = workload(lg[5:], T=0.8, K=10, P=0.9, R=1.1, u=0.4)
+    orc = O.sample_workload(O.MIRROR, ok, out_cap=8)
+    assert tok[5] == orc[1][0]
+    assert sampler.status() == _lib.LLMK_STATUS_INVALID_PARAMS
+    assert sampler.status() == 0  # reading clears it
+
+
+def test_history_overflow_is_reported(sampler):
+    """More distinct history tokens in one vocabulary segment than the LDS
+    table holds raises LLMK_STATUS_HISTORY_OVERFLOW."""
+    V = 151936
+    lg = np.random.default_rng(8).normal(0, 3, (1, V)).astype(np.float32)
+    w = workload(lg, T=0.8, K=40, P=0.95, R=1.1, hists=[np.arange(20000)], u=0.3)
+    print("[case] history overflow", flush=True)
+    run_gpu(sampler, w, 0)
+    assert sampler.status() & _lib.LLMK_STATUS_HISTORY_OVERFLOW
+
+
+def test_host_errors(sampler):
+    import torch
+    w = workload(np.zeros((2, 100), np.float32))
+    db = w.to_device()
+    with pytest.raises(llmk.SamplerError) as e:
+        db.vocab = 0
+        sampler.sample_batch(db)
+    assert e.value.code == _lib.LLMK_ERR_EMPTY_LOGITS
+    db.vocab = 100
+    big = workload(np.zeros((2, 300000), np.float32)).to_device()
+    with pytest.raises(llmk.SamplerError) as e:
+        sampler.sample_batch(big)
+    assert e.value.code == _lib.LLMK_ERR_CAPACITY
+    lg = torch.zeros(2, 101, device="cuda:0")
+    db.logits = lg[:, 1:]  # rows not 16-byte aligned
+    with pytest.raises(llmk.SamplerError) as e:
+        sampler.sample_batch(db)
+    assert e.value.code == _lib.LLMK_ERR_ALIGNMENT
+    # the reference's per-row call and sample() wrapper
+    lg = torch.tensor([0.1, 0.5, 3.0, 0.2], device="cuda:0")
+    assert llmk.sample(sampler, lg, 0.0, 0.5) == 2
+    with pytest.raises(llmk.SamplerError):
+        sampler.sample(torch.zeros(0, device="cuda:0"), llmk.SampleParams(), [], 0.5)
+
+
+@pytest.mark.parametrize("B", [1, 7, 9, 300])
+def test_batch_shapes(sampler, B):
+    """Batch sizes that change the segment count and the XCD mapping."""
+    w = synth.make("C3", B=B, V=50000)
+    check(sampler, w, label=f"C3 B={B} V=50000")
+
+
+@pytest.mark.parametrize("name", ["C1", "C2", "C4", "C5"])
+def test_full_size_configs(sampler, name):
+    w = synth.make(name)
+    check(sampler, w, label=f"full {name}")
+
+
+def test_repeated_calls_are_stable(sampler):
+    """The workspace (arrival counters, slots) is left clean by every call."""
+    w = synth.make("C2", B=16)
+    first = run_gpu(sampler, w, CAP)
+    for i in range(3):
+        again = run_gpu(sampler, w, CAP)
+        for a, b in zip(first, again):
+            assert np.array_equal(a, b)
