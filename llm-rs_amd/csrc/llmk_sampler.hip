@@ -72,6 +72,9 @@ constexpr uint32_t SORT_CAP = 4096;  // candidates sorted in finalize
 constexpr uint32_t KMAX = 1024;      // largest top-k served by the fast path
 constexpr uint32_t KCAND_NOK = 1024; // candidate target when top-k is off
 constexpr uint32_t MAX_TILES = 1024; // max_vocab <= 2^20
+constexpr uint32_t CHUNK_TILES = 16;  // tiles per history chunk (segments are whole chunks)
+constexpr uint32_t MAX_CHUNKS = MAX_TILES / CHUNK_TILES;
+constexpr uint32_t MAX_SLOTS = MAX_TILES + MAX_CHUNKS;  // partials per row: tiles, then chunks
 constexpr uint32_t MAX_SEG = 64;     // segments per row
 constexpr uint32_t MAX_WGS = 4096;   // candidate-buffer pool entries
 constexpr uint32_t SLOW_SLOTS = 64;  // global scratch slots of the slow path
@@ -95,13 +98,13 @@ struct Args {
   uint32_t *out_tok, *out_ids, *out_cnt;
   float* out_probs;
   uint32_t out_cap;
-  uint32_t G, tps, ntiles;
+  uint32_t G, tps, ntiles, nchunks;
   uint32_t xcd_map;  // 1: the segments of a row share an XCD
 };
 
 struct Ws {
   uint32_t* row_arrive;  // [max_batch]
-  f2v* tile_part;        // [max_batch][MAX_TILES]: tile max, tile sum
+  f2v* tile_part;        // [max_batch][MAX_SLOTS]: max, sum (or first argmax) per slot
   u4v* seg_meta;         // [pool]: count, beta, flags, -
   u2v* cand;             // [pool][CAND_CAP]: value bits, index
   uint32_t* slow_lock;   // [SLOW_SLOTS]
@@ -754,12 +757,12 @@ __device__ __forceinline__ void write_outputs(const Args& a, uint32_t b, uint32_
 enum : uint32_t { M_BETA = 0, M_CCOUNT = 1, M_FLAGS = 2, M_LAST = 3, M_NEXT = 4, M_NMISC = 16 };
 
 __host__ __device__ inline size_t stream_lds_words(uint32_t tps) {
-  return 64 + M_NMISC + NBINS + 64 + hist_lds_words(tps * 32);
+  return 64 + M_NMISC + MAX_CHUNKS + 16 + NBINS + 64 + hist_lds_words(tps * 32);
 }
 __host__ __device__ inline size_t finalize_lds_words() {
-  // tiles (2 x MAX_TILES) + keys + sorted keys (2 x SORT_CAP u64) + p + idx
-  // + segment tables + scratch
-  return 2 * MAX_TILES + 4 * SORT_CAP + 2 * SORT_CAP + 128 + MAX_SEG + 1;
+  // slots (2 x MAX_SLOTS) + keys + sorted keys (2 x SORT_CAP u64) + p + idx
+  // + scratch + segment table + reductions + block sums
+  return 2 * MAX_SLOTS + 4 * SORT_CAP + 2 * SORT_CAP + 128 + MAX_SEG + 16 + 64 + 2 * MAX_SLOTS / 64;
 }
 __host__ __device__ inline size_t slow_lds_words(uint32_t V) {
   return 128 + 256 + NW * 256 + 256 + STAGE + hist_lds_words((V + 31) / 32);
@@ -993,224 +996,525 @@ __device__ __forceinline__ uint32_t kth_largest_key(LDS const float* cval, uint3
 }
 
 // ---------------------------------------------------------------------------
-// Finalize one row.  The candidate path runs in wave 0 alone (no workgroup
-// barriers); if it cannot prove its result exact, the whole workgroup runs
-// the slow path.
+// Finalize one row (the whole workgroup).  Partials and candidates are read
+// block-wide; the sequential semantics run in wave 0.  If the candidate path
+// cannot prove its result exact, the whole workgroup runs the slow path.
 // ---------------------------------------------------------------------------
-enum : uint32_t { F_DONE = 0, F_S = 1, F_M = 2, F_N = 3, F_CNT = 4, F_SCR = 8 };
+enum : uint32_t { F_DONE = 0, F_S = 1, F_M = 2, F_TOTAL = 3, F_LAM = 4, F_OVF = 5, F_SCR = 8 };
 
 template <int DT>
 __device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_t b,
-                                             const RowP& P, LDS uint32_t* smem) {
+                                             const RowP& P, bool have_vt, LDS uint32_t* smem) {
   const uint32_t tid = threadIdx.x;
   const int lane = (int)(tid & 63), wv = (int)(tid >> 6);
-  LDS float* tl = (LDS float*)smem;                          // MAX_TILES
-  LDS float* ts = tl + MAX_TILES;                            // MAX_TILES
-  LDS uint64_t* keys = (LDS uint64_t*)(smem + 2 * MAX_TILES);  // SORT_CAP
-  LDS uint64_t* skeys = keys + SORT_CAP;                     // SORT_CAP (sorted)
-  LDS float* pp = (LDS float*)(skeys + SORT_CAP);            // SORT_CAP
-  LDS uint32_t* pidx = (LDS uint32_t*)(pp + SORT_CAP);       // SORT_CAP
-  LDS uint32_t* fm = pidx + SORT_CAP;                        // 128
-  LDS uint32_t* soff = fm + 128;                             // MAX_SEG+1
-  using SY = WaveSync;
+  LDS float* tl = (LDS float*)smem;                              // MAX_SLOTS
+  LDS float* ts = tl + MAX_SLOTS;                                // MAX_SLOTS
+  LDS uint64_t* keys = (LDS uint64_t*)(smem + 2 * MAX_SLOTS);    // SORT_CAP
+  LDS uint64_t* skeys = keys + SORT_CAP;                         // SORT_CAP (sorted)
+  LDS float* pp = (LDS float*)(skeys + SORT_CAP);                // SORT_CAP
+  LDS uint32_t* pidx = (LDS uint32_t*)(pp + SORT_CAP);           // SORT_CAP
+  LDS uint32_t* fm = pidx + SORT_CAP;                            // 128
+  LDS uint32_t* soff = fm + 128;                                 // MAX_SEG + 1
+  LDS uint32_t* red = soff + MAX_SEG + 16;                       // 64
+  LDS float* blk = (LDS float*)(red + 64);                       // 2 * MAX_SLOTS / 64
+  const uint32_t nslots = a.ntiles + (have_vt ? a.nchunks : 0u);
+  const GLB f2v* part = G(w.tile_part) + (uint64_t)b * MAX_SLOTS;
+
+  // ---- partials into LDS; row maximum L
+  float L = NEG_INF;
+  for (uint32_t c = tid; c < nslots; c += NT) {
+    const f2v q = part[c];
+    tl[c] = q.x;
+    ts[c] = q.y;
+    L = fmaxf(L, q.x);
+  }
+  L = block_max(L, (LDS float*)red);
+  if (P.mode == MODE_GREEDY) {
+    // sampler.rs:40-50: the first index holding the maximum.
+    uint32_t bi = EMPTY;
+    for (uint32_t c = tid; c < nslots; c += NT)
+      if (tl[c] == L) bi = umin(bi, __float_as_uint(ts[c]));
+    bi = block_min_u32(bi, red);
+    if (bi == EMPTY) bi = 0;
+    if (tid == 0) {
+      G(a.out_tok)[b] = bi;
+      if (a.out_cnt) G(a.out_cnt)[b] = 1;
+      if (a.out_cap) {
+        if (a.out_ids) G(a.out_ids)[(uint64_t)b * a.out_cap] = bi;
+        if (a.out_probs) G(a.out_probs)[(uint64_t)b * a.out_cap] = 1.0f;
+      }
+    }
+    return;
+  }
+
+  // ---- normaliser S: balanced tree over max(64, next_pow2(nslots)) slots,
+  // as trees of 64 slots (one per wave) and a tree over those
+  const float c2 = LOG2E_F / P.T;
+  uint32_t ntp = 64;
+  while (ntp < nslots) ntp <<= 1;
+  const uint32_t nblk = ntp / 64;
+  for (uint32_t k = (uint32_t)wv; k < nblk; k += NW) {
+    const uint32_t c = 64 * k + (uint32_t)lane;
+    float x = 0.0f;
+    if (c < nslots && L != NEG_INF) x = ts[c] * exp2_f((tl[c] - L) * c2);
+    x = wave_tree_sum(x);
+    if (lane == 0) blk[k] = x;
+  }
+  // ---- segment table (wave 0): counts, thresholds, flags
   if (wv == 0) {
-    uint32_t done = 0;
-    const uint32_t nt = a.ntiles;
-    const GLB f2v* part = G(w.tile_part) + (uint64_t)b * MAX_TILES;
-    float L = NEG_INF;
-    for (uint32_t c = (uint32_t)lane; c < nt; c += WAVE) {
-      const f2v q = part[c];
-      tl[c] = q.x;
-      ts[c] = q.y;
-      L = fmaxf(L, q.x);
+    uint32_t cnt = 0, beta = 0, flg = 0;
+    if ((uint32_t)lane < a.G) {
+      const u4v sm = G(w.seg_meta)[row_seg_to_wg(a, b, (uint32_t)lane)];
+      cnt = sm.x < CAND_CAP ? sm.x : CAND_CAP;
+      beta = sm.y;
+      flg = sm.z;
     }
-    L = wave_max(L);
-    SY::sync();
-    float S = 0.0f, m = L;
-    if (P.mode == MODE_GREEDY) {
-      // sampler.rs:40-50: the first index holding the maximum.
-      uint32_t bi = EMPTY;
-      for (uint32_t c = (uint32_t)lane; c < nt; c += WAVE)
-        if (tl[c] == L) bi = umin(bi, __float_as_uint(ts[c]));
-      bi = wave_min_u32(bi);
-      if (bi == EMPTY) bi = 0;
-      if (lane == 0) {
-        G(a.out_tok)[b] = bi;
-        if (a.out_cnt) G(a.out_cnt)[b] = 1;
-        if (a.out_cap) {
-          if (a.out_ids) G(a.out_ids)[(uint64_t)b * a.out_cap] = bi;
-          if (a.out_probs) G(a.out_probs)[(uint64_t)b * a.out_cap] = 1.0f;
-        }
-      }
-      done = 1;
-    } else {
-      // ---- normaliser S: tree over next_pow2(#tiles) in blocks of 64 tiles
-      const float c2 = LOG2E_F / P.T;
-      uint32_t ntp = 1;
-      while (ntp < nt) ntp <<= 1;
-      const uint32_t nblk = (ntp + 63) / 64;
-      float blk[MAX_TILES / 64];
-#pragma unroll
-      for (uint32_t k = 0; k < MAX_TILES / 64; ++k) {
-        blk[k] = 0.0f;
-        if (k < nblk) {
-          const uint32_t c = 64 * k + (uint32_t)lane;
-          float x = 0.0f;
-          if (c < nt && L != NEG_INF) x = ts[c] * exp2_f((tl[c] - L) * c2);
-          blk[k] = wave_tree_sum(x);
-        }
-      }
-      for (uint32_t len = nblk; len > 1; len >>= 1)
-#pragma unroll
-        for (uint32_t i = 0; i < MAX_TILES / 128; ++i)
-          if (i < len / 2) blk[i] = blk[2 * i] + blk[2 * i + 1];
-      S = (L != NEG_INF) ? blk[0] : 0.0f;
-      m = (P.T != 1.0f) ? L / P.T : L;
-      // ---- candidate bound: every element outside the candidate buffers
-      // has a key below lam, hence probability at most plim
-      uint32_t cnt = 0, beta = 0, flg = 0;
-      if ((uint32_t)lane < a.G) {
-        const u4v sm = G(w.seg_meta)[row_seg_to_wg(a, b, (uint32_t)lane)];
-        cnt = sm.x < CAND_CAP ? sm.x : CAND_CAP;
-        beta = sm.y;
-        flg = sm.z;
-      }
-      uint32_t lam = wave_max_u32(beta << BIN_SHIFT);
-      const bool ovf = __ballot((flg & FLAG_OVERFLOW) != 0) != 0;
-      // segment g holds candidates [soff[g], soff[g+1]); written with the
-      // whole wave active, looked up from LDS in the divergent gather below
-      const uint32_t off_incl = wave_incl_scan(cnt);
-      const uint32_t total = bcast63u(off_incl);
-      if ((uint32_t)lane <= a.G) soff[lane] = off_incl - cnt;  // lane G: total
-      SY::sync();
-      bool ok = !(L == NEG_INF || P.Kc == 0 || ovf);
-      // ---- gather the candidates at or above lam (values and indices)
-      LDS float* cval = pp;
-      LDS uint32_t* cidx = pidx;
-      uint32_t n0 = 0;
-      if (ok) {
-        for (uint32_t i0 = 0; i0 < total; i0 += WAVE) {
-          const uint32_t i = i0 + (uint32_t)lane;
-          float v = NEG_INF;
-          uint32_t ix = 0;
-          if (i < total) {
-            uint32_t g = 0;
-            while (g + 1 < a.G && soff[g + 1] <= i) ++g;
-            const u2v e = G(w.cand)[(uint64_t)row_seg_to_wg(a, b, g) * CAND_CAP + (i - soff[g])];
-            v = __uint_as_float(e.x);
-            ix = e.y;
-          }
-          const bool keep = v > NEG_INF && fkey(v) >= lam;
-          const uint64_t mk = __ballot(keep);
-          if (keep) {
-            const uint32_t pos = n0 + lanes_below(mk);
-            if (pos < SORT_CAP) {
-              cval[pos] = v;
-              cidx[pos] = ix;
-            }
-          }
-          n0 += (uint32_t)__popcll(mk);
-        }
-        if (n0 > SORT_CAP) ok = false;
-      }
-      SY::sync();
-      uint32_t n = 0;
-      if (ok) {
-        // ---- top-k rows: the exact K-th largest candidate logit tightens
-        // the bound (every element below it has p <= plim of that bound)
-        const bool topk = P.K > 0 && (uint32_t)P.K < a.V;
-        float plim = lam > 0x007fffffu ? prob_of(funkey(lam - 1), P.T, m, S) : 0.0f;
-        uint32_t lam_e = lam;
-        float plim_e = plim;
-        if (topk && n0 > 2u * (uint32_t)P.K && n0 >= (uint32_t)P.K) {
-          const uint32_t tau = kth_largest_key<SY>(cval, n0, (uint32_t)P.K,
-                                                   (LDS uint32_t*)keys, fm + F_SCR);
-          lam_e = tau;
-          plim_e = tau > 0x007fffffu ? prob_of(funkey(tau - 1), P.T, m, S) : 0.0f;
-        }
-        for (int attempt = 0; attempt < 2; ++attempt) {
-          n = 0;
-          for (uint32_t i0 = 0; i0 < n0; i0 += WAVE) {
-            const uint32_t i = i0 + (uint32_t)lane;
-            bool keep = false;
-            uint64_t key = 0;
-            if (i < n0) {
-              const float v = cval[i];
-              if (fkey(v) >= lam_e) {
-                const float pv = prob_of(v, P.T, m, S);
-                if (pv > plim_e) {
-                  keep = true;
-                  key = pkey(pv, cidx[i]);
-                }
-              }
-            }
-            const uint64_t mk = __ballot(keep);
-            if (keep) keys[n + lanes_below(mk)] = key;
-            n += (uint32_t)__popcll(mk);
-          }
-          // a tightened bound that keeps fewer than K (ties in p across it)
-          // falls back to the gather bound
-          if (!(topk && n < (uint32_t)P.K && lam_e != lam)) break;
-          lam_e = lam;
-          plim_e = plim;
-        }
-        SY::sync();
-        // ---- sort ascending; keys are distinct (indices differ)
-        if (n <= 512) {
-          for (uint32_t i = (uint32_t)lane; i < n; i += WAVE) {
-            const uint64_t k = keys[i];
-            uint32_t r = 0;
-            for (uint32_t j = 0; j < n; ++j) r += (keys[j] < k) ? 1u : 0u;
-            skeys[r] = k;
-          }
-        } else {
-          uint32_t npad = 1;
-          while (npad < n) npad <<= 1;
-          for (uint32_t i = (uint32_t)lane; i < npad; i += WAVE) skeys[i] = i < n ? keys[i] : ~0ull;
-          SY::sync();
-          for (uint32_t k = 2; k <= npad; k <<= 1)
-            for (uint32_t j = k >> 1; j > 0; j >>= 1) {
-              for (uint32_t i = (uint32_t)lane; i < npad / 2; i += WAVE) {
-                const uint32_t lo = ((i & ~(j - 1)) << 1) | (i & (j - 1));
-                const uint32_t hi = lo | j;
-                const uint64_t x = skeys[lo], y = skeys[hi];
-                const bool up = (lo & k) == 0;
-                if ((x > y) == up) {
-                  skeys[lo] = y;
-                  skeys[hi] = x;
-                }
-              }
-              SY::sync();
-            }
-        }
-        SY::sync();
-        for (uint32_t i = (uint32_t)lane; i < n; i += WAVE) {
-          const uint64_t k = skeys[i];
-          pp[i] = __uint_as_float(~(uint32_t)(k >> 32));
-          pidx[i] = (uint32_t)k;
-        }
-        SY::sync();
-        LdsList<SY> Ls{pp, pidx, (LDS float*)keys, Chain{0.f, 0.f, 0.f, 0}};
-        uint32_t tok = 0, len = 0;
-        ok = run_semantics<SY>(P, G(a.u)[b], n, a.V, Ls, fm + F_SCR, tok, len);
-        if (ok && a.out_cap && len > n && a.out_cap > n) ok = false;
-        if (ok) {
-          write_outputs<SY>(a, b, tok, len, Ls);
-          done = 1;
-        }
-      }
-    }
+    const uint32_t lam = wave_max_u32(beta << BIN_SHIFT);
+    const bool ovf = __ballot((flg & FLAG_OVERFLOW) != 0) != 0;
+    const uint32_t off_incl = wave_incl_scan(cnt);
+    if ((uint32_t)lane <= a.G) soff[lane] = off_incl - cnt;  // lane G: the total
     if (lane == 0) {
-      fm[F_DONE] = done;
-      fm[F_S] = __float_as_uint(S);
-      fm[F_M] = __float_as_uint(m);
+      fm[F_TOTAL] = bcast63u(off_incl);
+      fm[F_LAM] = lam;
+      fm[F_OVF] = ovf ? 1u : 0u;
     }
   }
   __syncthreads();
-  const uint32_t done = fm[F_DONE];
-  const float S = __uint_as_float(fm[F_S]), m = __uint_as_float(fm[F_M]);
+  float S = 0.0f;
+  {
+    float x = ((uint32_t)lane < nblk) ? blk[lane] : 0.0f;
+    x = wave_tree_sum(x);
+    S = (L != NEG_INF) ? x : 0.0f;
+  }
+  const float m = (P.T != 1.0f) ? L / P.T : L;
+  const uint32_t total = fm[F_TOTAL], lam = fm[F_LAM];
+  bool ok = !(L == NEG_INF || P.Kc == 0 || fm[F_OVF] != 0);
+  uint32_t done = 0;
+  if (ok) {
+    // ---- gather the candidates at or above lam: every element not in the
+    // candidate buffers has a key below lam
+    LDS float* cval = pp;
+    LDS uint32_t* cidx = pidx;
+    uint32_t n0 = 0;
+    for (uint32_t i0 = 0; i0 < total; i0 += NT) {
+      const uint32_t i = i0 + tid;
+      float v = NEG_INF;
+      uint32_t ix = 0;
+      if (i < total) {
+        uint32_t lo = 0, hi = a.G;  // soff[lo] <= i < soff[hi]
+        while (hi - lo > 1) {
+          const uint32_t mid = (lo + hi) >> 1;
+          if (soff[mid] <= i) lo = mid;
+          else hi = mid;
+        }
+        const u2v e = G(w.cand)[(uint64_t)row_seg_to_wg(a, b, lo) * CAND_CAP + (i - soff[lo])];
+        v = __uint_as_float(e.x);
+        ix = e.y;
+      }
+      const bool keep = v > NEG_INF && fkey(v) >= lam;
+      uint32_t tot;
+      const uint32_t pos = n0 + block_excl_scan(keep ? 1u : 0u, red, tot);
+      if (keep && pos < SORT_CAP) {
+        cval[pos] = v;
+        cidx[pos] = ix;
+      }
+      n0 += tot;
+    }
+    if (n0 > SORT_CAP) ok = false;
+    __syncthreads();
+    if (ok) {
+      // ---- top-k rows: the exact K-th largest candidate logit tightens the
+      // bound (every element below it has p <= plim of that bound)
+      const bool topk = P.K > 0 && (uint32_t)P.K < a.V;
+      const float plim = lam > 0x007fffffu ? prob_of(funkey(lam - 1), P.T, m, S) : 0.0f;
+      uint32_t lam_e = lam;
+      float plim_e = plim;
+      if (topk && n0 > 2u * (uint32_t)P.K) {
+        const uint32_t tau = kth_largest_key<BlockSync>(cval, n0, (uint32_t)P.K,
+                                                        (LDS uint32_t*)keys, fm + F_SCR);
+        lam_e = tau;
+        plim_e = tau > 0x007fffffu ? prob_of(funkey(tau - 1), P.T, m, S) : 0.0f;
+      }
+      uint32_t n = 0;
+      for (int attempt = 0; attempt < 2; ++attempt) {
+        n = 0;
+        for (uint32_t i0 = 0; i0 < n0; i0 += NT) {
+          const uint32_t i = i0 + tid;
+          bool keep = false;
+          uint64_t key = 0;
+          if (i < n0) {
+            const float v = cval[i];
+            if (fkey(v) >= lam_e) {
+              const float pv = prob_of(v, P.T, m, S);
+              if (pv > plim_e) {
+                keep = true;
+                key = pkey(pv, cidx[i]);
+              }
+            }
+          }
+          uint32_t tot;
+          const uint32_t pos = n + block_excl_scan(keep ? 1u : 0u, red, tot);
+          if (keep) keys[pos] = key;
+          n += tot;
+        }
+        // a tightened bound that keeps fewer than K (ties in p across it)
+        // falls back to the gather bound
+        if (!(topk && n < (uint32_t)P.K && lam_e != lam)) break;
+        lam_e = lam;
+        plim_e = plim;
+      }
+      __syncthreads();
+      // ---- sort ascending by key; keys are distinct (indices differ)
+      if (n <= (uint32_t)NT) {
+        if (tid < n) {
+          const uint64_t k = keys[tid];
+          uint32_t r = 0;
+          for (uint32_t j = 0; j < n; ++j) r += (keys[j] < k) ? 1u : 0u;
+          skeys[r] = k;
+        }
+      } else {
+        uint32_t npad = 1;
+        while (npad < n) npad <<= 1;
+        for (uint32_t i = tid; i < npad; i += NT) skeys[i] = i < n ? keys[i] : ~0ull;
+        __syncthreads();
+        for (uint32_t k = 2; k <= npad; k <<= 1)
+          for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+            for (uint32_t i = tid; i < npad / 2; i += NT) {
+              const uint32_t lo = ((i & ~(j - 1)) << 1) | (i & (j - 1));
+              const uint32_t hi = lo | j;
+              const uint64_t x = skeys[lo], y = skeys[hi];
+              const bool up = (lo & k) == 0;
+              if ((x > y) == up) {
+                skeys[lo] = y;
+                skeys[hi] = x;
+              }
+            }
+            __syncthreads();
+          }
+      }
+      __syncthreads();
+      for (uint32_t i = tid; i < n; i += NT) {
+        const uint64_t k = skeys[i];
+        pp[i] = __uint_as_float(~(uint32_t)(k >> 32));
+        pidx[i] = (uint32_t)k;
+      }
+      __syncthreads();
+      // ---- min-p / top-k / top-p / draw in wave 0
+      if (wv == 0) {
+        using SY = WaveSync;
+        LdsList<SY> Ls{pp, pidx, (LDS float*)keys, Chain{0.f, 0.f, 0.f, 0}};
+        uint32_t tok = 0, len = 0;
+        bool good = run_semantics<SY>(P, G(a.u)[b], n, a.V, Ls, fm + F_SCR, tok, len);
+        if (good && a.out_cap && len > n && a.out_cap > n) good = false;
+        if (good) write_outputs<SY>(a, b, tok, len, Ls);
+        if (lane == 0) fm[F_DONE] = good ? 1u : 0u;
+      }
+      __syncthreads();
+      done = fm[F_DONE];
+    }
+  }
   __syncthreads();
   if (!done) slow_row<DT>(a, w, b, P, S, m, smem);
+}
+
+// ---------------------------------------------------------------------------
+// Per-tile reduction, shared by vocabulary tiles and virtual (history) tiles
+// ---------------------------------------------------------------------------
+struct TileEnv {
+  RowP P;
+  float c2;
+  uint32_t V;
+  bool collect;
+  uint32_t recompute_at;
+  LDS uint32_t* misc;
+  LDS uint32_t* hf;
+  LDS uint32_t* hcoarse;
+  GLB u2v* cbuf;
+  GLB f2v* part;
+};
+
+// v[j], j = 4r + q: the lane's values at tile positions 256r + 4*lane + q,
+// excluded positions already -inf.  idx(j): the vocabulary index of value j
+// (EMPTY or >= V for a position that holds no token).  Writes the slot's
+// partial (tile max, tree sum of 2^((v - max) c2)) -- or (max, first index of
+// the max) for greedy rows -- and appends candidates above the row's rising
+// threshold.  `since` is the wave's count of appends since its last threshold
+// update (EMPTY before its first counted tile).
+//
+// nr (wave-uniform, 1..4): runs r >= nr hold only -inf positions; each of
+// their terms is exactly exp2_f(-inf) = 2^-125, so such a run sums to 2^-123
+// and is not evaluated.
+template <class IDX>
+__device__ __forceinline__ void tile_reduce(const TileEnv& E, const float (&v)[16],
+                                            uint32_t slot, const IDX& idx,
+                                            uint32_t& since, int lane, uint32_t nr = 4) {
+  float lm = NEG_INF;
+#pragma unroll
+  for (int j = 0; j < 16; ++j)
+    if ((uint32_t)(j >> 2) < nr) lm = fmaxf(lm, v[j]);
+  lm = wave_max(lm);
+  if (E.P.mode == MODE_GREEDY) {
+    uint32_t bi = EMPTY;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const bool hit = (v[j] == lm) || (lm == NEG_INF && !(v[j] > NEG_INF));
+      if (hit) {
+        const uint32_t e = idx(j);
+        if (e < E.V) bi = umin(bi, e);
+      }
+    }
+    bi = wave_min_u32(bi);
+    if (lane == 0) E.part[slot] = f2v{lm, __uint_as_float(bi)};
+    return;
+  }
+  float s = 0.0f;
+  if (lm != NEG_INF) {
+    // per lane: ((run0 + run1) + (run2 + run3)), each run ((e0+e1)+(e2+e3));
+    // then a balanced tree over the 64 lanes
+    const float nb = -(lm * E.c2);
+    float sr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if ((uint32_t)r >= nr) {
+        sr[r] = 0x1p-123f;
+        continue;
+      }
+      const float e0 = exp2_f(__builtin_fmaf(v[4 * r + 0], E.c2, nb));
+      const float e1 = exp2_f(__builtin_fmaf(v[4 * r + 1], E.c2, nb));
+      const float e2 = exp2_f(__builtin_fmaf(v[4 * r + 2], E.c2, nb));
+      const float e3 = exp2_f(__builtin_fmaf(v[4 * r + 3], E.c2, nb));
+      sr[r] = (e0 + e1) + (e2 + e3);
+    }
+    s = wave_tree_sum((sr[0] + sr[1]) + (sr[2] + sr[3]));
+  }
+  if (lane == 0) E.part[slot] = f2v{lm, s};
+  if (!E.collect) return;
+  // ---- candidates above the rising histogram threshold
+  uint32_t beta = __atomic_load_n(&E.misc[M_BETA], __ATOMIC_RELAXED);
+  float th = theta_of(beta);
+  if (!(lm >= th)) return;  // no element of this tile can pass
+  bool counted = false;
+  if (since == EMPTY) {
+    // a wave's first such tile: count each lane's maximum (a subset of the
+    // row, so the counts stay lower bounds), raise the threshold, then
+    // append without counting again
+    float lmax = NEG_INF;
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if ((uint32_t)(j >> 2) < nr) lmax = fmaxf(lmax, v[j]);
+    if (lmax >= th) {
+      const uint32_t bin = fkey(lmax) >> BIN_SHIFT;
+      __atomic_fetch_add(&E.hf[bin], 1u, __ATOMIC_RELAXED);
+      __atomic_fetch_add(&E.hcoarse[bin >> (CBIN_SHIFT - BIN_SHIFT)], 1u, __ATOMIC_RELAXED);
+    }
+    const uint32_t nbeta = compute_beta(E.hcoarse, E.hf, E.P.Kc, lane);
+    if (nbeta > beta) {
+      if (lane == 0) __atomic_fetch_max(&E.misc[M_BETA], nbeta, __ATOMIC_RELAXED);
+      beta = nbeta;
+      th = theta_of(beta);
+    }
+    since = 0;
+    counted = true;
+  }
+  uint32_t npass = 0;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) npass += (uint32_t)__popcll(__ballot(v[j] >= th));
+  if (npass == 0) return;
+  uint32_t base = 0;
+  if (lane == 0) base = __atomic_fetch_add(&E.misc[M_CCOUNT], npass, __ATOMIC_RELAXED);
+  base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+  if (base + npass > CAND_CAP) {
+    if (lane == 0) __atomic_fetch_or(&E.misc[M_FLAGS], FLAG_OVERFLOW, __ATOMIC_RELAXED);
+    return;
+  }
+  // append, and count what was appended in the histogram
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const uint64_t mk = __ballot(v[j] >= th);
+    if (mk) {
+      if ((mk >> lane) & 1ull) {
+        if (!counted) {
+          const uint32_t bin = fkey(v[j]) >> BIN_SHIFT;
+          __atomic_fetch_add(&E.hf[bin], 1u, __ATOMIC_RELAXED);
+          __atomic_fetch_add(&E.hcoarse[bin >> (CBIN_SHIFT - BIN_SHIFT)], 1u, __ATOMIC_RELAXED);
+        }
+        E.cbuf[base + lanes_below(mk)] = u2v{__float_as_uint(v[j]), idx(j)};
+      }
+      base += (uint32_t)__popcll(mk);
+    }
+  }
+  if (counted) return;
+  since += npass;
+  if (since >= E.recompute_at) {
+    since = 0;
+    const uint32_t nbeta = compute_beta(E.hcoarse, E.hf, E.P.Kc, lane);
+    if (nbeta > beta && lane == 0) __atomic_fetch_max(&E.misc[M_BETA], nbeta, __ATOMIC_RELAXED);
+  }
+}
+
+// Sets v to -inf where bit (sh + q) of x is set (x: one exclusion word).
+__device__ __forceinline__ float exclude(float v, uint32_t x, uint32_t pos) {
+  const uint32_t m = (uint32_t)__builtin_amdgcn_sbfe((int)x, pos, 1);
+  const uint32_t bits = __float_as_uint(v);
+  return __uint_as_float(bits ^ ((bits ^ 0xff800000u) & m));
+}
+
+// ---------------------------------------------------------------------------
+// Virtual tiles: the history tokens of one 16-tile chunk, reduced by one
+// wave.  Lane l owns chunk tokens 256l .. 256l+255 (bitmap words 8l..8l+7 of
+// the chunk); its terms are summed sequentially in increasing token order,
+// the lanes by a balanced tree.
+// ---------------------------------------------------------------------------
+constexpr int VB = 8;  // tokens per lane gathered together
+
+// Removes the lowest set bit of the lane's 256-bit set wd[0..7] and returns
+// its position (EMPTY if the set is empty).
+__device__ __forceinline__ uint32_t pop_lowest(uint32_t (&wd)[8]) {
+  uint32_t pos = EMPTY;
+#pragma unroll
+  for (int j = 7; j >= 0; --j)
+    if (wd[j]) pos = 32u * j + (uint32_t)__builtin_ctz(wd[j]);
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if ((pos >> 5) == (uint32_t)j) wd[j] &= wd[j] - 1;
+  return pos;
+}
+
+// Penalised, masked values of the lane's next (up to) VB tokens: tk[i] (EMPTY
+// past the lane's tokens), v[i].  rank0: rank of the first of them.
+template <int DT>
+__device__ __forceinline__ void vt_batch(const Args& a, const RowP& P, const void* row,
+                                         const GLB uint32_t* mrow, uint32_t base_tok,
+                                         uint32_t (&wd)[8], bool need_cnt, uint32_t rank0,
+                                         LDS const uint32_t* cnt, uint32_t (&tk)[VB],
+                                         float (&v)[VB]) {
+  float x[VB];
+  uint32_t mw[VB];
+#pragma unroll
+  for (int i = 0; i < VB; ++i) {
+    const uint32_t pos = pop_lowest(wd);
+    tk[i] = pos == EMPTY ? EMPTY : base_tok + pos;
+    x[i] = pos == EMPTY ? 0.0f : load_logit<DT>(row, tk[i]);
+    mw[i] = (pos != EMPTY && mrow) ? mrow[tk[i] >> 5] : 0xffffffffu;
+  }
+#pragma unroll
+  for (int i = 0; i < VB; ++i) {
+    float y = NEG_INF;
+    if (tk[i] != EMPTY) {
+      const uint32_t r = rank0 + (uint32_t)i;
+      y = (x[i] > NEG_INF) ? x[i] : NEG_INF;  // NaN acts as -inf
+      y = penalize(y, P, (need_cnt && r < U_MAX) ? cnt[r] : 1u);
+      if (!((mw[i] >> (tk[i] & 31)) & 1u)) y = NEG_INF;
+    }
+    v[i] = y;
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void vtile_chunk(const Args& a, const RowP& P, uint32_t b,
+                                         const void* row, uint32_t t0, uint32_t lo,
+                                         uint32_t nwords, uint32_t kk, const Hist& h,
+                                         LDS const uint32_t* cst, bool need_cnt,
+                                         const TileEnv& E, uint32_t& since, int lane) {
+  const uint32_t wb = 512u * kk + 8u * (uint32_t)lane;
+  uint32_t w0[8];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    u4v q = u4v{0u, 0u, 0u, 0u};
+    if (wb + 4 * j < nwords) q = *(LDS const u4v*)(h.bitmap + wb + 4 * j);
+    w0[4 * j + 0] = q.x;
+    w0[4 * j + 1] = q.y;
+    w0[4 * j + 2] = q.z;
+    w0[4 * j + 3] = q.w;
+  }
+  uint32_t n = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) n += __popc(w0[j]);
+  const uint32_t rank_lane = need_cnt ? cst[kk] + wave_incl_scan(n) - n : 0u;
+  const uint32_t nb_max = (wave_max_u32(n) + VB - 1) / VB;  // batches
+  const uint32_t base_tok = lo + 32u * wb;
+  const uint32_t slot = a.ntiles + t0 / CHUNK_TILES + kk;
+  const GLB uint32_t* mrow = a.mask ? G(a.mask) + (uint64_t)b * a.mask_words : nullptr;
+  LDS const uint32_t* cnt = (LDS const uint32_t*)h.pen;
+  const bool greedy = E.P.mode == MODE_GREEDY;
+  // pass 1: the chunk's maximum (and, for greedy rows, its first index)
+  uint32_t wd[8];
+  uint32_t tk[VB];
+  float v[VB];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) wd[j] = w0[j];
+  float lm = NEG_INF;
+  for (uint32_t bt = 0; bt < nb_max; ++bt) {
+    vt_batch<DT>(a, P, row, mrow, base_tok, wd, need_cnt, rank_lane + bt * VB, cnt, tk, v);
+#pragma unroll
+    for (int i = 0; i < VB; ++i) lm = fmaxf(lm, v[i]);
+  }
+  lm = wave_max(lm);
+  if (greedy) {
+    uint32_t bi = EMPTY;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) wd[j] = w0[j];
+    for (uint32_t bt = 0; bt < nb_max; ++bt) {
+      if (nb_max > 1)
+        vt_batch<DT>(a, P, row, mrow, base_tok, wd, need_cnt, rank_lane + bt * VB, cnt, tk, v);
+#pragma unroll
+      for (int i = 0; i < VB; ++i) {
+        const bool hit = tk[i] != EMPTY && ((v[i] == lm) || (lm == NEG_INF && !(v[i] > NEG_INF)));
+        if (hit) bi = umin(bi, tk[i]);
+      }
+    }
+    bi = wave_min_u32(bi);
+    if (lane == 0) E.part[slot] = f2v{lm, __uint_as_float(bi)};
+    return;
+  }
+  float s = 0.0f;
+  if (lm != NEG_INF) {
+    const float nbias = -(lm * E.c2);
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) wd[j] = w0[j];
+    for (uint32_t bt = 0; bt < nb_max; ++bt) {
+      if (nb_max > 1)
+        vt_batch<DT>(a, P, row, mrow, base_tok, wd, need_cnt, rank_lane + bt * VB, cnt, tk, v);
+#pragma unroll
+      for (int i = 0; i < VB; ++i)
+        if (tk[i] != EMPTY) acc = acc + exp2_f(__builtin_fmaf(v[i], E.c2, nbias));
+    }
+    s = wave_tree_sum(acc);
+  }
+  if (lane == 0) E.part[slot] = f2v{lm, s};
+  if (!E.collect || lm == NEG_INF) return;
+  // ---- candidates: the chunk's history tokens above the threshold
+  const float th = theta_of(__atomic_load_n(&E.misc[M_BETA], __ATOMIC_RELAXED));
+  if (!(lm >= th)) return;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) wd[j] = w0[j];
+  for (uint32_t bt = 0; bt < nb_max; ++bt) {
+    if (nb_max > 1)
+      vt_batch<DT>(a, P, row, mrow, base_tok, wd, need_cnt, rank_lane + bt * VB, cnt, tk, v);
+    uint32_t np = 0;
+#pragma unroll
+    for (int i = 0; i < VB; ++i) np += (tk[i] != EMPTY && v[i] >= th) ? 1u : 0u;
+    const uint32_t tot = bcast63u(wave_incl_scan(np));
+    if (tot == 0) continue;
+    uint32_t base = 0;
+    if (lane == 0) base = __atomic_fetch_add(&E.misc[M_CCOUNT], tot, __ATOMIC_RELAXED);
+    base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+    if (base + tot > CAND_CAP) {
+      if (lane == 0) __atomic_fetch_or(&E.misc[M_FLAGS], FLAG_OVERFLOW, __ATOMIC_RELAXED);
+      return;
+    }
+    uint32_t pos = base + wave_incl_scan(np) - np;
+#pragma unroll
+    for (int i = 0; i < VB; ++i)
+      if (tk[i] != EMPTY && v[i] >= th) {
+        const uint32_t bin = fkey(v[i]) >> BIN_SHIFT;
+        __atomic_fetch_add(&E.hf[bin], 1u, __ATOMIC_RELAXED);
+        __atomic_fetch_add(&E.hcoarse[bin >> (CBIN_SHIFT - BIN_SHIFT)], 1u, __ATOMIC_RELAXED);
+        E.cbuf[pos++] = u2v{__float_as_uint(v[i]), tk[i]};
+      }
+  }
+  (void)since;
 }
 
 // ---------------------------------------------------------------------------
@@ -1234,175 +1538,141 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   }
   const uint32_t t0 = g * a.tps;
   const uint32_t t1 = min(t0 + a.tps, a.ntiles);
+  const uint32_t lo = t0 * TILE, hi = min(a.V, t1 * TILE);
   LDS uint32_t* sm = (LDS uint32_t*)smem;
   LDS uint32_t* red = sm;                    // 64
   LDS uint32_t* misc = red + 64;             // M_NMISC
-  LDS uint32_t* hf = misc + M_NMISC;         // NBINS
+  LDS uint32_t* cst = misc + M_NMISC;        // MAX_CHUNKS + 16
+  LDS uint32_t* hf = cst + MAX_CHUNKS + 16;  // NBINS
   LDS uint32_t* hcoarse = hf + NBINS;        // 64
   LDS uint32_t* hb = hcoarse + 64;           // history tables
   const uint32_t nwords = (t1 - t0) * 32;
   Hist h;
   hist_carve(h, hb, nwords);
-  h.lo = t0 * TILE;
+  h.lo = lo;
+  const bool need_pen = P.rp != 1.0f || P.pp != 0.0f || P.fp != 0.0f;
+  uint32_t h0 = 0, h1 = 0;
+  if (a.hoff) {  // loaded unconditionally, in parallel with the parameters
+    h0 = G(a.hoff)[b];
+    h1 = G(a.hoff)[b + 1];
+  }
+  if (!need_pen) h1 = h0;
+  // history tokens exist: their positions are excluded from the vocabulary
+  // tiles and reduced in virtual tiles, one per 16-tile chunk
+  const bool have = h1 > h0;
+  const bool need_cnt = have && P.fp != 0.0f;
   const bool collect = P.mode == MODE_SAMPLE && P.Kc > 0;
+  const void* row = (const char*)a.logits +
+                    (uint64_t)b * a.stride * (DT == LLMK_F32 ? 4u : 2u);
+  const uint32_t* mrow = a.mask ? a.mask + (uint64_t)b * a.mask_words : nullptr;
+  // The first two tiles of every wave, and the history tokens, are requested
+  // before the tables are set up, so HBM works meanwhile.
+  Raw ra, rb;
+  uint32_t ta = t0 + (uint32_t)wv, tb2 = t0 + (uint32_t)wv + NW;
+  ta = ta < t1 ? ta : EMPTY;
+  tb2 = tb2 < t1 ? tb2 : EMPTY;
+  if (ta != EMPTY) load_tile<DT>(a, row, mrow, h, ta, lane, ra);
+  if (tb2 != EMPTY) load_tile<DT>(a, row, mrow, h, tb2, lane, rb);
+  uint32_t tk[HTPT];
+#pragma unroll
+  for (int q = 0; q < HTPT; ++q) {
+    const uint32_t i = h0 + q * NT + tid;
+    tk[q] = (i < h1) ? G(a.htok)[i] : EMPTY;
+  }
   if (collect) {
     for (uint32_t i = tid; i < NBINS; i += NT) hf[i] = 0;
     if (tid < 64) hcoarse[tid] = 0;
   }
   if (tid < M_NMISC) misc[tid] = 0;
-  const void* row = (const char*)a.logits +
-                    (uint64_t)b * a.stride * (DT == LLMK_F32 ? 4u : 2u);
-  const uint32_t* mrow0 = a.mask ? a.mask + (uint64_t)b * a.mask_words : nullptr;
-  // The first two tiles of every wave are requested before the history
-  // tables are built, so HBM works while the workgroup waits on them.
-  Raw ra, rb;
-  uint32_t ta = t0 + (uint32_t)wv, tb2 = t0 + (uint32_t)wv + NW;
-  ta = ta < t1 ? ta : EMPTY;
-  tb2 = tb2 < t1 ? tb2 : EMPTY;
-  if (ta != EMPTY) load_tile<DT>(a, row, mrow0, h, ta, lane, ra);
-  if (tb2 != EMPTY) load_tile<DT>(a, row, mrow0, h, tb2, lane, rb);
-  build_history<DT>(a, P, b, row, h.lo, min(a.V, t1 * TILE), nwords, h, red,
-                    &misc[M_FLAGS]);
-  const uint32_t* mrow = a.mask ? a.mask + (uint64_t)b * a.mask_words : nullptr;
-  GLB f2v* part = G(w.tile_part) + (uint64_t)b * MAX_TILES;
-  GLB u2v* cbuf = G(w.cand) + (uint64_t)blockIdx.x * CAND_CAP;
-  const float c2 = LOG2E_F / P.T;
-  const float NINF = NEG_INF;
-  const uint32_t recompute_at = P.Kc / 2 > 16 ? P.Kc / 2 : 16;
-  uint32_t since = EMPTY;  // candidates counted since the last beta update
+  if (have)
+    for (uint32_t i = tid; i < nwords; i += NT) h.bitmap[i] = 0;
+  __syncthreads();
+  if (have) {
+    for (uint32_t c0 = h0; c0 < h1; c0 += HTPT * NT) {
+#pragma unroll
+      for (int q = 0; q < HTPT; ++q) {
+        uint32_t t = tk[q];
+        if (c0 != h0) {
+          const uint32_t i = c0 + q * NT + tid;
+          t = (i < h1) ? G(a.htok)[i] : EMPTY;
+        }
+        if (t >= lo && t < hi)
+          __atomic_fetch_or(&h.bitmap[(t - lo) >> 5], 1u << (t & 31), __ATOMIC_RELAXED);
+      }
+    }
+    __syncthreads();
+  }
+  if (need_cnt) {
+    // ranks (popcount prefix over the words; first rank of every chunk) and
+    // occurrence counts by rank
+    const uint32_t wpt = (nwords + NT - 1) / NT;
+    const uint32_t w0 = tid * wpt < nwords ? tid * wpt : nwords;
+    const uint32_t w1 = (w0 + wpt < nwords) ? w0 + wpt : nwords;
+    uint32_t local = 0;
+    for (uint32_t wi = w0; wi < w1; ++wi) local += __popc(h.bitmap[wi]);
+    uint32_t U;
+    uint32_t run = block_excl_scan(local, red, U);
+    for (uint32_t wi = w0; wi < w1; ++wi) {
+      if ((wi & 511u) == 0) cst[wi >> 9] = run;
+      h.pre[wi] = (uint16_t)(run < 0xffffu ? run : 0xffffu);
+      run += __popc(h.bitmap[wi]);
+    }
+    if (U > U_MAX && tid == 0) misc[M_FLAGS] = FLAG_HIST_OVERFLOW;
+    const uint32_t Uc = U < U_MAX ? U : U_MAX;
+    LDS uint32_t* cnt = (LDS uint32_t*)h.pen;
+    for (uint32_t i = tid; i < Uc; i += NT) cnt[i] = 0;
+    __syncthreads();
+    for (uint32_t c0 = h0; c0 < h1; c0 += HTPT * NT) {
+#pragma unroll
+      for (int q = 0; q < HTPT; ++q) {
+        uint32_t t = tk[q];
+        if (c0 != h0) {
+          const uint32_t i = c0 + q * NT + tid;
+          t = (i < h1) ? G(a.htok)[i] : EMPTY;
+        }
+        if (t >= lo && t < hi) {
+          const uint32_t r = h.rank(t);
+          if (r < U_MAX) __atomic_fetch_add(&cnt[r], 1u, __ATOMIC_RELAXED);
+        }
+      }
+    }
+    __syncthreads();
+  }
+  TileEnv E;
+  E.P = P;
+  E.c2 = LOG2E_F / P.T;
+  E.V = a.V;
+  E.collect = collect;
+  E.recompute_at = P.Kc / 2 > 16 ? P.Kc / 2 : 16;
+  E.misc = misc;
+  E.hf = hf;
+  E.hcoarse = hcoarse;
+  E.cbuf = G(w.cand) + (uint64_t)blockIdx.x * CAND_CAP;
+  E.part = G(w.tile_part) + (uint64_t)b * MAX_SLOTS;
+  uint32_t since = EMPTY;
+  const uint32_t nch = (nwords + 511) / 512;  // chunks of this segment
 
+  const bool xmask = have || mrow != nullptr;
+  const uint32_t sh4 = (4u * (uint32_t)lane) & 31u;
   auto process = [&](const Raw& raw, uint32_t t) __attribute__((always_inline)) {
     float v[16];
     unpack<DT>(raw, v);
     const uint32_t tb = t * TILE;
-    // history tokens take their penalised value
-    const uint32_t sh4 = (4u * (uint32_t)lane) & 31u;
-    uint32_t bw[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      bw[r] = h.bitmap[((tb - h.lo) >> 5) + 8u * r + ((uint32_t)lane >> 3)];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const uint32_t nib = (bw[r] >> sh4) & 0xfu;
-      if (nib) {
-        const uint32_t wi = ((tb - h.lo) >> 5) + 8u * r + ((uint32_t)lane >> 3);
-        const uint32_t base = h.pre[wi] + __popc(bw[r] & ((1u << sh4) - 1u));
-        uint32_t k = 0;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if ((nib >> q) & 1u) {
-            const uint32_t rr = base + k;
-            if (rr < U_MAX) v[4 * r + q] = h.pen[rr];
-            ++k;
-          }
-      }
-    }
-    if (mrow) {
+    if (xmask) {
+      // history tokens and disallowed tokens become -inf
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const uint32_t nib = (raw.mw[r] >> ((4u * lane) & 31u)) & 0xfu;
+        uint32_t x = 0;
+        if (have) x = h.bitmap[((tb - lo) >> 5) + 8u * r + ((uint32_t)lane >> 3)];
+        if (mrow) x |= ~raw.mw[r];
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if (!((nib >> q) & 1u)) v[4 * r + q] = NINF;
+        for (int q = 0; q < 4; ++q) v[4 * r + q] = exclude(v[4 * r + q], x, sh4 + q);
       }
     }
-    float lm = NINF;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) lm = v[j] > lm ? v[j] : lm;
-    lm = wave_max(lm);
-    if (P.mode == MODE_GREEDY) {
-      uint32_t bi = EMPTY;
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float x = v[4 * r + q];
-          const uint32_t e = tb + 256u * r + 4u * lane + q;
-          const bool hit = (x == lm) || (lm == NINF && !(x > NINF));
-          if (hit && e < a.V) bi = umin(bi, e);
-        }
-      bi = wave_min_u32(bi);
-      if (lane == 0) part[t] = f2v{lm, __uint_as_float(bi)};
-      return;
-    }
-    float s = 0.0f;
-    if (lm != NINF) {
-      // per lane: ((run0 + run1) + (run2 + run3)), each run ((e0+e1)+(e2+e3));
-      // then a balanced tree over the 64 lanes
-      const float nb = -(lm * c2);
-      float sr[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float e0 = exp2_f(__builtin_fmaf(v[4 * r + 0], c2, nb));
-        const float e1 = exp2_f(__builtin_fmaf(v[4 * r + 1], c2, nb));
-        const float e2 = exp2_f(__builtin_fmaf(v[4 * r + 2], c2, nb));
-        const float e3 = exp2_f(__builtin_fmaf(v[4 * r + 3], c2, nb));
-        sr[r] = (e0 + e1) + (e2 + e3);
-      }
-      s = wave_tree_sum((sr[0] + sr[1]) + (sr[2] + sr[3]));
-    }
-    if (lane == 0) part[t] = f2v{lm, s};
-    if (!collect) return;
-    // ---- candidates above the rising histogram threshold
-    uint32_t beta = __atomic_load_n(&misc[M_BETA], __ATOMIC_RELAXED);
-    float th = theta_of(beta);
-    if (!(lm >= th)) return;  // no element of this tile can pass
-    bool counted = false;
-    if (since == EMPTY) {
-      // a wave's first tile: count it, raise the threshold, then append
-#pragma unroll
-      for (int j = 0; j < 16; ++j)
-        if (v[j] >= th) {
-          const uint32_t bin = fkey(v[j]) >> BIN_SHIFT;
-          __atomic_fetch_add(&hf[bin], 1u, __ATOMIC_RELAXED);
-          __atomic_fetch_add(&hcoarse[bin >> (CBIN_SHIFT - BIN_SHIFT)], 1u, __ATOMIC_RELAXED);
-        }
-      const uint32_t nb = compute_beta(hcoarse, hf, P.Kc, lane);
-      if (nb > beta) {
-        if (lane == 0) __atomic_fetch_max(&misc[M_BETA], nb, __ATOMIC_RELAXED);
-        beta = nb;
-        th = theta_of(beta);
-      }
-      since = 0;
-      counted = true;
-    }
-    uint32_t npass = 0;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) npass += (uint32_t)__popcll(__ballot(v[j] >= th));
-    if (npass == 0) return;
-    uint32_t base = 0;
-    if (lane == 0) base = __atomic_fetch_add(&misc[M_CCOUNT], npass, __ATOMIC_RELAXED);
-    base = __shfl(base, 0);
-    if (base + npass > CAND_CAP) {
-      if (lane == 0) __atomic_fetch_or(&misc[M_FLAGS], FLAG_OVERFLOW, __ATOMIC_RELAXED);
-      return;
-    }
-    // append, and count what was appended in the histogram
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const uint64_t mk = __ballot(v[j] >= th);
-      if (mk) {
-        if ((mk >> lane) & 1ull) {
-          if (!counted) {
-            const uint32_t bin = fkey(v[j]) >> BIN_SHIFT;
-            __atomic_fetch_add(&hf[bin], 1u, __ATOMIC_RELAXED);
-            __atomic_fetch_add(&hcoarse[bin >> (CBIN_SHIFT - BIN_SHIFT)], 1u, __ATOMIC_RELAXED);
-          }
-          cbuf[base + lanes_below(mk)] =
-              u2v{__float_as_uint(v[j]), tb + 256u * (j >> 2) + 4u * lane + (j & 3)};
-        }
-        base += (uint32_t)__popcll(mk);
-      }
-    }
-    if (counted) return;
-    since += npass;
-    if (since >= recompute_at) {
-      since = 0;
-      const uint32_t nb = compute_beta(hcoarse, hf, P.Kc, lane);
-      if (nb > beta && lane == 0) __atomic_fetch_max(&misc[M_BETA], nb, __ATOMIC_RELAXED);
-    }
+    tile_reduce(E, v, t, [&](int j) -> uint32_t {
+      return tb + 256u * (j >> 2) + 4u * (uint32_t)lane + (j & 3);
+    }, since, lane);
   };
-
   // Later tiles are claimed dynamically, so the waves finish together.
   auto grab = [&]() -> uint32_t {
     uint32_t k = 0;
@@ -1411,20 +1681,29 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
     const uint32_t t = t0 + 2u * NW + k;
     return t < t1 ? t : EMPTY;
   };
+  // Wave w reduces the virtual tiles of chunks w, w + NW, ... after its first
+  // vocabulary tile.
+  if (ta != EMPTY) {
+    process(ra, ta);
+    ta = grab();
+    if (ta != EMPTY) load_tile<DT>(a, row, mrow, h, ta, lane, ra);
+  }
+  if (have)
+    for (uint32_t k = (uint32_t)wv; k < nch; k += NW)
+      vtile_chunk<DT>(a, P, b, row, t0, lo, nwords, k, h, cst, need_cnt, E, since, lane);
   for (;;) {
     if (ta == EMPTY && tb2 == EMPTY) break;
-    if (ta != EMPTY) {
-      process(ra, ta);
-      ta = grab();
-      if (ta != EMPTY) load_tile<DT>(a, row, mrow, h, ta, lane, ra);
-    }
     if (tb2 != EMPTY) {
       process(rb, tb2);
       tb2 = grab();
       if (tb2 != EMPTY) load_tile<DT>(a, row, mrow, h, tb2, lane, rb);
     }
+    if (ta != EMPTY) {
+      process(ra, ta);
+      ta = grab();
+      if (ta != EMPTY) load_tile<DT>(a, row, mrow, h, ta, lane, ra);
+    }
   }
-
   // ---- publish the segment; the row's last workgroup finalizes
   wait_stores();
   __syncthreads();
@@ -1432,8 +1711,8 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
     const uint32_t fl = misc[M_FLAGS];
     if (fl & FLAG_HIST_OVERFLOW) atomicOr(w.status, LLMK_STATUS_HISTORY_OVERFLOW);
     uint32_t last = 1;
+    G(w.seg_meta)[blockIdx.x] = u4v{misc[M_CCOUNT], misc[M_BETA], fl, have ? 1u : 0u};
     if (a.G > 1) {
-      G(w.seg_meta)[blockIdx.x] = u4v{misc[M_CCOUNT], misc[M_BETA], fl, 0u};
       __threadfence();  // release this workgroup's stores (all waves waited above)
       const uint32_t old = atomicAdd(&w.row_arrive[b], 1u);
       last = (old == a.G - 1) ? 1u : 0u;
@@ -1442,7 +1721,6 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
         w.row_arrive[b] = 0;
       }
     } else {
-      G(w.seg_meta)[blockIdx.x] = u4v{misc[M_CCOUNT], misc[M_BETA], fl, 0u};
       wait_stores();
     }
     misc[M_LAST] = last;
@@ -1451,7 +1729,7 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   const uint32_t last = misc[M_LAST];
   __syncthreads();  // finalize reuses this shared memory
   if (!last) return;
-  finalize_row<DT>(a, w, b, P, sm);
+  finalize_row<DT>(a, w, b, P, have, sm);
 }
 
 }  // namespace llmk
@@ -1512,7 +1790,7 @@ extern "C" int llmk_sampler_create(llmk_sampler** out, int device,
     return o;
   };
   const size_t o_arrive = take(4ull * max_batch);
-  const size_t o_part = take(8ull * max_batch * MAX_TILES);
+  const size_t o_part = take(8ull * max_batch * MAX_SLOTS);
   const size_t o_meta = take(16ull * pool);
   const size_t o_cand = take(8ull * pool * CAND_CAP);
   const size_t o_lock = take(4ull * SLOW_SLOTS);
@@ -1623,17 +1901,18 @@ extern "C" int llmk_sample_batch(llmk_sampler* s,
   a.out_probs = in->out_probs;
   a.out_cap = in->out_cap;
   a.ntiles = (a.V + TILE - 1) / TILE;
-  // Segments per row: enough workgroups to cover the 256 CUs, at least 16
-  // tiles per segment, at most MAX_SEG segments.
+  a.nchunks = (a.ntiles + CHUNK_TILES - 1) / CHUNK_TILES;
+  // Segments per row: enough workgroups to cover the 256 CUs, whole 16-tile
+  // chunks per segment, at most MAX_SEG segments.
   const uint32_t pool = s->max_batch > MAX_WGS ? s->max_batch : MAX_WGS;
   uint32_t G = (256 + a.B - 1) / a.B;
-  const uint32_t gmax = (a.ntiles + 15) / 16;
-  if (G > gmax) G = gmax;
+  if (G > a.nchunks) G = a.nchunks;
   if (G > MAX_SEG) G = MAX_SEG;
   if (G < 1) G = 1;
   while (G > 1 && (uint64_t)a.B * G > pool) --G;
-  a.tps = (a.ntiles + G - 1) / G;
-  a.G = (a.ntiles + a.tps - 1) / a.tps;
+  const uint32_t cps = (a.nchunks + G - 1) / G;  // chunks per segment
+  a.tps = cps * CHUNK_TILES;
+  a.G = (a.nchunks + cps - 1) / cps;
   a.xcd_map = (a.G > 1 && (a.B % 8) == 0) ? 1u : 0u;
 
   HIPCHK(hipSetDevice(s->device));

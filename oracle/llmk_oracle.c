@@ -94,60 +94,99 @@ static void tree_sum_inplace(float* buf, uint32_t len) {
     for (uint32_t i = 0; i < len / 2; ++i) buf[i] = buf[2 * i] + buf[2 * i + 1];
 }
 
-float llmk_oracle_normalizer(const float* lp, uint32_t V, float temperature) {
-  /* Two-level log-sum-exp over 1024-wide vocabulary tiles.
-   *   c2 = fl(log2(e) / T)
-   *   tile c (positions past V count as -inf): lc = max lp (NaN ignored);
-   *     if lc = -inf the tile sum is 0, else with nb = -fl(lc*c2) each
-   *     element gives e = exp2_f(fma(lp, c2, nb)); position 256r + 4L + q
-   *     belongs to lane L, run r; a run sums ((e0+e1)+(e2+e3)), a lane
-   *     ((run0+run1)+(run2+run3)), the tile is the balanced tree over the
-   *     64 lanes.
-   *   row: L = max lc; S = balanced tree over next_pow2(#tiles) of
-   *     s_c * exp2_f((lc - L)*c2)  (padding entries are 0).
+/* Partial of one 1024-value tile x[0..1023] (excluded positions already
+ * -inf): its max lc and, relative to lc, the tree sum of the 2^ terms. */
+static void tile_partial(const float* x, float c2, float* lc_out, float* s_out) {
+  float m = -INFINITY;
+  for (uint32_t i = 0; i < TILE; ++i)
+    if (x[i] > m) m = x[i];
+  *lc_out = m;
+  if (m == -INFINITY) {
+    *s_out = 0.0f;
+    return;
+  }
+  const float nb = -(m * c2);
+  float lanes[64];
+  for (uint32_t L = 0; L < 64; ++L) {
+    float run[4];
+    for (uint32_t r = 0; r < 4; ++r) {
+      float e[4];
+      for (uint32_t q = 0; q < 4; ++q)
+        e[q] = llmk_oracle_exp2_f(fmaf(x[256 * r + 4 * L + q], c2, nb));
+      run[r] = (e[0] + e[1]) + (e[2] + e[3]);
+    }
+    lanes[L] = (run[0] + run[1]) + (run[2] + run[3]);
+  }
+  tree_sum_inplace(lanes, 64);
+  *s_out = lanes[0];
+}
+
+float llmk_oracle_normalizer(const float* lp, const uint8_t* is_hist, uint32_t V,
+                             float temperature) {
+  /* Two-level log-sum-exp over fixed partial slots.
+   *   c2 = fl(log2(e) / T).
+   *   Real tile c (1024 tokens; positions past V and history tokens count
+   *   as -inf): lc = max; if lc = -inf the sum is 0, else with
+   *   nb = -fl(lc*c2) each position gives e = exp2_f(fma(x, c2, nb));
+   *   position 256r + 4L + q belongs to lane L, run r; a run sums
+   *   ((e0+e1)+(e2+e3)), a lane ((run0+run1)+(run2+run3)), the tile is the
+   *   balanced tree over the 64 lanes.
+   *   Virtual tile k holds the history tokens of chunk k (16 real tiles,
+   *   tokens 16384k ..): lc = their max (-inf if none, sum 0); lane L owns
+   *   chunk tokens 256L .. 256L+255 and sums their terms
+   *   exp2_f(fma(x, c2, nb)) sequentially in increasing token order
+   *   (0 if none); the tile is the balanced tree over the 64 lanes.
+   *   Slots: real tiles 0..nt-1, then virtual tile k at nt + k.  Row:
+   *   L = max lc; S = balanced tree over the next power of two >= slots of
+   *   s_c * exp2_f((lc_c - L)*c2) (padding 0).
    * Mathematically S = sum_i e^{(lp_i - L)/T}, the reference's softmax
    * denominator (sampler.rs:57-66); the order of operations is fixed. */
   const float c2 = LOG2E_F / temperature;
   const uint32_t nt = (V + TILE - 1) / TILE;
+  const uint32_t nch = (nt + 15) / 16;
+  const uint32_t P = nt + nch;
   uint32_t ntp = 1;
-  while (ntp < nt) ntp <<= 1;
-  float* lc = (float*)malloc(sizeof(float) * nt);
+  while (ntp < P) ntp <<= 1;
+  float* lc = (float*)malloc(sizeof(float) * P);
   float* w = (float*)calloc(ntp, sizeof(float));
-  float lanes[64];
+  float buf[TILE];
   for (uint32_t c = 0; c < nt; ++c) {
-    const uint32_t base = c * TILE;
-    const uint32_t n = (V - base < TILE) ? V - base : TILE;
+    for (uint32_t i = 0; i < TILE; ++i) {
+      const uint32_t e = c * TILE + i;
+      buf[i] = (e < V && !(is_hist && is_hist[e])) ? lp[e] : -INFINITY;
+    }
+    tile_partial(buf, c2, &lc[c], &w[c]);
+  }
+  for (uint32_t k = 0; k < nch; ++k) {
+    const uint32_t slot = nt + k;
+    const uint32_t lo = k * 16 * TILE;
+    const uint32_t hi = (lo + 16 * TILE < V) ? lo + 16 * TILE : V;
     float m = -INFINITY;
-    for (uint32_t i = 0; i < n; ++i)
-      if (lp[base + i] > m) m = lp[base + i];
-    lc[c] = m;
+    if (is_hist)
+      for (uint32_t e = lo; e < hi; ++e)
+        if (is_hist[e] && lp[e] > m) m = lp[e];
+    lc[slot] = m;
     if (m == -INFINITY) {
-      w[c] = 0.0f;
+      w[slot] = 0.0f;
       continue;
     }
     const float nb = -(m * c2);
+    float lanes[64];
     for (uint32_t L = 0; L < 64; ++L) {
-      float run[4];
-      for (uint32_t r = 0; r < 4; ++r) {
-        float e[4];
-        for (uint32_t q = 0; q < 4; ++q) {
-          const uint32_t i = 256 * r + 4 * L + q;
-          const float x = (i < n) ? lp[base + i] : -INFINITY;
-          e[q] = llmk_oracle_exp2_f(fmaf(x, c2, nb));
-        }
-        run[r] = (e[0] + e[1]) + (e[2] + e[3]);
-      }
-      lanes[L] = (run[0] + run[1]) + (run[2] + run[3]);
+      float acc = 0.0f;
+      for (uint32_t e = lo + 256 * L; e < lo + 256 * (L + 1) && e < hi; ++e)
+        if (is_hist[e]) acc = acc + llmk_oracle_exp2_f(fmaf(lp[e], c2, nb));
+      lanes[L] = acc;
     }
     tree_sum_inplace(lanes, 64);
-    w[c] = lanes[0];
+    w[slot] = lanes[0];
   }
   float L = -INFINITY;
-  for (uint32_t c = 0; c < nt; ++c)
+  for (uint32_t c = 0; c < P; ++c)
     if (lc[c] > L) L = lc[c];
   float S = 0.0f;
   if (L != -INFINITY) {
-    for (uint32_t c = 0; c < nt; ++c)
+    for (uint32_t c = 0; c < P; ++c)
       w[c] = w[c] * llmk_oracle_exp2_f((lc[c] - L) * c2);
     tree_sum_inplace(w, ntp);
     S = w[0];
@@ -444,10 +483,21 @@ int llmk_oracle_sample_row(int mode, const float* logits, uint32_t V,
     return 0;
   }
 
-  /* The mirror normaliser works on the penalised, masked, unscaled logits. */
+  /* The mirror normaliser works on the penalised, masked, unscaled logits;
+   * when a penalty is on, the distinct in-vocabulary history tokens sit in
+   * its virtual tiles. */
   float S_mirror = 0.0f;
-  if (mode == LLMK_ORACLE_MIRROR)
-    S_mirror = llmk_oracle_normalizer(l, V, prm->temperature);
+  if (mode == LLMK_ORACLE_MIRROR) {
+    uint8_t* is_hist = NULL;
+    if (H > 0 && (prm->repetition_penalty != 1.0f || prm->presence_penalty != 0.0f ||
+                  prm->frequency_penalty != 0.0f)) {
+      is_hist = (uint8_t*)calloc(V, 1);
+      for (uint32_t i = 0; i < H; ++i)
+        if (hist[i] < V) is_hist[hist[i]] = 1;
+    }
+    S_mirror = llmk_oracle_normalizer(l, is_hist, V, prm->temperature);
+    free(is_hist);
+  }
 
   apply_temperature(l, V, prm->temperature); /* :53 */
 
@@ -676,7 +726,7 @@ void llmk_oracle_apply_top_p(int mode, float* logits, uint32_t V, float top_p) {
   if (mode == LLMK_ORACLE_MIRROR) {
     float* lp = (float*)malloc(sizeof(float) * V);
     for (uint32_t i = 0; i < V; ++i) lp[i] = isnan(logits[i]) ? -INFINITY : logits[i];
-    S = llmk_oracle_normalizer(lp, V, 1.0f);
+    S = llmk_oracle_normalizer(lp, NULL, V, 1.0f);
     free(lp);
   } else {
     S = 0.0f;

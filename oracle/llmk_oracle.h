@@ -116,8 +116,11 @@ uint32_t llmk_oracle_sample_simple(int mode, const float* logits, uint32_t V,
 float llmk_oracle_exp_m(float y);          /* e^y, y <= 0 */
 float llmk_oracle_exp2_f(float d);         /* 2^d, d <= 0 (normaliser terms) */
 float llmk_oracle_libm_expf(float y);      /* glibc expf, for comparisons */
-/* Mirror softmax normaliser over penalised+masked logits lp[0..V). */
-float llmk_oracle_normalizer(const float* lp, uint32_t V, float temperature);
+/* Mirror softmax normaliser over penalised+masked logits lp[0..V); is_hist
+ * (NULL = none) flags the distinct history tokens, which the engine reduces
+ * in virtual tiles when a penalty is on. */
+float llmk_oracle_normalizer(const float* lp, const uint8_t* is_hist, uint32_t V,
+                             float temperature);
 
 /* Exhaustive checks of exp_m over the float bit patterns [lo, hi] of
  * non-positive inputs (sign bit set, ascending magnitude): counts inputs

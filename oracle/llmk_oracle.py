@@ -46,7 +46,7 @@ def load():
     lib.llmk_oracle_exp2_f.restype = f32
     lib.llmk_oracle_libm_expf.argtypes = [f32]
     lib.llmk_oracle_libm_expf.restype = f32
-    lib.llmk_oracle_normalizer.argtypes = [P, u32, f32]
+    lib.llmk_oracle_normalizer.argtypes = [P, P, u32, f32]
     lib.llmk_oracle_normalizer.restype = f32
     lib.llmk_oracle_apply_repetition_penalty.argtypes = [P, u32, P, u32, f32]
     lib.llmk_oracle_apply_temperature.argtypes = [P, u32, f32]
@@ -203,9 +203,10 @@ def sample_simple(mode, logits, t, u):
     return int(load().llmk_oracle_sample_simple(mode, _p(l), l.size, t, u))
 
 
-def normalizer(lp, temperature):
+def normalizer(lp, temperature, is_hist=None):
     l = _f32p(lp)
-    return float(load().llmk_oracle_normalizer(_p(l), l.size, temperature))
+    h = None if is_hist is None else np.ascontiguousarray(is_hist, dtype=np.uint8)
+    return float(load().llmk_oracle_normalizer(_p(l), _p(h), l.size, temperature))
 
 
 def exp_m(y):

@@ -316,18 +316,25 @@ def test_exp2_f_error_bound_and_clamp():
     assert O.exp2_f(-1000.0) == 2.0 ** -125
 
 
+@pytest.mark.parametrize("hist", [False, True])
 @pytest.mark.parametrize("V,where", [(151936, "first"), (151936, "last"), (4097, "last"),
                                      (1000, "mid"), (256000, "mid")])
-def test_normalizer_against_fp64(V, where):
-    """The mirror normaliser (tiles of 1024, fixed trees) equals the fp64 sum
-    of exp((l - max)/T) to 1e-5 relative, wherever the maximum sits."""
+def test_normalizer_against_fp64(V, where, hist):
+    """The mirror normaliser (tiles of 1024, virtual tiles for history tokens,
+    fixed trees) equals the fp64 sum of exp((l - max)/T) to 1e-5 relative,
+    wherever the maximum sits, also when it is a history token."""
     rng = np.random.default_rng(V)
     lg = rng.normal(0, 3, V).astype(np.float32)
     i = {"first": 3, "last": V - 2, "mid": V // 2}[where]
     lg[i] = 20.0
     lg[rng.choice(V, V // 50, replace=False)] = -np.inf
+    is_hist = None
+    if hist:
+        is_hist = np.zeros(V, np.uint8)
+        is_hist[rng.choice(V, min(V, 3000), replace=False)] = 1
+        is_hist[i] = 1
     for T in (0.7, 1.0, 1.9):
-        S = O.normalizer(lg, T)
+        S = O.normalizer(lg, T, is_hist)
         x = lg.astype(np.float64) / np.float64(f32(T))
         want = np.sum(np.where(np.isneginf(x), 0.0, np.exp(x - x.max())))
         assert abs(S / want - 1) < 1e-5, (T, S, want)
