@@ -75,6 +75,7 @@ constexpr uint32_t MAX_TILES = 1024; // max_vocab <= 2^20
 constexpr uint32_t CHUNK_TILES = 16;  // tiles per history chunk (segments are whole chunks)
 constexpr uint32_t MAX_CHUNKS = MAX_TILES / CHUNK_TILES;
 constexpr uint32_t MAX_SLOTS = MAX_TILES + MAX_CHUNKS;  // partials per row: tiles, then chunks
+constexpr uint32_t LCAP = 1024;       // candidates a single-segment row keeps in LDS
 constexpr uint32_t MAX_SEG = 64;     // segments per row
 constexpr uint32_t MAX_WGS = 4096;   // candidate-buffer pool entries
 constexpr uint32_t SLOW_SLOTS = 64;  // global scratch slots of the slow path
@@ -99,6 +100,9 @@ struct Args {
   float* out_probs;
   uint32_t out_cap;
   uint32_t G, tps, ntiles, nchunks;
+  // single-segment rows: LDS word offsets of the kept partials (MAX_SLOTS
+  // f2v) and candidates (LCAP u2v), past both the stream and finalize layouts
+  uint32_t lds_part, lds_cand;
   uint32_t xcd_map;  // 1: the segments of a row share an XCD
 };
 
@@ -154,6 +158,7 @@ template <int CTRL, int RM, bool BC>
 __device__ __forceinline__ uint32_t dppu(uint32_t old, uint32_t src) {
   return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)src, CTRL, RM, 0xf, BC);
 }
+__device__ __forceinline__ uint32_t umax_(uint32_t a, uint32_t b) { return a > b ? a : b; }
 __device__ __forceinline__ float bcast63f(float x) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
 }
@@ -172,14 +177,20 @@ __device__ __forceinline__ float wave_tree_sum(float x) {
   x = x + dppf<0x143, 0xc, false>(0.0f, x);
   return bcast63f(x);
 }
+// Maximum over the lanes of x (never NaN): on order-preserving keys, whose
+// maximum needs no NaN handling, so each step is one v_max_u32 with DPP;
+// lanes outside a row read 0, the smallest key.
 __device__ __forceinline__ float wave_max(float x) {
-  x = fmaxf(x, dppf<0x111, 0xf, false>(x, x));
-  x = fmaxf(x, dppf<0x112, 0xf, false>(x, x));
-  x = fmaxf(x, dppf<0x114, 0xf, false>(x, x));
-  x = fmaxf(x, dppf<0x118, 0xf, false>(x, x));
-  x = fmaxf(x, dppf<0x142, 0xa, false>(x, x));
-  x = fmaxf(x, dppf<0x143, 0xc, false>(x, x));
-  return bcast63f(x);
+  const uint32_t b = __float_as_uint(x);
+  uint32_t k = b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);
+  k = umax_(k, dppu<0x111, 0xf, true>(0u, k));
+  k = umax_(k, dppu<0x112, 0xf, true>(0u, k));
+  k = umax_(k, dppu<0x114, 0xf, true>(0u, k));
+  k = umax_(k, dppu<0x118, 0xf, true>(0u, k));
+  k = umax_(k, dppu<0x142, 0xa, true>(0u, k));
+  k = umax_(k, dppu<0x143, 0xc, true>(0u, k));
+  const uint32_t r = bcast63u(k);
+  return __uint_as_float((r & 0x80000000u) ? (r & 0x7fffffffu) : ~r);
 }
 __device__ __forceinline__ uint32_t umin(uint32_t a, uint32_t b) { return a < b ? a : b; }
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
@@ -193,12 +204,12 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
 }
 __device__ __forceinline__ uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
-  x = umax(x, dppu<0x111, 0xf, false>(x, x));
-  x = umax(x, dppu<0x112, 0xf, false>(x, x));
-  x = umax(x, dppu<0x114, 0xf, false>(x, x));
-  x = umax(x, dppu<0x118, 0xf, false>(x, x));
-  x = umax(x, dppu<0x142, 0xa, false>(x, x));
-  x = umax(x, dppu<0x143, 0xc, false>(x, x));
+  x = umax(x, dppu<0x111, 0xf, true>(0u, x));
+  x = umax(x, dppu<0x112, 0xf, true>(0u, x));
+  x = umax(x, dppu<0x114, 0xf, true>(0u, x));
+  x = umax(x, dppu<0x118, 0xf, true>(0u, x));
+  x = umax(x, dppu<0x142, 0xa, true>(0u, x));
+  x = umax(x, dppu<0x143, 0xc, true>(0u, x));
   return bcast63u(x);
 }
 // Inclusive prefix sum over lanes.
@@ -285,6 +296,8 @@ struct Hist {
   LDS uint16_t* pre;     // nwords: distinct history tokens in words before
   LDS float* pen;        // U_MAX: penalised logit by rank (counts while building)
   LDS uint32_t* tokr;    // U_MAX: token of each rank
+  LDS uint32_t* hkey;    // HSLOTS: hash table of occurrence counts (stream phase)
+  LDS uint32_t* hcnt;    // HSLOTS
   uint32_t lo;
   __device__ __forceinline__ uint32_t rank(uint32_t t) const {
     const uint32_t o = t - lo, w = o >> 5;
@@ -300,6 +313,40 @@ __device__ __forceinline__ void hist_carve(Hist& h, LDS uint32_t* base, uint32_t
   h.pre = (LDS uint16_t*)(base + ((nwords + 3) & ~3u));
   h.pen = (LDS float*)(base + ((nwords + 3) & ~3u) + (((nwords + 1) / 2 + 3) & ~3u));
   h.tokr = (LDS uint32_t*)(h.pen + U_MAX);
+}
+
+// Occurrence counts of history tokens: open addressing, linear probing, in
+// LDS.  hash_add returns false when the table is full.
+constexpr uint32_t HSLOTS = 8192;
+__device__ __forceinline__ uint32_t hash_slot(uint32_t t) {
+  return (t * 2654435761u) >> (32 - 13);  // HSLOTS = 2^13
+}
+__device__ __forceinline__ bool hash_add(const Hist& h, uint32_t t) {
+  uint32_t i = hash_slot(t);
+  for (uint32_t n = 0; n < HSLOTS; ++n) {
+    uint32_t old = __atomic_load_n(&h.hkey[i], __ATOMIC_RELAXED);
+    if (old == EMPTY) {
+      // claim the slot, or learn which token claimed it first
+      __atomic_compare_exchange_n(&h.hkey[i], &old, t, false, __ATOMIC_RELAXED,
+                                  __ATOMIC_RELAXED);
+    }
+    if (old == EMPTY || old == t) {
+      __atomic_fetch_add(&h.hcnt[i], 1u, __ATOMIC_RELAXED);
+      return true;
+    }
+    i = (i + 1) & (HSLOTS - 1);
+  }
+  return false;
+}
+__device__ __forceinline__ uint32_t hash_count(const Hist& h, uint32_t t) {
+  uint32_t i = hash_slot(t);
+  for (uint32_t n = 0; n < HSLOTS; ++n) {
+    const uint32_t k = h.hkey[i];
+    if (k == t) return h.hcnt[i];
+    if (k == EMPTY) return 1u;  // not recorded (table full): counted once
+    i = (i + 1) & (HSLOTS - 1);
+  }
+  return 1u;
 }
 
 // Builds the history tables for tokens in [lo, hi) of row b.  All threads.
@@ -546,10 +593,16 @@ __device__ __forceinline__ uint64_t pkey(float p, uint32_t idx) {
 
 // Synchronisation policies: a whole workgroup (barriers) or one wave (LDS
 // traffic of a single wave completes in order; waiting for it suffices).
+// excl_scan(keep): this thread's position among the keeping threads of the
+// policy (in id order) and their total.
 struct BlockSync {
   static constexpr uint32_t N = NT;
   __device__ static __forceinline__ uint32_t id() { return threadIdx.x; }
   __device__ static __forceinline__ void sync() { __syncthreads(); }
+  __device__ static __forceinline__ uint32_t excl_scan(bool keep, LDS uint32_t* red,
+                                                       uint32_t& total) {
+    return block_excl_scan(keep ? 1u : 0u, red, total);
+  }
 };
 struct WaveSync {
   static constexpr uint32_t N = WAVE;
@@ -559,6 +612,12 @@ struct WaveSync {
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS ops done
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  __device__ static __forceinline__ uint32_t excl_scan(bool keep, LDS uint32_t*,
+                                                       uint32_t& total) {
+    const uint64_t mk = __ballot(keep);
+    total = (uint32_t)__popcll(mk);
+    return lanes_below(mk);
   }
 };
 
@@ -589,6 +648,7 @@ struct LdsList {
   LDS const float* p;
   LDS const uint32_t* idx;
   LDS float* stage;  // SORT_CAP floats
+  LDS float* pb;     // SORT_CAP floats: prefix sums of a window
   Chain c;
   __device__ uint32_t wmax() const { return SORT_CAP; }
   __device__ LDS const float* win(uint32_t j0, uint32_t n) const {
@@ -606,6 +666,7 @@ struct GlobList {
   const GLB float* p;
   const GLB uint32_t* idx;
   LDS float* stage;  // STAGE floats
+  LDS float* pb;     // STAGE floats: prefix sums of a window
   Chain c;
   __device__ uint32_t wmax() const { return STAGE; }
   __device__ LDS const float* win(uint32_t j0, uint32_t n) const {
@@ -618,7 +679,9 @@ struct GlobList {
   __device__ uint32_t id(uint32_t i) const { return idx[i]; }
 };
 
-// Sequential f32 scan of p[0..n) in order (the policy's thread 0 adds).
+// Sequential f32 scan of p[0..n) in order: the policy's thread 0 forms the
+// prefix sums ((p0 + p1) + p2) + ... window by window; for modes 1 and 2 all
+// threads then look for the first prefix meeting the condition.
 // mode 0: sum of all n.  mode 1: stop at the first j with cum >= thr.
 // mode 2: stop at the first j with thr <= cum (the draw's `r <= cumulative`).
 // Returns the stop index (n if none) and the cumulative including it.
@@ -629,37 +692,52 @@ __device__ __forceinline__ uint32_t seq_scan(const L& list, uint32_t n, int mode
   float cum = 0.0f;
   uint32_t stop = n;
   const uint32_t W = list.wmax();
+  LDS float* pb = list.pb;
   for (uint32_t j0 = 0; j0 < n; j0 += W) {
     const uint32_t cnt = (n - j0 < W) ? n - j0 : W;
     LDS const float* pw = list.win(j0, cnt);
     if (SY::id() == 0) {
-      uint32_t j = 0, hit = EMPTY;
-      for (; j + 8 <= cnt && hit == EMPTY; j += 8) {
-        const f4v lo4 = *(LDS const f4v*)(pw + j);
-        const f4v hi4 = *(LDS const f4v*)(pw + j + 4);
-        const float t[8] = {lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          if (hit != EMPTY) break;
-          cum += t[q];
-          if ((mode == 1 && cum >= thr) || (mode == 2 && thr <= cum)) hit = j + q;
+      float c = cum;
+      uint32_t j = 0;
+      for (; j + 8 <= cnt; j += 8) {
+        const f4v a4 = *(LDS const f4v*)(pw + j);
+        const f4v b4 = *(LDS const f4v*)(pw + j + 4);
+        const float t0 = c + a4.x, t1 = t0 + a4.y, t2 = t1 + a4.z, t3 = t2 + a4.w;
+        const float t4 = t3 + b4.x, t5 = t4 + b4.y, t6 = t5 + b4.z, t7 = t6 + b4.w;
+        if (mode != 0) {
+          *(LDS f4v*)(pb + j) = f4v{t0, t1, t2, t3};
+          *(LDS f4v*)(pb + j + 4) = f4v{t4, t5, t6, t7};
+        }
+        c = t7;
+      }
+      for (; j < cnt; ++j) {
+        c += pw[j];
+        if (mode != 0) pb[j] = c;
+      }
+      sh[0] = __float_as_uint(c);
+      sh[1] = EMPTY;
+    }
+    SY::sync();
+    const float wend = __uint_as_float(sh[0]);
+    if (mode != 0) {
+      for (uint32_t i = SY::id(); i < cnt; i += SY::N) {
+        const float c = pb[i];
+        if ((mode == 1 && c >= thr) || (mode == 2 && thr <= c)) {
+          __atomic_fetch_min(&sh[1], i, __ATOMIC_RELAXED);
+          break;
         }
       }
-      for (; j < cnt && hit == EMPTY; ++j) {
-        cum += pw[j];
-        if ((mode == 1 && cum >= thr) || (mode == 2 && thr <= cum)) hit = j;
-      }
-      sh[0] = __float_as_uint(cum);
-      sh[1] = hit;
+      SY::sync();
     }
-    SY::sync();
-    cum = __uint_as_float(sh[0]);
     const uint32_t hit = sh[1];
-    SY::sync();
     if (hit != EMPTY) {
+      cum = pb[hit];
       stop = j0 + hit;
+      SY::sync();
       break;
     }
+    cum = wend;
+    SY::sync();
   }
   cum_out = cum;
   return stop;
@@ -752,12 +830,151 @@ __device__ __forceinline__ void write_outputs(const Args& a, uint32_t b, uint32_
 }
 
 // ---------------------------------------------------------------------------
+// min-p / top-k / top-p / draw for a sorted list of at most 128 entries held
+// in registers of one wave: lane j holds entries j (p0, i0) and 64 + j (p1,
+// i1).  The same sequential f32 sums and divisions as run_semantics, in the
+// same order; the running sums are wave-uniform, each step reading one entry
+// with v_readlane.  Returns false if an entry beyond E = n would be needed.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float rl(float x, uint32_t j) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), (int)j));
+}
+// Every lane forms its own prefix: lane l of c0 receives ((p_0 + p_1) + ...)
+// + p_l and lane l of c1 the prefix through entry 64 + l -- the same f32
+// additions in the same order as one sequential sum.  z holds 64 zeros before
+// each half of the entries; lane l reads z[1 + l + t] at step t = 0..63, so it
+// adds 63 - l zeros (+0.0 + +0.0 stays +0.0) and then p_0..p_l.  Steps whose
+// reads are zeros for every lane below m are skipped.  Two operations per
+// entry (an LDS read and an add), no selects.  Lanes at or past m hold junk.
+__device__ __forceinline__ float prefix_half(LDS const float* zb, uint32_t m, float c) {
+  for (uint32_t t = (64u - m) & ~7u; t < 64u; t += 8) {
+    float x[8];
+#pragma unroll
+    for (uint32_t q = 0; q < 8; ++q) x[q] = zb[t + q];
+#pragma unroll
+    for (uint32_t q = 0; q < 8; ++q) c = c + x[q];
+  }
+  return c;
+}
+// z: 256 LDS words owned by the calling wave; 1 <= m <= 128.
+__device__ __forceinline__ void prefix_regs(float p0, float p1, uint32_t m, int lane,
+                                            LDS float* z, float& c0, float& c1) {
+  z[lane] = 0.0f;
+  z[64 + lane] = p0;
+  z[128 + lane] = 0.0f;
+  z[192 + lane] = p1;
+  WaveSync::sync();
+  c0 = prefix_half(z + 1 + lane, m < 64u ? m : 64u, 0.0f);
+  c1 = 0.0f;
+  if (m > 64u) c1 = prefix_half(z + 129 + lane, m - 64u, rl(c0, 63));
+  WaveSync::sync();  // z is rewritten by the next call
+}
+// ((p_0 + p_1) + ...) + p_{m-1}
+__device__ __forceinline__ float seq_sum_regs(float p0, float p1, uint32_t m, int lane,
+                                              LDS float* z) {
+  if (m == 0) return 0.0f;
+  float c0, c1;
+  prefix_regs(p0, p1, m, lane, z, c0, c1);
+  return m <= 64 ? rl(c0, m - 1) : rl(c1, m - 65);
+}
+// First j < m whose running sum meets the condition (mode 1: cum >= thr,
+// mode 2: thr <= cum), m if none; cum_out: the running sum there (or the
+// total).
+__device__ __forceinline__ uint32_t seq_find_regs(float p0, float p1, uint32_t m, int mode,
+                                                  float thr, int lane, LDS float* z,
+                                                  float& cum_out) {
+  if (m == 0) {
+    cum_out = 0.0f;
+    return 0;
+  }
+  float c0, c1;
+  prefix_regs(p0, p1, m, lane, z, c0, c1);
+  auto meets = [&](float x) { return mode == 1 ? x >= thr : thr <= x; };
+  const uint64_t m0 = __ballot((uint32_t)lane < m && meets(c0));
+  const uint64_t m1 = __ballot((uint32_t)lane + 64 < m && meets(c1));
+  uint32_t j = m;
+  if (m0) j = (uint32_t)__ffsll((unsigned long long)m0) - 1;
+  else if (m1) j = 64u + (uint32_t)__ffsll((unsigned long long)m1) - 1;
+  const uint32_t jc = j < m ? j : m - 1;
+  cum_out = jc < 64 ? rl(c0, jc) : rl(c1, jc - 64);
+  return j;
+}
+
+__device__ __forceinline__ bool semantics_regs(const RowP& P, float u, uint32_t n,
+                                               uint32_t full_len, float& p0, float& p1,
+                                               uint32_t i0, uint32_t i1, int lane,
+                                               LDS float* z, uint32_t& tok_out,
+                                               uint32_t& len_out) {
+  const uint32_t E = n;
+  uint32_t len = full_len;
+  bool trunc = E < full_len;
+  auto divide = [&](float s) {
+    if (s > 0.0f) {
+      p0 = p0 / s;
+      p1 = p1 / s;
+    }
+  };
+  // ---- min-p (extension): keep p >= min_p * p_max, renormalise if it cuts
+  if (P.min_p > 0.0f) {
+    if (E == 0) return false;
+    const float thr = P.min_p * rl(p0, 0);
+    const uint32_t lim = E < len ? E : len;
+    const uint64_t c0 = __ballot((uint32_t)lane < lim && p0 < thr);
+    const uint64_t c1 = __ballot((uint32_t)lane + 64 < lim && p1 < thr);
+    uint32_t cut = EMPTY;
+    if (c0) cut = (uint32_t)__ffsll((unsigned long long)c0) - 1;
+    else if (c1) cut = 64u + (uint32_t)__ffsll((unsigned long long)c1) - 1;
+    if (cut == EMPTY) {
+      if (trunc) return false;
+    } else if (cut < len) {
+      len = cut;
+      trunc = false;
+      divide(seq_sum_regs(p0, p1, len, lane, z));
+    }
+  }
+  // ---- top-k, sampler.rs:80-89
+  if (P.K > 0 && (uint32_t)P.K < len) {
+    if ((uint32_t)P.K > E) return false;
+    len = (uint32_t)P.K;
+    trunc = false;
+    divide(seq_sum_regs(p0, p1, len, lane, z));
+  }
+  // ---- top-p, sampler.rs:92-110
+  if (P.top_p < 1.0f) {
+    const uint32_t lim = (trunc && E < len) ? E : len;
+    float s;
+    const uint32_t j = seq_find_regs(p0, p1, lim, 1, P.top_p, lane, z, s);
+    if (j == lim && trunc) return false;
+    len = (j < lim) ? j + 1 : len;
+    trunc = false;
+    divide(s);
+  }
+  // ---- draw, sampler.rs:113-124
+  const uint32_t lim = (trunc && E < len) ? E : len;
+  float s;
+  const uint32_t j = seq_find_regs(p0, p1, lim, 2, u, lane, z, s);
+  uint32_t tok;
+  if (j < lim) tok = j < 64 ? (uint32_t)__builtin_amdgcn_readlane((int)i0, (int)j)
+                            : (uint32_t)__builtin_amdgcn_readlane((int)i1, (int)(j - 64));
+  else {
+    if (trunc) return false;
+    const uint32_t l1 = len - 1;
+    tok = len == 0 ? 0u
+                   : (l1 < 64 ? (uint32_t)__builtin_amdgcn_readlane((int)i0, (int)l1)
+                              : (uint32_t)__builtin_amdgcn_readlane((int)i1, (int)(l1 - 64)));
+  }
+  tok_out = tok;
+  len_out = len;
+  return true;
+}
+
+// ---------------------------------------------------------------------------
 // Shared-memory layouts (in 32-bit words)
 // ---------------------------------------------------------------------------
 enum : uint32_t { M_BETA = 0, M_CCOUNT = 1, M_FLAGS = 2, M_LAST = 3, M_NEXT = 4, M_NMISC = 16 };
 
 __host__ __device__ inline size_t stream_lds_words(uint32_t tps) {
-  return 64 + M_NMISC + MAX_CHUNKS + 16 + NBINS + 64 + hist_lds_words(tps * 32);
+  return 64 + M_NMISC + NBINS + 64 + ((tps * 32 + 3) & ~3u) + 2 * HSLOTS;
 }
 __host__ __device__ inline size_t finalize_lds_words() {
   // slots (2 x MAX_SLOTS) + keys + sorted keys (2 x SORT_CAP u64) + p + idx
@@ -765,7 +982,7 @@ __host__ __device__ inline size_t finalize_lds_words() {
   return 2 * MAX_SLOTS + 4 * SORT_CAP + 2 * SORT_CAP + 128 + MAX_SEG + 16 + 64 + 2 * MAX_SLOTS / 64;
 }
 __host__ __device__ inline size_t slow_lds_words(uint32_t V) {
-  return 128 + 256 + NW * 256 + 256 + STAGE + hist_lds_words((V + 31) / 32);
+  return 128 + 256 + NW * 256 + 256 + 2 * STAGE + hist_lds_words((V + 31) / 32);
 }
 
 // ---------------------------------------------------------------------------
@@ -783,8 +1000,8 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
   LDS uint32_t* digit_off = red + 64;        // 256
   LDS uint32_t* wcnt = digit_off + 256;      // NW*256
   LDS uint32_t* ttot = wcnt + NW * 256;      // 256
-  LDS float* stage = (LDS float*)(ttot + 256);   // STAGE
-  LDS uint32_t* hb = (LDS uint32_t*)(stage + STAGE);
+  LDS float* stage = (LDS float*)(ttot + 256);   // 2 x STAGE (window, prefixes)
+  LDS uint32_t* hb = (LDS uint32_t*)(stage + 2 * STAGE);
   const uint32_t nwords = (V + 31) / 32;
   Hist h;
   hist_carve(h, hb, nwords);
@@ -928,7 +1145,7 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
   if (tid == 0) __threadfence();
   __syncthreads();
   (void)lane;
-  GlobList<BlockSync> L{plist, ilist, stage, Chain{0.f, 0.f, 0.f, 0}};
+  GlobList<BlockSync> L{plist, ilist, stage, stage + STAGE, Chain{0.f, 0.f, 0.f, 0}};
   uint32_t tok = 0, len = 0;
   run_semantics<BlockSync>(P, G(a.u)[b], V, V, L, sh + 20, tok, len);
   wait_stores();
@@ -996,225 +1213,346 @@ __device__ __forceinline__ uint32_t kth_largest_key(LDS const float* cval, uint3
 }
 
 // ---------------------------------------------------------------------------
-// Finalize one row (the whole workgroup).  Partials and candidates are read
-// block-wide; the sequential semantics run in wave 0.  If the candidate path
-// cannot prove its result exact, the whole workgroup runs the slow path.
+// Finalize one row.  Wave 0 reduces the partials (normaliser S, maximum L)
+// and reads the segment table; the candidate path then runs in wave 0 when
+// the candidates are few, else in the whole workgroup; rows it cannot prove
+// exact take the slow path.
 // ---------------------------------------------------------------------------
-enum : uint32_t { F_DONE = 0, F_S = 1, F_M = 2, F_TOTAL = 3, F_LAM = 4, F_OVF = 5, F_SCR = 8 };
+enum : uint32_t {
+  F_DONE = 0, F_S = 1, F_M = 2, F_TOTAL = 3, F_LAM = 4, F_OVF = 5, F_L = 6, F_GREEDY = 7,
+  F_SCR = 8
+};
+// LDS layout of the finalize (words): slots, candidate lists, keys, tables
+struct FinLds {
+  LDS float* tl;        // MAX_SLOTS: slot maxima
+  LDS float* ts;        // MAX_SLOTS: slot sums (or first argmax)
+  LDS uint64_t* keys;   // SORT_CAP
+  LDS uint64_t* skeys;  // SORT_CAP (sorted)
+  LDS float* pp;        // SORT_CAP
+  LDS uint32_t* pidx;   // SORT_CAP
+  LDS uint32_t* fm;     // 128
+  LDS uint32_t* soff;   // MAX_SEG + 16
+  LDS uint32_t* red;    // 64
+};
+__device__ __forceinline__ FinLds fin_carve(LDS uint32_t* smem) {
+  FinLds f;
+  f.tl = (LDS float*)smem;
+  f.ts = f.tl + MAX_SLOTS;
+  f.keys = (LDS uint64_t*)(smem + 2 * MAX_SLOTS);
+  f.skeys = f.keys + SORT_CAP;
+  f.pp = (LDS float*)(f.skeys + SORT_CAP);
+  f.pidx = (LDS uint32_t*)(f.pp + SORT_CAP);
+  f.fm = f.pidx + SORT_CAP;
+  f.soff = f.fm + 128;
+  f.red = f.soff + MAX_SEG + 16;
+  return f;
+}
+constexpr uint32_t WAVE_GATHER = 512;  // candidates the wave path reads
+constexpr uint32_t WAVE_KEEP = 256;    // candidates the wave path sorts
 
-template <int DT>
-__device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_t b,
-                                             const RowP& P, bool have_vt, LDS uint32_t* smem) {
-  const uint32_t tid = threadIdx.x;
-  const int lane = (int)(tid & 63), wv = (int)(tid >> 6);
-  LDS float* tl = (LDS float*)smem;                              // MAX_SLOTS
-  LDS float* ts = tl + MAX_SLOTS;                                // MAX_SLOTS
-  LDS uint64_t* keys = (LDS uint64_t*)(smem + 2 * MAX_SLOTS);    // SORT_CAP
-  LDS uint64_t* skeys = keys + SORT_CAP;                         // SORT_CAP (sorted)
-  LDS float* pp = (LDS float*)(skeys + SORT_CAP);                // SORT_CAP
-  LDS uint32_t* pidx = (LDS uint32_t*)(pp + SORT_CAP);           // SORT_CAP
-  LDS uint32_t* fm = pidx + SORT_CAP;                            // 128
-  LDS uint32_t* soff = fm + 128;                                 // MAX_SEG + 1
-  LDS uint32_t* red = soff + MAX_SEG + 16;                       // 64
-  LDS float* blk = (LDS float*)(red + 64);                       // 2 * MAX_SLOTS / 64
-  const uint32_t nslots = a.ntiles + (have_vt ? a.nchunks : 0u);
-  const GLB f2v* part = G(w.tile_part) + (uint64_t)b * MAX_SLOTS;
-
-  // ---- partials into LDS; row maximum L
-  float L = NEG_INF;
-  for (uint32_t c = tid; c < nslots; c += NT) {
-    const f2v q = part[c];
-    tl[c] = q.x;
-    ts[c] = q.y;
-    L = fmaxf(L, q.x);
-  }
-  L = block_max(L, (LDS float*)red);
-  if (P.mode == MODE_GREEDY) {
-    // sampler.rs:40-50: the first index holding the maximum.
-    uint32_t bi = EMPTY;
-    for (uint32_t c = tid; c < nslots; c += NT)
-      if (tl[c] == L) bi = umin(bi, __float_as_uint(ts[c]));
-    bi = block_min_u32(bi, red);
-    if (bi == EMPTY) bi = 0;
-    if (tid == 0) {
-      G(a.out_tok)[b] = bi;
-      if (a.out_cnt) G(a.out_cnt)[b] = 1;
-      if (a.out_cap) {
-        if (a.out_ids) G(a.out_ids)[(uint64_t)b * a.out_cap] = bi;
-        if (a.out_probs) G(a.out_probs)[(uint64_t)b * a.out_cap] = 1.0f;
-      }
+// Ascending sort of keys[0..n) into skeys[0..n) (keys distinct).
+template <class SY>
+__device__ __forceinline__ void sort_keys(const FinLds& f, uint32_t n) {
+  if (n <= 4 * SY::N && (SY::N == WAVE || n <= SY::N)) {
+    // rank sort: up to 4 keys per thread, every key read once per thread
+    const uint32_t i0 = SY::id();
+    uint64_t k[4];
+    uint32_t r[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      k[q] = (i0 + q * SY::N < n) ? f.keys[i0 + q * SY::N] : ~0ull;
+      r[q] = 0;
     }
+    uint32_t j = 0;
+    for (; j + 8 <= n; j += 8) {  // eight independent reads per step
+      uint64_t x[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = f.keys[j + e];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) r[q] += (x[e] < k[q]) ? 1u : 0u;
+    }
+    for (; j < n; ++j) {
+      const uint64_t x = f.keys[j];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) r[q] += (x < k[q]) ? 1u : 0u;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (i0 + q * SY::N < n) f.skeys[r[q]] = k[q];
+    SY::sync();
     return;
   }
+  uint32_t npad = 1;
+  while (npad < n) npad <<= 1;
+  for (uint32_t i = SY::id(); i < npad; i += SY::N) f.skeys[i] = i < n ? f.keys[i] : ~0ull;
+  SY::sync();
+  for (uint32_t k = 2; k <= npad; k <<= 1)
+    for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+      for (uint32_t i = SY::id(); i < npad / 2; i += SY::N) {
+        const uint32_t lo = ((i & ~(j - 1)) << 1) | (i & (j - 1));
+        const uint32_t hi = lo | j;
+        const uint64_t x = f.skeys[lo], y = f.skeys[hi];
+        const bool up = (lo & k) == 0;
+        if ((x > y) == up) {
+          f.skeys[lo] = y;
+          f.skeys[hi] = x;
+        }
+      }
+      SY::sync();
+    }
+}
 
-  // ---- normaliser S: balanced tree over max(64, next_pow2(nslots)) slots,
-  // as trees of 64 slots (one per wave) and a tree over those
-  const float c2 = LOG2E_F / P.T;
-  uint32_t ntp = 64;
-  while (ntp < nslots) ntp <<= 1;
-  const uint32_t nblk = ntp / 64;
-  for (uint32_t k = (uint32_t)wv; k < nblk; k += NW) {
-    const uint32_t c = 64 * k + (uint32_t)lane;
-    float x = 0.0f;
-    if (c < nslots && L != NEG_INF) x = ts[c] * exp2_f((tl[c] - L) * c2);
-    x = wave_tree_sum(x);
-    if (lane == 0) blk[k] = x;
-  }
-  // ---- segment table (wave 0): counts, thresholds, flags
-  if (wv == 0) {
-    uint32_t cnt = 0, beta = 0, flg = 0;
-    if ((uint32_t)lane < a.G) {
-      const u4v sm = G(w.seg_meta)[row_seg_to_wg(a, b, (uint32_t)lane)];
-      cnt = sm.x < CAND_CAP ? sm.x : CAND_CAP;
-      beta = sm.y;
-      flg = sm.z;
-    }
-    const uint32_t lam = wave_max_u32(beta << BIN_SHIFT);
-    const bool ovf = __ballot((flg & FLAG_OVERFLOW) != 0) != 0;
-    const uint32_t off_incl = wave_incl_scan(cnt);
-    if ((uint32_t)lane <= a.G) soff[lane] = off_incl - cnt;  // lane G: the total
-    if (lane == 0) {
-      fm[F_TOTAL] = bcast63u(off_incl);
-      fm[F_LAM] = lam;
-      fm[F_OVF] = ovf ? 1u : 0u;
-    }
-  }
-  __syncthreads();
-  float S = 0.0f;
-  {
-    float x = ((uint32_t)lane < nblk) ? blk[lane] : 0.0f;
-    x = wave_tree_sum(x);
-    S = (L != NEG_INF) ? x : 0.0f;
-  }
-  const float m = (P.T != 1.0f) ? L / P.T : L;
-  const uint32_t total = fm[F_TOTAL], lam = fm[F_LAM];
-  bool ok = !(L == NEG_INF || P.Kc == 0 || fm[F_OVF] != 0);
-  uint32_t done = 0;
-  if (ok) {
-    // ---- gather the candidates at or above lam: every element not in the
-    // candidate buffers has a key below lam
-    LDS float* cval = pp;
-    LDS uint32_t* cidx = pidx;
-    uint32_t n0 = 0;
-    for (uint32_t i0 = 0; i0 < total; i0 += NT) {
-      const uint32_t i = i0 + tid;
-      float v = NEG_INF;
-      uint32_t ix = 0;
-      if (i < total) {
+// The candidate path under policy SY.  Returns 0 when the row is done, 1
+// when its candidates exceed what SY handles, 2 when it needs the slow path.
+template <class SY>
+__device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, uint32_t b,
+                                                   const RowP& P, float S, float m, float u,
+                                                   uint32_t total, uint32_t lam,
+                                                   const FinLds& f, uint32_t gather_cap,
+                                                   uint32_t keep_cap) {
+  LDS const u2v* lcand = (LDS const u2v*)((LDS uint32_t*)f.tl + a.lds_cand);
+  const uint32_t id = SY::id();
+  // ---- gather the candidates at or above lam: every element not in the
+  // candidate buffers has a key below lam
+  LDS float* cval = f.pp;
+  LDS uint32_t* cidx = f.pidx;
+  if (total > gather_cap) return 1;
+  uint32_t n0 = 0;
+  constexpr int GQ = 8;  // candidate loads in flight per thread
+  for (uint32_t i0 = 0; i0 < total; i0 += GQ * SY::N) {
+    u2v e[GQ];
+#pragma unroll
+    for (int q = 0; q < GQ; ++q) {
+      const uint32_t i = i0 + q * SY::N + id;
+      e[q] = u2v{0xff800000u, 0u};
+      if (i < total && a.G == 1 && i < LCAP) {
+        e[q] = lcand[i];
+      } else if (i < total) {
         uint32_t lo = 0, hi = a.G;  // soff[lo] <= i < soff[hi]
         while (hi - lo > 1) {
           const uint32_t mid = (lo + hi) >> 1;
-          if (soff[mid] <= i) lo = mid;
+          if (f.soff[mid] <= i) lo = mid;
           else hi = mid;
         }
-        const u2v e = G(w.cand)[(uint64_t)row_seg_to_wg(a, b, lo) * CAND_CAP + (i - soff[lo])];
-        v = __uint_as_float(e.x);
-        ix = e.y;
+        e[q] = G(w.cand)[(uint64_t)row_seg_to_wg(a, b, lo) * CAND_CAP + (i - f.soff[lo])];
       }
+    }
+#pragma unroll
+    for (int q = 0; q < GQ; ++q) {
+      if (i0 + q * SY::N >= total) break;
+      const float v = __uint_as_float(e[q].x);
       const bool keep = v > NEG_INF && fkey(v) >= lam;
       uint32_t tot;
-      const uint32_t pos = n0 + block_excl_scan(keep ? 1u : 0u, red, tot);
+      const uint32_t pos = n0 + SY::excl_scan(keep, f.red, tot);
       if (keep && pos < SORT_CAP) {
         cval[pos] = v;
-        cidx[pos] = ix;
+        cidx[pos] = e[q].y;
       }
       n0 += tot;
     }
-    if (n0 > SORT_CAP) ok = false;
-    __syncthreads();
-    if (ok) {
-      // ---- top-k rows: the exact K-th largest candidate logit tightens the
-      // bound (every element below it has p <= plim of that bound)
-      const bool topk = P.K > 0 && (uint32_t)P.K < a.V;
-      const float plim = lam > 0x007fffffu ? prob_of(funkey(lam - 1), P.T, m, S) : 0.0f;
-      uint32_t lam_e = lam;
-      float plim_e = plim;
-      if (topk && n0 > 2u * (uint32_t)P.K) {
-        const uint32_t tau = kth_largest_key<BlockSync>(cval, n0, (uint32_t)P.K,
-                                                        (LDS uint32_t*)keys, fm + F_SCR);
-        lam_e = tau;
-        plim_e = tau > 0x007fffffu ? prob_of(funkey(tau - 1), P.T, m, S) : 0.0f;
-      }
-      uint32_t n = 0;
-      for (int attempt = 0; attempt < 2; ++attempt) {
-        n = 0;
-        for (uint32_t i0 = 0; i0 < n0; i0 += NT) {
-          const uint32_t i = i0 + tid;
-          bool keep = false;
-          uint64_t key = 0;
-          if (i < n0) {
-            const float v = cval[i];
-            if (fkey(v) >= lam_e) {
-              const float pv = prob_of(v, P.T, m, S);
-              if (pv > plim_e) {
-                keep = true;
-                key = pkey(pv, cidx[i]);
-              }
-            }
+  }
+  SY::sync();
+  if (n0 > SORT_CAP) return 2;
+  // ---- top-k rows: the exact K-th largest candidate logit tightens the
+  // bound (every element below it has p <= plim of that bound)
+  const bool topk = P.K > 0 && (uint32_t)P.K < a.V;
+  const float plim = lam > 0x007fffffu ? prob_of(funkey(lam - 1), P.T, m, S) : 0.0f;
+  uint32_t lam_e = lam;
+  float plim_e = plim;
+  if (topk && n0 > 2u * (uint32_t)P.K) {
+    const uint32_t tau = kth_largest_key<SY>(cval, n0, (uint32_t)P.K,
+                                             (LDS uint32_t*)f.keys, f.fm + F_SCR);
+    lam_e = tau;
+    plim_e = tau > 0x007fffffu ? prob_of(funkey(tau - 1), P.T, m, S) : 0.0f;
+  }
+  uint32_t n = 0;
+  for (int attempt = 0; attempt < 2; ++attempt) {
+    n = 0;
+    for (uint32_t i0 = 0; i0 < n0; i0 += SY::N) {
+      const uint32_t i = i0 + id;
+      bool keep = false;
+      uint64_t key = 0;
+      if (i < n0) {
+        const float v = cval[i];
+        if (fkey(v) >= lam_e) {
+          const float pv = prob_of(v, P.T, m, S);
+          if (pv > plim_e) {
+            keep = true;
+            key = pkey(pv, cidx[i]);
           }
-          uint32_t tot;
-          const uint32_t pos = n + block_excl_scan(keep ? 1u : 0u, red, tot);
-          if (keep) keys[pos] = key;
-          n += tot;
         }
-        // a tightened bound that keeps fewer than K (ties in p across it)
-        // falls back to the gather bound
-        if (!(topk && n < (uint32_t)P.K && lam_e != lam)) break;
-        lam_e = lam;
-        plim_e = plim;
       }
-      __syncthreads();
-      // ---- sort ascending by key; keys are distinct (indices differ)
-      if (n <= (uint32_t)NT) {
-        if (tid < n) {
-          const uint64_t k = keys[tid];
-          uint32_t r = 0;
-          for (uint32_t j = 0; j < n; ++j) r += (keys[j] < k) ? 1u : 0u;
-          skeys[r] = k;
-        }
-      } else {
-        uint32_t npad = 1;
-        while (npad < n) npad <<= 1;
-        for (uint32_t i = tid; i < npad; i += NT) skeys[i] = i < n ? keys[i] : ~0ull;
-        __syncthreads();
-        for (uint32_t k = 2; k <= npad; k <<= 1)
-          for (uint32_t j = k >> 1; j > 0; j >>= 1) {
-            for (uint32_t i = tid; i < npad / 2; i += NT) {
-              const uint32_t lo = ((i & ~(j - 1)) << 1) | (i & (j - 1));
-              const uint32_t hi = lo | j;
-              const uint64_t x = skeys[lo], y = skeys[hi];
-              const bool up = (lo & k) == 0;
-              if ((x > y) == up) {
-                skeys[lo] = y;
-                skeys[hi] = x;
-              }
-            }
-            __syncthreads();
-          }
-      }
-      __syncthreads();
-      for (uint32_t i = tid; i < n; i += NT) {
-        const uint64_t k = skeys[i];
-        pp[i] = __uint_as_float(~(uint32_t)(k >> 32));
-        pidx[i] = (uint32_t)k;
-      }
-      __syncthreads();
-      // ---- min-p / top-k / top-p / draw in wave 0
-      if (wv == 0) {
-        using SY = WaveSync;
-        LdsList<SY> Ls{pp, pidx, (LDS float*)keys, Chain{0.f, 0.f, 0.f, 0}};
-        uint32_t tok = 0, len = 0;
-        bool good = run_semantics<SY>(P, G(a.u)[b], n, a.V, Ls, fm + F_SCR, tok, len);
-        if (good && a.out_cap && len > n && a.out_cap > n) good = false;
-        if (good) write_outputs<SY>(a, b, tok, len, Ls);
-        if (lane == 0) fm[F_DONE] = good ? 1u : 0u;
-      }
-      __syncthreads();
-      done = fm[F_DONE];
+      uint32_t tot;
+      const uint32_t pos = n + SY::excl_scan(keep, f.red, tot);
+      if (keep) f.keys[pos] = key;
+      n += tot;
     }
+    // a tightened bound that keeps fewer than K (ties in p across it) falls
+    // back to the gather bound
+    if (!(topk && n < (uint32_t)P.K && lam_e != lam)) break;
+    lam_e = lam;
+    plim_e = plim;
+  }
+  SY::sync();
+  if (n > keep_cap) return 1;
+  sort_keys<SY>(f, n);
+  for (uint32_t i = id; i < n; i += SY::N) {
+    const uint64_t k = f.skeys[i];
+    f.pp[i] = __uint_as_float(~(uint32_t)(k >> 32));
+    f.pidx[i] = (uint32_t)k;
+  }
+  SY::sync();
+  // ---- min-p / top-k / top-p / draw in wave 0
+  uint32_t res = 2;
+  if (n <= 128) {
+    if (threadIdx.x < WAVE) {
+      const int lane = (int)threadIdx.x;
+      float p0 = (uint32_t)lane < n ? f.pp[lane] : 0.0f;
+      float p1 = (uint32_t)lane + 64 < n ? f.pp[64 + lane] : 0.0f;
+      const uint32_t i0 = (uint32_t)lane < n ? f.pidx[lane] : 0u;
+      const uint32_t i1 = (uint32_t)lane + 64 < n ? f.pidx[64 + lane] : 0u;
+      uint32_t tok = 0, len = 0;
+      // f.keys is free once sorted into skeys and copied out
+      bool good = semantics_regs(P, u, n, a.V, p0, p1, i0, i1, lane, (LDS float*)f.keys, tok,
+                                 len);
+      if (good && a.out_cap && len > n && a.out_cap > n) good = false;
+      if (good) {
+        if (lane == 0) {
+          G(a.out_tok)[b] = tok;
+          if (a.out_cnt) G(a.out_cnt)[b] = len;
+        }
+        const uint32_t no = len < a.out_cap ? len : a.out_cap;
+        const uint64_t ob = (uint64_t)b * a.out_cap;
+        if ((uint32_t)lane < no) {
+          if (a.out_ids) G(a.out_ids)[ob + lane] = i0;
+          if (a.out_probs) G(a.out_probs)[ob + lane] = p0;
+        }
+        if ((uint32_t)lane + 64 < no) {
+          if (a.out_ids) G(a.out_ids)[ob + 64 + lane] = i1;
+          if (a.out_probs) G(a.out_probs)[ob + 64 + lane] = p1;
+        }
+      }
+      res = good ? 0u : 2u;
+    }
+  } else if (threadIdx.x < WAVE) {
+    using WS = WaveSync;
+    LdsList<WS> Ls{f.pp, f.pidx, (LDS float*)f.keys, (LDS float*)f.skeys,
+                   Chain{0.f, 0.f, 0.f, 0}};
+    uint32_t tok = 0, len = 0;
+    bool good = run_semantics<WS>(P, u, n, a.V, Ls, f.fm + F_SCR, tok, len);
+    if (good && a.out_cap && len > n && a.out_cap > n) good = false;
+    if (good) write_outputs<WS>(a, b, tok, len, Ls);
+    res = good ? 0u : 2u;
+  }
+  if (SY::N > WAVE) {
+    if (threadIdx.x == 0) f.fm[F_DONE] = res;
+    SY::sync();
+    res = f.fm[F_DONE];
+  }
+  return res;
+}
+
+// seg_own: for a single-segment row, this workgroup's (count, beta, flags).
+template <int DT>
+__device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_t b,
+                                             const RowP& P, bool have_vt, u4v seg_own,
+                                             LDS uint32_t* smem) {
+  const uint32_t tid = threadIdx.x;
+  const int lane = (int)(tid & 63), wv = (int)(tid >> 6);
+  const FinLds f = fin_carve(smem);
+  const uint32_t nslots = a.ntiles + (have_vt ? a.nchunks : 0u);
+  uint32_t path = 2;  // 0 done, 1 workgroup candidate path, 2 slow path
+  const float u = G(a.u)[b];
+  if (wv == 0) {
+    // ---- partials: row maximum L, then the normaliser S as balanced trees
+    // of 64 slots and a tree over those (next_pow2(slots) >= 64, padding 0)
+    const GLB f2v* part = G(w.tile_part) + (uint64_t)b * MAX_SLOTS;
+    LDS const f2v* lpart = (LDS const f2v*)(smem + a.lds_part);
+    float L = NEG_INF;
+    for (uint32_t c = (uint32_t)lane; c < nslots; c += WAVE) {
+      const f2v q = a.G == 1 ? lpart[c] : part[c];
+      f.tl[c] = q.x;
+      f.ts[c] = q.y;
+      L = fmaxf(L, q.x);
+    }
+    L = wave_max(L);
+    WaveSync::sync();
+    if (P.mode == MODE_GREEDY) {
+      // sampler.rs:40-50: the first index holding the maximum
+      uint32_t bi = EMPTY;
+      for (uint32_t c = (uint32_t)lane; c < nslots; c += WAVE)
+        if (f.tl[c] == L) bi = umin(bi, __float_as_uint(f.ts[c]));
+      bi = wave_min_u32(bi);
+      if (bi == EMPTY) bi = 0;
+      if (lane == 0) {
+        G(a.out_tok)[b] = bi;
+        if (a.out_cnt) G(a.out_cnt)[b] = 1;
+        if (a.out_cap) {
+          if (a.out_ids) G(a.out_ids)[(uint64_t)b * a.out_cap] = bi;
+          if (a.out_probs) G(a.out_probs)[(uint64_t)b * a.out_cap] = 1.0f;
+        }
+      }
+      path = 0;
+    } else {
+      const float c2 = LOG2E_F / P.T;
+      uint32_t ntp = 64;
+      while (ntp < nslots) ntp <<= 1;
+      const uint32_t nblk = ntp / 64;
+      float bsum = 0.0f;  // lane k: the tree of block k
+      for (uint32_t k = 0; k < nblk; ++k) {
+        const uint32_t c = 64 * k + (uint32_t)lane;
+        float x = 0.0f;
+        if (c < nslots && L != NEG_INF) x = f.ts[c] * exp2_f((f.tl[c] - L) * c2);
+        x = wave_tree_sum(x);
+        if ((uint32_t)lane == k) bsum = x;
+      }
+      const float S = (L != NEG_INF) ? wave_tree_sum(bsum) : 0.0f;
+      const float m = (P.T != 1.0f) ? L / P.T : L;
+      // ---- segment table: counts, thresholds, flags
+      uint32_t cnt = 0, beta = 0, flg = 0;
+      if (a.G == 1) {
+        if (lane == 0) {
+          cnt = seg_own.x < CAND_CAP ? seg_own.x : CAND_CAP;
+          beta = seg_own.y;
+          flg = seg_own.z;
+        }
+      } else if ((uint32_t)lane < a.G) {
+        const u4v sm = G(w.seg_meta)[row_seg_to_wg(a, b, (uint32_t)lane)];
+        cnt = sm.x < CAND_CAP ? sm.x : CAND_CAP;
+        beta = sm.y;
+        flg = sm.z;
+      }
+      const uint32_t lam = wave_max_u32(beta << BIN_SHIFT);
+      const bool ovf = __ballot((flg & FLAG_OVERFLOW) != 0) != 0;
+      const uint32_t off_incl = wave_incl_scan(cnt);
+      const uint32_t total = bcast63u(off_incl);
+      if ((uint32_t)lane <= a.G) f.soff[lane] = off_incl - cnt;  // lane G: the total
+      WaveSync::sync();
+      if (lane == 0) {
+        f.fm[F_S] = __float_as_uint(S);
+        f.fm[F_M] = __float_as_uint(m);
+        f.fm[F_TOTAL] = total;
+        f.fm[F_LAM] = lam;
+      }
+      if (!(L == NEG_INF || P.Kc == 0 || ovf))
+        path = candidate_path<WaveSync>(a, w, b, P, S, m, u, total, lam, f, WAVE_GATHER, WAVE_KEEP);
+    }
+    if (lane == 0) f.fm[F_DONE] = path;
   }
   __syncthreads();
-  if (!done) slow_row<DT>(a, w, b, P, S, m, smem);
+  path = f.fm[F_DONE];
+  if (path == 0) return;
+  const float S = __uint_as_float(f.fm[F_S]), m = __uint_as_float(f.fm[F_M]);
+  if (path == 1) {
+    const uint32_t total = f.fm[F_TOTAL], lam = f.fm[F_LAM];
+    __syncthreads();
+    path = candidate_path<BlockSync>(a, w, b, P, S, m, u, total, lam, f, EMPTY, SORT_CAP);
+    if (path == 0) return;
+  }
+  __syncthreads();
+  slow_row<DT>(a, w, b, P, S, m, smem);
 }
 
 // ---------------------------------------------------------------------------
@@ -1231,7 +1569,17 @@ struct TileEnv {
   LDS uint32_t* hcoarse;
   GLB u2v* cbuf;
   GLB f2v* part;
+  LDS f2v* lpart;  // non-null for a single-segment row: partials kept in LDS
+  LDS u2v* lcand;  //   and its first LCAP candidates
 };
+__device__ __forceinline__ void put_part(const TileEnv& E, uint32_t slot, f2v x) {
+  if (E.lpart) E.lpart[slot] = x;
+  else E.part[slot] = x;
+}
+__device__ __forceinline__ void put_cand(const TileEnv& E, uint32_t pos, u2v x) {
+  if (E.lcand && pos < LCAP) E.lcand[pos] = x;
+  else E.cbuf[pos] = x;
+}
 
 // v[j], j = 4r + q: the lane's values at tile positions 256r + 4*lane + q,
 // excluded positions already -inf.  idx(j): the vocabulary index of value j
@@ -1264,7 +1612,7 @@ __device__ __forceinline__ void tile_reduce(const TileEnv& E, const float (&v)[1
       }
     }
     bi = wave_min_u32(bi);
-    if (lane == 0) E.part[slot] = f2v{lm, __uint_as_float(bi)};
+    if (lane == 0) put_part(E, slot, f2v{lm, __uint_as_float(bi)});
     return;
   }
   float s = 0.0f;
@@ -1287,7 +1635,7 @@ __device__ __forceinline__ void tile_reduce(const TileEnv& E, const float (&v)[1
     }
     s = wave_tree_sum((sr[0] + sr[1]) + (sr[2] + sr[3]));
   }
-  if (lane == 0) E.part[slot] = f2v{lm, s};
+  if (lane == 0) put_part(E, slot, f2v{lm, s});
   if (!E.collect) return;
   // ---- candidates above the rising histogram threshold
   uint32_t beta = __atomic_load_n(&E.misc[M_BETA], __ATOMIC_RELAXED);
@@ -1316,9 +1664,13 @@ __device__ __forceinline__ void tile_reduce(const TileEnv& E, const float (&v)[1
     since = 0;
     counted = true;
   }
+  uint64_t mk[16];
   uint32_t npass = 0;
 #pragma unroll
-  for (int j = 0; j < 16; ++j) npass += (uint32_t)__popcll(__ballot(v[j] >= th));
+  for (int j = 0; j < 16; ++j) {
+    mk[j] = ((uint32_t)(j >> 2) < nr) ? __ballot(v[j] >= th) : 0ull;
+    npass += (uint32_t)__popcll(mk[j]);
+  }
   if (npass == 0) return;
   uint32_t base = 0;
   if (lane == 0) base = __atomic_fetch_add(&E.misc[M_CCOUNT], npass, __ATOMIC_RELAXED);
@@ -1330,17 +1682,16 @@ __device__ __forceinline__ void tile_reduce(const TileEnv& E, const float (&v)[1
   // append, and count what was appended in the histogram
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
-    const uint64_t mk = __ballot(v[j] >= th);
-    if (mk) {
-      if ((mk >> lane) & 1ull) {
+    if (mk[j]) {
+      if (v[j] >= th) {
         if (!counted) {
           const uint32_t bin = fkey(v[j]) >> BIN_SHIFT;
           __atomic_fetch_add(&E.hf[bin], 1u, __ATOMIC_RELAXED);
           __atomic_fetch_add(&E.hcoarse[bin >> (CBIN_SHIFT - BIN_SHIFT)], 1u, __ATOMIC_RELAXED);
         }
-        E.cbuf[base + lanes_below(mk)] = u2v{__float_as_uint(v[j]), idx(j)};
+        put_cand(E, base + lanes_below(mk[j]), u2v{__float_as_uint(v[j]), idx(j)});
       }
-      base += (uint32_t)__popcll(mk);
+      base += (uint32_t)__popcll(mk[j]);
     }
   }
   if (counted) return;
@@ -1355,8 +1706,9 @@ __device__ __forceinline__ void tile_reduce(const TileEnv& E, const float (&v)[1
 // Sets v to -inf where bit (sh + q) of x is set (x: one exclusion word).
 __device__ __forceinline__ float exclude(float v, uint32_t x, uint32_t pos) {
   const uint32_t m = (uint32_t)__builtin_amdgcn_sbfe((int)x, pos, 1);
-  const uint32_t bits = __float_as_uint(v);
-  return __uint_as_float(bits ^ ((bits ^ 0xff800000u) & m));
+  uint32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(m), "v"(0xff800000u), "v"(__float_as_uint(v)));
+  return __uint_as_float(r);
 }
 
 // ---------------------------------------------------------------------------
@@ -1385,14 +1737,13 @@ __device__ __forceinline__ uint32_t pop_lowest(uint32_t (&wd)[8]) {
 template <int DT>
 __device__ __forceinline__ void vt_batch(const Args& a, const RowP& P, const void* row,
                                          const GLB uint32_t* mrow, uint32_t base_tok,
-                                         uint32_t (&wd)[8], bool need_cnt, uint32_t rank0,
-                                         LDS const uint32_t* cnt, uint32_t (&tk)[VB],
-                                         float (&v)[VB]) {
+                                         uint32_t (&wd)[8], bool need_cnt, const Hist& h,
+                                         uint32_t nround, uint32_t (&tk)[VB], float (&v)[VB]) {
   float x[VB];
   uint32_t mw[VB];
 #pragma unroll
   for (int i = 0; i < VB; ++i) {
-    const uint32_t pos = pop_lowest(wd);
+    const uint32_t pos = (uint32_t)i < nround ? pop_lowest(wd) : EMPTY;  // nround: wave-uniform
     tk[i] = pos == EMPTY ? EMPTY : base_tok + pos;
     x[i] = pos == EMPTY ? 0.0f : load_logit<DT>(row, tk[i]);
     mw[i] = (pos != EMPTY && mrow) ? mrow[tk[i] >> 5] : 0xffffffffu;
@@ -1401,9 +1752,8 @@ __device__ __forceinline__ void vt_batch(const Args& a, const RowP& P, const voi
   for (int i = 0; i < VB; ++i) {
     float y = NEG_INF;
     if (tk[i] != EMPTY) {
-      const uint32_t r = rank0 + (uint32_t)i;
       y = (x[i] > NEG_INF) ? x[i] : NEG_INF;  // NaN acts as -inf
-      y = penalize(y, P, (need_cnt && r < U_MAX) ? cnt[r] : 1u);
+      y = penalize(y, P, need_cnt ? hash_count(h, tk[i]) : 1u);
       if (!((mw[i] >> (tk[i] & 31)) & 1u)) y = NEG_INF;
     }
     v[i] = y;
@@ -1414,8 +1764,7 @@ template <int DT>
 __device__ __forceinline__ void vtile_chunk(const Args& a, const RowP& P, uint32_t b,
                                          const void* row, uint32_t t0, uint32_t lo,
                                          uint32_t nwords, uint32_t kk, const Hist& h,
-                                         LDS const uint32_t* cst, bool need_cnt,
-                                         const TileEnv& E, uint32_t& since, int lane) {
+                                         bool need_cnt, const TileEnv& E, int lane) {
   const uint32_t wb = 512u * kk + 8u * (uint32_t)lane;
   uint32_t w0[8];
 #pragma unroll
@@ -1430,12 +1779,13 @@ __device__ __forceinline__ void vtile_chunk(const Args& a, const RowP& P, uint32
   uint32_t n = 0;
 #pragma unroll
   for (int j = 0; j < 8; ++j) n += __popc(w0[j]);
-  const uint32_t rank_lane = need_cnt ? cst[kk] + wave_incl_scan(n) - n : 0u;
-  const uint32_t nb_max = (wave_max_u32(n) + VB - 1) / VB;  // batches
+  const uint32_t n_max = wave_max_u32(n);
+  const uint32_t nb_max = (n_max + VB - 1) / VB;  // batches
+  // rounds of batch bt: the most tokens any lane still has, at most VB
+#define NROUND(bt) (n_max - (bt) * VB < VB ? n_max - (bt) * VB : (uint32_t)VB)
   const uint32_t base_tok = lo + 32u * wb;
   const uint32_t slot = a.ntiles + t0 / CHUNK_TILES + kk;
   const GLB uint32_t* mrow = a.mask ? G(a.mask) + (uint64_t)b * a.mask_words : nullptr;
-  LDS const uint32_t* cnt = (LDS const uint32_t*)h.pen;
   const bool greedy = E.P.mode == MODE_GREEDY;
   // pass 1: the chunk's maximum (and, for greedy rows, its first index)
   uint32_t wd[8];
@@ -1445,7 +1795,7 @@ __device__ __forceinline__ void vtile_chunk(const Args& a, const RowP& P, uint32
   for (int j = 0; j < 8; ++j) wd[j] = w0[j];
   float lm = NEG_INF;
   for (uint32_t bt = 0; bt < nb_max; ++bt) {
-    vt_batch<DT>(a, P, row, mrow, base_tok, wd, need_cnt, rank_lane + bt * VB, cnt, tk, v);
+    vt_batch<DT>(a, P, row, mrow, base_tok, wd, need_cnt, h, NROUND(bt), tk, v);
 #pragma unroll
     for (int i = 0; i < VB; ++i) lm = fmaxf(lm, v[i]);
   }
@@ -1456,7 +1806,7 @@ __device__ __forceinline__ void vtile_chunk(const Args& a, const RowP& P, uint32
     for (int j = 0; j < 8; ++j) wd[j] = w0[j];
     for (uint32_t bt = 0; bt < nb_max; ++bt) {
       if (nb_max > 1)
-        vt_batch<DT>(a, P, row, mrow, base_tok, wd, need_cnt, rank_lane + bt * VB, cnt, tk, v);
+        vt_batch<DT>(a, P, row, mrow, base_tok, wd, need_cnt, h, NROUND(bt), tk, v);
 #pragma unroll
       for (int i = 0; i < VB; ++i) {
         const bool hit = tk[i] != EMPTY && ((v[i] == lm) || (lm == NEG_INF && !(v[i] > NEG_INF)));
@@ -1464,7 +1814,7 @@ __device__ __forceinline__ void vtile_chunk(const Args& a, const RowP& P, uint32
       }
     }
     bi = wave_min_u32(bi);
-    if (lane == 0) E.part[slot] = f2v{lm, __uint_as_float(bi)};
+    if (lane == 0) put_part(E, slot, f2v{lm, __uint_as_float(bi)});
     return;
   }
   float s = 0.0f;
@@ -1475,14 +1825,14 @@ __device__ __forceinline__ void vtile_chunk(const Args& a, const RowP& P, uint32
     for (int j = 0; j < 8; ++j) wd[j] = w0[j];
     for (uint32_t bt = 0; bt < nb_max; ++bt) {
       if (nb_max > 1)
-        vt_batch<DT>(a, P, row, mrow, base_tok, wd, need_cnt, rank_lane + bt * VB, cnt, tk, v);
+        vt_batch<DT>(a, P, row, mrow, base_tok, wd, need_cnt, h, NROUND(bt), tk, v);
 #pragma unroll
       for (int i = 0; i < VB; ++i)
         if (tk[i] != EMPTY) acc = acc + exp2_f(__builtin_fmaf(v[i], E.c2, nbias));
     }
     s = wave_tree_sum(acc);
   }
-  if (lane == 0) E.part[slot] = f2v{lm, s};
+  if (lane == 0) put_part(E, slot, f2v{lm, s});
   if (!E.collect || lm == NEG_INF) return;
   // ---- candidates: the chunk's history tokens above the threshold
   const float th = theta_of(__atomic_load_n(&E.misc[M_BETA], __ATOMIC_RELAXED));
@@ -1491,7 +1841,7 @@ __device__ __forceinline__ void vtile_chunk(const Args& a, const RowP& P, uint32
   for (int j = 0; j < 8; ++j) wd[j] = w0[j];
   for (uint32_t bt = 0; bt < nb_max; ++bt) {
     if (nb_max > 1)
-      vt_batch<DT>(a, P, row, mrow, base_tok, wd, need_cnt, rank_lane + bt * VB, cnt, tk, v);
+      vt_batch<DT>(a, P, row, mrow, base_tok, wd, need_cnt, h, NROUND(bt), tk, v);
     uint32_t np = 0;
 #pragma unroll
     for (int i = 0; i < VB; ++i) np += (tk[i] != EMPTY && v[i] >= th) ? 1u : 0u;
@@ -1511,11 +1861,11 @@ __device__ __forceinline__ void vtile_chunk(const Args& a, const RowP& P, uint32
         const uint32_t bin = fkey(v[i]) >> BIN_SHIFT;
         __atomic_fetch_add(&E.hf[bin], 1u, __ATOMIC_RELAXED);
         __atomic_fetch_add(&E.hcoarse[bin >> (CBIN_SHIFT - BIN_SHIFT)], 1u, __ATOMIC_RELAXED);
-        E.cbuf[pos++] = u2v{__float_as_uint(v[i]), tk[i]};
+        put_cand(E, pos++, u2v{__float_as_uint(v[i]), tk[i]});
       }
   }
-  (void)since;
 }
+#undef NROUND
 
 // ---------------------------------------------------------------------------
 // The kernel
@@ -1542,13 +1892,14 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   LDS uint32_t* sm = (LDS uint32_t*)smem;
   LDS uint32_t* red = sm;                    // 64
   LDS uint32_t* misc = red + 64;             // M_NMISC
-  LDS uint32_t* cst = misc + M_NMISC;        // MAX_CHUNKS + 16
-  LDS uint32_t* hf = cst + MAX_CHUNKS + 16;  // NBINS
+  LDS uint32_t* hf = misc + M_NMISC;         // NBINS
   LDS uint32_t* hcoarse = hf + NBINS;        // 64
   LDS uint32_t* hb = hcoarse + 64;           // history tables
   const uint32_t nwords = (t1 - t0) * 32;
   Hist h;
-  hist_carve(h, hb, nwords);
+  h.bitmap = hb;
+  h.hkey = hb + ((nwords + 3) & ~3u);
+  h.hcnt = h.hkey + HSLOTS;
   h.lo = lo;
   const bool need_pen = P.rp != 1.0f || P.pp != 0.0f || P.fp != 0.0f;
   uint32_t h0 = 0, h1 = 0;
@@ -1565,90 +1916,78 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   const void* row = (const char*)a.logits +
                     (uint64_t)b * a.stride * (DT == LLMK_F32 ? 4u : 2u);
   const uint32_t* mrow = a.mask ? a.mask + (uint64_t)b * a.mask_words : nullptr;
-  // The first two tiles of every wave, and the history tokens, are requested
-  // before the tables are set up, so HBM works meanwhile.
+  // Waves 0..TW-1 request the history tokens first, then their first tiles;
+  // the other waves request their first two tiles at once, so HBM works
+  // while the tables are set up.
+  constexpr uint32_t TW = 8;
+  constexpr int TQ = 4;  // tokens per lane per pass
   Raw ra, rb;
   uint32_t ta = t0 + (uint32_t)wv, tb2 = t0 + (uint32_t)wv + NW;
   ta = ta < t1 ? ta : EMPTY;
   tb2 = tb2 < t1 ? tb2 : EMPTY;
-  if (ta != EMPTY) load_tile<DT>(a, row, mrow, h, ta, lane, ra);
-  if (tb2 != EMPTY) load_tile<DT>(a, row, mrow, h, tb2, lane, rb);
-  uint32_t tk[HTPT];
+  const bool tok_wave = (uint32_t)wv < TW;
+  if (!tok_wave) {
+    if (ta != EMPTY) load_tile<DT>(a, row, mrow, h, ta, lane, ra);
+    if (tb2 != EMPTY) load_tile<DT>(a, row, mrow, h, tb2, lane, rb);
+  }
+  uint32_t tk[TQ];
 #pragma unroll
-  for (int q = 0; q < HTPT; ++q) {
-    const uint32_t i = h0 + q * NT + tid;
-    tk[q] = (i < h1) ? G(a.htok)[i] : EMPTY;
+  for (int q = 0; q < TQ; ++q) {
+    const uint32_t i = h0 + q * (TW * WAVE) + tid;
+    tk[q] = (tok_wave && i < h1) ? G(a.htok)[i] : EMPTY;
+  }
+  if (tok_wave) {
+    if (ta != EMPTY) load_tile<DT>(a, row, mrow, h, ta, lane, ra);
+    if (tb2 != EMPTY) load_tile<DT>(a, row, mrow, h, tb2, lane, rb);
   }
   if (collect) {
     for (uint32_t i = tid; i < NBINS; i += NT) hf[i] = 0;
     if (tid < 64) hcoarse[tid] = 0;
   }
   if (tid < M_NMISC) misc[tid] = 0;
-  if (have)
-    for (uint32_t i = tid; i < nwords; i += NT) h.bitmap[i] = 0;
-  __syncthreads();
   if (have) {
-    for (uint32_t c0 = h0; c0 < h1; c0 += HTPT * NT) {
-#pragma unroll
-      for (int q = 0; q < HTPT; ++q) {
-        uint32_t t = tk[q];
-        if (c0 != h0) {
-          const uint32_t i = c0 + q * NT + tid;
-          t = (i < h1) ? G(a.htok)[i] : EMPTY;
-        }
-        if (t >= lo && t < hi)
-          __atomic_fetch_or(&h.bitmap[(t - lo) >> 5], 1u << (t & 31), __ATOMIC_RELAXED);
+    for (uint32_t i = tid; i < nwords; i += NT) h.bitmap[i] = 0;
+    if (need_cnt)
+      for (uint32_t i = tid; i < HSLOTS; i += NT) {
+        h.hkey[i] = EMPTY;
+        h.hcnt[i] = 0;
       }
-    }
-    __syncthreads();
   }
-  if (need_cnt) {
-    // ranks (popcount prefix over the words; first rank of every chunk) and
-    // occurrence counts by rank
-    const uint32_t wpt = (nwords + NT - 1) / NT;
-    const uint32_t w0 = tid * wpt < nwords ? tid * wpt : nwords;
-    const uint32_t w1 = (w0 + wpt < nwords) ? w0 + wpt : nwords;
-    uint32_t local = 0;
-    for (uint32_t wi = w0; wi < w1; ++wi) local += __popc(h.bitmap[wi]);
-    uint32_t U;
-    uint32_t run = block_excl_scan(local, red, U);
-    for (uint32_t wi = w0; wi < w1; ++wi) {
-      if ((wi & 511u) == 0) cst[wi >> 9] = run;
-      h.pre[wi] = (uint16_t)(run < 0xffffu ? run : 0xffffu);
-      run += __popc(h.bitmap[wi]);
-    }
-    if (U > U_MAX && tid == 0) misc[M_FLAGS] = FLAG_HIST_OVERFLOW;
-    const uint32_t Uc = U < U_MAX ? U : U_MAX;
-    LDS uint32_t* cnt = (LDS uint32_t*)h.pen;
-    for (uint32_t i = tid; i < Uc; i += NT) cnt[i] = 0;
-    __syncthreads();
-    for (uint32_t c0 = h0; c0 < h1; c0 += HTPT * NT) {
+  __syncthreads();
+  if (have && tok_wave) {
+    // the bitmap of the segment's history tokens and, for the frequency
+    // penalty, their occurrence counts in an LDS hash table
+    bool full = false;
+    for (uint32_t c0 = h0; c0 < h1; c0 += TQ * TW * WAVE) {
 #pragma unroll
-      for (int q = 0; q < HTPT; ++q) {
+      for (int q = 0; q < TQ; ++q) {
         uint32_t t = tk[q];
         if (c0 != h0) {
-          const uint32_t i = c0 + q * NT + tid;
+          const uint32_t i = c0 + q * (TW * WAVE) + tid;
           t = (i < h1) ? G(a.htok)[i] : EMPTY;
         }
         if (t >= lo && t < hi) {
-          const uint32_t r = h.rank(t);
-          if (r < U_MAX) __atomic_fetch_add(&cnt[r], 1u, __ATOMIC_RELAXED);
+          __atomic_fetch_or(&h.bitmap[(t - lo) >> 5], 1u << (t & 31), __ATOMIC_RELAXED);
+          if (need_cnt && !hash_add(h, t)) full = true;
         }
       }
     }
-    __syncthreads();
+    if (full) __atomic_fetch_or(&misc[M_FLAGS], FLAG_HIST_OVERFLOW, __ATOMIC_RELAXED);
   }
+  if (have) __syncthreads();
   TileEnv E;
   E.P = P;
   E.c2 = LOG2E_F / P.T;
   E.V = a.V;
   E.collect = collect;
-  E.recompute_at = P.Kc / 2 > 16 ? P.Kc / 2 : 16;
+  E.recompute_at = P.Kc / 4 > 8 ? P.Kc / 4 : 8;
   E.misc = misc;
   E.hf = hf;
   E.hcoarse = hcoarse;
   E.cbuf = G(w.cand) + (uint64_t)blockIdx.x * CAND_CAP;
   E.part = G(w.tile_part) + (uint64_t)b * MAX_SLOTS;
+  E.lpart = a.G == 1 ? (LDS f2v*)(smem + a.lds_part) : nullptr;
+  E.lcand = a.G == 1 ? (LDS u2v*)(smem + a.lds_cand) : nullptr;
   uint32_t since = EMPTY;
   const uint32_t nch = (nwords + 511) / 512;  // chunks of this segment
 
@@ -1690,7 +2029,7 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   }
   if (have)
     for (uint32_t k = (uint32_t)wv; k < nch; k += NW)
-      vtile_chunk<DT>(a, P, b, row, t0, lo, nwords, k, h, cst, need_cnt, E, since, lane);
+      vtile_chunk<DT>(a, P, b, row, t0, lo, nwords, k, h, need_cnt, E, lane);
   for (;;) {
     if (ta == EMPTY && tb2 == EMPTY) break;
     if (tb2 != EMPTY) {
@@ -1727,9 +2066,10 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   }
   __syncthreads();
   const uint32_t last = misc[M_LAST];
+  const u4v seg_own = u4v{misc[M_CCOUNT], misc[M_BETA], misc[M_FLAGS], 0u};
   __syncthreads();  // finalize reuses this shared memory
   if (!last) return;
-  finalize_row<DT>(a, w, b, P, have, sm);
+  finalize_row<DT>(a, w, b, P, have, seg_own, sm);
 }
 
 }  // namespace llmk
@@ -1919,8 +2259,15 @@ extern "C" int llmk_sample_batch(llmk_sampler* s,
   hipStream_t st = (hipStream_t)stream;
   size_t words = stream_lds_words(a.tps);
   if (finalize_lds_words() > words) words = finalize_lds_words();
+  // a single-segment row keeps its partials and first candidates past both
+  words = (words + 3) & ~(size_t)3;
+  a.lds_part = (uint32_t)words;
+  a.lds_cand = a.lds_part + 2 * MAX_SLOTS;
+  if (a.G == 1) words = a.lds_cand + 2 * LCAP;
   if (slow_lds_words(a.V) > words) words = slow_lds_words(a.V);
   const size_t lds = 4 * words;
+  if (lds > 160 * 1024)
+    return fail(LLMK_ERR_CAPACITY, "vocabulary too large for one workgroup's LDS tables");
   const dim3 grid(a.B * a.G), block(NT);
   if (a.dtype == LLMK_F32)
     hipLaunchKernelGGL(stream_kernel<LLMK_F32>, grid, block, lds, st, a, s->ws);
