@@ -296,8 +296,6 @@ struct Hist {
   LDS uint16_t* pre;     // nwords: distinct history tokens in words before
   LDS float* pen;        // U_MAX: penalised logit by rank (counts while building)
   LDS uint32_t* tokr;    // U_MAX: token of each rank
-  LDS uint32_t* hkey;    // HSLOTS: hash table of occurrence counts (stream phase)
-  LDS uint32_t* hcnt;    // HSLOTS
   uint32_t lo;
   __device__ __forceinline__ uint32_t rank(uint32_t t) const {
     const uint32_t o = t - lo, w = o >> 5;
@@ -315,38 +313,64 @@ __device__ __forceinline__ void hist_carve(Hist& h, LDS uint32_t* base, uint32_t
   h.tokr = (LDS uint32_t*)(h.pen + U_MAX);
 }
 
-// Occurrence counts of history tokens: open addressing, linear probing, in
-// LDS.  hash_add returns false when the table is full.
-constexpr uint32_t HSLOTS = 8192;
-__device__ __forceinline__ uint32_t hash_slot(uint32_t t) {
-  return (t * 2654435761u) >> (32 - 13);  // HSLOTS = 2^13
-}
-__device__ __forceinline__ bool hash_add(const Hist& h, uint32_t t) {
-  uint32_t i = hash_slot(t);
-  for (uint32_t n = 0; n < HSLOTS; ++n) {
-    uint32_t old = __atomic_load_n(&h.hkey[i], __ATOMIC_RELAXED);
-    if (old == EMPTY) {
-      // claim the slot, or learn which token claimed it first
-      __atomic_compare_exchange_n(&h.hkey[i], &old, t, false, __ATOMIC_RELAXED,
-                                  __ATOMIC_RELAXED);
-    }
-    if (old == EMPTY || old == t) {
-      __atomic_fetch_add(&h.hcnt[i], 1u, __ATOMIC_RELAXED);
-      return true;
-    }
-    i = (i + 1) & (HSLOTS - 1);
+// Ranks of the segment's history tokens once its bitmap is complete (all
+// threads; ends with a barrier).  Blocks of 64 words, one word per lane,
+// wave w taking blocks w, w + NW, ...: pre[w] = history tokens in the words
+// before w, tokr[r] = the token of rank r (tokens in increasing order).
+// Tokens of rank >= U_MAX are cleared from the bitmap and the overflow flag
+// is raised: they are then ordinary, unpenalised tokens.  Returns the number
+// of ranks (<= U_MAX).  btot: nwords / 64 words of scratch (nwords <= 32768).
+__device__ __forceinline__ uint32_t build_ranks(const Hist& h, uint32_t nwords,
+                                                LDS uint32_t* btot, LDS uint32_t* flags) {
+  const int lane = (int)(threadIdx.x & 63), wv = (int)(threadIdx.x >> 6);
+  const uint32_t nblk = (nwords + 63) / 64;
+  for (uint32_t j = (uint32_t)wv; j < nblk; j += NW) {
+    const uint32_t wi = 64 * j + (uint32_t)lane;
+    const uint32_t c = wi < nwords ? (uint32_t)__popc(h.bitmap[wi]) : 0u;
+    const uint32_t t = bcast63u(wave_incl_scan(c));
+    if (lane == 0) btot[j] = t;
   }
-  return false;
-}
-__device__ __forceinline__ uint32_t hash_count(const Hist& h, uint32_t t) {
-  uint32_t i = hash_slot(t);
-  for (uint32_t n = 0; n < HSLOTS; ++n) {
-    const uint32_t k = h.hkey[i];
-    if (k == t) return h.hcnt[i];
-    if (k == EMPTY) return 1u;  // not recorded (table full): counted once
-    i = (i + 1) & (HSLOTS - 1);
+  __syncthreads();
+  // every wave scans the block totals: lane L holds blocks 8L .. 8L+7
+  uint32_t bl[8], ls = 0;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const uint32_t j = 8u * (uint32_t)lane + q;
+    bl[q] = j < nblk ? btot[j] : 0u;
+    ls += bl[q];
   }
-  return 1u;
+  const uint32_t lincl = wave_incl_scan(ls);
+  const uint32_t total = bcast63u(lincl);
+  for (uint32_t j = (uint32_t)wv; j < nblk; j += NW) {
+    const uint32_t sub = j & 7u;
+    uint32_t mine = lincl - ls;
+#pragma unroll
+    for (uint32_t q = 0; q < 8; ++q) mine += q < sub ? bl[q] : 0u;
+    const uint32_t base = (uint32_t)__builtin_amdgcn_readlane((int)mine, (int)(j >> 3));
+    const uint32_t wi = 64 * j + (uint32_t)lane;
+    uint32_t bits = wi < nwords ? h.bitmap[wi] : 0u;
+    const uint32_t c = (uint32_t)__popc(bits);
+    uint32_t r = base + wave_incl_scan(c) - c;
+    if (wi < nwords) h.pre[wi] = (uint16_t)(r < U_MAX ? r : U_MAX);
+    if (r + c > U_MAX) {  // keep the first U_MAX - r tokens of the word
+      const uint32_t keep = r < U_MAX ? U_MAX - r : 0u;
+      uint32_t kept = 0, rest = bits;
+      for (uint32_t k = 0; k < keep; ++k) {
+        kept |= rest & (0u - rest);
+        rest &= rest - 1u;
+      }
+      bits = kept;
+      h.bitmap[wi] = kept;
+    }
+    while (bits) {
+      const uint32_t bit = (uint32_t)__builtin_ctz(bits);
+      bits &= bits - 1u;
+      h.tokr[r++] = h.lo + 32u * wi + bit;
+    }
+  }
+  if (total > U_MAX && threadIdx.x == 0) __atomic_fetch_or(flags, FLAG_HIST_OVERFLOW, __ATOMIC_RELAXED);
+  __syncthreads();
+  return total < U_MAX ? total : U_MAX;
 }
 
 // Builds the history tables for tokens in [lo, hi) of row b.  All threads.
@@ -974,7 +998,7 @@ __device__ __forceinline__ bool semantics_regs(const RowP& P, float u, uint32_t 
 enum : uint32_t { M_BETA = 0, M_CCOUNT = 1, M_FLAGS = 2, M_LAST = 3, M_NEXT = 4, M_NMISC = 16 };
 
 __host__ __device__ inline size_t stream_lds_words(uint32_t tps) {
-  return 64 + M_NMISC + NBINS + 64 + ((tps * 32 + 3) & ~3u) + 2 * HSLOTS;
+  return 64 + M_NMISC + NBINS + 64 + hist_lds_words(tps * 32) + ((tps * 32 / 64 + 3) & ~3u);
 }
 __host__ __device__ inline size_t finalize_lds_words() {
   // slots (2 x MAX_SLOTS) + keys + sorted keys (2 x SORT_CAP u64) + p + idx
@@ -1717,101 +1741,63 @@ __device__ __forceinline__ float exclude(float v, uint32_t x, uint32_t pos) {
 // the chunk); its terms are summed sequentially in increasing token order,
 // the lanes by a balanced tree.
 // ---------------------------------------------------------------------------
-constexpr int VB = 8;  // tokens per lane gathered together
+constexpr int VB = 8;  // rounds of 64 ranks gathered together
 
-// Removes the lowest set bit of the lane's 256-bit set wd[0..7] and returns
-// its position (EMPTY if the set is empty).
-__device__ __forceinline__ uint32_t pop_lowest(uint32_t (&wd)[8]) {
-  uint32_t pos = EMPTY;
-#pragma unroll
-  for (int j = 7; j >= 0; --j)
-    if (wd[j]) pos = 32u * j + (uint32_t)__builtin_ctz(wd[j]);
-#pragma unroll
-  for (int j = 0; j < 8; ++j)
-    if ((pos >> 5) == (uint32_t)j) wd[j] &= wd[j] - 1;
-  return pos;
-}
-
-// Penalised, masked values of the lane's next (up to) VB tokens: tk[i] (EMPTY
-// past the lane's tokens), v[i].  rank0: rank of the first of them.
-template <int DT>
-__device__ __forceinline__ void vt_batch(const Args& a, const RowP& P, const void* row,
-                                         const GLB uint32_t* mrow, uint32_t base_tok,
-                                         uint32_t (&wd)[8], bool need_cnt, const Hist& h,
-                                         uint32_t nround, uint32_t (&tk)[VB], float (&v)[VB]) {
-  float x[VB];
-  uint32_t mw[VB];
-#pragma unroll
-  for (int i = 0; i < VB; ++i) {
-    const uint32_t pos = (uint32_t)i < nround ? pop_lowest(wd) : EMPTY;  // nround: wave-uniform
-    tk[i] = pos == EMPTY ? EMPTY : base_tok + pos;
-    x[i] = pos == EMPTY ? 0.0f : load_logit<DT>(row, tk[i]);
-    mw[i] = (pos != EMPTY && mrow) ? mrow[tk[i] >> 5] : 0xffffffffu;
-  }
-#pragma unroll
-  for (int i = 0; i < VB; ++i) {
-    float y = NEG_INF;
-    if (tk[i] != EMPTY) {
-      y = (x[i] > NEG_INF) ? x[i] : NEG_INF;  // NaN acts as -inf
-      y = penalize(y, P, need_cnt ? hash_count(h, tk[i]) : 1u);
-      if (!((mw[i] >> (tk[i] & 31)) & 1u)) y = NEG_INF;
-    }
-    v[i] = y;
-  }
-}
-
+// The virtual tile of chunk kk of the segment: its history tokens are the
+// ranks [r0, r1) (pre at the chunk's first word and past its last);
+// lane L takes ranks r0 + L, r0 + L + 64, ... in increasing order.  Pass 1
+// gathers the logits (VB rounds of loads in flight), penalises them, keeps
+// them in pen[] (over the counts) and forms the maximum; pass 2 sums the
+// terms per lane in rank order, then as a balanced tree over the lanes.
 template <int DT>
 __device__ __forceinline__ void vtile_chunk(const Args& a, const RowP& P, uint32_t b,
-                                         const void* row, uint32_t t0, uint32_t lo,
-                                         uint32_t nwords, uint32_t kk, const Hist& h,
+                                         const void* row, uint32_t t0, uint32_t nwords,
+                                         uint32_t kk, uint32_t U, const Hist& h,
                                          bool need_cnt, const TileEnv& E, int lane) {
-  const uint32_t wb = 512u * kk + 8u * (uint32_t)lane;
-  uint32_t w0[8];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    u4v q = u4v{0u, 0u, 0u, 0u};
-    if (wb + 4 * j < nwords) q = *(LDS const u4v*)(h.bitmap + wb + 4 * j);
-    w0[4 * j + 0] = q.x;
-    w0[4 * j + 1] = q.y;
-    w0[4 * j + 2] = q.z;
-    w0[4 * j + 3] = q.w;
-  }
-  uint32_t n = 0;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) n += __popc(w0[j]);
-  const uint32_t n_max = wave_max_u32(n);
-  const uint32_t nb_max = (n_max + VB - 1) / VB;  // batches
-  // rounds of batch bt: the most tokens any lane still has, at most VB
-#define NROUND(bt) (n_max - (bt) * VB < VB ? n_max - (bt) * VB : (uint32_t)VB)
-  const uint32_t base_tok = lo + 32u * wb;
+  const uint32_t wf = 512u * kk;
+  const uint32_t r0 = h.pre[wf];
+  const uint32_t r1 = wf + 512u < nwords ? (uint32_t)h.pre[wf + 512u] : U;
+  const uint32_t n = r1 - r0;
   const uint32_t slot = a.ntiles + t0 / CHUNK_TILES + kk;
   const GLB uint32_t* mrow = a.mask ? G(a.mask) + (uint64_t)b * a.mask_words : nullptr;
   const bool greedy = E.P.mode == MODE_GREEDY;
-  // pass 1: the chunk's maximum (and, for greedy rows, its first index)
-  uint32_t wd[8];
-  uint32_t tk[VB];
-  float v[VB];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) wd[j] = w0[j];
+  LDS float* pen = h.pen + r0;
+  LDS const uint32_t* cnt = (LDS const uint32_t*)h.pen + r0;
+  LDS const uint32_t* tokr = h.tokr + r0;
   float lm = NEG_INF;
-  for (uint32_t bt = 0; bt < nb_max; ++bt) {
-    vt_batch<DT>(a, P, row, mrow, base_tok, wd, need_cnt, h, NROUND(bt), tk, v);
+  for (uint32_t j0 = 0; j0 < n; j0 += 64u * VB) {
+    uint32_t tk[VB], mw[VB];
+    float x[VB];
 #pragma unroll
-    for (int i = 0; i < VB; ++i) lm = fmaxf(lm, v[i]);
+    for (int i = 0; i < VB; ++i) {
+      const uint32_t r = j0 + 64u * i + (uint32_t)lane;
+      tk[i] = r < n ? tokr[r] : EMPTY;
+    }
+#pragma unroll
+    for (int i = 0; i < VB; ++i) {
+      x[i] = tk[i] != EMPTY ? load_logit<DT>(row, tk[i]) : 0.0f;
+      mw[i] = (tk[i] != EMPTY && mrow) ? mrow[tk[i] >> 5] : 0xffffffffu;
+    }
+#pragma unroll
+    for (int i = 0; i < VB; ++i) {
+      const uint32_t r = j0 + 64u * i + (uint32_t)lane;
+      if (tk[i] != EMPTY) {
+        float y = (x[i] > NEG_INF) ? x[i] : NEG_INF;  // NaN acts as -inf
+        y = penalize(y, P, need_cnt ? cnt[r] : 1u);
+        if (!((mw[i] >> (tk[i] & 31)) & 1u)) y = NEG_INF;
+        pen[r] = y;
+        lm = fmaxf(lm, y);
+      }
+    }
   }
   lm = wave_max(lm);
+  WaveSync::sync();  // pen[] written by this wave's lanes, read across them below
   if (greedy) {
+    // the first (lowest) token holding the maximum; all -inf: the first token
     uint32_t bi = EMPTY;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) wd[j] = w0[j];
-    for (uint32_t bt = 0; bt < nb_max; ++bt) {
-      if (nb_max > 1)
-        vt_batch<DT>(a, P, row, mrow, base_tok, wd, need_cnt, h, NROUND(bt), tk, v);
-#pragma unroll
-      for (int i = 0; i < VB; ++i) {
-        const bool hit = tk[i] != EMPTY && ((v[i] == lm) || (lm == NEG_INF && !(v[i] > NEG_INF)));
-        if (hit) bi = umin(bi, tk[i]);
-      }
+    for (uint32_t r = (uint32_t)lane; r < n; r += 64u) {
+      const float y = pen[r];
+      if (y == lm || (lm == NEG_INF && !(y > NEG_INF))) bi = umin(bi, tokr[r]);
     }
     bi = wave_min_u32(bi);
     if (lane == 0) put_part(E, slot, f2v{lm, __uint_as_float(bi)});
@@ -1821,32 +1807,29 @@ __device__ __forceinline__ void vtile_chunk(const Args& a, const RowP& P, uint32
   if (lm != NEG_INF) {
     const float nbias = -(lm * E.c2);
     float acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) wd[j] = w0[j];
-    for (uint32_t bt = 0; bt < nb_max; ++bt) {
-      if (nb_max > 1)
-        vt_batch<DT>(a, P, row, mrow, base_tok, wd, need_cnt, h, NROUND(bt), tk, v);
-#pragma unroll
-      for (int i = 0; i < VB; ++i)
-        if (tk[i] != EMPTY) acc = acc + exp2_f(__builtin_fmaf(v[i], E.c2, nbias));
+    uint32_t r = (uint32_t)lane;
+    for (; r + 192u < n; r += 256u) {
+      const float y0 = pen[r], y1 = pen[r + 64u], y2 = pen[r + 128u], y3 = pen[r + 192u];
+      acc = acc + exp2_f(__builtin_fmaf(y0, E.c2, nbias));
+      acc = acc + exp2_f(__builtin_fmaf(y1, E.c2, nbias));
+      acc = acc + exp2_f(__builtin_fmaf(y2, E.c2, nbias));
+      acc = acc + exp2_f(__builtin_fmaf(y3, E.c2, nbias));
     }
+    for (; r < n; r += 64u) acc = acc + exp2_f(__builtin_fmaf(pen[r], E.c2, nbias));
     s = wave_tree_sum(acc);
   }
   if (lane == 0) put_part(E, slot, f2v{lm, s});
   if (!E.collect || lm == NEG_INF) return;
-  // ---- candidates: the chunk's history tokens above the threshold
+  // ---- candidates: the chunk's history tokens at or above the threshold
   const float th = theta_of(__atomic_load_n(&E.misc[M_BETA], __ATOMIC_RELAXED));
   if (!(lm >= th)) return;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) wd[j] = w0[j];
-  for (uint32_t bt = 0; bt < nb_max; ++bt) {
-    if (nb_max > 1)
-      vt_batch<DT>(a, P, row, mrow, base_tok, wd, need_cnt, h, NROUND(bt), tk, v);
-    uint32_t np = 0;
-#pragma unroll
-    for (int i = 0; i < VB; ++i) np += (tk[i] != EMPTY && v[i] >= th) ? 1u : 0u;
-    const uint32_t tot = bcast63u(wave_incl_scan(np));
-    if (tot == 0) continue;
+  for (uint32_t j0 = 0; j0 < n; j0 += 64u) {
+    const uint32_t r = j0 + (uint32_t)lane;
+    const float y = r < n ? pen[r] : NEG_INF;
+    const bool keep = r < n && y >= th;
+    const uint64_t mk = __ballot(keep);
+    if (!mk) continue;
+    const uint32_t tot = (uint32_t)__popcll(mk);
     uint32_t base = 0;
     if (lane == 0) base = __atomic_fetch_add(&E.misc[M_CCOUNT], tot, __ATOMIC_RELAXED);
     base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
@@ -1854,18 +1837,14 @@ __device__ __forceinline__ void vtile_chunk(const Args& a, const RowP& P, uint32
       if (lane == 0) __atomic_fetch_or(&E.misc[M_FLAGS], FLAG_OVERFLOW, __ATOMIC_RELAXED);
       return;
     }
-    uint32_t pos = base + wave_incl_scan(np) - np;
-#pragma unroll
-    for (int i = 0; i < VB; ++i)
-      if (tk[i] != EMPTY && v[i] >= th) {
-        const uint32_t bin = fkey(v[i]) >> BIN_SHIFT;
-        __atomic_fetch_add(&E.hf[bin], 1u, __ATOMIC_RELAXED);
-        __atomic_fetch_add(&E.hcoarse[bin >> (CBIN_SHIFT - BIN_SHIFT)], 1u, __ATOMIC_RELAXED);
-        put_cand(E, pos++, u2v{__float_as_uint(v[i]), tk[i]});
-      }
+    if (keep) {
+      const uint32_t bin = fkey(y) >> BIN_SHIFT;
+      __atomic_fetch_add(&E.hf[bin], 1u, __ATOMIC_RELAXED);
+      __atomic_fetch_add(&E.hcoarse[bin >> (CBIN_SHIFT - BIN_SHIFT)], 1u, __ATOMIC_RELAXED);
+      put_cand(E, base + lanes_below(mk), u2v{__float_as_uint(y), tokr[r]});
+    }
   }
 }
-#undef NROUND
 
 // ---------------------------------------------------------------------------
 // The kernel
@@ -1897,9 +1876,8 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   LDS uint32_t* hb = hcoarse + 64;           // history tables
   const uint32_t nwords = (t1 - t0) * 32;
   Hist h;
-  h.bitmap = hb;
-  h.hkey = hb + ((nwords + 3) & ~3u);
-  h.hcnt = h.hkey + HSLOTS;
+  hist_carve(h, hb, nwords);
+  LDS uint32_t* btot = hb + hist_lds_words(nwords);  // nwords / 64
   h.lo = lo;
   const bool need_pen = P.rp != 1.0f || P.pp != 0.0f || P.fp != 0.0f;
   uint32_t h0 = 0, h1 = 0;
@@ -1916,9 +1894,8 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   const void* row = (const char*)a.logits +
                     (uint64_t)b * a.stride * (DT == LLMK_F32 ? 4u : 2u);
   const uint32_t* mrow = a.mask ? a.mask + (uint64_t)b * a.mask_words : nullptr;
-  // Waves 0..TW-1 request the history tokens first, then their first tiles;
-  // the other waves request their first two tiles at once, so HBM works
-  // while the tables are set up.
+  // Waves 0..TW-1 load the history tokens (TQ per lane per pass); every
+  // wave then requests its first two tiles.
   constexpr uint32_t TW = 8;
   constexpr int TQ = 4;  // tokens per lane per pass
   Raw ra, rb;
@@ -1926,19 +1903,11 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   ta = ta < t1 ? ta : EMPTY;
   tb2 = tb2 < t1 ? tb2 : EMPTY;
   const bool tok_wave = (uint32_t)wv < TW;
-  if (!tok_wave) {
-    if (ta != EMPTY) load_tile<DT>(a, row, mrow, h, ta, lane, ra);
-    if (tb2 != EMPTY) load_tile<DT>(a, row, mrow, h, tb2, lane, rb);
-  }
   uint32_t tk[TQ];
 #pragma unroll
   for (int q = 0; q < TQ; ++q) {
     const uint32_t i = h0 + q * (TW * WAVE) + tid;
     tk[q] = (tok_wave && i < h1) ? G(a.htok)[i] : EMPTY;
-  }
-  if (tok_wave) {
-    if (ta != EMPTY) load_tile<DT>(a, row, mrow, h, ta, lane, ra);
-    if (tb2 != EMPTY) load_tile<DT>(a, row, mrow, h, tb2, lane, rb);
   }
   if (collect) {
     for (uint32_t i = tid; i < NBINS; i += NT) hf[i] = 0;
@@ -1948,33 +1917,55 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   if (have) {
     for (uint32_t i = tid; i < nwords; i += NT) h.bitmap[i] = 0;
     if (need_cnt)
-      for (uint32_t i = tid; i < HSLOTS; i += NT) {
-        h.hkey[i] = EMPTY;
-        h.hcnt[i] = 0;
-      }
+      for (uint32_t i = tid; i < U_MAX; i += NT) ((LDS uint32_t*)h.pen)[i] = 0;
   }
-  __syncthreads();
-  if (have && tok_wave) {
-    // the bitmap of the segment's history tokens and, for the frequency
-    // penalty, their occurrence counts in an LDS hash table
-    bool full = false;
-    for (uint32_t c0 = h0; c0 < h1; c0 += TQ * TW * WAVE) {
+  // The history tokens arrive before any tile is requested: behind the first
+  // tiles of every workgroup they would take several microseconds, and no
+  // tile can be reduced before the tables are built.  (Unconditional, so that
+  // no path reaches the insertion below with the tokens still in flight.)
 #pragma unroll
-      for (int q = 0; q < TQ; ++q) {
-        uint32_t t = tk[q];
-        if (c0 != h0) {
+  for (int q = 0; q < TQ; ++q) asm volatile("" ::"v"(tk[q]));
+  __syncthreads();
+  if (ta != EMPTY) load_tile<DT>(a, row, mrow, h, ta, lane, ra);
+  if (tb2 != EMPTY) load_tile<DT>(a, row, mrow, h, tb2, lane, rb);
+  // The history tables: the bitmap of the segment's history tokens, their
+  // ranks and, for the frequency penalty, occurrence counts by rank.
+  uint32_t U = 0;
+  if (have) {
+    const uint32_t step = TQ * TW * WAVE;
+    auto each_token = [&](auto&& fn) __attribute__((always_inline)) {
+      // the first pass from registers (no load in flight but the tiles'),
+      // the rest loaded here
+#pragma unroll
+      for (int q = 0; q < TQ; ++q)
+        if (tk[q] >= lo && tk[q] < hi) fn(tk[q]);
+      for (uint32_t c0 = h0 + step; c0 < h1; c0 += step) {
+#pragma unroll
+        for (int q = 0; q < TQ; ++q) {
           const uint32_t i = c0 + q * (TW * WAVE) + tid;
-          t = (i < h1) ? G(a.htok)[i] : EMPTY;
-        }
-        if (t >= lo && t < hi) {
-          __atomic_fetch_or(&h.bitmap[(t - lo) >> 5], 1u << (t & 31), __ATOMIC_RELAXED);
-          if (need_cnt && !hash_add(h, t)) full = true;
+          const uint32_t t = (i < h1) ? G(a.htok)[i] : EMPTY;
+          if (t >= lo && t < hi) fn(t);
         }
       }
+    };
+    if (tok_wave)
+      each_token([&](uint32_t t) {
+        __atomic_fetch_or(&h.bitmap[(t - lo) >> 5], 1u << (t & 31), __ATOMIC_RELAXED);
+      });
+    __syncthreads();
+    U = build_ranks(h, nwords, btot, &misc[M_FLAGS]);
+    if (need_cnt) {
+      if (tok_wave)
+        each_token([&](uint32_t t) {
+          const uint32_t o = t - lo, wd = h.bitmap[o >> 5], bit = 1u << (o & 31);
+          if (wd & bit) {  // not dropped by the rank limit
+            const uint32_t r = h.pre[o >> 5] + (uint32_t)__popc(wd & (bit - 1u));
+            __atomic_fetch_add(&((LDS uint32_t*)h.pen)[r], 1u, __ATOMIC_RELAXED);
+          }
+        });
+      __syncthreads();
     }
-    if (full) __atomic_fetch_or(&misc[M_FLAGS], FLAG_HIST_OVERFLOW, __ATOMIC_RELAXED);
   }
-  if (have) __syncthreads();
   TileEnv E;
   E.P = P;
   E.c2 = LOG2E_F / P.T;
@@ -2029,7 +2020,7 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   }
   if (have)
     for (uint32_t k = (uint32_t)wv; k < nch; k += NW)
-      vtile_chunk<DT>(a, P, b, row, t0, lo, nwords, k, h, need_cnt, E, lane);
+      vtile_chunk<DT>(a, P, b, row, t0, nwords, k, U, h, need_cnt, E, lane);
   for (;;) {
     if (ta == EMPTY && tb2 == EMPTY) break;
     if (tb2 != EMPTY) {

@@ -132,10 +132,10 @@ float llmk_oracle_normalizer(const float* lp, const uint8_t* is_hist, uint32_t V
    *   ((e0+e1)+(e2+e3)), a lane ((run0+run1)+(run2+run3)), the tile is the
    *   balanced tree over the 64 lanes.
    *   Virtual tile k holds the history tokens of chunk k (16 real tiles,
-   *   tokens 16384k ..): lc = their max (-inf if none, sum 0); lane L owns
-   *   chunk tokens 256L .. 256L+255 and sums their terms
-   *   exp2_f(fma(x, c2, nb)) sequentially in increasing token order
-   *   (0 if none); the tile is the balanced tree over the 64 lanes.
+   *   tokens 16384k ..): lc = their max (-inf if none, sum 0); numbered
+   *   0, 1, 2, ... in increasing token order, token j goes to lane j mod 64,
+   *   which sums its terms exp2_f(fma(x, c2, nb)) sequentially in that
+   *   order (0 if none); the tile is the balanced tree over the 64 lanes.
    *   Slots: real tiles 0..nt-1, then virtual tile k at nt + k.  Row:
    *   L = max lc; S = balanced tree over the next power of two >= slots of
    *   s_c * exp2_f((lc_c - L)*c2) (padding 0).
@@ -171,13 +171,13 @@ float llmk_oracle_normalizer(const float* lp, const uint8_t* is_hist, uint32_t V
       continue;
     }
     const float nb = -(m * c2);
-    float lanes[64];
-    for (uint32_t L = 0; L < 64; ++L) {
-      float acc = 0.0f;
-      for (uint32_t e = lo + 256 * L; e < lo + 256 * (L + 1) && e < hi; ++e)
-        if (is_hist[e]) acc = acc + llmk_oracle_exp2_f(fmaf(lp[e], c2, nb));
-      lanes[L] = acc;
-    }
+    float lanes[64] = {0.0f};
+    uint32_t j = 0;
+    for (uint32_t e = lo; e < hi; ++e)
+      if (is_hist[e]) {
+        lanes[j & 63] = lanes[j & 63] + llmk_oracle_exp2_f(fmaf(lp[e], c2, nb));
+        ++j;
+      }
     tree_sum_inplace(lanes, 64);
     w[slot] = lanes[0];
   }
