@@ -49,6 +49,9 @@ extern "C" {
 
 /* Bits of the device status word (llmk_sampler_status). */
 #define LLMK_STATUS_INVALID_PARAMS 0x1u
+/* More than 8192 distinct history tokens fell in one vocabulary segment of a
+ * row: the tokens past the first 8192 (by id) of that segment were sampled
+ * without penalties. */
 #define LLMK_STATUS_HISTORY_OVERFLOW 0x2u
 #define LLMK_STATUS_SLOT_TIMEOUT 0x4u /* slow-path scratch slot not acquired */
 

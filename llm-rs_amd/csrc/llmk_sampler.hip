@@ -313,24 +313,27 @@ __device__ __forceinline__ void hist_carve(Hist& h, LDS uint32_t* base, uint32_t
   h.tokr = (LDS uint32_t*)(h.pen + U_MAX);
 }
 
-// Ranks of the segment's history tokens once its bitmap is complete (all
-// threads; ends with a barrier).  Blocks of 64 words, one word per lane,
-// wave w taking blocks w, w + NW, ...: pre[w] = history tokens in the words
+// Ranks of the segment's history tokens once its bitmap is complete, built
+// by waves 0 .. nw-1, which call sync() together twice (the second time at
+// the end).  Blocks of 64 words, one word per lane,
+// wave w taking blocks w, w + nw, ...: pre[w] = history tokens in the words
 // before w, tokr[r] = the token of rank r (tokens in increasing order).
 // Tokens of rank >= U_MAX are cleared from the bitmap and the overflow flag
 // is raised: they are then ordinary, unpenalised tokens.  Returns the number
 // of ranks (<= U_MAX).  btot: nwords / 64 words of scratch (nwords <= 32768).
+template <class Sync>
 __device__ __forceinline__ uint32_t build_ranks(const Hist& h, uint32_t nwords,
-                                                LDS uint32_t* btot, LDS uint32_t* flags) {
+                                                LDS uint32_t* btot, LDS uint32_t* flags,
+                                                uint32_t nw, Sync& sync) {
   const int lane = (int)(threadIdx.x & 63), wv = (int)(threadIdx.x >> 6);
   const uint32_t nblk = (nwords + 63) / 64;
-  for (uint32_t j = (uint32_t)wv; j < nblk; j += NW) {
+  for (uint32_t j = (uint32_t)wv; j < nblk; j += nw) {
     const uint32_t wi = 64 * j + (uint32_t)lane;
     const uint32_t c = wi < nwords ? (uint32_t)__popc(h.bitmap[wi]) : 0u;
     const uint32_t t = bcast63u(wave_incl_scan(c));
     if (lane == 0) btot[j] = t;
   }
-  __syncthreads();
+  sync();
   // every wave scans the block totals: lane L holds blocks 8L .. 8L+7
   uint32_t bl[8], ls = 0;
 #pragma unroll
@@ -341,7 +344,7 @@ __device__ __forceinline__ uint32_t build_ranks(const Hist& h, uint32_t nwords,
   }
   const uint32_t lincl = wave_incl_scan(ls);
   const uint32_t total = bcast63u(lincl);
-  for (uint32_t j = (uint32_t)wv; j < nblk; j += NW) {
+  for (uint32_t j = (uint32_t)wv; j < nblk; j += nw) {
     const uint32_t sub = j & 7u;
     uint32_t mine = lincl - ls;
 #pragma unroll
@@ -369,9 +372,28 @@ __device__ __forceinline__ uint32_t build_ranks(const Hist& h, uint32_t nwords,
     }
   }
   if (total > U_MAX && threadIdx.x == 0) __atomic_fetch_or(flags, FLAG_HIST_OVERFLOW, __ATOMIC_RELAXED);
-  __syncthreads();
+  sync();
   return total < U_MAX ? total : U_MAX;
 }
+
+// A barrier among waves 0 .. n-1 while the others run on: an arrival count
+// in LDS that the waiting waves poll.  Every one of the n waves makes every
+// call, and none of them waits on the other waves in between, so each wait
+// ends.
+struct GroupSync {
+  LDS uint32_t* ctr;
+  uint32_t n, gen;
+  __device__ __forceinline__ void operator()() {
+    ++gen;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    if ((threadIdx.x & 63u) == 0) __atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED);
+    while (__atomic_load_n(ctr, __ATOMIC_RELAXED) < n * gen) __builtin_amdgcn_s_sleep(1);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  }
+};
+struct BarrierSync {
+  __device__ __forceinline__ void operator()() { __syncthreads(); }
+};
 
 // Builds the history tables for tokens in [lo, hi) of row b.  All threads.
 // Global round trips: the row's history (held in registers, HTPT tokens per
@@ -995,7 +1017,13 @@ __device__ __forceinline__ bool semantics_regs(const RowP& P, float u, uint32_t 
 // ---------------------------------------------------------------------------
 // Shared-memory layouts (in 32-bit words)
 // ---------------------------------------------------------------------------
-enum : uint32_t { M_BETA = 0, M_CCOUNT = 1, M_FLAGS = 2, M_LAST = 3, M_NEXT = 4, M_NMISC = 16 };
+enum : uint32_t {
+  M_BETA = 0, M_CCOUNT = 1, M_FLAGS = 2, M_LAST = 3, M_NEXT = 4,
+  M_GSYNC = 5,  // arrivals of the token waves' group barrier
+  M_VNEXT = 6,  // next virtual tile to claim
+  M_U = 7,      // history ranks of the segment
+  M_NMISC = 16
+};
 
 __host__ __device__ inline size_t stream_lds_words(uint32_t tps) {
   return 64 + M_NMISC + NBINS + 64 + hist_lds_words(tps * 32) + ((tps * 32 / 64 + 3) & ~3u);
@@ -1238,9 +1266,9 @@ __device__ __forceinline__ uint32_t kth_largest_key(LDS const float* cval, uint3
 
 // ---------------------------------------------------------------------------
 // Finalize one row.  Wave 0 reduces the partials (normaliser S, maximum L)
-// and reads the segment table; the candidate path then runs in wave 0 when
-// the candidates are few, else in the whole workgroup; rows it cannot prove
-// exact take the slow path.
+// and reads the segment table; the candidate path then runs in the whole
+// workgroup (a short form when the candidates are in LDS and at most 128
+// survive the filter); rows it cannot prove exact take the slow path.
 // ---------------------------------------------------------------------------
 enum : uint32_t {
   F_DONE = 0, F_S = 1, F_M = 2, F_TOTAL = 3, F_LAM = 4, F_OVF = 5, F_L = 6, F_GREEDY = 7,
@@ -1271,8 +1299,6 @@ __device__ __forceinline__ FinLds fin_carve(LDS uint32_t* smem) {
   f.red = f.soff + MAX_SEG + 16;
   return f;
 }
-constexpr uint32_t WAVE_GATHER = 512;  // candidates the wave path reads
-constexpr uint32_t WAVE_KEEP = 256;    // candidates the wave path sorts
 
 // Ascending sort of keys[0..n) into skeys[0..n) (keys distinct).
 template <class SY>
@@ -1478,6 +1504,123 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
   return res;
 }
 
+// The candidate path of a single-segment row whose candidates are all in
+// LDS (total <= LCAP), with the whole workgroup: one candidate per thread
+// for the gather and the filter, the rank sort split eight ways (each
+// thread compares one key with sixteen others), the semantics in wave 0
+// from registers.  Returns 0 when the row is done, 1 when it needs the
+// general path (more than 128 kept), 2 for the slow path.
+__device__ __forceinline__ uint32_t candidate_fast(const Args& a, uint32_t b, const RowP& P,
+                                                   float S, float m, float u, uint32_t total,
+                                                   uint32_t lam, const FinLds& f) {
+  using SY = BlockSync;
+  const uint32_t tid = threadIdx.x;
+  LDS const u2v* lcand = (LDS const u2v*)((LDS uint32_t*)f.tl + a.lds_cand);
+  LDS float* cval = f.pp;
+  LDS uint32_t* cidx = f.pidx;
+  // ---- gather the candidates at or above lam
+  uint32_t n0;
+  {
+    const u2v e = tid < total ? lcand[tid] : u2v{0xff800000u, 0u};
+    const float v = __uint_as_float(e.x);
+    const bool keep = v > NEG_INF && fkey(v) >= lam;
+    const uint32_t pos = SY::excl_scan(keep, f.red, n0);
+    if (keep) {
+      cval[pos] = v;
+      cidx[pos] = e.y;
+    }
+  }
+  SY::sync();
+  const bool topk = P.K > 0 && (uint32_t)P.K < a.V;
+  const float plim = lam > 0x007fffffu ? prob_of(funkey(lam - 1), P.T, m, S) : 0.0f;
+  uint32_t lam_e = lam;
+  float plim_e = plim;
+  if (topk && n0 > 2u * (uint32_t)P.K) {
+    const uint32_t tau = kth_largest_key<SY>(cval, n0, (uint32_t)P.K, (LDS uint32_t*)f.keys,
+                                             f.fm + F_SCR);
+    lam_e = tau;
+    plim_e = tau > 0x007fffffu ? prob_of(funkey(tau - 1), P.T, m, S) : 0.0f;
+  }
+  // ---- exact probabilities above the bound, as (p desc, idx asc) keys
+  uint32_t n = 0;
+  for (int attempt = 0; attempt < 2; ++attempt) {
+    bool keep = false;
+    uint64_t key = 0;
+    if (tid < n0) {
+      const float v = cval[tid];
+      if (fkey(v) >= lam_e) {
+        const float pv = prob_of(v, P.T, m, S);
+        if (pv > plim_e) {
+          keep = true;
+          key = pkey(pv, cidx[tid]);
+        }
+      }
+    }
+    const uint32_t pos = SY::excl_scan(keep, f.red, n);
+    if (keep) f.keys[pos] = key;
+    // a tightened bound that keeps fewer than K (ties in p across it) falls
+    // back to the gather bound
+    if (!(topk && n < (uint32_t)P.K && lam_e != lam)) break;
+    lam_e = lam;
+    plim_e = plim;
+  }
+  if (n > 128) return 1;
+  // ---- rank sort: key i against keys 16s .. 16s+15 in thread 128s + i
+  LDS uint32_t* rk = (LDS uint32_t*)cval;  // 128 ranks; cval is read no more
+  if (tid < 128) rk[tid] = 0;
+  SY::sync();
+  {
+    const uint32_t i = tid & 127u, s0 = 16u * (tid >> 7);
+    if (i < n && s0 < n) {
+      const uint64_t k = f.keys[i];
+      uint64_t x[16];
+#pragma unroll
+      for (uint32_t e = 0; e < 16; ++e) x[e] = (s0 + e < n) ? f.keys[s0 + e] : ~0ull;
+      uint32_t r = 0;
+#pragma unroll
+      for (uint32_t e = 0; e < 16; ++e) r += (x[e] < k) ? 1u : 0u;
+      if (r) __atomic_fetch_add(&rk[i], r, __ATOMIC_RELAXED);
+    }
+  }
+  SY::sync();
+  if (tid < n) f.skeys[rk[tid]] = f.keys[tid];
+  SY::sync();
+  // ---- min-p / top-k / top-p / draw in wave 0
+  uint32_t res = 2;
+  if (tid < WAVE) {
+    const int lane = (int)tid;
+    const uint64_t k0 = (uint32_t)lane < n ? f.skeys[lane] : 0ull;
+    const uint64_t k1 = (uint32_t)lane + 64 < n ? f.skeys[64 + lane] : 0ull;
+    float p0 = (uint32_t)lane < n ? __uint_as_float(~(uint32_t)(k0 >> 32)) : 0.0f;
+    float p1 = (uint32_t)lane + 64 < n ? __uint_as_float(~(uint32_t)(k1 >> 32)) : 0.0f;
+    const uint32_t i0 = (uint32_t)k0, i1 = (uint32_t)k1;
+    uint32_t tok = 0, len = 0;
+    // f.keys is free once sorted into skeys
+    bool good = semantics_regs(P, u, n, a.V, p0, p1, i0, i1, lane, (LDS float*)f.keys, tok, len);
+    if (good && a.out_cap && len > n && a.out_cap > n) good = false;
+    if (good) {
+      if (lane == 0) {
+        G(a.out_tok)[b] = tok;
+        if (a.out_cnt) G(a.out_cnt)[b] = len;
+      }
+      const uint32_t no = len < a.out_cap ? len : a.out_cap;
+      const uint64_t ob = (uint64_t)b * a.out_cap;
+      if ((uint32_t)lane < no) {
+        if (a.out_ids) G(a.out_ids)[ob + lane] = i0;
+        if (a.out_probs) G(a.out_probs)[ob + lane] = p0;
+      }
+      if ((uint32_t)lane + 64 < no) {
+        if (a.out_ids) G(a.out_ids)[ob + 64 + lane] = i1;
+        if (a.out_probs) G(a.out_probs)[ob + 64 + lane] = p1;
+      }
+    }
+    res = good ? 0u : 2u;
+    if (lane == 0) f.fm[F_DONE] = res;
+  }
+  SY::sync();
+  return f.fm[F_DONE];
+}
+
 // seg_own: for a single-segment row, this workgroup's (count, beta, flags).
 template <int DT>
 __device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_t b,
@@ -1487,7 +1630,7 @@ __device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_
   const int lane = (int)(tid & 63), wv = (int)(tid >> 6);
   const FinLds f = fin_carve(smem);
   const uint32_t nslots = a.ntiles + (have_vt ? a.nchunks : 0u);
-  uint32_t path = 2;  // 0 done, 1 workgroup candidate path, 2 slow path
+  uint32_t path = 2;  // 0 done, 1 workgroup candidate path, 2 slow path, 3 fast path
   const float u = G(a.u)[b];
   if (wv == 0) {
     // ---- partials: row maximum L, then the normaliser S as balanced trees
@@ -1561,7 +1704,7 @@ __device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_
         f.fm[F_LAM] = lam;
       }
       if (!(L == NEG_INF || P.Kc == 0 || ovf))
-        path = candidate_path<WaveSync>(a, w, b, P, S, m, u, total, lam, f, WAVE_GATHER, WAVE_KEEP);
+        path = (a.G == 1 && total <= LCAP) ? 3u : 1u;
     }
     if (lane == 0) f.fm[F_DONE] = path;
   }
@@ -1569,6 +1712,10 @@ __device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_
   path = f.fm[F_DONE];
   if (path == 0) return;
   const float S = __uint_as_float(f.fm[F_S]), m = __uint_as_float(f.fm[F_M]);
+  if (path == 3) {
+    path = candidate_fast(a, b, P, S, m, u, f.fm[F_TOTAL], f.fm[F_LAM], f);
+    if (path == 0) return;
+  }
   if (path == 1) {
     const uint32_t total = f.fm[F_TOTAL], lam = f.fm[F_LAM];
     __syncthreads();
@@ -1890,6 +2037,8 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   // tiles and reduced in virtual tiles, one per 16-tile chunk
   const bool have = h1 > h0;
   const bool need_cnt = have && P.fp != 0.0f;
+  // no more distinct history tokens than ranks: no token can be dropped
+  const bool early = h1 - h0 <= U_MAX;
   const bool collect = P.mode == MODE_SAMPLE && P.Kc > 0;
   const void* row = (const char*)a.logits +
                     (uint64_t)b * a.stride * (DT == LLMK_F32 ? 4u : 2u);
@@ -1930,7 +2079,6 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   if (tb2 != EMPTY) load_tile<DT>(a, row, mrow, h, tb2, lane, rb);
   // The history tables: the bitmap of the segment's history tokens, their
   // ranks and, for the frequency penalty, occurrence counts by rank.
-  uint32_t U = 0;
   if (have) {
     const uint32_t step = TQ * TW * WAVE;
     auto each_token = [&](auto&& fn) __attribute__((always_inline)) {
@@ -1953,16 +2101,30 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
         __atomic_fetch_or(&h.bitmap[(t - lo) >> 5], 1u << (t & 31), __ATOMIC_RELAXED);
       });
     __syncthreads();
-    U = build_ranks(h, nwords, btot, &misc[M_FLAGS]);
-    if (need_cnt) {
-      if (tok_wave)
-        each_token([&](uint32_t t) {
-          const uint32_t o = t - lo, wd = h.bitmap[o >> 5], bit = 1u << (o & 31);
-          if (wd & bit) {  // not dropped by the rank limit
-            const uint32_t r = h.pre[o >> 5] + (uint32_t)__popc(wd & (bit - 1u));
-            __atomic_fetch_add(&((LDS uint32_t*)h.pen)[r], 1u, __ATOMIC_RELAXED);
-          }
-        });
+    auto counts = [&]() __attribute__((always_inline)) {
+      each_token([&](uint32_t t) {
+        const uint32_t o = t - lo, wd = h.bitmap[o >> 5], bit = 1u << (o & 31);
+        if (wd & bit) {  // not dropped by the rank limit
+          const uint32_t r = h.pre[o >> 5] + (uint32_t)__popc(wd & (bit - 1u));
+          __atomic_fetch_add(&((LDS uint32_t*)h.pen)[r], 1u, __ATOMIC_RELAXED);
+        }
+      });
+    };
+    if (early) {
+      // At most U_MAX distinct tokens: the bitmap is final, so the other
+      // waves go on to their tiles while the token waves build the ranks.
+      if (tok_wave) {
+        GroupSync gs{&misc[M_GSYNC], TW, 0};
+        const uint32_t U = build_ranks(h, nwords, btot, &misc[M_FLAGS], TW, gs);
+        if (need_cnt) counts();
+        if (tid == 0) misc[M_U] = U;
+        gs();  // the tables are ready once all TW waves arrive a third time
+      }
+    } else {
+      BarrierSync bs;
+      const uint32_t U = build_ranks(h, nwords, btot, &misc[M_FLAGS], NW, bs);
+      if (need_cnt && tok_wave) counts();
+      if (tid == 0) misc[M_U] = U;
       __syncthreads();
     }
   }
@@ -2011,18 +2173,36 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
     const uint32_t t = t0 + 2u * NW + k;
     return t < t1 ? t : EMPTY;
   };
-  // Wave w reduces the virtual tiles of chunks w, w + NW, ... after its first
-  // vocabulary tile.
+  // Virtual tiles (history chunks) are claimed one at a time between
+  // vocabulary tiles once the tables are ready; a wave with no tile left
+  // waits for them.
+  const uint32_t ready_at = early ? 3u * TW : 0u;
+  bool vmore = have;
+  auto vtile_step = [&](bool wait) __attribute__((always_inline)) {
+    if (__atomic_load_n(&misc[M_GSYNC], __ATOMIC_RELAXED) < ready_at) {
+      if (!wait) return;
+      while (__atomic_load_n(&misc[M_GSYNC], __ATOMIC_RELAXED) < ready_at)
+        __builtin_amdgcn_s_sleep(2);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    uint32_t k = 0;
+    if (lane == 0) k = __atomic_fetch_add(&misc[M_VNEXT], 1u, __ATOMIC_RELAXED);
+    k = (uint32_t)__builtin_amdgcn_readfirstlane((int)k);
+    if (k >= nch) {
+      vmore = false;
+      return;
+    }
+    vtile_chunk<DT>(a, P, b, row, t0, nwords, k, misc[M_U], h, need_cnt, E, lane);
+  };
   if (ta != EMPTY) {
     process(ra, ta);
     ta = grab();
     if (ta != EMPTY) load_tile<DT>(a, row, mrow, h, ta, lane, ra);
   }
-  if (have)
-    for (uint32_t k = (uint32_t)wv; k < nch; k += NW)
-      vtile_chunk<DT>(a, P, b, row, t0, nwords, k, U, h, need_cnt, E, lane);
   for (;;) {
-    if (ta == EMPTY && tb2 == EMPTY) break;
+    const bool tiles = ta != EMPTY || tb2 != EMPTY;
+    if (!tiles && !vmore) break;
+    if (vmore) vtile_step(!tiles);
     if (tb2 != EMPTY) {
       process(rb, tb2);
       tb2 = grab();

@@ -158,15 +158,24 @@ def test_invalid_parameters_and_status(sampler):
     assert sampler.status() == 0  # reading clears it
 
 
-def test_history_overflow_is_reported(sampler):
-    """More distinct history tokens in one vocabulary segment than the LDS
-    table holds raises LLMK_STATUS_HISTORY_OVERFLOW."""
+def test_history_overflow_keeps_the_first_ranks(sampler):
+    """Past 8192 distinct history tokens in one vocabulary segment (16384
+    tokens for a one-row batch of this vocabulary), the segment's later
+    tokens by id are sampled as ordinary tokens, and the status word says
+    so.  The result equals the oracle's on the history without them."""
     V = 151936
     lg = np.random.default_rng(8).normal(0, 3, (1, V)).astype(np.float32)
-    w = workload(lg, T=0.8, K=40, P=0.95, R=1.1, hists=[np.arange(20000)], u=0.3)
+    hist = np.concatenate([np.arange(20000), [5, 5, 9000, 17000, 17000]])
+    kept = hist[(hist < 8192) | (hist >= 16384)]  # segment 1 holds 3616 < 8192
+    args = dict(T=0.8, K=40, P=0.95, R=1.1, PR=0.3, FR=0.2, u=0.3)
+    w = workload(lg, hists=[hist], **args)
+    sampler.status()
     print("[case] history overflow", flush=True)
-    run_gpu(sampler, w, 0)
+    gpu = run_gpu(sampler, w, CAP)
     assert sampler.status() & _lib.LLMK_STATUS_HISTORY_OVERFLOW
+    w2 = workload(lg, hists=[kept], **args)
+    orc = O.sample_workload(O.MIRROR, w2, out_cap=CAP, nthreads=16)
+    assert_bit_exact(w2, gpu, orc, CAP, "history overflow")
 
 
 def test_host_errors(sampler):
