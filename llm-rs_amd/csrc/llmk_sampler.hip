@@ -889,17 +889,15 @@ __device__ __forceinline__ float rl(float x, uint32_t j) {
 // + p_l and lane l of c1 the prefix through entry 64 + l -- the same f32
 // additions in the same order as one sequential sum.  z holds 64 zeros before
 // each half of the entries; lane l reads z[1 + l + t] at step t = 0..63, so it
-// adds 63 - l zeros (+0.0 + +0.0 stays +0.0) and then p_0..p_l.  Steps whose
-// reads are zeros for every lane below m are skipped.  Two operations per
-// entry (an LDS read and an add), no selects.  Lanes at or past m hold junk.
-__device__ __forceinline__ float prefix_half(LDS const float* zb, uint32_t m, float c) {
-  for (uint32_t t = (64u - m) & ~7u; t < 64u; t += 8) {
-    float x[8];
+// adds 63 - l zeros (+0.0 + +0.0 stays +0.0) and then p_0..p_l.  All 64 reads
+// are issued before the adds and there is no branch: two operations per step.
+// Lanes at or past m hold junk.
+__device__ __forceinline__ float prefix_half(LDS const float* zb, float c) {
+  float x[64];
 #pragma unroll
-    for (uint32_t q = 0; q < 8; ++q) x[q] = zb[t + q];
+  for (uint32_t t = 0; t < 64u; ++t) x[t] = zb[t];
 #pragma unroll
-    for (uint32_t q = 0; q < 8; ++q) c = c + x[q];
-  }
+  for (uint32_t t = 0; t < 64u; ++t) c = c + x[t];
   return c;
 }
 // z: 256 LDS words owned by the calling wave; 1 <= m <= 128.
@@ -910,9 +908,9 @@ __device__ __forceinline__ void prefix_regs(float p0, float p1, uint32_t m, int 
   z[128 + lane] = 0.0f;
   z[192 + lane] = p1;
   WaveSync::sync();
-  c0 = prefix_half(z + 1 + lane, m < 64u ? m : 64u, 0.0f);
+  c0 = prefix_half(z + 1 + lane, 0.0f);
   c1 = 0.0f;
-  if (m > 64u) c1 = prefix_half(z + 129 + lane, m - 64u, rl(c0, 63));
+  if (m > 64u) c1 = prefix_half(z + 129 + lane, rl(c0, 63));
   WaveSync::sync();  // z is rewritten by the next call
 }
 // ((p_0 + p_1) + ...) + p_{m-1}
