@@ -26,6 +26,19 @@ HBM_PEAK_GBPS = 8000.0
 MALL_BYTES = 256 << 20
 
 
+def measured_traffic(config):
+    """HBM bytes per launch of the stream kernel from the committed counter
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy), or None."""
+    import re
+    path = os.path.join(ROOT, "profiles", f"stream_kernel_{config}_hbm_traffic.md")
+    try:
+        with open(path) as f:
+            m = re.search(r"^traffic_bytes_per_launch = (\d+)$", f.read(), re.M)
+        return int(m.group(1)) if m else None
+    except OSError:
+        return None
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -71,6 +84,9 @@ def main():
     ap.add_argument("--config", default="C3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--sets", type=int, default=0, help="logit copies rotated (0 = auto)")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                    help="only run a plain device-to-device copy of BYTES, 10 times (the "
+                         "reference kernel for scaling HBM traffic counters)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -80,6 +96,15 @@ def main():
 
     import numpy as np
     import torch
+    if args.copy_probe:
+        n = args.copy_probe // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": 4 * n, "copies": 10}), flush=True)
+        return
     import llmk
     from llmk import synth
     w = synth.make(args.config)
@@ -104,36 +129,32 @@ def main():
     torch.cuda.synchronize()
 
     K = args.steps
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
+    # timed steps: K back-to-back launches between two events (the job rate)
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_start.record(stream)
     for i in range(K):
-        ev[i][0].record(stream)
         s.launch(dbs[i % nsets], tok, out_count=cnt, stream=stream)
-        ev[i][1].record(stream)
     t_end.record(stream)
     torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_end)
-    kern_ms = [a.elapsed_time(b) for a, b in ev]
     ms_per_step = total_ms / K
-    kern_avg_ms = float(np.mean(kern_ms))
     value = B / (ms_per_step * 1e-3)
+    # the kernel's own duration: K more launches, each between two events on
+    # the launch stream
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
+    for i in range(K):
+        ev[i][0].record(stream)
+        s.launch(dbs[i % nsets], tok, out_count=cnt, stream=stream)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    kern_ms = [a.elapsed_time(b) for a, b in ev]
+    kern_avg_ms = float(np.mean(kern_ms))
     achieved = step_bytes / (kern_avg_ms * 1e-3) / 1e9
 
-    # same-buffer (Infinity-Cache-warm) rate, for reference only
-    torch.cuda.synchronize()
-    a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a0.record(stream)
-    for i in range(K):
-        s.launch(db0, tok, out_count=cnt, stream=stream)
-    a1.record(stream)
-    torch.cuda.synchronize()
-    warm_ms = a0.elapsed_time(a1) / K
-
     log(f"[bench] {w.name}: {ms_per_step*1e3:.2f} us/step (kernel avg {kern_avg_ms*1e3:.2f} us, "
-        f"min {min(kern_ms)*1e3:.2f}, max {max(kern_ms)*1e3:.2f}), warm {warm_ms*1e3:.2f} us, "
+        f"min {min(kern_ms)*1e3:.2f}, max {max(kern_ms)*1e3:.2f}), "
         f"{achieved:.0f} GB/s algorithmic, sets {nsets}")
 
     cpu = None
@@ -168,11 +189,10 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBPS,
-            "traffic": None,
+            "traffic": measured_traffic(args.config),
             "kernel": "llmk::stream_kernel",
             "kernel_avg_us": kern_avg_ms * 1e3,
         },
-        "warm_us_per_step": warm_ms * 1e3,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -1725,7 +1725,7 @@ __device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_
 }
 
 // ---------------------------------------------------------------------------
-// Per-tile reduction, shared by vocabulary tiles and virtual (history) tiles
+// Per-tile reduction of the vocabulary tiles
 // ---------------------------------------------------------------------------
 struct TileEnv {
   RowP P;
@@ -1882,9 +1882,9 @@ __device__ __forceinline__ float exclude(float v, uint32_t x, uint32_t pos) {
 
 // ---------------------------------------------------------------------------
 // Virtual tiles: the history tokens of one 16-tile chunk, reduced by one
-// wave.  Lane l owns chunk tokens 256l .. 256l+255 (bitmap words 8l..8l+7 of
-// the chunk); its terms are summed sequentially in increasing token order,
-// the lanes by a balanced tree.
+// wave.  The chunk's j-th token (in increasing id) belongs to lane j mod 64,
+// which sums its terms sequentially in that order; the lanes are combined by
+// a balanced tree.
 // ---------------------------------------------------------------------------
 constexpr int VB = 8;  // rounds of 64 ranks gathered together
 
