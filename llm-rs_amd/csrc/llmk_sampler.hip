@@ -1583,53 +1583,59 @@ __device__ __forceinline__ uint32_t candidate_fast(const Args& a, uint32_t b, co
   SY::sync();
   if (tid < n) f.skeys[rk[tid]] = f.keys[tid];
   SY::sync();
-  // ---- min-p / top-k / top-p / draw in wave 0
-  uint32_t res = 2;
+  // ---- min-p / top-k / top-p / draw in wave 0; the outputs are written
+  // after the barrier that publishes the result, which then waits for no
+  // global store
+  float p0 = 0.0f, p1 = 0.0f;
+  uint32_t i0 = 0, i1 = 0, tok = 0, len = 0;
+  bool good = false;
   if (tid < WAVE) {
     const int lane = (int)tid;
     const uint64_t k0 = (uint32_t)lane < n ? f.skeys[lane] : 0ull;
     const uint64_t k1 = (uint32_t)lane + 64 < n ? f.skeys[64 + lane] : 0ull;
-    float p0 = (uint32_t)lane < n ? __uint_as_float(~(uint32_t)(k0 >> 32)) : 0.0f;
-    float p1 = (uint32_t)lane + 64 < n ? __uint_as_float(~(uint32_t)(k1 >> 32)) : 0.0f;
-    const uint32_t i0 = (uint32_t)k0, i1 = (uint32_t)k1;
-    uint32_t tok = 0, len = 0;
+    p0 = (uint32_t)lane < n ? __uint_as_float(~(uint32_t)(k0 >> 32)) : 0.0f;
+    p1 = (uint32_t)lane + 64 < n ? __uint_as_float(~(uint32_t)(k1 >> 32)) : 0.0f;
+    i0 = (uint32_t)k0;
+    i1 = (uint32_t)k1;
     // f.keys is free once sorted into skeys
-    bool good = semantics_regs(P, u, n, a.V, p0, p1, i0, i1, lane, (LDS float*)f.keys, tok, len);
+    good = semantics_regs(P, u, n, a.V, p0, p1, i0, i1, lane, (LDS float*)f.keys, tok, len);
     if (good && a.out_cap && len > n && a.out_cap > n) good = false;
-    if (good) {
-      if (lane == 0) {
-        G(a.out_tok)[b] = tok;
-        if (a.out_cnt) G(a.out_cnt)[b] = len;
-      }
-      const uint32_t no = len < a.out_cap ? len : a.out_cap;
-      const uint64_t ob = (uint64_t)b * a.out_cap;
-      if ((uint32_t)lane < no) {
-        if (a.out_ids) G(a.out_ids)[ob + lane] = i0;
-        if (a.out_probs) G(a.out_probs)[ob + lane] = p0;
-      }
-      if ((uint32_t)lane + 64 < no) {
-        if (a.out_ids) G(a.out_ids)[ob + 64 + lane] = i1;
-        if (a.out_probs) G(a.out_probs)[ob + 64 + lane] = p1;
-      }
-    }
-    res = good ? 0u : 2u;
-    if (lane == 0) f.fm[F_DONE] = res;
+    if (lane == 0) f.fm[F_DONE] = good ? 0u : 2u;
   }
   SY::sync();
-  return f.fm[F_DONE];
+  const uint32_t res = f.fm[F_DONE];
+  if (tid < WAVE && res == 0) {
+    const int lane = (int)tid;
+    if (lane == 0) {
+      G(a.out_tok)[b] = tok;
+      if (a.out_cnt) G(a.out_cnt)[b] = len;
+    }
+    const uint32_t no = len < a.out_cap ? len : a.out_cap;
+    const uint64_t ob = (uint64_t)b * a.out_cap;
+    if ((uint32_t)lane < no) {
+      if (a.out_ids) G(a.out_ids)[ob + lane] = i0;
+      if (a.out_probs) G(a.out_probs)[ob + lane] = p0;
+    }
+    if ((uint32_t)lane + 64 < no) {
+      if (a.out_ids) G(a.out_ids)[ob + 64 + lane] = i1;
+      if (a.out_probs) G(a.out_probs)[ob + 64 + lane] = p1;
+    }
+  }
+  return res;
 }
 
-// seg_own: for a single-segment row, this workgroup's (count, beta, flags).
+// seg_own: for a single-segment row, this workgroup's (count, beta, flags);
+// u: the row's uniform (loaded with the parameters, so that no global load
+// is outstanding at the finalize's barriers).
 template <int DT>
 __device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_t b,
                                              const RowP& P, bool have_vt, u4v seg_own,
-                                             LDS uint32_t* smem) {
+                                             float u, LDS uint32_t* smem) {
   const uint32_t tid = threadIdx.x;
   const int lane = (int)(tid & 63), wv = (int)(tid >> 6);
   const FinLds f = fin_carve(smem);
   const uint32_t nslots = a.ntiles + (have_vt ? a.nchunks : 0u);
   uint32_t path = 2;  // 0 done, 1 workgroup candidate path, 2 slow path, 3 fast path
-  const float u = G(a.u)[b];
   if (wv == 0) {
     // ---- partials: row maximum L, then the normaliser S as balanced trees
     // of 64 slots and a tree over those (next_pow2(slots) >= 64, padding 0)
@@ -2002,6 +2008,7 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   uint32_t b, g;
   wg_to_row_seg(a, blockIdx.x, b, g);
   const RowP P = row_params(a, b);
+  const float u_row = G(a.u)[b];
   if (P.mode == MODE_INVALID) {
     if (g == 0 && tid == 0) {
       a.out_tok[b] = LLMK_INVALID_TOKEN;
@@ -2142,19 +2149,25 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   uint32_t since = EMPTY;
   const uint32_t nch = (nwords + 511) / 512;  // chunks of this segment
 
-  const bool xmask = have || mrow != nullptr;
   const uint32_t sh4 = (4u * (uint32_t)lane) & 31u;
   auto process = [&](const Raw& raw, uint32_t t) __attribute__((always_inline)) {
     float v[16];
     unpack<DT>(raw, v);
     const uint32_t tb = t * TILE;
-    if (xmask) {
-      // history tokens and disallowed tokens become -inf
+    // history tokens and disallowed tokens become -inf (a uniform branch per
+    // case, so a row without a mask spends nothing on one)
+    if (mrow) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        uint32_t x = 0;
-        if (have) x = h.bitmap[((tb - lo) >> 5) + 8u * r + ((uint32_t)lane >> 3)];
-        if (mrow) x |= ~raw.mw[r];
+        uint32_t x = ~raw.mw[r];
+        if (have) x |= h.bitmap[((tb - lo) >> 5) + 8u * r + ((uint32_t)lane >> 3)];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[4 * r + q] = exclude(v[4 * r + q], x, sh4 + q);
+      }
+    } else if (have) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t x = h.bitmap[((tb - lo) >> 5) + 8u * r + ((uint32_t)lane >> 3)];
 #pragma unroll
         for (int q = 0; q < 4; ++q) v[4 * r + q] = exclude(v[4 * r + q], x, sh4 + q);
       }
@@ -2238,7 +2251,7 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   const u4v seg_own = u4v{misc[M_CCOUNT], misc[M_BETA], misc[M_FLAGS], 0u};
   __syncthreads();  // finalize reuses this shared memory
   if (!last) return;
-  finalize_row<DT>(a, w, b, P, have, seg_own, sm);
+  finalize_row<DT>(a, w, b, P, have, seg_own, u_row, sm);
 }
 
 }  // namespace llmk
