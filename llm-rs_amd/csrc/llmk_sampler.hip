@@ -314,48 +314,37 @@ __device__ __forceinline__ void hist_carve(Hist& h, LDS uint32_t* base, uint32_t
 }
 
 // Ranks of the segment's history tokens once its bitmap is complete, built
-// by waves 0 .. nw-1, which call sync() together twice (the second time at
-// the end).  Blocks of 64 words, one word per lane,
-// wave w taking blocks w, w + nw, ...: pre[w] = history tokens in the words
-// before w, tokr[r] = the token of rank r (tokens in increasing order).
-// Tokens of rank >= U_MAX are cleared from the bitmap and the overflow flag
-// is raised: they are then ordinary, unpenalised tokens.  Returns the number
-// of ranks (<= U_MAX).  btot: nwords / 64 words of scratch (nwords <= 32768).
+// by the first nw waves, which call sync() together twice (the second time
+// at the end).  Thread i of them owns a contiguous run of bitmap words: the
+// run's popcount, an exclusive scan over the threads, then pre[w] = history
+// tokens in the words before w and tokr[r] = the token of rank r (tokens in
+// increasing order).  Tokens of rank >= U_MAX are cleared from the bitmap
+// and the overflow flag is raised: they are then ordinary, unpenalised
+// tokens.  Returns the number of ranks (<= U_MAX).  wtot: nw words.
 template <class Sync>
 __device__ __forceinline__ uint32_t build_ranks(const Hist& h, uint32_t nwords,
-                                                LDS uint32_t* btot, LDS uint32_t* flags,
+                                                LDS uint32_t* wtot, LDS uint32_t* flags,
                                                 uint32_t nw, Sync& sync) {
-  const int lane = (int)(threadIdx.x & 63), wv = (int)(threadIdx.x >> 6);
-  const uint32_t nblk = (nwords + 63) / 64;
-  for (uint32_t j = (uint32_t)wv; j < nblk; j += nw) {
-    const uint32_t wi = 64 * j + (uint32_t)lane;
-    const uint32_t c = wi < nwords ? (uint32_t)__popc(h.bitmap[wi]) : 0u;
-    const uint32_t t = bcast63u(wave_incl_scan(c));
-    if (lane == 0) btot[j] = t;
-  }
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
+  const uint32_t per = (nwords + 64u * nw - 1u) / (64u * nw);
+  const uint32_t w0 = tid * per < nwords ? tid * per : nwords;
+  const uint32_t w1 = w0 + per < nwords ? w0 + per : nwords;
+  uint32_t c = 0;
+  for (uint32_t wi = w0; wi < w1; ++wi) c += (uint32_t)__popc(h.bitmap[wi]);
+  const uint32_t incl = wave_incl_scan(c);
+  if (lane == 63) wtot[wv] = incl;
   sync();
-  // every wave scans the block totals: lane L holds blocks 8L .. 8L+7
-  uint32_t bl[8], ls = 0;
-#pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const uint32_t j = 8u * (uint32_t)lane + q;
-    bl[q] = j < nblk ? btot[j] : 0u;
-    ls += bl[q];
+  uint32_t r = incl - c, total = 0;
+  for (uint32_t i = 0; i < nw; ++i) {
+    const uint32_t t = wtot[i];
+    r += i < wv ? t : 0u;
+    total += t;
   }
-  const uint32_t lincl = wave_incl_scan(ls);
-  const uint32_t total = bcast63u(lincl);
-  for (uint32_t j = (uint32_t)wv; j < nblk; j += nw) {
-    const uint32_t sub = j & 7u;
-    uint32_t mine = lincl - ls;
-#pragma unroll
-    for (uint32_t q = 0; q < 8; ++q) mine += q < sub ? bl[q] : 0u;
-    const uint32_t base = (uint32_t)__builtin_amdgcn_readlane((int)mine, (int)(j >> 3));
-    const uint32_t wi = 64 * j + (uint32_t)lane;
-    uint32_t bits = wi < nwords ? h.bitmap[wi] : 0u;
-    const uint32_t c = (uint32_t)__popc(bits);
-    uint32_t r = base + wave_incl_scan(c) - c;
-    if (wi < nwords) h.pre[wi] = (uint16_t)(r < U_MAX ? r : U_MAX);
-    if (r + c > U_MAX) {  // keep the first U_MAX - r tokens of the word
+  for (uint32_t wi = w0; wi < w1; ++wi) {
+    uint32_t bits = h.bitmap[wi];
+    const uint32_t cw = (uint32_t)__popc(bits);
+    h.pre[wi] = (uint16_t)(r < U_MAX ? r : U_MAX);
+    if (r + cw > U_MAX) {  // keep the first U_MAX - r tokens of the word
       const uint32_t keep = r < U_MAX ? U_MAX - r : 0u;
       uint32_t kept = 0, rest = bits;
       for (uint32_t k = 0; k < keep; ++k) {
@@ -371,7 +360,7 @@ __device__ __forceinline__ uint32_t build_ranks(const Hist& h, uint32_t nwords,
       h.tokr[r++] = h.lo + 32u * wi + bit;
     }
   }
-  if (total > U_MAX && threadIdx.x == 0) __atomic_fetch_or(flags, FLAG_HIST_OVERFLOW, __ATOMIC_RELAXED);
+  if (total > U_MAX && tid == 0) __atomic_fetch_or(flags, FLAG_HIST_OVERFLOW, __ATOMIC_RELAXED);
   sync();
   return total < U_MAX ? total : U_MAX;
 }
@@ -1018,13 +1007,11 @@ __device__ __forceinline__ bool semantics_regs(const RowP& P, float u, uint32_t 
 enum : uint32_t {
   M_BETA = 0, M_CCOUNT = 1, M_FLAGS = 2, M_LAST = 3, M_NEXT = 4,
   M_GSYNC = 5,  // arrivals of the token waves' group barrier
-  M_VNEXT = 6,  // next virtual tile to claim
-  M_U = 7,      // history ranks of the segment
   M_NMISC = 16
 };
 
 __host__ __device__ inline size_t stream_lds_words(uint32_t tps) {
-  return 64 + M_NMISC + NBINS + 64 + hist_lds_words(tps * 32) + ((tps * 32 / 64 + 3) & ~3u);
+  return 64 + M_NMISC + NBINS + 64 + hist_lds_words(tps * 32) + NW;
 }
 __host__ __device__ inline size_t finalize_lds_words() {
   // slots (2 x MAX_SLOTS) + keys + sorted keys (2 x SORT_CAP u64) + p + idx
@@ -1892,37 +1879,25 @@ __device__ __forceinline__ float exclude(float v, uint32_t x, uint32_t pos) {
 // which sums its terms sequentially in that order; the lanes are combined by
 // a balanced tree.
 // ---------------------------------------------------------------------------
-constexpr int VB = 8;  // rounds of 64 ranks gathered together
+constexpr int VB = 8;  // gathers in flight per thread
 
-// The virtual tile of chunk kk of the segment: its history tokens are the
-// ranks [r0, r1) (pre at the chunk's first word and past its last);
-// lane L takes ranks r0 + L, r0 + L + 64, ... in increasing order.  Pass 1
-// gathers the logits (VB rounds of loads in flight), penalises them, keeps
-// them in pen[] (over the counts) and forms the maximum; pass 2 sums the
-// terms per lane in rank order, then as a balanced tree over the lanes.
+// The penalised, masked logit of every history rank r < U into pen[r] (over
+// the counts), by the first nw waves of the workgroup: VB gathers in flight
+// per thread, then the arithmetic.
 template <int DT>
-__device__ __forceinline__ void vtile_chunk(const Args& a, const RowP& P, uint32_t b,
-                                         const void* row, uint32_t t0, uint32_t nwords,
-                                         uint32_t kk, uint32_t U, const Hist& h,
-                                         bool need_cnt, const TileEnv& E, int lane) {
-  const uint32_t wf = 512u * kk;
-  const uint32_t r0 = h.pre[wf];
-  const uint32_t r1 = wf + 512u < nwords ? (uint32_t)h.pre[wf + 512u] : U;
-  const uint32_t n = r1 - r0;
-  const uint32_t slot = a.ntiles + t0 / CHUNK_TILES + kk;
+__device__ __forceinline__ void gather_penalised(const Args& a, const RowP& P, uint32_t b,
+                                                 const void* row, uint32_t U, const Hist& h,
+                                                 bool need_cnt, uint32_t nw) {
+  const uint32_t tid = threadIdx.x, step = nw * WAVE;
   const GLB uint32_t* mrow = a.mask ? G(a.mask) + (uint64_t)b * a.mask_words : nullptr;
-  const bool greedy = E.P.mode == MODE_GREEDY;
-  LDS float* pen = h.pen + r0;
-  LDS const uint32_t* cnt = (LDS const uint32_t*)h.pen + r0;
-  LDS const uint32_t* tokr = h.tokr + r0;
-  float lm = NEG_INF;
-  for (uint32_t j0 = 0; j0 < n; j0 += 64u * VB) {
+  LDS const uint32_t* cnt = (LDS const uint32_t*)h.pen;
+  for (uint32_t r0 = 0; r0 < U; r0 += VB * step) {
     uint32_t tk[VB], mw[VB];
     float x[VB];
 #pragma unroll
     for (int i = 0; i < VB; ++i) {
-      const uint32_t r = j0 + 64u * i + (uint32_t)lane;
-      tk[i] = r < n ? tokr[r] : EMPTY;
+      const uint32_t r = r0 + i * step + tid;
+      tk[i] = r < U ? h.tokr[r] : EMPTY;
     }
 #pragma unroll
     for (int i = 0; i < VB; ++i) {
@@ -1931,18 +1906,36 @@ __device__ __forceinline__ void vtile_chunk(const Args& a, const RowP& P, uint32
     }
 #pragma unroll
     for (int i = 0; i < VB; ++i) {
-      const uint32_t r = j0 + 64u * i + (uint32_t)lane;
+      const uint32_t r = r0 + i * step + tid;
       if (tk[i] != EMPTY) {
         float y = (x[i] > NEG_INF) ? x[i] : NEG_INF;  // NaN acts as -inf
         y = penalize(y, P, need_cnt ? cnt[r] : 1u);
         if (!((mw[i] >> (tk[i] & 31)) & 1u)) y = NEG_INF;
-        pen[r] = y;
-        lm = fmaxf(lm, y);
+        h.pen[r] = y;
       }
     }
   }
+}
+
+// The virtual tile of chunk kk of the segment: its history tokens are the
+// ranks [r0, r1) (pre at the chunk's first word and past its last), their
+// penalised values already in pen[]; lane L takes ranks r0 + L, r0 + L + 64,
+// ... in increasing order.  The maximum, then the terms summed per lane in
+// rank order and as a balanced tree over the lanes, then the candidates.
+__device__ __forceinline__ void vtile_chunk(const Args& a, uint32_t t0, uint32_t nwords,
+                                         uint32_t kk, uint32_t U, const Hist& h,
+                                         const TileEnv& E, int lane) {
+  const uint32_t wf = 512u * kk;
+  const uint32_t r0 = h.pre[wf];
+  const uint32_t r1 = wf + 512u < nwords ? (uint32_t)h.pre[wf + 512u] : U;
+  const uint32_t n = r1 - r0;
+  const uint32_t slot = a.ntiles + t0 / CHUNK_TILES + kk;
+  const bool greedy = E.P.mode == MODE_GREEDY;
+  LDS const float* pen = h.pen + r0;
+  LDS const uint32_t* tokr = h.tokr + r0;
+  float lm = NEG_INF;
+  for (uint32_t r = (uint32_t)lane; r < n; r += 64u) lm = fmaxf(lm, pen[r]);
   lm = wave_max(lm);
-  WaveSync::sync();  // pen[] written by this wave's lanes, read across them below
   if (greedy) {
     // the first (lowest) token holding the maximum; all -inf: the first token
     uint32_t bi = EMPTY;
@@ -2029,7 +2022,7 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   const uint32_t nwords = (t1 - t0) * 32;
   Hist h;
   hist_carve(h, hb, nwords);
-  LDS uint32_t* btot = hb + hist_lds_words(nwords);  // nwords / 64
+  LDS uint32_t* btot = hb + hist_lds_words(nwords);  // NW words
   h.lo = lo;
   const bool need_pen = P.rp != 1.0f || P.pp != 0.0f || P.fp != 0.0f;
   uint32_t h0 = 0, h1 = 0;
@@ -2080,10 +2073,31 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
 #pragma unroll
   for (int q = 0; q < TQ; ++q) asm volatile("" ::"v"(tk[q]));
   __syncthreads();
+  // the logits of the first pass's history tokens, requested ahead of the
+  // tiles so that the gather after the rank tables finds them in L2
+  float pf[TQ];
+#pragma unroll
+  for (int q = 0; q < TQ; ++q)
+    pf[q] = (have && tk[q] >= lo && tk[q] < hi) ? load_logit<DT>(row, tk[q]) : 0.0f;
   if (ta != EMPTY) load_tile<DT>(a, row, mrow, h, ta, lane, ra);
   if (tb2 != EMPTY) load_tile<DT>(a, row, mrow, h, tb2, lane, rb);
+  TileEnv E;
+  E.P = P;
+  E.c2 = LOG2E_F / P.T;
+  E.V = a.V;
+  E.collect = collect;
+  E.recompute_at = P.Kc / 4 > 8 ? P.Kc / 4 : 8;
+  E.misc = misc;
+  E.hf = hf;
+  E.hcoarse = hcoarse;
+  E.cbuf = G(w.cand) + (uint64_t)blockIdx.x * CAND_CAP;
+  E.part = G(w.tile_part) + (uint64_t)b * MAX_SLOTS;
+  E.lpart = a.G == 1 ? (LDS f2v*)(smem + a.lds_part) : nullptr;
+  E.lcand = a.G == 1 ? (LDS u2v*)(smem + a.lds_cand) : nullptr;
+  const uint32_t nch = (nwords + 511) / 512;  // chunks of this segment
   // The history tables: the bitmap of the segment's history tokens, their
-  // ranks and, for the frequency penalty, occurrence counts by rank.
+  // ranks, for the frequency penalty occurrence counts by rank, and the
+  // penalised logits by rank; then the virtual tiles (one per 16-tile chunk).
   if (have) {
     const uint32_t step = TQ * TW * WAVE;
     auto each_token = [&](auto&& fn) __attribute__((always_inline)) {
@@ -2117,37 +2131,35 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
     };
     if (early) {
       // At most U_MAX distinct tokens: the bitmap is final, so the other
-      // waves go on to their tiles while the token waves build the ranks.
+      // waves go on to their tiles while the token waves build the tables
+      // and reduce the virtual tiles (the gathers' latency hidden behind
+      // the streaming waves).
       if (tok_wave) {
         GroupSync gs{&misc[M_GSYNC], TW, 0};
         const uint32_t U = build_ranks(h, nwords, btot, &misc[M_FLAGS], TW, gs);
-        if (need_cnt) counts();
-        if (tid == 0) misc[M_U] = U;
-        gs();  // the tables are ready once all TW waves arrive a third time
+        if (need_cnt) {
+          counts();
+          gs();
+        }
+#pragma unroll
+        for (int q = 0; q < TQ; ++q) asm volatile("" ::"v"(pf[q]));  // the prefetch is done
+        gather_penalised<DT>(a, P, b, row, U, h, need_cnt, TW);
+        gs();
+        for (uint32_t k = (uint32_t)wv; k < nch; k += TW) vtile_chunk(a, t0, nwords, k, U, h, E, lane);
       }
     } else {
       BarrierSync bs;
       const uint32_t U = build_ranks(h, nwords, btot, &misc[M_FLAGS], NW, bs);
-      if (need_cnt && tok_wave) counts();
-      if (tid == 0) misc[M_U] = U;
+      if (need_cnt) {
+        if (tok_wave) counts();
+        __syncthreads();
+      }
+      gather_penalised<DT>(a, P, b, row, U, h, need_cnt, NW);
       __syncthreads();
+      for (uint32_t k = (uint32_t)wv; k < nch; k += NW) vtile_chunk(a, t0, nwords, k, U, h, E, lane);
     }
   }
-  TileEnv E;
-  E.P = P;
-  E.c2 = LOG2E_F / P.T;
-  E.V = a.V;
-  E.collect = collect;
-  E.recompute_at = P.Kc / 4 > 8 ? P.Kc / 4 : 8;
-  E.misc = misc;
-  E.hf = hf;
-  E.hcoarse = hcoarse;
-  E.cbuf = G(w.cand) + (uint64_t)blockIdx.x * CAND_CAP;
-  E.part = G(w.tile_part) + (uint64_t)b * MAX_SLOTS;
-  E.lpart = a.G == 1 ? (LDS f2v*)(smem + a.lds_part) : nullptr;
-  E.lcand = a.G == 1 ? (LDS u2v*)(smem + a.lds_cand) : nullptr;
   uint32_t since = EMPTY;
-  const uint32_t nch = (nwords + 511) / 512;  // chunks of this segment
 
   const uint32_t sh4 = (4u * (uint32_t)lane) & 31u;
   auto process = [&](const Raw& raw, uint32_t t) __attribute__((always_inline)) {
@@ -2184,36 +2196,13 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
     const uint32_t t = t0 + 2u * NW + k;
     return t < t1 ? t : EMPTY;
   };
-  // Virtual tiles (history chunks) are claimed one at a time between
-  // vocabulary tiles once the tables are ready; a wave with no tile left
-  // waits for them.
-  const uint32_t ready_at = early ? 3u * TW : 0u;
-  bool vmore = have;
-  auto vtile_step = [&](bool wait) __attribute__((always_inline)) {
-    if (__atomic_load_n(&misc[M_GSYNC], __ATOMIC_RELAXED) < ready_at) {
-      if (!wait) return;
-      while (__atomic_load_n(&misc[M_GSYNC], __ATOMIC_RELAXED) < ready_at)
-        __builtin_amdgcn_s_sleep(2);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    uint32_t k = 0;
-    if (lane == 0) k = __atomic_fetch_add(&misc[M_VNEXT], 1u, __ATOMIC_RELAXED);
-    k = (uint32_t)__builtin_amdgcn_readfirstlane((int)k);
-    if (k >= nch) {
-      vmore = false;
-      return;
-    }
-    vtile_chunk<DT>(a, P, b, row, t0, nwords, k, misc[M_U], h, need_cnt, E, lane);
-  };
   if (ta != EMPTY) {
     process(ra, ta);
     ta = grab();
     if (ta != EMPTY) load_tile<DT>(a, row, mrow, h, ta, lane, ra);
   }
   for (;;) {
-    const bool tiles = ta != EMPTY || tb2 != EMPTY;
-    if (!tiles && !vmore) break;
-    if (vmore) vtile_step(!tiles);
+    if (ta == EMPTY && tb2 == EMPTY) break;
     if (tb2 != EMPTY) {
       process(rb, tb2);
       tb2 = grab();
