@@ -329,8 +329,16 @@ __device__ __forceinline__ uint32_t build_ranks(const Hist& h, uint32_t nwords,
   const uint32_t per = (nwords + 64u * nw - 1u) / (64u * nw);
   const uint32_t w0 = tid * per < nwords ? tid * per : nwords;
   const uint32_t w1 = w0 + per < nwords ? w0 + per : nwords;
+  // runs of up to 8 words are read at once (taken branches cost a lone
+  // wave more than the reads)
   uint32_t c = 0;
-  for (uint32_t wi = w0; wi < w1; ++wi) c += (uint32_t)__popc(h.bitmap[wi]);
+  for (uint32_t b0 = w0; b0 < w1; b0 += 8) {
+    uint32_t x[8];
+#pragma unroll
+    for (uint32_t q = 0; q < 8; ++q) x[q] = b0 + q < w1 ? h.bitmap[b0 + q] : 0u;
+#pragma unroll
+    for (uint32_t q = 0; q < 8; ++q) c += (uint32_t)__popc(x[q]);
+  }
   const uint32_t incl = wave_incl_scan(c);
   if (lane == 63) wtot[wv] = incl;
   sync();
@@ -340,24 +348,37 @@ __device__ __forceinline__ uint32_t build_ranks(const Hist& h, uint32_t nwords,
     r += i < wv ? t : 0u;
     total += t;
   }
-  for (uint32_t wi = w0; wi < w1; ++wi) {
-    uint32_t bits = h.bitmap[wi];
-    const uint32_t cw = (uint32_t)__popc(bits);
-    h.pre[wi] = (uint16_t)(r < U_MAX ? r : U_MAX);
-    if (r + cw > U_MAX) {  // keep the first U_MAX - r tokens of the word
-      const uint32_t keep = r < U_MAX ? U_MAX - r : 0u;
-      uint32_t kept = 0, rest = bits;
-      for (uint32_t k = 0; k < keep; ++k) {
-        kept |= rest & (0u - rest);
-        rest &= rest - 1u;
+  for (uint32_t b0 = w0; b0 < w1; b0 += 8) {
+    uint32_t x[8];
+#pragma unroll
+    for (uint32_t q = 0; q < 8; ++q) x[q] = b0 + q < w1 ? h.bitmap[b0 + q] : 0u;
+#pragma unroll
+    for (uint32_t q = 0; q < 8; ++q) {
+      const uint32_t wi = b0 + q;
+      uint32_t bits = x[q];
+      const uint32_t cw = (uint32_t)__popc(bits);
+      if (wi < w1) h.pre[wi] = (uint16_t)(r < U_MAX ? r : U_MAX);
+      if (wi < w1 && r + cw > U_MAX) {  // keep the first U_MAX - r tokens of the word
+        const uint32_t keep = r < U_MAX ? U_MAX - r : 0u;
+        uint32_t kept = 0, rest = bits;
+        for (uint32_t k = 0; k < keep; ++k) {
+          kept |= rest & (0u - rest);
+          rest &= rest - 1u;
+        }
+        bits = kept;
+        h.bitmap[wi] = kept;
       }
-      bits = kept;
-      h.bitmap[wi] = kept;
-    }
-    while (bits) {
-      const uint32_t bit = (uint32_t)__builtin_ctz(bits);
-      bits &= bits - 1u;
-      h.tokr[r++] = h.lo + 32u * wi + bit;
+      // two tokens per step
+      while (bits) {
+        const uint32_t b1 = (uint32_t)__builtin_ctz(bits);
+        bits &= bits - 1u;
+        h.tokr[r++] = h.lo + 32u * wi + b1;
+        if (bits) {
+          const uint32_t b2 = (uint32_t)__builtin_ctz(bits);
+          bits &= bits - 1u;
+          h.tokr[r++] = h.lo + 32u * wi + b2;
+        }
+      }
     }
   }
   if (total > U_MAX && tid == 0) __atomic_fetch_or(flags, FLAG_HIST_OVERFLOW, __ATOMIC_RELAXED);
