@@ -1524,51 +1524,54 @@ __device__ __forceinline__ uint32_t candidate_fast(const Args& a, uint32_t b, co
   LDS const u2v* lcand = (LDS const u2v*)((LDS uint32_t*)f.tl + a.lds_cand);
   LDS float* cval = f.pp;
   LDS uint32_t* cidx = f.pidx;
-  // ---- gather the candidates at or above lam
-  uint32_t n0;
-  {
-    const u2v e = tid < total ? lcand[tid] : u2v{0xff800000u, 0u};
-    const float v = __uint_as_float(e.x);
-    const bool keep = v > NEG_INF && fkey(v) >= lam;
-    const uint32_t pos = SY::excl_scan(keep, f.red, n0);
-    if (keep) {
-      cval[pos] = v;
-      cidx[pos] = e.y;
-    }
-  }
-  SY::sync();
+  // ---- gather the candidates at or above lam, and in the same pass their
+  // exact probabilities above the bound as (p desc, idx asc) keys; one scan
+  // counts both (packed in 16-bit halves: total <= LCAP)
   const bool topk = P.K > 0 && (uint32_t)P.K < a.V;
   const float plim = lam > 0x007fffffu ? prob_of(funkey(lam - 1), P.T, m, S) : 0.0f;
-  uint32_t lam_e = lam;
-  float plim_e = plim;
-  if (topk && n0 > 2u * (uint32_t)P.K) {
+  const u2v e = tid < total ? lcand[tid] : u2v{0xff800000u, 0u};
+  const float v0 = __uint_as_float(e.x);
+  const bool g0 = v0 > NEG_INF && fkey(v0) >= lam;
+  const float pv0 = g0 ? prob_of(v0, P.T, m, S) : 0.0f;
+  const bool k0 = g0 && pv0 > plim;
+  uint32_t both;
+  const uint32_t pos = block_excl_scan((g0 ? 1u : 0u) + (k0 ? 0x10000u : 0u), f.red, both);
+  const uint32_t n0 = both & 0xffffu;
+  uint32_t n = both >> 16;
+  if (n <= 128 || !topk) {
+    if (k0) f.keys[pos >> 16] = pkey(pv0, e.y);
+  } else {
+    // more than 128 kept: the exact K-th largest tightens the bound
+    if (g0) {
+      cval[pos & 0xffffu] = v0;
+      cidx[pos & 0xffffu] = e.y;
+    }
+    SY::sync();
     const uint32_t tau = kth_largest_key<SY>(cval, n0, (uint32_t)P.K, (LDS uint32_t*)f.keys,
                                              f.fm + F_SCR);
-    lam_e = tau;
-    plim_e = tau > 0x007fffffu ? prob_of(funkey(tau - 1), P.T, m, S) : 0.0f;
-  }
-  // ---- exact probabilities above the bound, as (p desc, idx asc) keys
-  uint32_t n = 0;
-  for (int attempt = 0; attempt < 2; ++attempt) {
-    bool keep = false;
-    uint64_t key = 0;
-    if (tid < n0) {
-      const float v = cval[tid];
-      if (fkey(v) >= lam_e) {
-        const float pv = prob_of(v, P.T, m, S);
-        if (pv > plim_e) {
-          keep = true;
-          key = pkey(pv, cidx[tid]);
+    uint32_t lam_e = tau;
+    float plim_e = tau > 0x007fffffu ? prob_of(funkey(tau - 1), P.T, m, S) : 0.0f;
+    for (int attempt = 0; attempt < 2; ++attempt) {
+      bool keep = false;
+      uint64_t key = 0;
+      if (tid < n0) {
+        const float v = cval[tid];
+        if (fkey(v) >= lam_e) {
+          const float pv = prob_of(v, P.T, m, S);
+          if (pv > plim_e) {
+            keep = true;
+            key = pkey(pv, cidx[tid]);
+          }
         }
       }
+      const uint32_t p2 = SY::excl_scan(keep, f.red, n);
+      if (keep) f.keys[p2] = key;
+      // a tightened bound that keeps fewer than K (ties in p across it)
+      // falls back to the gather bound
+      if (!(n < (uint32_t)P.K && lam_e != lam)) break;
+      lam_e = lam;
+      plim_e = plim;
     }
-    const uint32_t pos = SY::excl_scan(keep, f.red, n);
-    if (keep) f.keys[pos] = key;
-    // a tightened bound that keeps fewer than K (ties in p across it) falls
-    // back to the gather bound
-    if (!(topk && n < (uint32_t)P.K && lam_e != lam)) break;
-    lam_e = lam;
-    plim_e = plim;
   }
   if (n > 128) return 1;
   // ---- rank sort: key i against keys 16s .. 16s+15 in thread 128s + i
@@ -1650,11 +1653,29 @@ __device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_
     const GLB f2v* part = G(w.tile_part) + (uint64_t)b * MAX_SLOTS;
     LDS const f2v* lpart = (LDS const f2v*)(smem + a.lds_part);
     float L = NEG_INF;
-    for (uint32_t c = (uint32_t)lane; c < nslots; c += WAVE) {
-      const f2v q = a.G == 1 ? lpart[c] : part[c];
-      f.tl[c] = q.x;
-      f.ts[c] = q.y;
-      L = fmaxf(L, q.x);
+    if (a.G == 1 && nslots <= 256) {
+      f2v q[4];
+#pragma unroll
+      for (uint32_t k = 0; k < 4; ++k) {
+        const uint32_t c = 64 * k + (uint32_t)lane;
+        q[k] = c < nslots ? lpart[c] : f2v{NEG_INF, 0.0f};
+      }
+#pragma unroll
+      for (uint32_t k = 0; k < 4; ++k) {
+        const uint32_t c = 64 * k + (uint32_t)lane;
+        if (c < nslots) {
+          f.tl[c] = q[k].x;
+          f.ts[c] = q[k].y;
+        }
+        L = fmaxf(L, q[k].x);
+      }
+    } else {
+      for (uint32_t c = (uint32_t)lane; c < nslots; c += WAVE) {
+        const f2v q = a.G == 1 ? lpart[c] : part[c];
+        f.tl[c] = q.x;
+        f.ts[c] = q.y;
+        L = fmaxf(L, q.x);
+      }
     }
     L = wave_max(L);
     WaveSync::sync();
@@ -1680,12 +1701,30 @@ __device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_
       while (ntp < nslots) ntp <<= 1;
       const uint32_t nblk = ntp / 64;
       float bsum = 0.0f;  // lane k: the tree of block k
-      for (uint32_t k = 0; k < nblk; ++k) {
-        const uint32_t c = 64 * k + (uint32_t)lane;
-        float x = 0.0f;
-        if (c < nslots && L != NEG_INF) x = f.ts[c] * exp2_f((f.tl[c] - L) * c2);
-        x = wave_tree_sum(x);
-        if ((uint32_t)lane == k) bsum = x;
+      if (nblk <= 4) {
+        // up to four blocks at once: the reads, the terms and the four trees
+        // are independent
+        float x[4];
+#pragma unroll
+        for (uint32_t k = 0; k < 4; ++k) {
+          const uint32_t c = 64 * k + (uint32_t)lane;
+          const bool in = k < nblk && c < nslots;
+          const float tl = in ? f.tl[c] : 0.0f, ts = in ? f.ts[c] : 0.0f;
+          x[k] = (in && L != NEG_INF) ? ts * exp2_f((tl - L) * c2) : 0.0f;
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < 4; ++k) {
+          const float t = wave_tree_sum(x[k]);
+          if ((uint32_t)lane == k) bsum = t;
+        }
+      } else {
+        for (uint32_t k = 0; k < nblk; ++k) {
+          const uint32_t c = 64 * k + (uint32_t)lane;
+          float x = 0.0f;
+          if (c < nslots && L != NEG_INF) x = f.ts[c] * exp2_f((f.tl[c] - L) * c2);
+          x = wave_tree_sum(x);
+          if ((uint32_t)lane == k) bsum = x;
+        }
       }
       const float S = (L != NEG_INF) ? wave_tree_sum(bsum) : 0.0f;
       const float m = (P.T != 1.0f) ? L / P.T : L;
@@ -2242,8 +2281,8 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
     const uint32_t fl = misc[M_FLAGS];
     if (fl & FLAG_HIST_OVERFLOW) atomicOr(w.status, LLMK_STATUS_HISTORY_OVERFLOW);
     uint32_t last = 1;
-    G(w.seg_meta)[blockIdx.x] = u4v{misc[M_CCOUNT], misc[M_BETA], fl, have ? 1u : 0u};
-    if (a.G > 1) {
+    if (a.G > 1) {  // a single-segment row passes its table in registers
+      G(w.seg_meta)[blockIdx.x] = u4v{misc[M_CCOUNT], misc[M_BETA], fl, have ? 1u : 0u};
       __threadfence();  // release this workgroup's stores (all waves waited above)
       const uint32_t old = atomicAdd(&w.row_arrive[b], 1u);
       last = (old == a.G - 1) ? 1u : 0u;
@@ -2251,8 +2290,6 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
         __threadfence();  // acquire the other segments' stores
         w.row_arrive[b] = 0;
       }
-    } else {
-      wait_stores();
     }
     misc[M_LAST] = last;
   }
