@@ -2101,6 +2101,22 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   const void* row = (const char*)a.logits +
                     (uint64_t)b * a.stride * (DT == LLMK_F32 ? 4u : 2u);
   const uint32_t* mrow = a.mask ? a.mask + (uint64_t)b * a.mask_words : nullptr;
+  // The tile environment first: its kernel-argument loads then complete
+  // before the tiles are requested (behind them they take microseconds).
+  TileEnv E;
+  E.P = P;
+  E.c2 = LOG2E_F / P.T;
+  E.V = a.V;
+  E.collect = collect;
+  E.recompute_at = P.Kc / 4 > 8 ? P.Kc / 4 : 8;
+  E.misc = misc;
+  E.hf = hf;
+  E.hcoarse = hcoarse;
+  E.cbuf = G(w.cand) + (uint64_t)blockIdx.x * CAND_CAP;
+  E.part = G(w.tile_part) + (uint64_t)b * MAX_SLOTS;
+  E.lpart = a.G == 1 ? (LDS f2v*)(smem + a.lds_part) : nullptr;
+  E.lcand = a.G == 1 ? (LDS u2v*)(smem + a.lds_cand) : nullptr;
+  const uint32_t nch = (nwords + 511) / 512;  // chunks of this segment
   // Waves 0..TW-1 load the history tokens (TQ per lane per pass); every
   // wave then requests its first two tiles.
   constexpr uint32_t TW = 8;
@@ -2139,22 +2155,13 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
 #pragma unroll
   for (int q = 0; q < TQ; ++q)
     pf[q] = (have && tk[q] >= lo && tk[q] < hi) ? load_logit<DT>(row, tk[q]) : 0.0f;
-  if (ta != EMPTY) load_tile<DT>(a, row, mrow, h, ta, lane, ra);
-  if (tb2 != EMPTY) load_tile<DT>(a, row, mrow, h, tb2, lane, rb);
-  TileEnv E;
-  E.P = P;
-  E.c2 = LOG2E_F / P.T;
-  E.V = a.V;
-  E.collect = collect;
-  E.recompute_at = P.Kc / 4 > 8 ? P.Kc / 4 : 8;
-  E.misc = misc;
-  E.hf = hf;
-  E.hcoarse = hcoarse;
-  E.cbuf = G(w.cand) + (uint64_t)blockIdx.x * CAND_CAP;
-  E.part = G(w.tile_part) + (uint64_t)b * MAX_SLOTS;
-  E.lpart = a.G == 1 ? (LDS f2v*)(smem + a.lds_part) : nullptr;
-  E.lcand = a.G == 1 ? (LDS u2v*)(smem + a.lds_cand) : nullptr;
-  const uint32_t nch = (nwords + 511) / 512;  // chunks of this segment
+  // With history, the tiles are requested after the bitmap barrier: a wave
+  // whose requests fill the memory pipeline stalls at its next request for
+  // microseconds, and every wave waits at that barrier.
+  if (!have) {
+    if (ta != EMPTY) load_tile<DT>(a, row, mrow, h, ta, lane, ra);
+    if (tb2 != EMPTY) load_tile<DT>(a, row, mrow, h, tb2, lane, rb);
+  }
   // The history tables: the bitmap of the segment's history tokens, their
   // ranks, for the frequency penalty occurrence counts by rank, and the
   // penalised logits by rank; then the virtual tiles (one per 16-tile chunk).
@@ -2180,6 +2187,11 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
         __atomic_fetch_or(&h.bitmap[(t - lo) >> 5], 1u << (t & 31), __ATOMIC_RELAXED);
       });
     __syncthreads();
+    // the token waves of the early path request theirs after the tables
+    if (!(early && tok_wave)) {
+      if (ta != EMPTY) load_tile<DT>(a, row, mrow, h, ta, lane, ra);
+      if (tb2 != EMPTY) load_tile<DT>(a, row, mrow, h, tb2, lane, rb);
+    }
     auto counts = [&]() __attribute__((always_inline)) {
       each_token([&](uint32_t t) {
         const uint32_t o = t - lo, wd = h.bitmap[o >> 5], bit = 1u << (o & 31);
@@ -2201,6 +2213,8 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
           counts();
           gs();
         }
+        if (ta != EMPTY) load_tile<DT>(a, row, mrow, h, ta, lane, ra);
+        if (tb2 != EMPTY) load_tile<DT>(a, row, mrow, h, tb2, lane, rb);
 #pragma unroll
         for (int q = 0; q < TQ; ++q) asm volatile("" ::"v"(pf[q]));  // the prefetch is done
         gather_penalised<DT>(a, P, b, row, U, h, need_cnt, TW);
