@@ -1952,22 +1952,27 @@ __device__ __forceinline__ void gather_penalised(const Args& a, const RowP& P, u
   const GLB uint32_t* mrow = a.mask ? G(a.mask) + (uint64_t)b * a.mask_words : nullptr;
   LDS const uint32_t* cnt = (LDS const uint32_t*)h.pen;
   for (uint32_t r0 = 0; r0 < U; r0 += VB * step) {
+    const uint32_t nr = (U - r0 + step - 1) / step;  // rounds holding ranks (uniform)
     uint32_t tk[VB], mw[VB];
     float x[VB];
 #pragma unroll
     for (int i = 0; i < VB; ++i) {
       const uint32_t r = r0 + i * step + tid;
-      tk[i] = r < U ? h.tokr[r] : EMPTY;
+      tk[i] = ((uint32_t)i < nr && r < U) ? h.tokr[r] : EMPTY;
     }
 #pragma unroll
     for (int i = 0; i < VB; ++i) {
-      x[i] = tk[i] != EMPTY ? load_logit<DT>(row, tk[i]) : 0.0f;
-      mw[i] = (tk[i] != EMPTY && mrow) ? mrow[tk[i] >> 5] : 0xffffffffu;
+      x[i] = 0.0f;
+      mw[i] = 0xffffffffu;
+      if ((uint32_t)i < nr) {
+        x[i] = tk[i] != EMPTY ? load_logit<DT>(row, tk[i]) : 0.0f;
+        if (tk[i] != EMPTY && mrow) mw[i] = mrow[tk[i] >> 5];
+      }
     }
 #pragma unroll
     for (int i = 0; i < VB; ++i) {
       const uint32_t r = r0 + i * step + tid;
-      if (tk[i] != EMPTY) {
+      if ((uint32_t)i < nr && tk[i] != EMPTY) {
         float y = (x[i] > NEG_INF) ? x[i] : NEG_INF;  // NaN acts as -inf
         y = penalize(y, P, need_cnt ? cnt[r] : 1u);
         if (!((mw[i] >> (tk[i] & 31)) & 1u)) y = NEG_INF;
