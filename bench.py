@@ -39,6 +39,66 @@ def measured_traffic(config):
         return None
 
 
+def time_config(llmk, synth, torch, name, steps=20, warmup=5):
+    """Mean kernel time (event pairs on the launch stream) of one config, its
+    logits rotated over enough copies to leave the 256 MB MALL."""
+    import numpy as np
+    w = synth.make(name)
+    db0 = w.to_device()
+    nbytes = db0.logits.numel() * db0.logits.element_size()
+    nsets = max(1, int(np.ceil(2 * MALL_BYTES / nbytes)) + 1)
+    dbs = [db0]
+    for _ in range(nsets - 1):
+        d = llmk.DeviceBatch(**{k: getattr(db0, k) for k in db0.__dataclass_fields__})
+        d.logits = db0.logits.clone()
+        dbs.append(d)
+    s = llmk.HipSampler(max_batch=w.B, max_vocab=w.V)
+    tok = torch.empty(w.B, dtype=torch.int32, device="cuda:0")
+    stream = torch.cuda.current_stream()
+    for i in range(warmup):
+        s.launch(dbs[i % nsets], tok, stream=stream)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    for i in range(steps):
+        ev[i][0].record(stream)
+        s.launch(dbs[i % nsets], tok, stream=stream)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    us = float(np.mean([a.elapsed_time(b) for a, b in ev])) * 1e3
+    gbps = w.algorithmic_bytes() / (us * 1e-6) / 1e9
+    s.close()
+    return {"B": w.B, "V": w.V, "dtype": w.dtype, "us_per_step": us,
+            "tokens_per_s": w.B / (us * 1e-6), "achieved_GBps": gbps,
+            "frac_of_8TBps": gbps / HBM_PEAK_GBPS}
+
+
+def stream_read_gbps(torch, nbytes=2 << 30, reps=5):
+    """The box's achievable streaming-read bandwidth: llmk_read_probe (every
+    lane reads 128-bit words with non-temporal loads, as the sampler does)
+    over nbytes, best over a few grid sizes and repetitions."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(ROOT, "llm-rs_amd", "llmk", "libllmk_read_probe.so"))
+    lib.llmk_read_probe.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p,
+                                    ctypes.c_uint32, ctypes.c_void_p]
+    x = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda:0")
+    out = torch.zeros(1, dtype=torch.float32, device="cuda:0")
+    stream = torch.cuda.current_stream()
+    best = 0.0
+    for blocks in (512, 1024, 2048):
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            rc = lib.llmk_read_probe(x.data_ptr(), nbytes, out.data_ptr(), blocks,
+                                     ctypes.c_void_p(stream.cuda_stream))
+            b.record(stream)
+            torch.cuda.synchronize()
+            if rc != 0:
+                raise RuntimeError(f"llmk_read_probe failed: {rc}")
+            best = max(best, nbytes / (a.elapsed_time(b) * 1e-3) / 1e9)
+    del x
+    return best
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -84,6 +144,8 @@ def main():
     ap.add_argument("--config", default="C3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--sets", type=int, default=0, help="logit copies rotated (0 = auto)")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip the short runs of the other configs")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run a plain device-to-device copy of BYTES, 10 times (the "
                          "reference kernel for scaling HBM traffic counters)")
@@ -157,6 +219,17 @@ def main():
         f"min {min(kern_ms)*1e3:.2f}, max {max(kern_ms)*1e3:.2f}), "
         f"{achieved:.0f} GB/s algorithmic, sets {nsets}")
 
+    read_gbps = stream_read_gbps(torch)
+    log(f"[bench] streaming read probe (2 GiB): {read_gbps:.0f} GB/s")
+    others = None
+    if not args.no_other_configs:
+        others = {}
+        for name in ("C1", "C2", "C3", "C4", "C5"):
+            if name == args.config:
+                continue
+            others[name] = time_config(llmk, synth, torch, name)
+            log(f"[bench] {name}: {others[name]}")
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(w)
@@ -191,8 +264,11 @@ def main():
             "frac": achieved / HBM_PEAK_GBPS,
             "traffic": measured_traffic(args.config),
             "kernel": "llmk::stream_kernel",
+            "achievable_read_GBps": read_gbps,
+            "frac_of_achievable": achieved / read_gbps,
             "kernel_avg_us": kern_avg_ms * 1e3,
         },
+        "other_configs": others,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
