@@ -1116,15 +1116,15 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
       if (!(x > NEG_INF)) x = NEG_INF;  // NaN acts as -inf
       p = prob_of(x, P.T, m, S);
     }
+    // one scan counts both lists (16-bit halves: at most NT per chunk)
     uint32_t tot;
     const bool pos_f = valid && p > 0.0f;
-    const uint32_t pos = block_excl_scan(pos_f ? 1u : 0u, red, tot);
-    if (pos_f) kA[npos + pos] = pkey(p, e);
-    npos += tot;
     const bool zero_f = valid && !(p > 0.0f);
-    const uint32_t zpos = block_excl_scan(zero_f ? 1u : 0u, red, tot);
-    if (zero_f) zl[nzero + zpos] = e;
-    nzero += tot;
+    const uint32_t both = block_excl_scan((pos_f ? 1u : 0u) + (zero_f ? 0x10000u : 0u), red, tot);
+    if (pos_f) kA[npos + (both & 0xffffu)] = pkey(p, e);
+    if (zero_f) zl[nzero + (both >> 16)] = e;
+    npos += tot & 0xffffu;
+    nzero += tot >> 16;
   }
   wait_stores();
   __syncthreads();
@@ -1133,12 +1133,26 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
   // stable LSD radix sort of kA[0..npos) on bits 32..63, 4 passes of 8 bits
   GLB uint64_t* src = kA;
   GLB uint64_t* dst = kB;
+  for (uint32_t j = tid; j < NW * 256; j += NT) wcnt[j] = 0;
   for (int pass = 0; pass < 4; ++pass) {
     const int sh_bits = 32 + 8 * pass;
     if (tid < 256) digit_off[tid] = 0;
     __syncthreads();
-    for (uint32_t i = tid; i < npos; i += NT)
-      __atomic_fetch_add(&digit_off[(uint32_t)(src[i] >> sh_bits) & 255u], 1u, __ATOMIC_RELAXED);
+    // the digit histogram: one atomic per distinct digit per wave and step
+    // (the top digits of p keys are few and equal, and per-element atomics
+    // on one address serialise)
+    for (uint32_t i = tid; i - (uint32_t)lane < npos; i += NT) {
+      const bool valid = i < npos;
+      const uint32_t d = valid ? (uint32_t)(src[i] >> sh_bits) & 255u : 0u;
+      uint64_t peers = __ballot(valid);
+#pragma unroll
+      for (int bit = 0; bit < 8; ++bit) {
+        const uint64_t bb = __ballot(((d >> bit) & 1u) != 0);
+        peers &= ((d >> bit) & 1u) ? bb : ~bb;
+      }
+      if (valid && lanes_below(peers) == 0)
+        __atomic_fetch_add(&digit_off[d], (uint32_t)__popcll(peers), __ATOMIC_RELAXED);
+    }
     __syncthreads();
     if (tid == 0) {
       uint32_t acc = 0;
@@ -1149,6 +1163,10 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
       }
     }
     __syncthreads();
+    // stable scatter, 1024 keys per step: ranks among equal digits within a
+    // wave (ballots), then across waves (a prefix per digit, written over
+    // the counts); each wave clears its own row after its scatter, so two
+    // barriers per step suffice
     for (uint32_t base = 0; base < npos; base += NT) {
       const uint32_t i = base + tid;
       const bool valid = i < npos;
@@ -1161,24 +1179,22 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
         peers &= ((d >> bit) & 1u) ? bb : ~bb;
       }
       const uint32_t rank = lanes_below(peers);
-      for (uint32_t j = tid; j < NW * 256; j += NT) wcnt[j] = 0;
-      __syncthreads();
       if (valid && rank == 0) wcnt[wv * 256 + d] = __popcll(peers);
       __syncthreads();
       if (tid < 256) {
-        uint32_t acc = 0;
+        uint32_t acc = digit_off[tid];
         for (int q = 0; q < NW; ++q) {
           const uint32_t c = wcnt[q * 256 + tid];
           wcnt[q * 256 + tid] = acc;
           acc += c;
         }
-        ttot[tid] = acc;
+        digit_off[tid] = acc;
       }
       __syncthreads();
-      if (valid) dst[digit_off[d] + wcnt[wv * 256 + d] + rank] = key;
-      __syncthreads();
-      if (tid < 256) digit_off[tid] += ttot[tid];
-      __syncthreads();
+      if (valid) dst[wcnt[wv * 256 + d] + rank] = key;
+      WaveSync::sync();  // this wave's reads of its row are done
+#pragma unroll
+      for (int q = 0; q < 4; ++q) wcnt[wv * 256 + 64 * q + lane] = 0;
     }
     wait_stores();
     __syncthreads();
