@@ -1102,29 +1102,43 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
   const GLB uint32_t* mrow = a.mask ? G(a.mask) + (uint64_t)b * a.mask_words : nullptr;
   // pass 1: exact p of every element, stable split into p>0 / p==0 lists
   uint32_t npos = 0, nzero = 0;
-  for (uint32_t base = 0; base < V; base += NT) {
-    const uint32_t e = base + tid;
-    float p = 0.0f;
-    const bool valid = e < V;
-    if (valid) {
-      float x = load_logit<DT>(row, e);
-      if ((h.bitmap[e >> 5] >> (e & 31)) & 1u) {
-        const uint32_t r = h.rank(e);
-        if (r < U_MAX) x = h.pen[r];
-      }
-      if (mrow && !((mrow[e >> 5] >> (e & 31)) & 1u)) x = NEG_INF;
-      if (!(x > NEG_INF)) x = NEG_INF;  // NaN acts as -inf
-      p = prob_of(x, P.T, m, S);
+  constexpr int PE = 4;  // chunks of NT elements whose loads are issued together
+  for (uint32_t b0 = 0; b0 < V; b0 += PE * NT) {
+    float xs[PE];
+    uint32_t ms[PE];
+#pragma unroll
+    for (int q = 0; q < PE; ++q) {
+      const uint32_t e = b0 + q * NT + tid;
+      xs[q] = e < V ? load_logit<DT>(row, e) : NEG_INF;
+      ms[q] = (e < V && mrow) ? mrow[e >> 5] : 0xffffffffu;
     }
-    // one scan counts both lists (16-bit halves: at most NT per chunk)
-    uint32_t tot;
-    const bool pos_f = valid && p > 0.0f;
-    const bool zero_f = valid && !(p > 0.0f);
-    const uint32_t both = block_excl_scan((pos_f ? 1u : 0u) + (zero_f ? 0x10000u : 0u), red, tot);
-    if (pos_f) kA[npos + (both & 0xffffu)] = pkey(p, e);
-    if (zero_f) zl[nzero + (both >> 16)] = e;
-    npos += tot & 0xffffu;
-    nzero += tot >> 16;
+#pragma unroll
+    for (int q = 0; q < PE; ++q) {
+      if (b0 + q * NT >= V) break;
+      const uint32_t e = b0 + q * NT + tid;
+      float p = 0.0f;
+      const bool valid = e < V;
+      if (valid) {
+        float x = xs[q];
+        if ((h.bitmap[e >> 5] >> (e & 31)) & 1u) {
+          const uint32_t r = h.rank(e);
+          if (r < U_MAX) x = h.pen[r];
+        }
+        if (!((ms[q] >> (e & 31)) & 1u)) x = NEG_INF;
+        if (!(x > NEG_INF)) x = NEG_INF;  // NaN acts as -inf
+        p = prob_of(x, P.T, m, S);
+      }
+      // one scan counts both lists (16-bit halves: at most NT per chunk)
+      uint32_t tot;
+      const bool pos_f = valid && p > 0.0f;
+      const bool zero_f = valid && !(p > 0.0f);
+      const uint32_t both =
+          block_excl_scan((pos_f ? 1u : 0u) + (zero_f ? 0x10000u : 0u), red, tot);
+      if (pos_f) kA[npos + (both & 0xffffu)] = pkey(p, e);
+      if (zero_f) zl[nzero + (both >> 16)] = e;
+      npos += tot & 0xffffu;
+      nzero += tot >> 16;
+    }
   }
   wait_stores();
   __syncthreads();
@@ -1138,63 +1152,91 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
     const int sh_bits = 32 + 8 * pass;
     if (tid < 256) digit_off[tid] = 0;
     __syncthreads();
-    // the digit histogram: one atomic per distinct digit per wave and step
+    // the digit histogram: one atomic per distinct digit per wave and slot
     // (the top digits of p keys are few and equal, and per-element atomics
-    // on one address serialise)
-    for (uint32_t i = tid; i - (uint32_t)lane < npos; i += NT) {
-      const bool valid = i < npos;
-      const uint32_t d = valid ? (uint32_t)(src[i] >> sh_bits) & 255u : 0u;
-      uint64_t peers = __ballot(valid);
+    // on one address serialise); RE keys per thread loaded at once
+    constexpr int RE = 8;
+    for (uint32_t b0 = 0; b0 < npos; b0 += RE * NT) {
+      uint32_t dg[RE];
 #pragma unroll
-      for (int bit = 0; bit < 8; ++bit) {
-        const uint64_t bb = __ballot(((d >> bit) & 1u) != 0);
-        peers &= ((d >> bit) & 1u) ? bb : ~bb;
+      for (int q = 0; q < RE; ++q) {
+        const uint32_t i = b0 + q * NT + tid;
+        dg[q] = i < npos ? (uint32_t)(src[i] >> sh_bits) & 255u : 256u;
       }
-      if (valid && lanes_below(peers) == 0)
-        __atomic_fetch_add(&digit_off[d], (uint32_t)__popcll(peers), __ATOMIC_RELAXED);
+#pragma unroll
+      for (int q = 0; q < RE; ++q) {
+        if (b0 + q * NT >= npos) break;
+        const uint32_t d = dg[q] & 255u;
+        uint64_t peers = __ballot(dg[q] < 256u);
+#pragma unroll
+        for (int bit = 0; bit < 8; ++bit) {
+          const uint64_t bb = __ballot(((d >> bit) & 1u) != 0);
+          peers &= ((d >> bit) & 1u) ? bb : ~bb;
+        }
+        if (dg[q] < 256u && lanes_below(peers) == 0)
+          __atomic_fetch_add(&digit_off[d], (uint32_t)__popcll(peers), __ATOMIC_RELAXED);
+      }
     }
     __syncthreads();
-    if (tid == 0) {
-      uint32_t acc = 0;
-      for (int d = 0; d < 256; ++d) {
-        const uint32_t c = digit_off[d];
-        digit_off[d] = acc;
-        acc += c;
-      }
-    }
-    __syncthreads();
-    // stable scatter, 1024 keys per step: ranks among equal digits within a
-    // wave (ballots), then across waves (a prefix per digit, written over
-    // the counts); each wave clears its own row after its scatter, so two
-    // barriers per step suffice
-    for (uint32_t base = 0; base < npos; base += NT) {
-      const uint32_t i = base + tid;
-      const bool valid = i < npos;
-      const uint64_t key = valid ? src[i] : 0ull;
-      const uint32_t d = (uint32_t)(key >> sh_bits) & 255u;
-      uint64_t peers = __ballot(valid);
-#pragma unroll
-      for (int bit = 0; bit < 8; ++bit) {
-        const uint64_t bb = __ballot(((d >> bit) & 1u) != 0);
-        peers &= ((d >> bit) & 1u) ? bb : ~bb;
-      }
-      const uint32_t rank = lanes_below(peers);
-      if (valid && rank == 0) wcnt[wv * 256 + d] = __popcll(peers);
+    // exclusive prefix of the 256 digit counts: waves 0..3, one digit a lane
+    {
+      const uint32_t c = tid < 256 ? digit_off[tid] : 0u;
+      const uint32_t incl = wave_incl_scan(c);
+      if (tid < 256 && lane == 63) red[wv] = incl;
       __syncthreads();
       if (tid < 256) {
-        uint32_t acc = digit_off[tid];
-        for (int q = 0; q < NW; ++q) {
-          const uint32_t c = wcnt[q * 256 + tid];
-          wcnt[q * 256 + tid] = acc;
-          acc += c;
-        }
-        digit_off[tid] = acc;
-      }
-      __syncthreads();
-      if (valid) dst[wcnt[wv * 256 + d] + rank] = key;
-      WaveSync::sync();  // this wave's reads of its row are done
+        uint32_t base = 0;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) wcnt[wv * 256 + 64 * q + lane] = 0;
+        for (int q = 0; q < 4; ++q) base += q < wv ? red[q] : 0u;
+        digit_off[tid] = base + incl - c;
+      }
+    }
+    __syncthreads();
+    // stable scatter, RE slots of 1024 keys per step, the slot's keys loaded
+    // together: ranks among equal digits within a wave (ballots), then
+    // across waves (a prefix per digit, written over the counts); each wave
+    // clears its own row after its scatter, so two barriers per slot suffice
+    for (uint32_t b0 = 0; b0 < npos; b0 += RE * NT) {
+      uint64_t ky[RE];
+#pragma unroll
+      for (int q = 0; q < RE; ++q) {
+        const uint32_t i = b0 + q * NT + tid;
+        ky[q] = i < npos ? src[i] : 0ull;
+      }
+#pragma unroll
+      for (int q = 0; q < RE; ++q) {
+        if (b0 + q * NT >= npos) break;
+        const bool valid = b0 + q * NT + tid < npos;
+        const uint64_t key = ky[q];
+        const uint32_t d = (uint32_t)(key >> sh_bits) & 255u;
+        uint64_t peers = __ballot(valid);
+#pragma unroll
+        for (int bit = 0; bit < 8; ++bit) {
+          const uint64_t bb = __ballot(((d >> bit) & 1u) != 0);
+          peers &= ((d >> bit) & 1u) ? bb : ~bb;
+        }
+        const uint32_t rank = lanes_below(peers);
+        if (valid && rank == 0) wcnt[wv * 256 + d] = __popcll(peers);
+        __syncthreads();
+        if (tid < 256) {
+          // the sixteen counts read at once, then the prefix
+          uint32_t c[NW];
+#pragma unroll
+          for (int w2 = 0; w2 < NW; ++w2) c[w2] = wcnt[w2 * 256 + tid];
+          uint32_t acc = digit_off[tid];
+#pragma unroll
+          for (int w2 = 0; w2 < NW; ++w2) {
+            wcnt[w2 * 256 + tid] = acc;
+            acc += c[w2];
+          }
+          digit_off[tid] = acc;
+        }
+        __syncthreads();
+        if (valid) dst[wcnt[wv * 256 + d] + rank] = key;
+        WaveSync::sync();  // this wave's reads of its row are done
+#pragma unroll
+        for (int w2 = 0; w2 < 4; ++w2) wcnt[wv * 256 + 64 * w2 + lane] = 0;
+      }
     }
     wait_stores();
     __syncthreads();
