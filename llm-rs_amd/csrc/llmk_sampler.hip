@@ -79,7 +79,7 @@ constexpr uint32_t LCAP = 1024;       // candidates a single-segment row keeps i
 constexpr uint32_t MAX_SEG = 64;     // segments per row
 constexpr uint32_t MAX_WGS = 4096;   // candidate-buffer pool entries
 constexpr uint32_t SLOW_SLOTS = 64;  // global scratch slots of the slow path
-constexpr uint32_t STAGE = 2048;     // slow path: LDS window of the sorted list
+constexpr uint32_t SLOW_BINS = 2048; // slow path: bins of the processed logits
 constexpr uint32_t EMPTY = 0xffffffffu;
 constexpr float NEG_INF = -__builtin_huge_valf();
 
@@ -681,8 +681,6 @@ struct WaveSync {
 // computed; renormalisations (sampler.rs:84-87, :104-109) are recorded as a
 // chain of divisors and applied on every read, fl(fl(p/s1)/s2), exactly as
 // the reference's in-place divisions, so the list itself is never rewritten.
-// `win(j0, n)` returns an LDS pointer to the current values of
-// p[j0 .. j0+n) (n <= wmax()); every thread of the policy calls it.
 struct Chain {
   float d0, d1, d2;
   int n;
@@ -699,186 +697,313 @@ struct Chain {
     ++n;
   }
 };
-template <class SY>
-struct LdsList {
-  LDS const float* p;
-  LDS const uint32_t* idx;
-  LDS float* stage;  // SORT_CAP floats
-  LDS float* pb;     // SORT_CAP floats: prefix sums of a window
+// p and idx are generic pointers (LDS or global memory): one type, so the
+// semantics below are compiled once.
+struct List {
+  const float* p;
+  const uint32_t* idx;
   Chain c;
-  __device__ uint32_t wmax() const { return SORT_CAP; }
-  __device__ LDS const float* win(uint32_t j0, uint32_t n) const {
-    if (c.n == 0) return p + j0;
-    SY::sync();
-    for (uint32_t i = SY::id(); i < n; i += SY::N) stage[i] = c.apply(p[j0 + i]);
-    SY::sync();
-    return stage;
-  }
   __device__ float get(uint32_t i) const { return c.apply(p[i]); }
   __device__ uint32_t id(uint32_t i) const { return idx[i]; }
 };
-template <class SY>
-struct GlobList {
-  const GLB float* p;
-  const GLB uint32_t* idx;
-  LDS float* stage;  // STAGE floats
-  LDS float* pb;     // STAGE floats: prefix sums of a window
-  Chain c;
-  __device__ uint32_t wmax() const { return STAGE; }
-  __device__ LDS const float* win(uint32_t j0, uint32_t n) const {
-    SY::sync();
-    for (uint32_t i = SY::id(); i < n; i += SY::N) stage[i] = c.apply(p[j0 + i]);
-    SY::sync();
-    return stage;
-  }
-  __device__ float get(uint32_t i) const { return c.apply(p[i]); }
-  __device__ uint32_t id(uint32_t i) const { return idx[i]; }
-};
+template <class T>
+__device__ __forceinline__ const T* flat(LDS const T* x) {
+  return (const T*)x;
+}
+template <class T>
+__device__ __forceinline__ const T* flat(const GLB T* x) {
+  return (const T*)x;
+}
 
-// Sequential f32 scan of p[0..n) in order: the policy's thread 0 forms the
-// prefix sums ((p0 + p1) + p2) + ... window by window; for modes 1 and 2 all
-// threads then look for the first prefix meeting the condition.
+__device__ __forceinline__ float rl(float x, uint32_t j) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), (int)j));
+}
+
+// Increments of the running sum, in units of the binade's quantum, from an
+// even (a0) and from an odd (a1) running sum.
+struct Par {
+  uint32_t a0, a1;
+};
+// f, then g
+__device__ __forceinline__ Par par_then(Par f, Par g) {
+  return Par{f.a0 + ((f.a0 & 1u) ? g.a1 : g.a0), f.a1 + ((f.a1 & 1u) ? g.a0 : g.a1)};
+}
+
+// The sequential f32 running sums ((p_0 + p_1) + p_2) + ... of list[0..n),
+// exactly, computed by wave 0 a window of 512 entries at a time (8
+// consecutive entries per lane).  While the running sum c lies in the binade
+// [2^e, 2^(e+1)) (e >= -126 also covers the subnormals), c is a multiple of
+// q = 2^(e-23), c/q < 2^24, and fl(c + p) is c + q*r with r the nearest
+// integer to p/q, a tie going to the even sum: r depends on p alone except
+// for a tie, where it depends on the parity of c/q.  So every entry is a
+// pair of integer increments (from an even, from an odd sum), and a wave scan
+// of the pairs gives every running sum of the binade exactly.  The first
+// addition whose result would reach 2^(e+1) is done as one f32 addition and
+// the scan resumes after it (a sum of probabilities crosses a few tens of
+// binades at most).  Every thread calls it.
 // mode 0: sum of all n.  mode 1: stop at the first j with cum >= thr.
 // mode 2: stop at the first j with thr <= cum (the draw's `r <= cumulative`).
-// Returns the stop index (n if none) and the cumulative including it.
-template <class SY, class L>
-__device__ __forceinline__ uint32_t seq_scan(const L& list, uint32_t n, int mode,
-                                             float thr, float& cum_out,
-                                             LDS uint32_t* sh) {
-  float cum = 0.0f;
-  uint32_t stop = n;
-  const uint32_t W = list.wmax();
-  LDS float* pb = list.pb;
-  for (uint32_t j0 = 0; j0 < n; j0 += W) {
-    const uint32_t cnt = (n - j0 < W) ? n - j0 : W;
-    LDS const float* pw = list.win(j0, cnt);
-    if (SY::id() == 0) {
-      float c = cum;
-      uint32_t j = 0;
-      for (; j + 8 <= cnt; j += 8) {
-        const f4v a4 = *(LDS const f4v*)(pw + j);
-        const f4v b4 = *(LDS const f4v*)(pw + j + 4);
-        const float t0 = c + a4.x, t1 = t0 + a4.y, t2 = t1 + a4.z, t3 = t2 + a4.w;
-        const float t4 = t3 + b4.x, t5 = t4 + b4.y, t6 = t5 + b4.z, t7 = t6 + b4.w;
-        if (mode != 0) {
-          *(LDS f4v*)(pb + j) = f4v{t0, t1, t2, t3};
-          *(LDS f4v*)(pb + j + 4) = f4v{t4, t5, t6, t7};
-        }
-        c = t7;
-      }
-      for (; j < cnt; ++j) {
-        c += pw[j];
-        if (mode != 0) pb[j] = c;
-      }
-      sh[0] = __float_as_uint(c);
-      sh[1] = EMPTY;
+// Returns the stop index (n if none) and the running sum including it (the
+// total if none).  sh: 2 words.
+// Exclusive scan of the pairs over the wave (DPP row shifts and row
+// broadcasts; shifted-in lanes read (0, 0), the identity).
+template <int CTRL, int RM, bool BC>
+__device__ __forceinline__ Par dpp_par(Par x) {
+  return Par{dppu<CTRL, RM, BC>(0u, x.a0), dppu<CTRL, RM, BC>(0u, x.a1)};
+}
+__device__ __forceinline__ Par wave_par_excl(Par x) {
+  x = par_then(dpp_par<0x111, 0xf, true>(x), x);
+  x = par_then(dpp_par<0x112, 0xf, true>(x), x);
+  x = par_then(dpp_par<0x114, 0xf, true>(x), x);
+  x = par_then(dpp_par<0x118, 0xf, true>(x), x);
+  x = par_then(dpp_par<0x142, 0xa, false>(x), x);
+  x = par_then(dpp_par<0x143, 0xc, false>(x), x);
+  return dpp_par<0x138, 0xf, true>(x);  // wave_shr:1
+}
+template <int Q>
+__device__ __forceinline__ float pickf(const float (&x)[Q], uint32_t k) {
+  float r = x[0];
+#pragma unroll
+  for (int q = 1; q < Q; ++q) r = (k == (uint32_t)q) ? x[q] : r;
+  return r;
+}
+__device__ __forceinline__ uint32_t seq_scan(const List& list, uint32_t n, int mode, float thr,
+                                             float& cum_out, LDS uint32_t* sh) {
+  if (threadIdx.x < WAVE) {
+    constexpr uint32_t Q = 8, W = Q * WAVE;
+    constexpr uint32_t TOP = 1u << 24;
+    const uint32_t lane = threadIdx.x, l0 = Q * lane;
+    const bool stops = mode != 0;
+    uint32_t stop = n;
+    float c = 0.0f;
+    if (n > 0 && stops && thr <= 0.0f) {  // the first running sum already meets it
+      stop = 0;
+      c = 0.0f + list.get(0);
     }
-    SY::sync();
-    const float wend = __uint_as_float(sh[0]);
-    if (mode != 0) {
-      for (uint32_t i = SY::id(); i < cnt; i += SY::N) {
-        const float c = pb[i];
-        if ((mode == 1 && c >= thr) || (mode == 2 && thr <= c)) {
-          __atomic_fetch_min(&sh[1], i, __ATOMIC_RELAXED);
+    for (uint32_t j = 0; j < n && stop == n; j += W) {
+      const uint32_t lim = umin(n - j, W);
+      float p[Q];
+#pragma unroll
+      for (uint32_t q = 0; q < Q; ++q) p[q] = (l0 + q < lim) ? list.get(j + l0 + q) : 0.0f;
+      uint32_t s = 0;  // window entries before s are summed
+      while (s < lim) {
+        if (c == 0.0f) {
+          // 0 + p is exact: the first nonzero entry starts the sum (zeros
+          // leave it 0, below thr > 0)
+          uint32_t fz = EMPTY;
+#pragma unroll
+          for (int q = (int)Q - 1; q >= 0; --q)
+            if (l0 + q >= s && l0 + q < lim && p[q] != 0.0f) fz = l0 + q;
+          fz = wave_min_u32(fz);
+          if (fz == EMPTY) {
+            s = lim;
+            break;
+          }
+          c = 0.0f + rl(pickf(p, fz % Q), fz / Q);
+          s = fz + 1;
+          if (stops && c >= thr) {
+            stop = j + fz;
+            break;
+          }
+          continue;
+        }
+        const uint32_t cb = __float_as_uint(c);
+        const int e = (int)umax((cb >> 23) & 255u, 1u) - 127;
+        const uint32_t C = (uint32_t)__builtin_ldexpf(c, 23 - e);
+        uint32_t r[Q], tie = 0;  // increments; ties: the value from an even sum differs
+#pragma unroll
+        for (uint32_t q = 0; q < Q; ++q) {
+          const float x = __builtin_ldexpf(p[q], 23 - e);  // exact, < 2^24
+          const float k = __builtin_floorf(x);
+          const float fr = x - k;
+          const uint32_t ki = (uint32_t)k;
+          const bool live = l0 + q >= s && l0 + q < lim;
+          r[q] = !live ? 0u : (fr > 0.5f ? ki + 1u : ki);
+          if (live && fr == 0.5f) tie |= 1u << q;
+        }
+        // this lane's increments from an even and from an odd sum (a tie
+        // adds k or k + 1, whichever makes the sum even)
+        uint32_t s0 = 0, s1 = 1;
+#pragma unroll
+        for (uint32_t q = 0; q < Q; ++q) {
+          const uint32_t t = (tie >> q) & 1u;
+          s0 += r[q] + (t & ((s0 ^ r[q]) & 1u));
+          s1 += r[q] + (t & ((s1 ^ r[q]) & 1u));
+        }
+        const Par ex = wave_par_excl(Par{s0, s1 - 1u});
+        uint32_t cur = C + ((C & 1u) ? ex.a1 : ex.a0);
+        // the lane's first event (crossing or stop) with the sum before (a
+        // crossing) or at (a stop) it, and the sum at the window's last entry
+        uint32_t ev = EMPTY, evv = 0, endv = 0, evx = 0;
+#pragma unroll
+        for (uint32_t q = 0; q < Q; ++q) {
+          const uint32_t t = (tie >> q) & 1u;
+          const uint32_t nx = cur + r[q] + (t & ((cur ^ r[q]) & 1u));
+          if (ev == EMPTY && l0 + q >= s && l0 + q < lim) {
+            if (nx >= TOP) {
+              ev = l0 + q;
+              evx = 1;
+              evv = cur;
+            } else if (stops && __builtin_ldexpf((float)nx, e - 23) >= thr) {
+              ev = l0 + q;
+              evv = nx;
+            }
+          }
+          if (l0 + q == lim - 1) endv = nx;
+          cur = nx;
+        }
+        const uint32_t evm = wave_min_u32(ev);
+        if (evm == EMPTY) {
+          const uint32_t v = (uint32_t)__builtin_amdgcn_readlane((int)endv, (int)((lim - 1) / Q));
+          c = __builtin_ldexpf((float)v, e - 23);
+          s = lim;
+          break;
+        }
+        const int ol = (int)(evm / Q);
+        const float v =
+            __builtin_ldexpf((float)(uint32_t)__builtin_amdgcn_readlane((int)evv, ol), e - 23);
+        if (!__builtin_amdgcn_readlane((int)evx, ol)) {
+          stop = j + evm;
+          c = v;
+          break;
+        }
+        // the addition that leaves the binade, as one f32 addition
+        c = v + rl(pickf(p, evm % Q), (uint32_t)ol);
+        s = evm + 1;
+        if (stops && c >= thr) {
+          stop = j + evm;
           break;
         }
       }
-      SY::sync();
     }
-    const uint32_t hit = sh[1];
-    if (hit != EMPTY) {
-      cum = pb[hit];
-      stop = j0 + hit;
-      SY::sync();
-      break;
+    if (lane == 0) {
+      sh[0] = stop;
+      sh[1] = __float_as_uint(c);
     }
-    cum = wend;
-    SY::sync();
   }
-  cum_out = cum;
+  __syncthreads();
+  const uint32_t stop = sh[0];
+  cum_out = __uint_as_float(sh[1]);
+  __syncthreads();
   return stop;
 }
 
-template <class L>
-__device__ __forceinline__ void div_all(L& list, float s) {
+__device__ __forceinline__ void div_all(List& list, float s) {
   if (s > 0.0f) list.c.push(s);
 }
 
+// First i < n with list[i] < thr (strict) or <= thr, n if none; the list is
+// sorted descending, so the predicate is monotone: one probe per thread
+// finds the block of n/NT entries holding the first hit, then the block is
+// searched.  n <= NT * NT.  sh: 1 word.
+__device__ __forceinline__ uint32_t first_below(const List& list, uint32_t n, float thr,
+                                                bool strict,
+                                LDS uint32_t* sh) {
+  const uint32_t tid = threadIdx.x;
+  auto hit = [&](uint32_t i) {
+    const float v = list.get(i);
+    return strict ? v < thr : v <= thr;
+  };
+  const uint32_t step = (n + NT - 1) / NT;
+  if (tid == 0) sh[0] = EMPTY;
+  __syncthreads();
+  const uint32_t lo = tid * step;
+  if (lo < n && hit(umin(lo + step, n) - 1)) __atomic_fetch_min(&sh[0], tid, __ATOMIC_RELAXED);
+  __syncthreads();
+  const uint32_t kb = sh[0];
+  __syncthreads();
+  if (kb == EMPTY) return n;
+  if (tid == 0) sh[0] = EMPTY;
+  __syncthreads();
+  const uint32_t b0 = kb * step;
+  if (tid < step && b0 + tid < n && hit(b0 + tid))
+    __atomic_fetch_min(&sh[0], b0 + tid, __ATOMIC_RELAXED);
+  __syncthreads();
+  const uint32_t r = sh[0];
+  __syncthreads();
+  return r;
+}
+
 // min-p / top-k / top-p / draw (sampler.rs:77-124 + min-p) over a sorted list
-// whose first E entries are exact and which has full_len entries.  Every
-// thread of the policy.  Returns false if an entry beyond E would be needed.
-template <class SY, class L>
+// of full_len entries whose first E are exact; every entry past E has
+// p <= ptail.  Every thread of the workgroup.  Returns false if an entry
+// beyond E would be needed.  The four steps share one running-sum call.
 __device__ __forceinline__ bool run_semantics(const RowP& P, float u, uint32_t E,
-                                              uint32_t full_len, L& list,
+                                              uint32_t full_len, float ptail, List& list,
                                               LDS uint32_t* sh, uint32_t& tok_out,
                                               uint32_t& len_out) {
   uint32_t len = full_len;
   bool trunc = E < full_len;
-  float s;
-  // ---- min-p (extension): keep p >= min_p * p_max, renormalise if it cuts
-  if (P.min_p > 0.0f) {
-    if (E == 0) return false;
-    const float thr = P.min_p * list.get(0);
-    if (SY::id() == 0) sh[2] = EMPTY;
-    SY::sync();
-    const uint32_t lim = E < len ? E : len;
-    for (uint32_t i = SY::id(); i < lim; i += SY::N)
-      if (list.get(i) < thr) __atomic_fetch_min(&sh[2], i, __ATOMIC_RELAXED);
-    SY::sync();
-    const uint32_t cut = sh[2];
-    SY::sync();
-    if (cut == EMPTY) {
-      if (trunc) return false;
-    } else if (cut < len) {
+  for (int step = 0; step < 4; ++step) {
+    uint32_t n;
+    int mode = 0;
+    float thr = 0.0f;
+    if (step == 0) {
+      // ---- min-p (extension): keep p >= min_p * p_max, renormalise if it cuts
+      if (!(P.min_p > 0.0f)) continue;
+      if (E == 0) return false;
+      const float t = P.min_p * list.get(0);
+      const uint32_t lim = E < len ? E : len;
+      uint32_t cut = first_below(list, lim, t, true, sh);
+      if (cut == lim) cut = EMPTY;
+      // every entry past E is below the threshold: the cut is at E
+      if (cut == EMPTY && trunc && ptail < t) cut = E;
+      if (cut == EMPTY) {
+        if (trunc) return false;
+        continue;
+      }
+      if (cut >= len) continue;
       len = cut;
       trunc = false;
-      seq_scan<SY>(list, len, 0, 0.0f, s, sh);
-      div_all(list, s);
+      n = len;
+    } else if (step == 1) {
+      // ---- top-k, sampler.rs:80-89
+      if (!(P.K > 0 && (uint32_t)P.K < len)) continue;
+      if ((uint32_t)P.K > E) return false;
+      len = (uint32_t)P.K;
+      trunc = false;
+      n = len;
+    } else {
+      // ---- top-p, sampler.rs:92-110; the draw, sampler.rs:113-124
+      if (step == 2 && !(P.top_p < 1.0f)) continue;
+      n = (trunc && E < len) ? E : len;
+      mode = step == 2 ? 1 : 2;
+      thr = step == 2 ? P.top_p : u;
     }
-  }
-  // ---- top-k, sampler.rs:80-89
-  if (P.K > 0 && (uint32_t)P.K < len) {
-    if ((uint32_t)P.K > E) return false;
-    len = (uint32_t)P.K;
-    trunc = false;
-    seq_scan<SY>(list, len, 0, 0.0f, s, sh);
+    float s;
+    const uint32_t j = seq_scan(list, n, mode, thr, s, sh);
+    if (step == 3) {
+      uint32_t tok;
+      if (j < n) tok = list.id(j);
+      else {
+        if (trunc) return false;
+        tok = len > 0 ? list.id(len - 1) : 0u;
+      }
+      tok_out = tok;
+      len_out = len;
+      return true;
+    }
+    if (step == 2) {
+      if (j == n && trunc) return false;
+      // the renormalisation sum over the kept prefix is the same sequential
+      // sum as the cumulative at the cut
+      len = (j < n) ? j + 1 : len;
+      trunc = false;
+    }
     div_all(list, s);
   }
-  // ---- top-p, sampler.rs:92-110
-  if (P.top_p < 1.0f) {
-    const uint32_t lim = (trunc && E < len) ? E : len;
-    const uint32_t j = seq_scan<SY>(list, lim, 1, P.top_p, s, sh);
-    if (j == lim && trunc) return false;
-    // the renormalisation sum over the kept prefix is the same sequential
-    // sum as the cumulative at the cut
-    len = (j < lim) ? j + 1 : len;
-    trunc = false;
-    div_all(list, s);
-  }
-  // ---- draw, sampler.rs:113-124
-  const uint32_t lim = (trunc && E < len) ? E : len;
-  const uint32_t j = seq_scan<SY>(list, lim, 2, u, s, sh);
-  uint32_t tok;
-  if (j < lim) tok = list.id(j);
-  else {
-    if (trunc) return false;
-    tok = len > 0 ? list.id(len - 1) : 0u;
-  }
-  tok_out = tok;
-  len_out = len;
-  return true;
+  return false;
 }
 
-template <class SY, class L>
 __device__ __forceinline__ void write_outputs(const Args& a, uint32_t b, uint32_t tok,
-                                              uint32_t len, const L& list) {
-  if (SY::id() == 0) {
+                                              uint32_t len, const List& list) {
+  if (threadIdx.x == 0) {
     G(a.out_tok)[b] = tok;
     if (a.out_cnt) G(a.out_cnt)[b] = len;
   }
   if (a.out_cap) {
     const uint32_t n = len < a.out_cap ? len : a.out_cap;
-    for (uint32_t j = SY::id(); j < n; j += SY::N) {
+    for (uint32_t j = threadIdx.x; j < n; j += NT) {
       if (a.out_ids) G(a.out_ids)[(uint64_t)b * a.out_cap + j] = list.id(j);
       if (a.out_probs) G(a.out_probs)[(uint64_t)b * a.out_cap + j] = list.get(j);
     }
@@ -892,9 +1017,6 @@ __device__ __forceinline__ void write_outputs(const Args& a, uint32_t b, uint32_
 // same order; the running sums are wave-uniform, each step reading one entry
 // with v_readlane.  Returns false if an entry beyond E = n would be needed.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float rl(float x, uint32_t j) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), (int)j));
-}
 // Every lane forms its own prefix: lane l of c0 receives ((p_0 + p_1) + ...)
 // + p_l and lane l of c1 the prefix through entry 64 + l -- the same f32
 // additions in the same order as one sequential sum.  z holds 64 zeros before
@@ -955,7 +1077,8 @@ __device__ __forceinline__ uint32_t seq_find_regs(float p0, float p1, uint32_t m
 }
 
 __device__ __forceinline__ bool semantics_regs(const RowP& P, float u, uint32_t n,
-                                               uint32_t full_len, float& p0, float& p1,
+                                               uint32_t full_len, float ptail, float& p0,
+                                               float& p1,
                                                uint32_t i0, uint32_t i1, int lane,
                                                LDS float* z, uint32_t& tok_out,
                                                uint32_t& len_out) {
@@ -978,6 +1101,8 @@ __device__ __forceinline__ bool semantics_regs(const RowP& P, float u, uint32_t 
     uint32_t cut = EMPTY;
     if (c0) cut = (uint32_t)__ffsll((unsigned long long)c0) - 1;
     else if (c1) cut = 64u + (uint32_t)__ffsll((unsigned long long)c1) - 1;
+    // every entry past E is below the threshold: the cut is at E
+    if (cut == EMPTY && trunc && ptail < thr) cut = E;
     if (cut == EMPTY) {
       if (trunc) return false;
     } else if (cut < len) {
@@ -1040,15 +1165,58 @@ __host__ __device__ inline size_t finalize_lds_words() {
   return 2 * MAX_SLOTS + 4 * SORT_CAP + 2 * SORT_CAP + 128 + MAX_SEG + 16 + 64 + 2 * MAX_SLOTS / 64;
 }
 __host__ __device__ inline size_t slow_lds_words(uint32_t V) {
-  return 128 + 256 + NW * 256 + 256 + 2 * STAGE + hist_lds_words((V + 31) / 32);
+  return 128 + 256 + NW * 256 + SLOW_BINS + hist_lds_words((V + 31) / 32);
 }
 
 // ---------------------------------------------------------------------------
 // Slow path (one workgroup, one row)
 // ---------------------------------------------------------------------------
+// Eight consecutive logits of a row from e0 (zeros past V).
+template <int DT>
+__device__ __forceinline__ void load8(const void* row, uint32_t e0, uint32_t V, float x[8]) {
+  if (e0 + 8 <= V) {
+    if (DT == LLMK_F32) {
+      const GLB f4v* r = (const GLB f4v*)((const GLB float*)row + e0);
+      const f4v a = r[0], b = r[1];
+      x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+      x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+    } else {
+      const GLB u2v* r = (const GLB u2v*)((const GLB uint16_t*)row + e0);
+      const u2v a = r[0], b = r[1];
+      const uint32_t w[4] = {a.x, a.y, b.x, b.y};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        x[2 * q] = __uint_as_float(w[q] << 16);
+        x[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) x[q] = e0 + q < V ? load_logit<DT>(row, e0 + q) : 0.0f;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Slow path (one workgroup, one row).  Rows the candidate path cannot prove:
+//   A  every processed logit l falls in a bin of d = (l - L) log2(e)/T (1/16
+//      per bin, the last bin open-ended), counted in LDS;
+//   B  the bins that the semantics can reach are chosen from those counts:
+//      the first bins (largest l) whose lower bound on sum 2^d reaches
+//      (top_p, or the uniform when top-p is off) * S + 0.002 S, and for a
+//      top-k row the first bins holding K elements -- a guess, checked
+//      below;
+//   C  the exact p of every element of the chosen bins, kept in index order
+//      (p > 0 as (p, idx) keys, p == 0 as indices when nothing is left out);
+//      the largest logit left out bounds the p of everything left out
+//      (p_lim);
+//   D  a stable LSD radix sort of the keys, then min-p / top-k / top-p / the
+//      draw over the sorted list, whose exact prefix is the entries with
+//      p > p_lim.  If the semantics need an entry past it, C and D are done
+//      again with every bin chosen.
+// ---------------------------------------------------------------------------
 template <int DT>
 __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b, const RowP& P,
-                         float S, float m, LDS uint32_t* smem) {
+                                         float S, float m, float L, LDS uint32_t* smem) {
   const uint32_t tid = threadIdx.x;
   const int lane = (int)(tid & 63), wv = (int)(tid >> 6);
   const uint32_t V = a.V;
@@ -1057,9 +1225,8 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
   LDS uint32_t* red = sh + 64;               // 64
   LDS uint32_t* digit_off = red + 64;        // 256
   LDS uint32_t* wcnt = digit_off + 256;      // NW*256
-  LDS uint32_t* ttot = wcnt + NW * 256;      // 256
-  LDS float* stage = (LDS float*)(ttot + 256);   // 2 x STAGE (window, prefixes)
-  LDS uint32_t* hb = (LDS uint32_t*)(stage + 2 * STAGE);
+  LDS uint32_t* bins = wcnt + NW * 256;      // SLOW_BINS
+  LDS uint32_t* hb = bins + SLOW_BINS;
   const uint32_t nwords = (V + 31) / 32;
   Hist h;
   hist_carve(h, hb, nwords);
@@ -1100,50 +1267,138 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
   GLB float* plist = G(w.slow_p) + (uint64_t)slot * w.max_vocab;
   GLB uint32_t* ilist = G(w.slow_idx) + (uint64_t)slot * w.max_vocab;
   const GLB uint32_t* mrow = a.mask ? G(a.mask) + (uint64_t)b * a.mask_words : nullptr;
-  // pass 1: exact p of every element, stable split into p>0 / p==0 lists
-  uint32_t npos = 0, nzero = 0;
-  constexpr int PE = 4;  // chunks of NT elements whose loads are issued together
-  for (uint32_t b0 = 0; b0 < V; b0 += PE * NT) {
-    float xs[PE];
-    uint32_t ms[PE];
+  const float u = G(a.u)[b];
+  const float c2 = LOG2E_F / P.T;
+  const float nbL = -(L * c2);
+  // processed logits (penalties, mask, NaN as -inf) of e0 .. e0+7 and their bins
+  auto processed = [&](uint32_t e0, float v[8]) __attribute__((always_inline)) {
+    load8<DT>(row, e0, V, v);
+    const uint32_t mw = (mrow && e0 < V) ? mrow[e0 >> 5] : 0xffffffffu;
 #pragma unroll
-    for (int q = 0; q < PE; ++q) {
-      const uint32_t e = b0 + q * NT + tid;
-      xs[q] = e < V ? load_logit<DT>(row, e) : NEG_INF;
-      ms[q] = (e < V && mrow) ? mrow[e >> 5] : 0xffffffffu;
-    }
-#pragma unroll
-    for (int q = 0; q < PE; ++q) {
-      if (b0 + q * NT >= V) break;
-      const uint32_t e = b0 + q * NT + tid;
-      float p = 0.0f;
-      const bool valid = e < V;
-      if (valid) {
-        float x = xs[q];
-        if ((h.bitmap[e >> 5] >> (e & 31)) & 1u) {
-          const uint32_t r = h.rank(e);
-          if (r < U_MAX) x = h.pen[r];
-        }
-        if (!((ms[q] >> (e & 31)) & 1u)) x = NEG_INF;
-        if (!(x > NEG_INF)) x = NEG_INF;  // NaN acts as -inf
-        p = prob_of(x, P.T, m, S);
+    for (int q = 0; q < 8; ++q) {
+      const uint32_t e = e0 + q;
+      float x = v[q];
+      if (e < V && ((h.bitmap[e >> 5] >> (e & 31)) & 1u)) {
+        const uint32_t r = h.rank(e);
+        if (r < U_MAX) x = h.pen[r];
       }
-      // one scan counts both lists (16-bit halves: at most NT per chunk)
+      if (!((mw >> (e & 31)) & 1u)) x = NEG_INF;
+      if (!(x > NEG_INF) || e >= V) x = NEG_INF;
+      v[q] = x;
+    }
+  };
+  auto bin_of = [&](float x) __attribute__((always_inline)) {
+    const float t = -__builtin_fmaf(x, c2, nbL) * 16.0f;
+    return (uint32_t)__builtin_fminf(__builtin_fmaxf(t, 0.0f), (float)(SLOW_BINS - 1));
+  };
+  // ---- A: bin counts
+  for (uint32_t j = tid; j < SLOW_BINS; j += NT) bins[j] = 0;
+  __syncthreads();
+  for (uint32_t b0 = 0; b0 < V; b0 += 8 * NT) {
+    float v[8];
+    processed(b0 + 8 * tid, v);
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      if (v[q] > NEG_INF) __atomic_fetch_add(&bins[bin_of(v[q])], 1u, __ATOMIC_RELAXED);
+  }
+  __syncthreads();
+  // ---- B: the last chosen bin (wave 0; lane l sums bins 32l .. 32l+31)
+  if (wv == 0) {
+    constexpr uint32_t PER = SLOW_BINS / WAVE;
+    const bool topk = P.K > 0 && (uint32_t)P.K < V;
+    const float tm = (P.top_p < 1.0f ? P.top_p : u) + 0.002f;
+    const bool use_mass = tm < 1.0f && S > 0.0f;
+    uint32_t cnt = 0;
+    float mass = 0.0f;
+    for (uint32_t k = 0; k < PER; ++k) {
+      const uint32_t bi = PER * (uint32_t)lane + k;
+      const uint32_t c = bins[bi];
+      cnt += c;
+      if (bi + 1 < SLOW_BINS) mass += (float)c * __builtin_exp2f(-(float)(bi + 1) * 0.0625f);
+    }
+    const uint32_t cincl = wave_incl_scan(cnt);
+    float mincl = mass;  // inclusive scan of the lane masses (order fixed)
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const float o = __shfl_up(mincl, d);
+      if (lane >= d) mincl += o;
+    }
+    const float mneed = tm * S;
+    uint32_t last = SLOW_BINS - 1;
+    const uint64_t hm = use_mass ? __ballot(mincl >= mneed) : 0ull;
+    const uint64_t hk = topk ? __ballot(cincl >= (uint32_t)P.K) : 0ull;
+    auto bin_in = [&](uint32_t l, bool by_mass) {
+      // the first bin of lane l where the running total meets the target
+      const uint32_t c0 = (uint32_t)__shfl((int)(cincl - cnt), (int)l);
+      const float m0 = __shfl(mincl - mass, (int)l);
+      uint32_t cc = c0;
+      float mm = m0;
+      uint32_t r = PER * l + PER - 1;
+      for (uint32_t k = 0; k < PER; ++k) {
+        const uint32_t bi = PER * l + k;
+        const uint32_t c = bins[bi];
+        cc += c;
+        if (bi + 1 < SLOW_BINS) mm += (float)c * __builtin_exp2f(-(float)(bi + 1) * 0.0625f);
+        if (by_mass ? mm >= mneed : cc >= (uint32_t)P.K) {
+          r = bi;
+          break;
+        }
+      }
+      return r;
+    };
+    if (hm) last = umin(last, bin_in((uint32_t)__ffsll((unsigned long long)hm) - 1, true));
+    if (hk) last = umin(last, bin_in((uint32_t)__ffsll((unsigned long long)hk) - 1, false));
+    if (lane == 0) sh[11] = last;
+  }
+  __syncthreads();
+  uint32_t last = sh[11];
+  uint32_t tok = 0, len = 0;
+  List Lst{flat(plist), flat(ilist), Chain{0.f, 0.f, 0.f, 0}};
+  for (int attempt = 0; attempt < 2; ++attempt) {
+    const bool filt = last < SLOW_BINS - 1;
+    // ---- C: exact p of the chosen elements, in index order
+    uint32_t npos = 0, nzero = 0, lkey = 0;
+    for (uint32_t b0 = 0; b0 < V; b0 += 8 * NT) {
+      const uint32_t e0 = b0 + 8 * tid;
+      float v[8];
+      processed(e0, v);
+      float p[8];
+      uint32_t np = 0, nz = 0;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        p[q] = -1.0f;  // not chosen
+        if (e0 + q < V) {
+          if (v[q] > NEG_INF && bin_of(v[q]) > last) {
+            lkey = umax(lkey, fkey(v[q]));
+          } else {
+            p[q] = prob_of(v[q], P.T, m, S);
+            if (p[q] > 0.0f) ++np;
+            else if (!filt) ++nz;
+          }
+        }
+      }
       uint32_t tot;
-      const bool pos_f = valid && p > 0.0f;
-      const bool zero_f = valid && !(p > 0.0f);
-      const uint32_t both =
-          block_excl_scan((pos_f ? 1u : 0u) + (zero_f ? 0x10000u : 0u), red, tot);
-      if (pos_f) kA[npos + (both & 0xffffu)] = pkey(p, e);
-      if (zero_f) zl[nzero + (both >> 16)] = e;
+      const uint32_t off = block_excl_scan(np + (nz << 16), red, tot);
+      uint32_t ip = npos + (off & 0xffffu), iz = nzero + (off >> 16);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        if (p[q] > 0.0f) kA[ip++] = pkey(p[q], e0 + q);
+        else if (p[q] == 0.0f && !filt) zl[iz++] = e0 + q;
+      }
       npos += tot & 0xffffu;
       nzero += tot >> 16;
     }
-  }
-  wait_stores();
-  __syncthreads();
-  if (tid == 0) __threadfence();  // drop stale vector-L1 lines before re-reads
-  __syncthreads();
+    lkey = wave_max_u32(lkey);
+    if (lane == 0) red[NW + wv] = lkey;
+    wait_stores();
+    __syncthreads();
+    lkey = 0;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) lkey = umax(lkey, red[NW + i]);
+    const float p_lim = (filt && lkey > 0x007fffffu) ? prob_of(funkey(lkey), P.T, m, S) : 0.0f;
+    if (tid == 0) __threadfence();  // drop stale vector-L1 lines before re-reads
+    __syncthreads();
+    // ---- D: sort, then the semantics
   // stable LSD radix sort of kA[0..npos) on bits 32..63, 4 passes of 8 bits
   GLB uint64_t* src = kA;
   GLB uint64_t* dst = kB;
@@ -1246,27 +1501,33 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
     src = dst;
     dst = tmp;
   }
-  // unpack into p / idx lists (sorted positives, then zeros by index)
-  for (uint32_t i = tid; i < npos; i += NT) {
-    const uint64_t k = src[i];
-    plist[i] = __uint_as_float(~(uint32_t)(k >> 32));
-    ilist[i] = (uint32_t)k;
-  }
-  for (uint32_t i = tid; i < nzero; i += NT) {
-    plist[npos + i] = 0.0f;
-    ilist[npos + i] = zl[i];
+    // unpack into p / idx lists (sorted positives, then zeros by index)
+    for (uint32_t i = tid; i < npos; i += NT) {
+      const uint64_t k = src[i];
+      plist[i] = __uint_as_float(~(uint32_t)(k >> 32));
+      ilist[i] = (uint32_t)k;
+    }
+    if (!filt)
+      for (uint32_t i = tid; i < nzero; i += NT) {
+        plist[npos + i] = 0.0f;
+        ilist[npos + i] = zl[i];
+      }
+    wait_stores();
+    __syncthreads();
+    if (tid == 0) __threadfence();
+    __syncthreads();
+    Lst.c = Chain{0.f, 0.f, 0.f, 0};
+    // the exact prefix: every entry with p > p_lim (all V when nothing is left out)
+    const uint32_t E = filt ? first_below(Lst, npos, p_lim, false, sh + 12) : V;
+    const bool good = run_semantics(P, u, E, V, p_lim, Lst, sh + 20, tok, len) &&
+                      !(filt && a.out_cap && len > E && a.out_cap > E);
+    if (good) break;
+    last = SLOW_BINS - 1;
+    __syncthreads();
   }
   wait_stores();
   __syncthreads();
-  if (tid == 0) __threadfence();
-  __syncthreads();
-  (void)lane;
-  GlobList<BlockSync> L{plist, ilist, stage, stage + STAGE, Chain{0.f, 0.f, 0.f, 0}};
-  uint32_t tok = 0, len = 0;
-  run_semantics<BlockSync>(P, G(a.u)[b], V, V, L, sh + 20, tok, len);
-  wait_stores();
-  __syncthreads();
-  write_outputs<BlockSync>(a, b, tok, len, L);
+  write_outputs(a, b, tok, len, Lst);
   wait_stores();
   __syncthreads();
   if (tid == 0) {
@@ -1529,8 +1790,8 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
       const uint32_t i1 = (uint32_t)lane + 64 < n ? f.pidx[64 + lane] : 0u;
       uint32_t tok = 0, len = 0;
       // f.keys is free once sorted into skeys and copied out
-      bool good = semantics_regs(P, u, n, a.V, p0, p1, i0, i1, lane, (LDS float*)f.keys, tok,
-                                 len);
+      bool good = semantics_regs(P, u, n, a.V, plim_e, p0, p1, i0, i1, lane,
+                                 (LDS float*)f.keys, tok, len);
       if (good && a.out_cap && len > n && a.out_cap > n) good = false;
       if (good) {
         if (lane == 0) {
@@ -1550,14 +1811,12 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
       }
       res = good ? 0u : 2u;
     }
-  } else if (threadIdx.x < WAVE) {
-    using WS = WaveSync;
-    LdsList<WS> Ls{f.pp, f.pidx, (LDS float*)f.keys, (LDS float*)f.skeys,
-                   Chain{0.f, 0.f, 0.f, 0}};
+  } else {
+    List Ls{flat(f.pp), flat(f.pidx), Chain{0.f, 0.f, 0.f, 0}};
     uint32_t tok = 0, len = 0;
-    bool good = run_semantics<WS>(P, u, n, a.V, Ls, f.fm + F_SCR, tok, len);
+    bool good = run_semantics(P, u, n, a.V, plim_e, Ls, f.fm + F_SCR, tok, len);
     if (good && a.out_cap && len > n && a.out_cap > n) good = false;
-    if (good) write_outputs<WS>(a, b, tok, len, Ls);
+    if (good) write_outputs(a, b, tok, len, Ls);
     res = good ? 0u : 2u;
   }
   if (SY::N > WAVE) {
@@ -1596,6 +1855,7 @@ __device__ __forceinline__ uint32_t candidate_fast(const Args& a, uint32_t b, co
   const uint32_t pos = block_excl_scan((g0 ? 1u : 0u) + (k0 ? 0x10000u : 0u), f.red, both);
   const uint32_t n0 = both & 0xffffu;
   uint32_t n = both >> 16;
+  float ptail = plim;  // every element not kept has p <= ptail
   if (n <= 128 || !topk) {
     if (k0) f.keys[pos >> 16] = pkey(pv0, e.y);
   } else {
@@ -1630,6 +1890,7 @@ __device__ __forceinline__ uint32_t candidate_fast(const Args& a, uint32_t b, co
       lam_e = lam;
       plim_e = plim;
     }
+    ptail = plim_e;
   }
   if (n > 128) return 1;
   // ---- rank sort: key i against keys 16s .. 16s+15 in thread 128s + i
@@ -1667,7 +1928,8 @@ __device__ __forceinline__ uint32_t candidate_fast(const Args& a, uint32_t b, co
     i0 = (uint32_t)k0;
     i1 = (uint32_t)k1;
     // f.keys is free once sorted into skeys
-    good = semantics_regs(P, u, n, a.V, p0, p1, i0, i1, lane, (LDS float*)f.keys, tok, len);
+    good = semantics_regs(P, u, n, a.V, ptail, p0, p1, i0, i1, lane, (LDS float*)f.keys, tok,
+                          len);
     if (good && a.out_cap && len > n && a.out_cap > n) good = false;
     if (lane == 0) f.fm[F_DONE] = good ? 0u : 2u;
   }
@@ -1809,6 +2071,7 @@ __device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_
       if (lane == 0) {
         f.fm[F_S] = __float_as_uint(S);
         f.fm[F_M] = __float_as_uint(m);
+        f.fm[F_L] = __float_as_uint(L);
         f.fm[F_TOTAL] = total;
         f.fm[F_LAM] = lam;
       }
@@ -1831,8 +2094,9 @@ __device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_
     path = candidate_path<BlockSync>(a, w, b, P, S, m, u, total, lam, f, EMPTY, SORT_CAP);
     if (path == 0) return;
   }
+  const float L = __uint_as_float(f.fm[F_L]);
   __syncthreads();
-  slow_row<DT>(a, w, b, P, S, m, smem);
+  slow_row<DT>(a, w, b, P, S, m, L, smem);
 }
 
 // ---------------------------------------------------------------------------
