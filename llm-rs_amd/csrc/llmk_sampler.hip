@@ -78,7 +78,7 @@ constexpr uint32_t MAX_SLOTS = MAX_TILES + MAX_CHUNKS;  // partials per row: til
 constexpr uint32_t LCAP = 1024;       // candidates a single-segment row keeps in LDS
 constexpr uint32_t MAX_SEG = 64;     // segments per row
 constexpr uint32_t MAX_WGS = 4096;   // candidate-buffer pool entries
-constexpr uint32_t SLOW_SLOTS = 64;  // global scratch slots of the slow path
+constexpr uint32_t SLOW_SLOTS = 512;  // most global scratch slots of the slow path
 constexpr uint32_t SLOW_BINS = 2048; // slow path: bins of the processed logits
 constexpr uint32_t EMPTY = 0xffffffffu;
 constexpr float NEG_INF = -__builtin_huge_valf();
@@ -111,12 +111,13 @@ struct Ws {
   f2v* tile_part;        // [max_batch][MAX_SLOTS]: max, sum (or first argmax) per slot
   u4v* seg_meta;         // [pool]: count, beta, flags, -
   u2v* cand;             // [pool][CAND_CAP]: value bits, index
-  uint32_t* slow_lock;   // [SLOW_SLOTS]
-  uint64_t* slow_keys;   // [SLOW_SLOTS][3][max_vocab]
-  float* slow_p;         // [SLOW_SLOTS][max_vocab]
-  uint32_t* slow_idx;    // [SLOW_SLOTS][max_vocab]
+  uint32_t* slow_lock;   // [slow_slots]
+  uint64_t* slow_keys;   // [slow_slots][3][max_vocab]
+  float* slow_p;         // [slow_slots][max_vocab]
+  uint32_t* slow_idx;    // [slow_slots][max_vocab]
   uint32_t* status;      // [1]
   uint32_t max_vocab;
+  uint32_t slow_slots;   // min(max_batch, SLOW_SLOTS): rows b, b + slow_slots, ... share one
 };
 
 struct RowP {
@@ -1231,9 +1232,10 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
   Hist h;
   hist_carve(h, hb, nwords);
   h.lo = 0;
-  // Acquire scratch slot b % SLOW_SLOTS.  A holder waits on nothing, so the
-  // wait ends; the spin is bounded all the same.
-  const uint32_t slot = b % SLOW_SLOTS;
+  // Acquire scratch slot b % slow_slots (a row has its own up to 512 rows).
+  // A holder waits on nothing, so the wait ends; the spin is bounded all the
+  // same.
+  const uint32_t slot = b % w.slow_slots;
   if (tid == 0) {
     uint32_t got = 0;
     for (uint32_t n = 0; n < (1u << 26); ++n) {
@@ -1367,15 +1369,14 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
         p[q] = -1.0f;  // not chosen
-        if (e0 + q < V) {
-          if (v[q] > NEG_INF && bin_of(v[q]) > last) {
-            lkey = umax(lkey, fkey(v[q]));
-          } else {
-            p[q] = prob_of(v[q], P.T, m, S);
-            if (p[q] > 0.0f) ++np;
-            else if (!filt) ++nz;
-          }
-        }
+        const bool inr = e0 + q < V, fin = inr && v[q] > NEG_INF;
+        const bool chosen = fin && bin_of(v[q]) <= last;
+        if (fin && !chosen) lkey = umax(lkey, fkey(v[q]));
+        if (inr && !fin) p[q] = 0.0f;
+        // the exact p only where a lane of the wave needs one
+        if (__ballot(chosen) != 0 && chosen) p[q] = prob_of(v[q], P.T, m, S);
+        if (p[q] > 0.0f) ++np;
+        else if (p[q] == 0.0f && !filt) ++nz;
       }
       uint32_t tot;
       const uint32_t off = block_excl_scan(np + (nz << 16), red, tot);
@@ -1729,20 +1730,129 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
     }
   }
   SY::sync();
-  if (n0 > SORT_CAP) return 2;
-  // ---- top-k rows: the exact K-th largest candidate logit tightens the
-  // bound (every element below it has p <= plim of that bound)
   const bool topk = P.K > 0 && (uint32_t)P.K < a.V;
   const float plim = lam > 0x007fffffu ? prob_of(funkey(lam - 1), P.T, m, S) : 0.0f;
   uint32_t lam_e = lam;
   float plim_e = plim;
-  if (topk && n0 > 2u * (uint32_t)P.K) {
+  uint32_t n = 0;
+  if (!topk || n0 > SORT_CAP) {
+    // ---- probability bins: the exact p of every gathered candidate above
+    // plim falls in a bin of its top bits (exponent and 4 mantissa bits,
+    // 2033 bins for p <= 1) with its count and mass; the kept set is the
+    // bins from the top down to the first that brings the count to K (top-k
+    // rows) or the mass to top_p (the uniform when top-p is off) + 0.002.
+    // Entries below the last kept bin then have p < its lower edge.
+    LDS uint32_t* bcnt = (LDS uint32_t*)f.pidx;  // 2048 words each, free here
+    LDS float* bmass = f.pp;
+    for (uint32_t i = id; i < 2048; i += SY::N) {
+      bcnt[i] = 0;
+      bmass[i] = 0.0f;
+    }
+    SY::sync();
+    auto each = [&](auto&& fn) __attribute__((always_inline)) {
+      for (uint32_t i0 = 0; i0 < total; i0 += GQ * SY::N) {
+        u2v e[GQ];
+#pragma unroll
+        for (int q = 0; q < GQ; ++q) {
+          const uint32_t i = i0 + q * SY::N + id;
+          e[q] = u2v{0xff800000u, 0u};
+          if (i < total && a.G == 1 && i < LCAP) {
+            e[q] = lcand[i];
+          } else if (i < total) {
+            uint32_t lo = 0, hi = a.G;
+            while (hi - lo > 1) {
+              const uint32_t mid = (lo + hi) >> 1;
+              if (f.soff[mid] <= i) lo = mid;
+              else hi = mid;
+            }
+            e[q] = G(w.cand)[(uint64_t)row_seg_to_wg(a, b, lo) * CAND_CAP + (i - f.soff[lo])];
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < GQ; ++q) {
+          if (i0 + q * SY::N >= total) break;
+          const float v = __uint_as_float(e[q].x);
+          float pv = 0.0f;
+          const bool g = v > NEG_INF && fkey(v) >= lam;
+          if (__ballot(g) != 0 && g) pv = prob_of(v, P.T, m, S);
+          fn(g && pv > plim, pv, e[q].y);
+        }
+      }
+    };
+    each([&](bool k, float pv, uint32_t) __attribute__((always_inline)) {
+      if (k) {
+        const uint32_t bi = __float_as_uint(pv) >> 19;
+        __atomic_fetch_add(&bcnt[bi], 1u, __ATOMIC_RELAXED);
+        __atomic_fetch_add(&bmass[bi], pv, __ATOMIC_RELAXED);
+      }
+    });
+    SY::sync();
+    if (threadIdx.x < WAVE) {
+      // lane l: bins 2047 - 32 l down to 2016 - 32 l
+      const int lane = (int)threadIdx.x;
+      const float tm = (P.top_p < 1.0f ? P.top_p : u) + 0.002f;
+      const bool use_mass = !topk && tm < 1.0f;
+      uint32_t c = 0;
+      float ms = 0.0f;
+      for (int k = 0; k < 32; ++k) {
+        const uint32_t bi = 2047u - 32u * (uint32_t)lane - (uint32_t)k;
+        c += bcnt[bi];
+        ms += bmass[bi];
+      }
+      const uint32_t cincl = wave_incl_scan(c);
+      float mincl = ms;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const float o = __shfl_up(mincl, d);
+        if (lane >= d) mincl += o;
+      }
+      const uint64_t hit = topk ? __ballot(cincl >= (uint32_t)P.K)
+                                : (use_mass ? __ballot(mincl >= tm) : 0ull);
+      uint32_t tb = 0;  // the last kept bin (0: every bin)
+      if (hit) {
+        const int l = __ffsll((unsigned long long)hit) - 1;
+        uint32_t cc = (uint32_t)__shfl((int)(cincl - c), l);
+        float mm = __shfl(mincl - ms, l);
+        for (int k = 0; k < 32; ++k) {
+          const uint32_t bi = 2047u - 32u * (uint32_t)l - (uint32_t)k;
+          cc += bcnt[bi];
+          mm += bmass[bi];
+          if (topk ? cc >= (uint32_t)P.K : mm >= tm) {
+            tb = bi;
+            break;
+          }
+        }
+      }
+      uint32_t nk = 0;
+      for (uint32_t k = (uint32_t)lane; k < 2048; k += WAVE) nk += k >= tb ? bcnt[k] : 0u;
+      nk = bcast63u(wave_incl_scan(nk));
+      if (lane == 0) {
+        f.fm[F_SCR] = tb;
+        f.fm[F_SCR + 1] = nk;
+      }
+    }
+    SY::sync();
+    const uint32_t tb = f.fm[F_SCR], nk = f.fm[F_SCR + 1];
+    SY::sync();
+    if (nk > SORT_CAP) return 2;
+    const uint32_t tbits = tb << 19;
+    if (tbits > 0) plim_e = fmaxf(plim, __uint_as_float(tbits - 1));
+    each([&](bool k, float pv, uint32_t ix) __attribute__((always_inline)) {
+      const bool keep = k && __float_as_uint(pv) >= tbits;
+      uint32_t tot;
+      const uint32_t pos = n + SY::excl_scan(keep, f.red, tot);
+      if (keep) f.keys[pos] = pkey(pv, ix);
+      n += tot;
+    });
+  } else {
+  // ---- top-k rows: the exact K-th largest candidate logit tightens the
+  // bound (every element below it has p <= plim of that bound)
+  if (n0 > 2u * (uint32_t)P.K) {
     const uint32_t tau = kth_largest_key<SY>(cval, n0, (uint32_t)P.K,
                                              (LDS uint32_t*)f.keys, f.fm + F_SCR);
     lam_e = tau;
     plim_e = tau > 0x007fffffu ? prob_of(funkey(tau - 1), P.T, m, S) : 0.0f;
   }
-  uint32_t n = 0;
   for (int attempt = 0; attempt < 2; ++attempt) {
     n = 0;
     for (uint32_t i0 = 0; i0 < n0; i0 += SY::N) {
@@ -1769,6 +1879,7 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
     if (!(topk && n < (uint32_t)P.K && lam_e != lam)) break;
     lam_e = lam;
     plim_e = plim;
+  }
   }
   SY::sync();
   if (n > keep_cap) return 1;
@@ -2703,10 +2814,11 @@ extern "C" int llmk_sampler_create(llmk_sampler** out, int device,
   const size_t o_part = take(8ull * max_batch * MAX_SLOTS);
   const size_t o_meta = take(16ull * pool);
   const size_t o_cand = take(8ull * pool * CAND_CAP);
-  const size_t o_lock = take(4ull * SLOW_SLOTS);
-  const size_t o_skeys = take(8ull * SLOW_SLOTS * 3 * max_vocab);
-  const size_t o_sp = take(4ull * SLOW_SLOTS * max_vocab);
-  const size_t o_si = take(4ull * SLOW_SLOTS * max_vocab);
+  const uint32_t slots = max_batch < SLOW_SLOTS ? max_batch : SLOW_SLOTS;
+  const size_t o_lock = take(4ull * slots);
+  const size_t o_skeys = take(8ull * slots * 3 * max_vocab);
+  const size_t o_sp = take(4ull * slots * max_vocab);
+  const size_t o_si = take(4ull * slots * max_vocab);
   const size_t o_status = take(256);
   void* mem = nullptr;
   HIPCHK(hipMalloc(&mem, off));
@@ -2733,6 +2845,7 @@ extern "C" int llmk_sampler_create(llmk_sampler** out, int device,
   s->ws.slow_idx = (uint32_t*)(base + o_si);
   s->ws.status = (uint32_t*)(base + o_status);
   s->ws.max_vocab = max_vocab;
+  s->ws.slow_slots = slots;
   *out = s;
   g_last_error.clear();
   return LLMK_OK;
