@@ -1350,6 +1350,13 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
     };
     if (hm) last = umin(last, bin_in((uint32_t)__ffsll((unsigned long long)hm) - 1, true));
     if (hk) last = umin(last, bin_in((uint32_t)__ffsll((unsigned long long)hk) - 1, false));
+    // min-p: the chosen bins reach below p_max * min_p (d = log2(min_p)),
+    // so that its cut is seen or lies past every chosen entry
+    if (P.min_p > 0.0f && last < SLOW_BINS - 1) {
+      const float bm = __builtin_ceilf(-16.0f * __builtin_log2f(P.min_p)) + 2.0f;
+      last = umax(last, (uint32_t)__builtin_fminf(__builtin_fmaxf(bm, 0.0f),
+                                                   (float)(SLOW_BINS - 1)));
+    }
     if (lane == 0) sh[11] = last;
   }
   __syncthreads();
@@ -1748,6 +1755,7 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
       bcnt[i] = 0;
       bmass[i] = 0.0f;
     }
+    if (id == 0) f.fm[F_SCR + 2] = 0;
     SY::sync();
     auto each = [&](auto&& fn) __attribute__((always_inline)) {
       for (uint32_t i0 = 0; i0 < total; i0 += GQ * SY::N) {
@@ -1784,6 +1792,7 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
         const uint32_t bi = __float_as_uint(pv) >> 19;
         __atomic_fetch_add(&bcnt[bi], 1u, __ATOMIC_RELAXED);
         __atomic_fetch_add(&bmass[bi], pv, __ATOMIC_RELAXED);
+        __atomic_fetch_max(&f.fm[F_SCR + 2], __float_as_uint(pv), __ATOMIC_RELAXED);
       }
     });
     SY::sync();
@@ -1822,6 +1831,12 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
             break;
           }
         }
+      }
+      // min-p: the kept bins reach below the threshold, so that its cut is
+      // seen (or lies past every kept entry)
+      if (P.min_p > 0.0f) {
+        const uint32_t tk = __float_as_uint(P.min_p * __uint_as_float(f.fm[F_SCR + 2])) >> 19;
+        tb = umin(tb, tk > 0 ? tk - 1 : 0u);
       }
       uint32_t nk = 0;
       for (uint32_t k = (uint32_t)lane; k < 2048; k += WAVE) nk += k >= tb ? bcnt[k] : 0u;

@@ -121,6 +121,20 @@ def test_min_p_rows(sampler):
     check(sampler, w, cap=256, label="min-p")
 
 
+def test_wide_nuclei(sampler):
+    """Flat rows whose nucleus holds 10^3..10^5 tokens: the slow path's
+    choice of bins and its fallback, the exact running sums over long sorted
+    lists (many binade crossings and rounding ties), a top-k above the fast
+    path's limit and a min-p cut next to the chosen bins."""
+    V = 151936
+    rng = np.random.default_rng(11)
+    lg = rng.normal(0, 0.8, (6, V)).astype(np.float32)
+    w = workload(lg, T=[1.0, 1.2, 0.9, 1.0, 1.1, 1.0], K=[0, 0, 0, 0, 5000, 0],
+                 P=[0.5, 0.9, 0.99, 0.9995, 0.95, 1.0], MP=[0.0, 0.0, 0.3, 0.0, 0.0, 0.02],
+                 u=rng.random(6).astype(np.float32))
+    check(sampler, w, cap=4096, label="wide nuclei")
+
+
 def test_empty_and_out_of_vocab_histories(sampler):
     V = 30000
     rng = np.random.default_rng(6)
