@@ -125,10 +125,21 @@ def cpu_baseline(w, budget_s=12.0):
     t0 = time.perf_counter()
     O.sample_workload(O.REF, w, nthreads=nth)
     t_all = time.perf_counter() - t0
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
     return {
         "value": 1e6 / us_per_row,
         "unit": "tokens/s",
         "cores": 1,
+        "cpu_model": model,
+        "host_cpus": os.cpu_count(),
         "kind": "port",
         "sample": f"{rows_done} rows of the {w.name} workload (oracle ref mode, 1 thread, "
                   f"{t_total:.1f} s); us/row {us_per_row:.0f}",

@@ -1604,7 +1604,7 @@ __device__ __forceinline__ uint32_t kth_largest_key(LDS const float* cval, uint3
 // survive the filter); rows it cannot prove exact take the slow path.
 // ---------------------------------------------------------------------------
 enum : uint32_t {
-  F_DONE = 0, F_S = 1, F_M = 2, F_TOTAL = 3, F_LAM = 4, F_OVF = 5, F_L = 6, F_GREEDY = 7,
+  F_DONE = 0, F_S = 1, F_M = 2, F_TOTAL = 3, F_LAM = 4, F_PLIM = 5, F_L = 6, F_GREEDY = 7,
   F_SCR = 8
 };
 // LDS layout of the finalize (words): slots, candidate lists, keys, tables
@@ -1738,7 +1738,7 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
   }
   SY::sync();
   const bool topk = P.K > 0 && (uint32_t)P.K < a.V;
-  const float plim = lam > 0x007fffffu ? prob_of(funkey(lam - 1), P.T, m, S) : 0.0f;
+  const float plim = __uint_as_float(f.fm[F_PLIM]);
   uint32_t lam_e = lam;
   float plim_e = plim;
   uint32_t n = 0;
@@ -1971,7 +1971,7 @@ __device__ __forceinline__ uint32_t candidate_fast(const Args& a, uint32_t b, co
   // exact probabilities above the bound as (p desc, idx asc) keys; one scan
   // counts both (packed in 16-bit halves: total <= LCAP)
   const bool topk = P.K > 0 && (uint32_t)P.K < a.V;
-  const float plim = lam > 0x007fffffu ? prob_of(funkey(lam - 1), P.T, m, S) : 0.0f;
+  const float plim = __uint_as_float(f.fm[F_PLIM]);
   const u2v e = tid < total ? lcand[tid] : u2v{0xff800000u, 0u};
   const float v0 = __uint_as_float(e.x);
   const bool g0 = v0 > NEG_INF && fkey(v0) >= lam;
@@ -2194,10 +2194,14 @@ __device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_
       const uint32_t total = bcast63u(off_incl);
       if ((uint32_t)lane <= a.G) f.soff[lane] = off_incl - cnt;  // lane G: the total
       WaveSync::sync();
+      // the bound on p of every element outside the candidate buffers, once
+      // (wave 0) rather than in every thread of the candidate path
+      const float plim = lam > 0x007fffffu ? prob_of(funkey(lam - 1), P.T, m, S) : 0.0f;
       if (lane == 0) {
         f.fm[F_S] = __float_as_uint(S);
         f.fm[F_M] = __float_as_uint(m);
         f.fm[F_L] = __float_as_uint(L);
+        f.fm[F_PLIM] = __float_as_uint(plim);
         f.fm[F_TOTAL] = total;
         f.fm[F_LAM] = lam;
       }
