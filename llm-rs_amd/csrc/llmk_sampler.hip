@@ -745,7 +745,34 @@ __device__ __forceinline__ Par par_then(Par f, Par g) {
 // mode 0: sum of all n.  mode 1: stop at the first j with cum >= thr.
 // mode 2: stop at the first j with thr <= cum (the draw's `r <= cumulative`).
 // Returns the stop index (n if none) and the running sum including it (the
-// total if none).  sh: 2 words.
+// total if none).  sh: 2 words; z: 128 words.
+// Every lane forms its own prefix: lane l of c0 receives ((p_0 + p_1) + ...)
+// + p_l and lane l of c1 the prefix through entry 64 + l -- the same f32
+// additions in the same order as one sequential sum.  z holds 64 zeros before
+// each half of the entries; lane l reads z[1 + l + t] at step t = 0..63, so it
+// adds 63 - l zeros (+0.0 + +0.0 stays +0.0) and then p_0..p_l.  All 64 reads
+// are issued before the adds and there is no branch: two operations per step.
+// Lanes at or past m hold junk.
+__device__ __forceinline__ float prefix_half(LDS const float* zb, float c) {
+  float x[64];
+#pragma unroll
+  for (uint32_t t = 0; t < 64u; ++t) x[t] = zb[t];
+#pragma unroll
+  for (uint32_t t = 0; t < 64u; ++t) c = c + x[t];
+  return c;
+}
+// prefix_half with sixteen reads in flight at a time (fewer registers)
+__device__ __forceinline__ float prefix_half16(LDS const float* zb, float c) {
+#pragma unroll
+  for (uint32_t t0 = 0; t0 < 64u; t0 += 16u) {
+    float x[16];
+#pragma unroll
+    for (uint32_t t = 0; t < 16u; ++t) x[t] = zb[t0 + t];
+#pragma unroll
+    for (uint32_t t = 0; t < 16u; ++t) c = c + x[t];
+  }
+  return c;
+}
 // Exclusive scan of the pairs over the wave (DPP row shifts and row
 // broadcasts; shifted-in lanes read (0, 0), the identity).
 template <int CTRL, int RM, bool BC>
@@ -769,7 +796,7 @@ __device__ __forceinline__ float pickf(const float (&x)[Q], uint32_t k) {
   return r;
 }
 __device__ __forceinline__ uint32_t seq_scan(const List& list, uint32_t n, int mode, float thr,
-                                             float& cum_out, LDS uint32_t* sh) {
+                                             float& cum_out, LDS uint32_t* sh, LDS float* z) {
   if (threadIdx.x < WAVE) {
     constexpr uint32_t Q = 8, W = Q * WAVE;
     constexpr uint32_t TOP = 1u << 24;
@@ -777,11 +804,30 @@ __device__ __forceinline__ uint32_t seq_scan(const List& list, uint32_t n, int m
     const bool stops = mode != 0;
     uint32_t stop = n;
     float c = 0.0f;
+    uint32_t j0 = 0;
     if (n > 0 && stops && thr <= 0.0f) {  // the first running sum already meets it
       stop = 0;
       c = 0.0f + list.get(0);
+    } else if (n > 0) {
+      // the first 64 entries, where the sum crosses binades often: every
+      // lane forms its own running sum (prefix_half: 63 - lane zeros, then
+      // p_0 .. p_lane, the same f32 additions in the same order)
+      const uint32_t h = umin(n, (uint32_t)WAVE);
+      z[lane] = 0.0f;
+      z[WAVE + lane] = lane < h ? list.get(lane) : 0.0f;
+      WaveSync::sync();
+      const float cl = prefix_half16(z + 1 + lane, 0.0f);
+      WaveSync::sync();
+      const uint64_t hit = stops ? __ballot(lane < h && cl >= thr) : 0ull;
+      if (hit) {
+        stop = (uint32_t)__ffsll((unsigned long long)hit) - 1;
+        c = rl(cl, stop);
+      } else {
+        c = rl(cl, h - 1);
+        j0 = h;
+      }
     }
-    for (uint32_t j = 0; j < n && stop == n; j += W) {
+    for (uint32_t j = j0; j < n && stop == n; j += W) {
       const uint32_t lim = umin(n - j, W);
       float p[Q];
 #pragma unroll
@@ -931,8 +977,8 @@ __device__ __forceinline__ uint32_t first_below(const List& list, uint32_t n, fl
 // beyond E would be needed.  The four steps share one running-sum call.
 __device__ __forceinline__ bool run_semantics(const RowP& P, float u, uint32_t E,
                                               uint32_t full_len, float ptail, List& list,
-                                              LDS uint32_t* sh, uint32_t& tok_out,
-                                              uint32_t& len_out) {
+                                              LDS uint32_t* sh, LDS float* z,
+                                              uint32_t& tok_out, uint32_t& len_out) {
   uint32_t len = full_len;
   bool trunc = E < full_len;
   for (int step = 0; step < 4; ++step) {
@@ -972,7 +1018,7 @@ __device__ __forceinline__ bool run_semantics(const RowP& P, float u, uint32_t E
       thr = step == 2 ? P.top_p : u;
     }
     float s;
-    const uint32_t j = seq_scan(list, n, mode, thr, s, sh);
+    const uint32_t j = seq_scan(list, n, mode, thr, s, sh, z);
     if (step == 3) {
       uint32_t tok;
       if (j < n) tok = list.id(j);
@@ -1018,21 +1064,6 @@ __device__ __forceinline__ void write_outputs(const Args& a, uint32_t b, uint32_
 // same order; the running sums are wave-uniform, each step reading one entry
 // with v_readlane.  Returns false if an entry beyond E = n would be needed.
 // ---------------------------------------------------------------------------
-// Every lane forms its own prefix: lane l of c0 receives ((p_0 + p_1) + ...)
-// + p_l and lane l of c1 the prefix through entry 64 + l -- the same f32
-// additions in the same order as one sequential sum.  z holds 64 zeros before
-// each half of the entries; lane l reads z[1 + l + t] at step t = 0..63, so it
-// adds 63 - l zeros (+0.0 + +0.0 stays +0.0) and then p_0..p_l.  All 64 reads
-// are issued before the adds and there is no branch: two operations per step.
-// Lanes at or past m hold junk.
-__device__ __forceinline__ float prefix_half(LDS const float* zb, float c) {
-  float x[64];
-#pragma unroll
-  for (uint32_t t = 0; t < 64u; ++t) x[t] = zb[t];
-#pragma unroll
-  for (uint32_t t = 0; t < 64u; ++t) c = c + x[t];
-  return c;
-}
 // z: 256 LDS words owned by the calling wave; 1 <= m <= 128.
 __device__ __forceinline__ void prefix_regs(float p0, float p1, uint32_t m, int lane,
                                             LDS float* z, float& c0, float& c1) {
@@ -1527,7 +1558,7 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
     Lst.c = Chain{0.f, 0.f, 0.f, 0};
     // the exact prefix: every entry with p > p_lim (all V when nothing is left out)
     const uint32_t E = filt ? first_below(Lst, npos, p_lim, false, sh + 12) : V;
-    const bool good = run_semantics(P, u, E, V, p_lim, Lst, sh + 20, tok, len) &&
+    const bool good = run_semantics(P, u, E, V, p_lim, Lst, sh + 20, (LDS float*)wcnt, tok, len) &&
                       !(filt && a.out_cap && len > E && a.out_cap > E);
     if (good) break;
     last = SLOW_BINS - 1;
@@ -1633,37 +1664,39 @@ __device__ __forceinline__ FinLds fin_carve(LDS uint32_t* smem) {
   return f;
 }
 
-// Ascending sort of keys[0..n) into skeys[0..n) (keys distinct).
+// Ascending sort of keys[0..n) into skeys[0..n) (keys distinct), by the
+// whole workgroup.  Up to 1024 keys: a rank sort split over the threads --
+// key i is compared with one of NT / npad segments of the keys by thread
+// g * npad + i (eight reads in flight), and the partial ranks meet in LDS
+// (pp, free until the sorted keys are unpacked); waves past the keys skip.
+// Larger n: a bitonic sort.
 template <class SY>
 __device__ __forceinline__ void sort_keys(const FinLds& f, uint32_t n) {
-  if (n <= 4 * SY::N && (SY::N == WAVE || n <= SY::N)) {
-    // rank sort: up to 4 keys per thread, every key read once per thread
-    const uint32_t i0 = SY::id();
-    uint64_t k[4];
-    uint32_t r[4];
+  if (n <= SY::N) {
+    uint32_t npad = WAVE;
+    while (npad < n) npad <<= 1;
+    const uint32_t ns = SY::N / npad;           // segments per key
+    const uint32_t seg = (n + ns - 1) / ns;
+    const uint32_t i = SY::id() % npad, g = SY::id() / npad;
+    LDS uint32_t* rk = (LDS uint32_t*)f.pp;
+    if (SY::id() < n) rk[SY::id()] = 0;
+    SY::sync();
+    const uint32_t j0 = g * seg, j1 = umin(j0 + seg, n);
+    if (i < n && j0 < j1) {
+      const uint64_t k = f.keys[i];
+      uint32_t r = 0, j = j0;
+      for (; j + 8 <= j1; j += 8) {
+        uint64_t x[8];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      k[q] = (i0 + q * SY::N < n) ? f.keys[i0 + q * SY::N] : ~0ull;
-      r[q] = 0;
+        for (int e = 0; e < 8; ++e) x[e] = f.keys[j + e];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r += (x[e] < k) ? 1u : 0u;
+      }
+      for (; j < j1; ++j) r += (f.keys[j] < k) ? 1u : 0u;
+      if (r) __atomic_fetch_add(&rk[i], r, __ATOMIC_RELAXED);
     }
-    uint32_t j = 0;
-    for (; j + 8 <= n; j += 8) {  // eight independent reads per step
-      uint64_t x[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = f.keys[j + e];
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) r[q] += (x[e] < k[q]) ? 1u : 0u;
-    }
-    for (; j < n; ++j) {
-      const uint64_t x = f.keys[j];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) r[q] += (x < k[q]) ? 1u : 0u;
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      if (i0 + q * SY::N < n) f.skeys[r[q]] = k[q];
+    SY::sync();
+    if (SY::id() < n) f.skeys[rk[SY::id()]] = f.keys[SY::id()];
     SY::sync();
     return;
   }
@@ -1940,7 +1973,8 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
   } else {
     List Ls{flat(f.pp), flat(f.pidx), Chain{0.f, 0.f, 0.f, 0}};
     uint32_t tok = 0, len = 0;
-    bool good = run_semantics(P, u, n, a.V, plim_e, Ls, f.fm + F_SCR, tok, len);
+    bool good = run_semantics(P, u, n, a.V, plim_e, Ls, f.fm + F_SCR, (LDS float*)f.keys, tok,
+                              len);
     if (good && a.out_cap && len > n && a.out_cap > n) good = false;
     if (good) write_outputs(a, b, tok, len, Ls);
     res = good ? 0u : 2u;
