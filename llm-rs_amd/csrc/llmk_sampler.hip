@@ -704,6 +704,7 @@ struct List {
   const float* p;
   const uint32_t* idx;
   Chain c;
+  float* wp;  // p, writable (an LDS list): renormalisations rewrite it
   __device__ float get(uint32_t i) const { return c.apply(p[i]); }
   __device__ uint32_t id(uint32_t i) const { return idx[i]; }
 };
@@ -809,22 +810,27 @@ __device__ __forceinline__ uint32_t seq_scan(const List& list, uint32_t n, int m
       stop = 0;
       c = 0.0f + list.get(0);
     } else if (n > 0) {
-      // the first 64 entries, where the sum crosses binades often: every
-      // lane forms its own running sum (prefix_half: 63 - lane zeros, then
-      // p_0 .. p_lane, the same f32 additions in the same order)
-      const uint32_t h = umin(n, (uint32_t)WAVE);
-      z[lane] = 0.0f;
-      z[WAVE + lane] = lane < h ? list.get(lane) : 0.0f;
-      WaveSync::sync();
-      const float cl = prefix_half16(z + 1 + lane, 0.0f);
-      WaveSync::sync();
-      const uint64_t hit = stops ? __ballot(lane < h && cl >= thr) : 0ull;
-      if (hit) {
-        stop = (uint32_t)__ffsll((unsigned long long)hit) - 1;
-        c = rl(cl, stop);
-      } else {
+      // the first 256 entries, where the sum crosses binades often, 64 at a
+      // time: every lane forms its own running sum (prefix_half16 from c:
+      // 63 - lane zeros, which leave c as it is, then p_base .. p_base+lane,
+      // the same f32 additions in the same order)
+      const uint32_t hn = umin(n, 4u * WAVE);
+      while (j0 < hn) {
+        const uint32_t h = umin(hn - j0, (uint32_t)WAVE);
+        z[lane] = 0.0f;
+        z[WAVE + lane] = lane < h ? list.get(j0 + lane) : 0.0f;
+        WaveSync::sync();
+        const float cl = prefix_half16(z + 1 + lane, c);
+        WaveSync::sync();
+        const uint64_t hit = stops ? __ballot(lane < h && cl >= thr) : 0ull;
+        if (hit) {
+          const uint32_t js = (uint32_t)__ffsll((unsigned long long)hit) - 1;
+          stop = j0 + js;
+          c = rl(cl, js);
+          break;
+        }
         c = rl(cl, h - 1);
-        j0 = h;
+        j0 += h;
       }
     }
     for (uint32_t j = j0; j < n && stop == n; j += W) {
@@ -935,8 +941,17 @@ __device__ __forceinline__ uint32_t seq_scan(const List& list, uint32_t n, int m
   return stop;
 }
 
-__device__ __forceinline__ void div_all(List& list, float s) {
-  if (s > 0.0f) list.c.push(s);
+// The renormalisation p /= s of the first len entries (sampler.rs:84-87,
+// :104-109): rewritten in place for a writable list (every thread calls
+// it), else recorded in the divisor chain.
+__device__ __forceinline__ void div_all(List& list, float s, uint32_t len) {
+  if (!(s > 0.0f)) return;
+  if (list.wp) {
+    for (uint32_t i = threadIdx.x; i < len; i += NT) list.wp[i] = list.wp[i] / s;
+    __syncthreads();
+  } else {
+    list.c.push(s);
+  }
 }
 
 // First i < n with list[i] < thr (strict) or <= thr, n if none; the list is
@@ -1037,7 +1052,7 @@ __device__ __forceinline__ bool run_semantics(const RowP& P, float u, uint32_t E
       len = (j < n) ? j + 1 : len;
       trunc = false;
     }
-    div_all(list, s);
+    div_all(list, s, len);
   }
   return false;
 }
@@ -1393,7 +1408,7 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
   __syncthreads();
   uint32_t last = sh[11];
   uint32_t tok = 0, len = 0;
-  List Lst{flat(plist), flat(ilist), Chain{0.f, 0.f, 0.f, 0}};
+  List Lst{flat(plist), flat(ilist), Chain{0.f, 0.f, 0.f, 0}, nullptr};
   for (int attempt = 0; attempt < 2; ++attempt) {
     const bool filt = last < SLOW_BINS - 1;
     // ---- C: exact p of the chosen elements, in index order
@@ -1665,17 +1680,22 @@ __device__ __forceinline__ FinLds fin_carve(LDS uint32_t* smem) {
 }
 
 // Ascending sort of keys[0..n) into skeys[0..n) (keys distinct), by the
-// whole workgroup.  Up to 1024 keys: a rank sort split over the threads --
-// key i is compared with one of NT / npad segments of the keys by thread
-// g * npad + i (eight reads in flight), and the partial ranks meet in LDS
-// (pp, free until the sorted keys are unpacked); waves past the keys skip.
-// Larger n: a bitonic sort.
+// whole workgroup.
+//   n <= 256: a rank sort split over the threads (key i against one of
+//     NT / npad segments in thread g * npad + i; the partial ranks meet in
+//     LDS), three barriers;
+//   n <= NT: one key per thread: NT bins over the range of the keys' top
+//     words, the keys moved to bin order, then each key's rank among its bin
+//     (a key or two, more only for equal probabilities);
+//   larger n: a bitonic sort.
+// The ranks, bins and moved keys use pp / pidx, free until the sorted keys
+// are unpacked.
 template <class SY>
 __device__ __forceinline__ void sort_keys(const FinLds& f, uint32_t n) {
-  if (n <= SY::N) {
+  if (n <= 256) {
     uint32_t npad = WAVE;
     while (npad < n) npad <<= 1;
-    const uint32_t ns = SY::N / npad;           // segments per key
+    const uint32_t ns = SY::N / npad;
     const uint32_t seg = (n + ns - 1) / ns;
     const uint32_t i = SY::id() % npad, g = SY::id() / npad;
     LDS uint32_t* rk = (LDS uint32_t*)f.pp;
@@ -1684,19 +1704,46 @@ __device__ __forceinline__ void sort_keys(const FinLds& f, uint32_t n) {
     const uint32_t j0 = g * seg, j1 = umin(j0 + seg, n);
     if (i < n && j0 < j1) {
       const uint64_t k = f.keys[i];
-      uint32_t r = 0, j = j0;
-      for (; j + 8 <= j1; j += 8) {
-        uint64_t x[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = f.keys[j + e];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) r += (x[e] < k) ? 1u : 0u;
-      }
-      for (; j < j1; ++j) r += (f.keys[j] < k) ? 1u : 0u;
+      uint32_t r = 0;
+      for (uint32_t j = j0; j < j1; ++j) r += (f.keys[j] < k) ? 1u : 0u;
       if (r) __atomic_fetch_add(&rk[i], r, __ATOMIC_RELAXED);
     }
     SY::sync();
     if (SY::id() < n) f.skeys[rk[SY::id()]] = f.keys[SY::id()];
+    SY::sync();
+    return;
+  }
+  if (n <= SY::N) {
+    const uint32_t id = SY::id();
+    LDS uint64_t* tmp = (LDS uint64_t*)f.pp;  // n keys in bin order
+    LDS uint32_t* bo = (LDS uint32_t*)f.pp + 2 * SY::N;  // NT bin offsets
+    LDS uint32_t* bq = bo + SY::N;                       // NT cursors
+    const uint64_t k = id < n ? f.keys[id] : ~0ull;
+    const uint32_t hi = (uint32_t)(k >> 32);
+    const uint32_t hmin = block_min_u32(id < n ? hi : EMPTY, f.red);
+    const uint32_t hmax = ~block_min_u32(id < n ? ~hi : EMPTY, f.red);
+    uint32_t sh = 0;
+    while (((hmax - hmin) >> sh) >= SY::N) ++sh;
+    const uint32_t bi = (hi - hmin) >> sh;
+    bo[id] = 0;
+    SY::sync();
+    if (id < n) __atomic_fetch_add(&bo[bi], 1u, __ATOMIC_RELAXED);
+    SY::sync();
+    {
+      uint32_t tot;
+      const uint32_t ex = block_excl_scan(bo[id], f.red, tot);
+      bo[id] = ex;
+      bq[id] = ex;
+    }
+    SY::sync();
+    if (id < n) tmp[__atomic_fetch_add(&bq[bi], 1u, __ATOMIC_RELAXED)] = k;
+    SY::sync();
+    if (id < n) {
+      const uint32_t o = bo[bi], oe = bi + 1 < SY::N ? bo[bi + 1] : n;
+      uint32_t r = o;
+      for (uint32_t j = o; j < oe; ++j) r += tmp[j] < k ? 1u : 0u;
+      f.skeys[r] = k;
+    }
     SY::sync();
     return;
   }
@@ -1730,105 +1777,130 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
                                                    uint32_t keep_cap) {
   LDS const u2v* lcand = (LDS const u2v*)((LDS uint32_t*)f.tl + a.lds_cand);
   const uint32_t id = SY::id();
-  // ---- gather the candidates at or above lam: every element not in the
-  // candidate buffers has a key below lam
-  LDS float* cval = f.pp;
-  LDS uint32_t* cidx = f.pidx;
   if (total > gather_cap) return 1;
-  uint32_t n0 = 0;
-  constexpr int GQ = 8;  // candidate loads in flight per thread
-  for (uint32_t i0 = 0; i0 < total; i0 += GQ * SY::N) {
-    u2v e[GQ];
-#pragma unroll
-    for (int q = 0; q < GQ; ++q) {
-      const uint32_t i = i0 + q * SY::N + id;
-      e[q] = u2v{0xff800000u, 0u};
-      if (i < total && a.G == 1 && i < LCAP) {
-        e[q] = lcand[i];
-      } else if (i < total) {
-        uint32_t lo = 0, hi = a.G;  // soff[lo] <= i < soff[hi]
-        while (hi - lo > 1) {
-          const uint32_t mid = (lo + hi) >> 1;
-          if (f.soff[mid] <= i) lo = mid;
-          else hi = mid;
-        }
-        e[q] = G(w.cand)[(uint64_t)row_seg_to_wg(a, b, lo) * CAND_CAP + (i - f.soff[lo])];
-      }
-    }
-#pragma unroll
-    for (int q = 0; q < GQ; ++q) {
-      if (i0 + q * SY::N >= total) break;
-      const float v = __uint_as_float(e[q].x);
-      const bool keep = v > NEG_INF && fkey(v) >= lam;
-      uint32_t tot;
-      const uint32_t pos = n0 + SY::excl_scan(keep, f.red, tot);
-      if (keep && pos < SORT_CAP) {
-        cval[pos] = v;
-        cidx[pos] = e[q].y;
-      }
-      n0 += tot;
-    }
-  }
-  SY::sync();
   const bool topk = P.K > 0 && (uint32_t)P.K < a.V;
   const float plim = __uint_as_float(f.fm[F_PLIM]);
   uint32_t lam_e = lam;
   float plim_e = plim;
-  uint32_t n = 0;
-  if (!topk || n0 > SORT_CAP) {
-    // ---- probability bins: the exact p of every gathered candidate above
-    // plim falls in a bin of its top bits (exponent and 4 mantissa bits,
-    // 2033 bins for p <= 1) with its count and mass; the kept set is the
-    // bins from the top down to the first that brings the count to K (top-k
-    // rows) or the mass to top_p (the uniform when top-p is off) + 0.002.
-    // Entries below the last kept bin then have p < its lower edge.
-    LDS uint32_t* bcnt = (LDS uint32_t*)f.pidx;  // 2048 words each, free here
-    LDS float* bmass = f.pp;
+  constexpr int GQ = 8;  // candidate loads in flight per thread
+  // candidate i of the row: the LDS list, else the segments' global buffers
+  auto load = [&](uint32_t i) __attribute__((always_inline)) {
+    u2v e = u2v{0xff800000u, 0u};
+    if (i < total && a.G == 1 && i < LCAP) {
+      e = lcand[i];
+    } else if (i < total) {
+      uint32_t lo = 0, hi = a.G;  // soff[lo] <= i < soff[hi]
+      while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (f.soff[mid] <= i) lo = mid;
+        else hi = mid;
+      }
+      e = G(w.cand)[(uint64_t)row_seg_to_wg(a, b, lo) * CAND_CAP + (i - f.soff[lo])];
+    }
+    return e;
+  };
+  // Probability bins: the exact p of a candidate above plim falls in a bin
+  // of its top bits (exponent and 4 mantissa bits, 2033 bins for p <= 1),
+  // with its count and mass.  The kept set is the bins from the top down to
+  // the first that brings the count to K (top-k rows) or the mass to top_p
+  // (the uniform when top-p is off) + 0.002; entries below the last kept
+  // bin then have p below its lower edge.  The bins live in skeys, free
+  // until the kept keys are sorted.
+  LDS uint32_t* bcnt = (LDS uint32_t*)f.skeys;
+  LDS float* bmass = (LDS float*)f.skeys + 2048;
+  auto hist_clear = [&]() __attribute__((always_inline)) {
     for (uint32_t i = id; i < 2048; i += SY::N) {
       bcnt[i] = 0;
       bmass[i] = 0.0f;
     }
     if (id == 0) f.fm[F_SCR + 2] = 0;
+  };
+  auto hist_add = [&](float pv) __attribute__((always_inline)) {
+    const uint32_t bi = __float_as_uint(pv) >> 19;
+    __atomic_fetch_add(&bcnt[bi], 1u, __ATOMIC_RELAXED);
+    __atomic_fetch_add(&bmass[bi], pv, __ATOMIC_RELAXED);
+    __atomic_fetch_max(&f.fm[F_SCR + 2], __float_as_uint(pv), __ATOMIC_RELAXED);
+  };
+  // pv of candidate e if it is at or above lam (0 otherwise), where a lane
+  // of the wave needs one
+  auto exact_p = [&](u2v e, bool& g) __attribute__((always_inline)) {
+    const float v = __uint_as_float(e.x);
+    g = v > NEG_INF && fkey(v) >= lam;
+    float pv = 0.0f;
+    if (__ballot(g) != 0 && g) pv = prob_of(v, P.T, m, S);
+    return pv;
+  };
+  // a further pass over the candidates from their buffers: fn(kept, p, idx)
+  auto each = [&](auto&& fn) __attribute__((always_inline)) {
+    for (uint32_t i0 = 0; i0 < total; i0 += GQ * SY::N) {
+      u2v e[GQ];
+#pragma unroll
+      for (int q = 0; q < GQ; ++q) e[q] = load(i0 + q * SY::N + id);
+#pragma unroll
+      for (int q = 0; q < GQ; ++q) {
+        if (i0 + q * SY::N >= total) break;
+        bool g;
+        const float pv = exact_p(e[q], g);
+        fn(g && pv > plim, pv, e[q].y);
+      }
+    }
+  };
+  // ---- one pass over the candidates at or above lam (every element not in
+  // the buffers has a key below lam): top-k rows keep (logit, idx), other
+  // rows (p, idx) of those with p > plim, binned; one scan per GQ slots
+  LDS float* cval = f.pp;
+  LDS uint32_t* cidx = f.pidx;
+  if (!topk) {
+    hist_clear();
     SY::sync();
-    auto each = [&](auto&& fn) __attribute__((always_inline)) {
-      for (uint32_t i0 = 0; i0 < total; i0 += GQ * SY::N) {
-        u2v e[GQ];
+  }
+  uint32_t n0 = 0;
+  for (uint32_t i0 = 0; i0 < total; i0 += GQ * SY::N) {
+    u2v e[GQ];
 #pragma unroll
-        for (int q = 0; q < GQ; ++q) {
-          const uint32_t i = i0 + q * SY::N + id;
-          e[q] = u2v{0xff800000u, 0u};
-          if (i < total && a.G == 1 && i < LCAP) {
-            e[q] = lcand[i];
-          } else if (i < total) {
-            uint32_t lo = 0, hi = a.G;
-            while (hi - lo > 1) {
-              const uint32_t mid = (lo + hi) >> 1;
-              if (f.soff[mid] <= i) lo = mid;
-              else hi = mid;
-            }
-            e[q] = G(w.cand)[(uint64_t)row_seg_to_wg(a, b, lo) * CAND_CAP + (i - f.soff[lo])];
-          }
-        }
+    for (int q = 0; q < GQ; ++q) e[q] = load(i0 + q * SY::N + id);
+    float val[GQ];
+    uint32_t km = 0;
 #pragma unroll
-        for (int q = 0; q < GQ; ++q) {
-          if (i0 + q * SY::N >= total) break;
-          const float v = __uint_as_float(e[q].x);
-          float pv = 0.0f;
-          const bool g = v > NEG_INF && fkey(v) >= lam;
-          if (__ballot(g) != 0 && g) pv = prob_of(v, P.T, m, S);
-          fn(g && pv > plim, pv, e[q].y);
+    for (int q = 0; q < GQ; ++q) {
+      if (topk) {
+        const float v = __uint_as_float(e[q].x);
+        val[q] = v;
+        if (v > NEG_INF && fkey(v) >= lam) km |= 1u << q;
+      } else {
+        bool g;
+        val[q] = exact_p(e[q], g);
+        if (g && val[q] > plim) {
+          km |= 1u << q;
+          hist_add(val[q]);
         }
       }
-    };
-    each([&](bool k, float pv, uint32_t) __attribute__((always_inline)) {
-      if (k) {
-        const uint32_t bi = __float_as_uint(pv) >> 19;
-        __atomic_fetch_add(&bcnt[bi], 1u, __ATOMIC_RELAXED);
-        __atomic_fetch_add(&bmass[bi], pv, __ATOMIC_RELAXED);
-        __atomic_fetch_max(&f.fm[F_SCR + 2], __float_as_uint(pv), __ATOMIC_RELAXED);
+    }
+    uint32_t tot;
+    uint32_t pos = n0 + block_excl_scan((uint32_t)__popc(km), f.red, tot);
+#pragma unroll
+    for (int q = 0; q < GQ; ++q)
+      if ((km >> q) & 1u) {
+        if (pos < SORT_CAP) {
+          cval[pos] = val[q];
+          cidx[pos] = e[q].y;
+        }
+        ++pos;
       }
-    });
-    SY::sync();
+    n0 += tot;
+  }
+  SY::sync();
+  uint32_t n = 0;
+  if (!topk || n0 > SORT_CAP) {
+    if (topk) {
+      // more than SORT_CAP top-k candidates: bin them by p, a second pass
+      hist_clear();
+      SY::sync();
+      each([&](bool k, float pv, uint32_t) __attribute__((always_inline)) {
+        if (k) hist_add(pv);
+      });
+      SY::sync();
+    }
     if (threadIdx.x < WAVE) {
       // lane l: bins 2047 - 32 l down to 2016 - 32 l
       const int lane = (int)threadIdx.x;
@@ -1885,13 +1957,25 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
     if (nk > SORT_CAP) return 2;
     const uint32_t tbits = tb << 19;
     if (tbits > 0) plim_e = fmaxf(plim, __uint_as_float(tbits - 1));
-    each([&](bool k, float pv, uint32_t ix) __attribute__((always_inline)) {
-      const bool keep = k && __float_as_uint(pv) >= tbits;
-      uint32_t tot;
-      const uint32_t pos = n + SY::excl_scan(keep, f.red, tot);
-      if (keep) f.keys[pos] = pkey(pv, ix);
-      n += tot;
-    });
+    if (!topk && n0 <= SORT_CAP) {
+      // the kept bins, from the gathered (p, idx) in LDS
+      for (uint32_t i0 = 0; i0 < n0; i0 += SY::N) {
+        const uint32_t i = i0 + id;
+        const bool keep = i < n0 && __float_as_uint(cval[i]) >= tbits;
+        uint32_t tot;
+        const uint32_t pos = n + SY::excl_scan(keep, f.red, tot);
+        if (keep) f.keys[pos] = pkey(cval[i], cidx[i]);
+        n += tot;
+      }
+    } else {
+      each([&](bool k, float pv, uint32_t ix) __attribute__((always_inline)) {
+        const bool keep = k && __float_as_uint(pv) >= tbits;
+        uint32_t tot;
+        const uint32_t pos = n + SY::excl_scan(keep, f.red, tot);
+        if (keep) f.keys[pos] = pkey(pv, ix);
+        n += tot;
+      });
+    }
   } else {
   // ---- top-k rows: the exact K-th largest candidate logit tightens the
   // bound (every element below it has p <= plim of that bound)
@@ -1971,7 +2055,7 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
       res = good ? 0u : 2u;
     }
   } else {
-    List Ls{flat(f.pp), flat(f.pidx), Chain{0.f, 0.f, 0.f, 0}};
+    List Ls{flat(f.pp), flat(f.pidx), Chain{0.f, 0.f, 0.f, 0}, (float*)f.pp};
     uint32_t tok = 0, len = 0;
     bool good = run_semantics(P, u, n, a.V, plim_e, Ls, f.fm + F_SCR, (LDS float*)f.keys, tok,
                               len);
