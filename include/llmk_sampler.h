@@ -57,11 +57,14 @@ extern "C" {
 
 typedef struct llmk_sampler llmk_sampler; /* opaque; owns device workspace */
 
-typedef enum { LLMK_F32 = 0, LLMK_BF16 = 1 } llmk_dtype;
+/* Logit element types.  bf16 and f16 (IEEE half, the lm_head output of
+ * half-precision models) are converted exactly to f32 as they are read, as
+ * candle's to_dtype(F32) does before sampling (candle.rs:2007-2010). */
+typedef enum { LLMK_F32 = 0, LLMK_BF16 = 1, LLMK_F16 = 2 } llmk_dtype;
 
 typedef struct {
   /* logits[b * row_stride + v], v < vocab; row_stride in elements.  fp32 rows
-   * must be 16-byte aligned, bf16 rows 8-byte aligned. */
+   * must be 16-byte aligned, bf16 and f16 rows 8-byte aligned. */
   const void* logits;
   int32_t dtype; /* llmk_dtype */
   uint32_t batch;

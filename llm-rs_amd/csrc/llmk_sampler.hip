@@ -286,10 +286,16 @@ __device__ __forceinline__ float penalize(float x, const RowP& P,
   return x;
 }
 
+// A 16-bit logit (bf16 or f16 bits) as f32, exactly.
+template <int DT>
+__device__ __forceinline__ float cvt16(uint32_t h) {
+  if (DT == LLMK_BF16) return __uint_as_float(h << 16);
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
 template <int DT>
 __device__ __forceinline__ float load_logit(const void* row, uint32_t e) {
   if (DT == LLMK_F32) return G((const float*)row)[e];
-  return __uint_as_float((uint32_t)G((const uint16_t*)row)[e] << 16);
+  return cvt16<DT>(G((const uint16_t*)row)[e]);
 }
 
 struct Hist {
@@ -597,11 +603,12 @@ __device__ __forceinline__ void load_tile(const Args& a, const void* row,
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const uint32_t e = tb + 256u * r + 4u * lane + q;
-        uint32_t bits = 0xff800000u;  // -inf beyond the vocabulary
-        if (e < a.V) bits = __float_as_uint(load_logit<DT>(row, e));
-        if (DT == LLMK_F32) raw.d[4 * r + q] = bits;
-        else {
-          const uint32_t hv = bits >> 16;
+        if (DT == LLMK_F32) {
+          raw.d[4 * r + q] = e < a.V ? G((const uint32_t*)row)[e] : 0xff800000u;  // -inf past V
+        } else {
+          // the raw 16-bit value, -inf past V
+          const uint32_t hv = e < a.V ? (uint32_t)G((const uint16_t*)row)[e]
+                                      : (DT == LLMK_BF16 ? 0xff80u : 0xfc00u);
           const int w = 2 * r + (q >> 1);
           if ((q & 1) == 0) raw.d[w] = hv;
           else raw.d[w] |= hv << 16;
@@ -625,10 +632,17 @@ __device__ __forceinline__ void unpack(const Raw& raw, float v[16]) {
   } else {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      v[4 * r + 0] = __uint_as_float(raw.d[2 * r] << 16);
-      v[4 * r + 1] = __uint_as_float(raw.d[2 * r] & 0xffff0000u);
-      v[4 * r + 2] = __uint_as_float(raw.d[2 * r + 1] << 16);
-      v[4 * r + 3] = __uint_as_float(raw.d[2 * r + 1] & 0xffff0000u);
+      if (DT == LLMK_BF16) {
+        v[4 * r + 0] = __uint_as_float(raw.d[2 * r] << 16);
+        v[4 * r + 1] = __uint_as_float(raw.d[2 * r] & 0xffff0000u);
+        v[4 * r + 2] = __uint_as_float(raw.d[2 * r + 1] << 16);
+        v[4 * r + 3] = __uint_as_float(raw.d[2 * r + 1] & 0xffff0000u);
+      } else {
+        v[4 * r + 0] = cvt16<DT>(raw.d[2 * r] & 0xffffu);
+        v[4 * r + 1] = cvt16<DT>(raw.d[2 * r] >> 16);
+        v[4 * r + 2] = cvt16<DT>(raw.d[2 * r + 1] & 0xffffu);
+        v[4 * r + 3] = cvt16<DT>(raw.d[2 * r + 1] >> 16);
+      }
     }
   }
 }
@@ -1233,8 +1247,8 @@ __device__ __forceinline__ void load8(const void* row, uint32_t e0, uint32_t V, 
       const uint32_t w[4] = {a.x, a.y, b.x, b.y};
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        x[2 * q] = __uint_as_float(w[q] << 16);
-        x[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
+        x[2 * q] = cvt16<DT>(w[q] & 0xffffu);
+        x[2 * q + 1] = cvt16<DT>(w[q] >> 16);
       }
     }
   } else {
@@ -2940,6 +2954,8 @@ extern "C" int llmk_sampler_create(llmk_sampler** out, int device,
                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
   HIPCHK(hipFuncSetAttribute((const void*)stream_kernel<LLMK_BF16>,
                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+  HIPCHK(hipFuncSetAttribute((const void*)stream_kernel<LLMK_F16>,
+                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
   const uint32_t pool = max_batch > MAX_WGS ? max_batch : MAX_WGS;
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -3020,8 +3036,8 @@ extern "C" int llmk_sample_batch(llmk_sampler* s,
   if (in->batch == 0) return fail(LLMK_ERR_INVALID_ARGUMENT, "batch is 0");
   if (!in->logits || !in->out_tokens || !in->uniforms)
     return fail(LLMK_ERR_INVALID_ARGUMENT, "logits, uniforms and out_tokens are required");
-  if (in->dtype != LLMK_F32 && in->dtype != LLMK_BF16)
-    return fail(LLMK_ERR_INVALID_ARGUMENT, "dtype must be LLMK_F32 or LLMK_BF16");
+  if (in->dtype != LLMK_F32 && in->dtype != LLMK_BF16 && in->dtype != LLMK_F16)
+    return fail(LLMK_ERR_INVALID_ARGUMENT, "dtype must be LLMK_F32, LLMK_BF16 or LLMK_F16");
   if (in->batch > s->max_batch || in->vocab > s->max_vocab)
     return fail(LLMK_ERR_CAPACITY, "batch or vocab above the sampler's maxima");
   if (in->row_stride < in->vocab)
@@ -3091,8 +3107,10 @@ extern "C" int llmk_sample_batch(llmk_sampler* s,
   const dim3 grid(a.B * a.G), block(NT);
   if (a.dtype == LLMK_F32)
     hipLaunchKernelGGL(stream_kernel<LLMK_F32>, grid, block, lds, st, a, s->ws);
-  else
+  else if (a.dtype == LLMK_BF16)
     hipLaunchKernelGGL(stream_kernel<LLMK_BF16>, grid, block, lds, st, a, s->ws);
+  else
+    hipLaunchKernelGGL(stream_kernel<LLMK_F16>, grid, block, lds, st, a, s->ws);
   HIPCHK(hipGetLastError());
   return LLMK_OK;
 }

@@ -23,6 +23,7 @@ LLMK_STATUS_HISTORY_OVERFLOW = 0x2
 LLMK_STATUS_SLOT_TIMEOUT = 0x4
 LLMK_F32 = 0
 LLMK_BF16 = 1
+LLMK_F16 = 2
 
 # Every symbol include/llmk_sampler.h declares (checked by the CPU tests).
 EXPORTED_SYMBOLS = (

@@ -63,7 +63,7 @@ class BatchResult:
 class DeviceBatch:
     """Device-resident inputs of one sampling step (all torch CUDA tensors)."""
 
-    logits: torch.Tensor                      # [B, >=V] float32 or bfloat16
+    logits: torch.Tensor                      # [B, >=V] float32, bfloat16 or float16
     uniforms: torch.Tensor                    # [B] float32
     vocab: Optional[int] = None
     temperature: Optional[torch.Tensor] = None
@@ -115,8 +115,11 @@ class HipSampler:
             dt = _lib.LLMK_F32
         elif lg.dtype == torch.bfloat16:
             dt = _lib.LLMK_BF16
+        elif lg.dtype == torch.float16:
+            dt = _lib.LLMK_F16
         else:
-            raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT, "logits must be float32 or bfloat16")
+            raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT,
+                               "logits must be float32, bfloat16 or float16")
         B = lg.shape[0]
         V = db.vocab if db.vocab is not None else lg.shape[1]
         a = _lib.SampleBatchArgs()

@@ -24,9 +24,9 @@ class Workload:
     name: str
     B: int
     V: int
-    dtype: str                 # "f32" or "bf16"
+    dtype: str                 # "f32", "bf16" or "f16"
     logits: np.ndarray         # float32 [B,V] (for bf16: the exact upcast of bf16_bits)
-    bf16_bits: Optional[np.ndarray]  # uint16 [B,V] when dtype == "bf16"
+    bf16_bits: Optional[np.ndarray]  # uint16 [B,V]: the 16-bit logits when dtype is "bf16" or "f16"
     temperature: np.ndarray
     top_k: np.ndarray          # int32
     top_p: np.ndarray
@@ -51,6 +51,8 @@ class Workload:
             np.ascontiguousarray(a) if dt is None else np.ascontiguousarray(a).view(dt)).to(dev)
         if self.dtype == "bf16":
             lg = T(self.bf16_bits, np.int16).view(torch.bfloat16)
+        elif self.dtype == "f16":
+            lg = T(self.bf16_bits, np.int16).view(torch.float16)
         else:
             lg = T(self.logits)
         ht = self.hist_tokens if self.hist_tokens.size else np.zeros(1, np.uint32)

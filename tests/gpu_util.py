@@ -48,6 +48,10 @@ def workload(logits, T=1.0, K=0, P=1.0, MP=0.0, R=1.0, PR=0.0, FR=0.0, hists=Non
     if dtype == "bf16":
         bf = synth.to_bf16_bits(lg)
         lg = synth.bf16_bits_to_f32(bf)
+    elif dtype == "f16":  # round to half, keep its exact upcast
+        h = lg.astype(np.float16)
+        bf = h.view(np.uint16)
+        lg = h.astype(np.float32)
     col = lambda x, dt=np.float32: np.broadcast_to(np.asarray(x, dt), (B,)).copy()
     hists = hists if hists is not None else [[] for _ in range(B)]
     offs, toks = synth._csr([np.asarray(h, np.uint32) for h in hists])
@@ -61,10 +65,11 @@ def run_gpu_strided(sampler, w, out_cap=64, extra=4):
     import torch
     db = w.to_device()
     stride = ((w.V + extra + 7) // 8) * 8
-    if w.dtype == "bf16":
-        pad = np.full((w.B, stride), 0x7F80, np.uint16)
+    if w.dtype in ("bf16", "f16"):
+        pad = np.full((w.B, stride), 0x7F80 if w.dtype == "bf16" else 0x7C00, np.uint16)
         pad[:, :w.V] = w.bf16_bits
-        lg = torch.from_numpy(pad.view(np.int16)).to("cuda:0").view(torch.bfloat16)
+        lg = torch.from_numpy(pad.view(np.int16)).to("cuda:0").view(
+            torch.bfloat16 if w.dtype == "bf16" else torch.float16)
     else:
         pad = np.full((w.B, stride), np.inf, np.float32)
         pad[:, :w.V] = w.logits

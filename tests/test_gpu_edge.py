@@ -2,7 +2,7 @@
 mirror oracle (tokens, kept counts, kept ids and probabilities): the
 reference's known-answer vectors, tiny and ragged vocabularies, padded rows,
 fully masked rows, top-k at and beyond its limits, extreme top-p and
-uniforms, bf16 ties, history ids outside the vocabulary, invalid parameters
+uniforms, bf16 and f16 ties, f16 logits, history ids outside the vocabulary, invalid parameters
 and the device status word.  Marked gpu."""
 import json
 import os
@@ -65,7 +65,7 @@ def test_ragged_vocabularies(sampler, V):
     check(sampler, w, strided=True, label=f"ragged V={V}")
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 def test_fully_masked_rows(sampler, dtype):
     V = 5000
     lg = np.random.default_rng(1).normal(0, 2, (5, V)).astype(np.float32)
@@ -97,7 +97,7 @@ def test_extreme_top_p_and_uniforms(sampler):
     check(sampler, w, label="extreme top-p / u")
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 def test_ties(sampler, dtype):
     """Quantised logits make many equal probabilities: (p desc, idx asc)."""
     V = 40000
@@ -222,6 +222,17 @@ def test_batch_shapes(sampler, B):
     """Batch sizes that change the segment count and the XCD mapping."""
     w = synth.make("C3", B=B, V=50000)
     check(sampler, w, label=f"C3 B={B} V=50000")
+
+
+def test_f16_logits(sampler):
+    """f16 logits (half-precision lm_head output) read and upcast exactly:
+    C2's rows and parameters with the logits rounded to half."""
+    c2 = synth.make("C2", B=32)
+    hists = [c2.hist_tokens[c2.hist_offsets[b]:c2.hist_offsets[b + 1]] for b in range(c2.B)]
+    w = workload(c2.logits, T=c2.temperature, K=c2.top_k, P=c2.top_p, MP=c2.min_p,
+                 R=c2.repetition, PR=c2.presence, FR=c2.frequency, hists=hists,
+                 u=c2.uniforms, dtype="f16", name="C2 f16")
+    check(sampler, w, label="C2 rows, f16 logits")
 
 
 @pytest.mark.parametrize("name", ["C1", "C2", "C4", "C5"])

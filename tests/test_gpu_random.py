@@ -1,6 +1,6 @@
 """A seeded sweep of random workloads through the C ABI, each compared bit
 for bit with the CPU mirror oracle (tokens, kept counts, kept ids and
-probabilities): random batch and vocabulary sizes, f32 and bf16 logits of
+probabilities): random batch and vocabulary sizes, f32, bf16 and f16 logits of
 several shapes (flat, peaked, quantised, with spikes), per-row parameters
 mixing greedy rows, top-k from 1 to beyond V, top-p, min-p, all three
 penalties, histories with duplicates and out-of-vocabulary ids, allow-masks
@@ -67,7 +67,7 @@ def make_case(seed):
     u = rng.random(B).astype(np.float32)
     u[rng.random(B) < 0.1] = 0.0
     u[rng.random(B) < 0.1] = np.float32(1.0 - 2.0 ** -24)
-    dtype = "bf16" if seed % 2 else "f32"
+    dtype = ("f32", "bf16", "f16")[(seed // 3) % 3]
     w = workload(lg, T=T, K=K, P=P, MP=MP, R=R, PR=PR, FR=FR, hists=hists, mask=mask, u=u,
                  dtype=dtype, name=f"random-{seed}")
     cap = int(rng.choice([0, 16, 300]))
