@@ -114,6 +114,31 @@ int llmk_sampler_create(llmk_sampler** out, int device, uint32_t max_batch,
 int llmk_sample_batch(llmk_sampler* s, const llmk_sample_batch_args* args,
                       void* hip_stream);
 
+/* Mask-form top-k, batched and in place: replaces apply_top_k
+ * (llm-core/src/sampler.rs:160-173) called on each row.  In row b every
+ * logit below the top_k[b]-th largest value becomes -inf; values equal to
+ * that threshold stay, so more than top_k[b] can remain.  Rows with
+ * top_k[b] <= 0 or >= vocab are left as they are (sampler.rs:161-163).
+ * logits: device f32 [batch][row_stride] (the reference's &mut [f32]; any
+ * stride, no alignment beyond the f32 one); top_k: device [batch].  Enqueued on hip_stream;
+ * allocates nothing; uses no workspace of the handle. */
+int llmk_apply_top_k(llmk_sampler* s, float* logits, uint32_t batch, uint32_t vocab,
+                     uint64_t row_stride, const int32_t* top_k, void* hip_stream);
+
+/* Mask-form top-p, batched and in place: replaces apply_top_p
+ * (llm-core/src/sampler.rs:176-216) called on each row.  Softmax of the row,
+ * order by (probability desc, index asc), keep the shortest prefix whose
+ * sequential f32 running sum reaches top_p[b], set every other logit to
+ * -inf.  Rows with top_p[b] >= 1 or NaN, or whose probabilities sum to 0
+ * (every logit -inf), are left as they are.  The probabilities are those of
+ * llmk_sample_batch at temperature 1 (the same exp and normaliser), and the
+ * kept set is what llmk_sample_batch keeps with that top_p alone.  Rows as
+ * for llmk_sample_batch (f32, 16-byte aligned); batch and vocab within the handle's
+ * maxima; uses the handle's workspace (stream order, like
+ * llmk_sample_batch); allocates nothing. */
+int llmk_apply_top_p(llmk_sampler* s, float* logits, uint32_t batch, uint32_t vocab,
+                     uint64_t row_stride, const float* top_p, void* hip_stream);
+
 /* Reads and clears the device status word (OR of LLMK_STATUS_* bits raised by
  * calls since the last read).  Synchronises `hip_stream`. */
 int llmk_sampler_status(llmk_sampler* s, void* hip_stream, uint32_t* status);

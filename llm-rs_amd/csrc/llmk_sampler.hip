@@ -104,6 +104,11 @@ struct Args {
   // f2v) and candidates (LCAP u2v), past both the stream and finalize layouts
   uint32_t lds_part, lds_cand;
   uint32_t xcd_map;  // 1: the segments of a row share an XCD
+  // apply_top_p: per row, the last kept entry's index, the kept count and
+  // the m and S its probabilities used; top_p clamped to [0, 1], NaN read as 1
+  // (the mask form's no-op, not an invalid row)
+  u4v* cut;
+  uint32_t tp_clamp;
 };
 
 struct Ws {
@@ -116,6 +121,9 @@ struct Ws {
   float* slow_p;         // [slow_slots][max_vocab]
   uint32_t* slow_idx;    // [slow_slots][max_vocab]
   uint32_t* status;      // [1]
+  u4v* cut;              // [max_batch]: apply_top_p's cut per row
+  uint32_t* mtok;        // [max_batch]: apply_top_p's (unused) draws
+  float* zu;             // [max_batch]: zeros, its uniforms
   uint32_t max_vocab;
   uint32_t slow_slots;   // min(max_batch, SLOW_SLOTS): rows b, b + slow_slots, ... share one
 };
@@ -133,6 +141,7 @@ __device__ __forceinline__ RowP row_params(const Args& a, uint32_t b) {
   RowP r;
   r.T = a.T ? a.T[b] : 1.0f;
   r.top_p = a.top_p ? a.top_p[b] : 1.0f;
+  if (a.tp_clamp) r.top_p = r.top_p < 0.0f ? 0.0f : (r.top_p < 1.0f ? r.top_p : 1.0f);
   r.min_p = a.min_p ? a.min_p[b] : 0.0f;
   r.rp = a.rp ? a.rp[b] : 1.0f;
   r.pp = a.pp ? a.pp[b] : 0.0f;
@@ -1072,10 +1081,14 @@ __device__ __forceinline__ bool run_semantics(const RowP& P, float u, uint32_t E
 }
 
 __device__ __forceinline__ void write_outputs(const Args& a, uint32_t b, uint32_t tok,
-                                              uint32_t len, const List& list) {
+                                              uint32_t len, const List& list, float m,
+                                              float S) {
   if (threadIdx.x == 0) {
     G(a.out_tok)[b] = tok;
     if (a.out_cnt) G(a.out_cnt)[b] = len;
+    if (a.cut)
+      G(a.cut)[b] = u4v{(len > 0 && len < a.V) ? list.id(len - 1) : 0u, len,
+                        __float_as_uint(m), __float_as_uint(S)};
   }
   if (a.out_cap) {
     const uint32_t n = len < a.out_cap ? len : a.out_cap;
@@ -1135,6 +1148,15 @@ __device__ __forceinline__ uint32_t seq_find_regs(float p0, float p1, uint32_t m
   const uint32_t jc = j < m ? j : m - 1;
   cum_out = jc < 64 ? rl(c0, jc) : rl(c1, jc - 64);
   return j;
+}
+
+// Index of kept entry len - 1 of a register list of n (wave-uniform), 0 when
+// it is not held (len 0, or every entry kept).
+__device__ __forceinline__ uint32_t cut_id(uint32_t len, uint32_t n, uint32_t i0, uint32_t i1) {
+  const uint32_t lc = (len > 0 && len <= n) ? len - 1 : 0u;
+  const uint32_t v = lc < 64 ? (uint32_t)__builtin_amdgcn_readlane((int)i0, (int)lc)
+                             : (uint32_t)__builtin_amdgcn_readlane((int)i1, (int)(lc - 64));
+  return (len > 0 && len <= n) ? v : 0u;
 }
 
 __device__ __forceinline__ bool semantics_regs(const RowP& P, float u, uint32_t n,
@@ -1595,7 +1617,7 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
   }
   wait_stores();
   __syncthreads();
-  write_outputs(a, b, tok, len, Lst);
+  write_outputs(a, b, tok, len, Lst, m, S);
   wait_stores();
   __syncthreads();
   if (tid == 0) {
@@ -2051,9 +2073,11 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
                                  (LDS float*)f.keys, tok, len);
       if (good && a.out_cap && len > n && a.out_cap > n) good = false;
       if (good) {
+        const uint32_t ic = a.cut ? cut_id(len, n, i0, i1) : 0u;
         if (lane == 0) {
           G(a.out_tok)[b] = tok;
           if (a.out_cnt) G(a.out_cnt)[b] = len;
+          if (a.cut) G(a.cut)[b] = u4v{ic, len, __float_as_uint(m), __float_as_uint(S)};
         }
         const uint32_t no = len < a.out_cap ? len : a.out_cap;
         const uint64_t ob = (uint64_t)b * a.out_cap;
@@ -2074,7 +2098,7 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
     bool good = run_semantics(P, u, n, a.V, plim_e, Ls, f.fm + F_SCR, (LDS float*)f.keys, tok,
                               len);
     if (good && a.out_cap && len > n && a.out_cap > n) good = false;
-    if (good) write_outputs(a, b, tok, len, Ls);
+    if (good) write_outputs(a, b, tok, len, Ls, m, S);
     res = good ? 0u : 2u;
   }
   if (SY::N > WAVE) {
@@ -2195,9 +2219,11 @@ __device__ __forceinline__ uint32_t candidate_fast(const Args& a, uint32_t b, co
   const uint32_t res = f.fm[F_DONE];
   if (tid < WAVE && res == 0) {
     const int lane = (int)tid;
+    const uint32_t ic = a.cut ? cut_id(len, n, i0, i1) : 0u;
     if (lane == 0) {
       G(a.out_tok)[b] = tok;
       if (a.out_cnt) G(a.out_cnt)[b] = len;
+      if (a.cut) G(a.cut)[b] = u4v{ic, len, __float_as_uint(m), __float_as_uint(S)};
     }
     const uint32_t no = len < a.out_cap ? len : a.out_cap;
     const uint64_t ob = (uint64_t)b * a.out_cap;
@@ -2904,6 +2930,242 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   finalize_row<DT>(a, w, b, P, have, seg_own, u_row, sm);
 }
 
+
+// ===========================================================================
+// Mask-form top-k and top-p (sampler.rs:160-216), in place on f32 rows
+// ===========================================================================
+// Order key with -0 folded onto +0: key order is then the order of `<` on
+// every non-NaN value (the reference compares with `<`, sampler.rs:168).
+__device__ __forceinline__ uint32_t ckey(float v) { return fkey(v == 0.0f ? 0.0f : v); }
+
+constexpr uint32_t MK_BINS = 2048;  // 11-bit digits: key bits 31..21, 20..10, then 10 bits
+constexpr uint32_t MK_CAP = NW * MK_BINS / 2;  // entries of the chosen bin gathered in LDS
+constexpr uint32_t MK_LDS_WORDS = NW * MK_BINS + 512;
+
+// Every element of row[e0..e1) once: float4 loads from the first 16-byte
+// boundary on (lane-strided), single elements before it and after the last
+// whole float4.  f(e, x) gets the first element's index and the values; the
+// high bit of e marks a single element (in x.x).
+template <class F>
+__device__ __forceinline__ void each4(const float* row, uint32_t e0, uint32_t e1, F&& f) {
+  const uint32_t mis = (uint32_t)(((uintptr_t)(row + e0) >> 2) & 3u);
+  uint32_t a0 = e0 + (mis ? 4u - mis : 0u);
+  if (a0 > e1) a0 = e1;
+  const uint32_t v4 = a0 + ((e1 - a0) & ~3u);
+  for (uint32_t e = a0 + 4 * threadIdx.x; e < v4; e += 4 * NT) {
+    const f4v x = *(const GLB f4v*)G(row + e);
+    f(e, x);
+  }
+  const uint32_t nh = a0 - e0, ns = nh + (e1 - v4);
+  for (uint32_t i = threadIdx.x; i < ns; i += NT) {
+    const uint32_t e = i < nh ? e0 + i : v4 + (i - nh);
+    f4v x;
+    x.x = G(row)[e];
+    x.y = x.z = x.w = NEG_INF;
+    f(e | 0x80000000u, x);
+  }
+}
+
+// apply_top_k (sampler.rs:160-173) for one row per workgroup: the key of
+// the top_k-th largest value by a radix select over the row (11-bit digits
+// counted in per-wave LDS histograms), stopping once the chosen digit holds
+// at most MK_CAP values; those are gathered into LDS and the select ends
+// there, while the same pass masks every value whose key prefix lies below.
+__global__ __launch_bounds__(NT) void topk_mask_kernel(float* logits, uint32_t V,
+                                                       uint64_t stride,
+                                                       const int32_t* top_k) {
+  extern __shared__ __align__(16) uint32_t smem[];
+  const uint32_t b = blockIdx.x, tid = threadIdx.x;
+  const uint32_t wv = tid >> 6;
+  const int32_t k = G(top_k)[b];
+  if (k <= 0 || (uint32_t)k >= V) return;  // sampler.rs:161-163
+  float* row = logits + (uint64_t)b * stride;
+  LDS uint32_t* hist = (LDS uint32_t*)smem;  // NW * MK_BINS
+  LDS uint32_t* sh = hist + NW * MK_BINS;     // 512: select histogram, scalars
+  uint32_t pbits = 0, pref = 0, need = (uint32_t)k, cnt = V;
+  while (pbits < 32 && cnt > MK_CAP) {
+    const uint32_t dbits = pbits == 22 ? 10u : 11u;
+    const uint32_t shift = 32 - pbits - dbits, dmask = (1u << dbits) - 1u;
+    for (uint32_t i = tid; i < NW * MK_BINS; i += NT) hist[i] = 0;
+    __syncthreads();
+    LDS uint32_t* wh = hist + wv * MK_BINS;
+    each4(row, 0, V, [&](uint32_t e, f4v x) {
+      const float vv[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (q > 0 && (e & 0x80000000u)) break;
+        const uint32_t key = ckey(vv[q]);
+        if (pbits == 0 || (key >> (32 - pbits)) == pref)
+          __atomic_fetch_add(&wh[(key >> shift) & dmask], 1u, __ATOMIC_RELAXED);
+      }
+    });
+    __syncthreads();
+    // thread t: digits 2047 - 2t and 2046 - 2t (descending), summed over waves
+    uint32_t c2[2] = {0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t d = MK_BINS - 1 - 2 * tid - j;
+      for (uint32_t w2 = 0; w2 < NW; ++w2) c2[j] += hist[w2 * MK_BINS + d];
+    }
+    uint32_t total;
+    const uint32_t above = block_excl_scan(c2[0] + c2[1], sh + 256, total);
+    if (above < need && above + c2[0] + c2[1] >= need) {
+      const bool first = above + c2[0] >= need;
+      const uint32_t d = MK_BINS - 1 - 2 * tid - (first ? 0 : 1);
+      sh[300] = d & dmask;
+      sh[301] = need - above - (first ? 0 : c2[0]);
+      sh[302] = first ? c2[0] : c2[1];
+    }
+    __syncthreads();
+    pref = (pref << dbits) | sh[300];
+    pbits += dbits;
+    need = sh[301];
+    cnt = sh[302];
+    __syncthreads();
+  }
+  // Final pass: values whose key prefix is below pref are below the
+  // threshold; with pbits == 32 the threshold is known and the rest stay,
+  // otherwise the cnt values of prefix pref are gathered for the last select.
+  LDS float* cval = (LDS float*)hist;
+  LDS uint32_t* cidx = hist + MK_CAP;
+  if (tid == 0) sh[303] = 0;
+  __syncthreads();
+  const uint32_t pshift = 32 - pbits;
+  each4(row, 0, V, [&](uint32_t e, f4v x) {
+    const bool one = (e & 0x80000000u) != 0;
+    const uint32_t e0 = e & 0x7fffffffu;
+    float vv[4] = {x.x, x.y, x.z, x.w};
+    bool dirty = false;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (q > 0 && one) break;
+      const float v = vv[q];
+      if (v != v) continue;  // NaN: `v < threshold` is false
+      const uint32_t kp = pshift == 32 ? 0u : ckey(v) >> pshift;
+      if (kp < pref) {
+        if (v != NEG_INF) {
+          vv[q] = NEG_INF;
+          dirty = true;
+        }
+      } else if (kp == pref && pbits < 32) {
+        const uint32_t at = __atomic_fetch_add(&sh[303], 1u, __ATOMIC_RELAXED);
+        if (at < MK_CAP) {
+          cval[at] = v == 0.0f ? 0.0f : v;
+          cidx[at] = e0 + q;
+        }
+      }
+    }
+    if (dirty) {
+      if (one) G(row)[e0] = vv[0];
+      else *(GLB f4v*)G(row + e0) = f4v{vv[0], vv[1], vv[2], vv[3]};
+    }
+  });
+  if (pbits == 32) return;
+  // the float4 stores above may cover gathered entries masked below
+  wait_stores();
+  __syncthreads();
+  const uint32_t n = sh[303] < MK_CAP ? sh[303] : MK_CAP;  // cnt less the NaNs
+  if (n == 0) return;
+  const float thr =
+      funkey(kth_largest_key<BlockSync>(cval, n, need < n ? need : n, sh, sh + 304));
+  for (uint32_t i = tid; i < n; i += NT)
+    if (cval[i] < thr) G(row)[cidx[i]] = NEG_INF;
+}
+
+// The last key k in [lo, hi) with pred(k), given pred(lo) and !pred(hi),
+// pred true then false over [lo, hi]: a 64-way search by one wave, six
+// rounds for 32-bit keys (bounded to eight).
+template <class P>
+__device__ __forceinline__ uint32_t band_edge(uint32_t lo, uint32_t hi, int lane, P&& pred) {
+  for (int it = 0; it < 8 && hi - lo > 1u; ++it) {
+    const uint32_t step = (hi - lo + 63u) / 64u;
+    const uint64_t kj = (uint64_t)lo + (uint64_t)step * (uint32_t)lane;
+    const bool in = lane > 0 && kj < hi;
+    const bool t = in && pred((uint32_t)kj);
+    const uint64_t mi = __ballot(in), mf = __ballot(in && !t);
+    if (mf) {
+      const uint32_t f = (uint32_t)__ffsll((long long)mf) - 1u;  // >= 1
+      hi = lo + step * f;
+      lo = lo + step * (f - 1u);
+    } else {
+      lo = lo + step * (uint32_t)(63 - __clzll((long long)mi));
+    }
+  }
+  return lo;
+}
+
+// apply_top_p (sampler.rs:176-216) after the sampling kernel has found the
+// row's cut with the same probabilities (temperature 1, nothing else): the
+// kept prefix, in (p desc, index asc) order, ends at token c of probability
+// p_c.  p is non-decreasing in the value, so the values of probability p_c
+// form one key interval [klo, khi], found by two 64-way searches in wave 0;
+// a value is kept if its key is above khi, or within the interval at an
+// index <= c.  Grid: rows x segments of seg elements.
+__global__ __launch_bounds__(NT) void topp_mask_kernel(float* logits, uint32_t V,
+                                                       uint64_t stride, const float* top_p,
+                                                       const u4v* cut, const uint32_t* tok,
+                                                       uint32_t nseg, uint32_t seg) {
+  __shared__ uint32_t band[4];
+  const uint32_t b = blockIdx.x / nseg, g = blockIdx.x % nseg;
+  const uint32_t tid = threadIdx.x;
+  const int lane = (int)(tid & 63);
+  float* row = logits + (uint64_t)b * stride;
+  if (tid < WAVE) {
+    const float tp = G(top_p)[b];
+    const u4v r = G(cut)[b];
+    const uint32_t t = G(tok)[b];
+    const float m = __uint_as_float(r.z), S = __uint_as_float(r.w);
+    // no-op rows: top_p >= 1 or NaN (sampler.rs:177-179), softmax sum 0
+    // (sampler.rs:190-192), everything kept (the cut never reached), or the
+    // sampling kernel could not serve the row
+    bool run = tp < 1.0f && t != LLMK_INVALID_TOKEN && r.y < V && S > 0.0f && r.x < V;
+    uint32_t klo = 0, khi = 0;
+    if (run) {
+      const float pc = prob_of(G(row)[r.x], 1.0f, m, S);
+      const uint32_t kc = ckey(G(row)[r.x]);
+      auto pk = [&](uint32_t key) { return prob_of(funkey(key), 1.0f, m, S); };
+      // khi: the last key with p <= pc, in [kc, key(m)]
+      const uint32_t km = ckey(m);
+      khi = (km <= kc || !(pk(km) > pc))
+                ? 0xffffffffu
+                : band_edge(kc, km, lane, [&](uint32_t key) { return pk(key) <= pc; });
+      // klo: the first key with p >= pc, in (key(-inf), kc]: p(-inf) = 0 < pc
+      klo = 1u + band_edge(0x007fffffu, kc, lane, [&](uint32_t key) { return pk(key) < pc; });
+    }
+    if (lane == 0) {
+      band[0] = run ? 1u : 0u;
+      band[1] = klo;
+      band[2] = khi;
+      band[3] = r.x;
+    }
+  }
+  __syncthreads();
+  if (!band[0]) return;
+  const uint32_t klo = band[1], khi = band[2], c = band[3];
+  const uint32_t e0 = g * seg, e1 = e0 + seg < V ? e0 + seg : V;
+  each4(row, e0, e1, [&](uint32_t e, f4v x) {
+    const bool one = (e & 0x80000000u) != 0;
+    const uint32_t ea = e & 0x7fffffffu;
+    float vv[4] = {x.x, x.y, x.z, x.w};
+    bool dirty = false;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (q > 0 && one) break;
+      const float v = vv[q];
+      const uint32_t key = ckey(v);
+      const bool keep = key > khi || (key >= klo && ea + q <= c);
+      if (!keep && v != NEG_INF) {
+        vv[q] = NEG_INF;
+        dirty = true;
+      }
+    }
+    if (dirty) {
+      if (one) G(row)[ea] = vv[0];
+      else *(GLB f4v*)G(row + ea) = f4v{vv[0], vv[1], vv[2], vv[3]};
+    }
+  });
+}
+
 }  // namespace llmk
 
 // ===========================================================================
@@ -2956,6 +3218,8 @@ extern "C" int llmk_sampler_create(llmk_sampler** out, int device,
                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
   HIPCHK(hipFuncSetAttribute((const void*)stream_kernel<LLMK_F16>,
                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+  HIPCHK(hipFuncSetAttribute((const void*)topk_mask_kernel,
+                             hipFuncAttributeMaxDynamicSharedMemorySize, 4 * MK_LDS_WORDS));
   const uint32_t pool = max_batch > MAX_WGS ? max_batch : MAX_WGS;
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -2973,6 +3237,9 @@ extern "C" int llmk_sampler_create(llmk_sampler** out, int device,
   const size_t o_sp = take(4ull * slots * max_vocab);
   const size_t o_si = take(4ull * slots * max_vocab);
   const size_t o_status = take(256);
+  const size_t o_cut = take(16ull * max_batch);
+  const size_t o_mtok = take(4ull * max_batch);
+  const size_t o_zu = take(4ull * max_batch);
   void* mem = nullptr;
   HIPCHK(hipMalloc(&mem, off));
   hipError_t e = hipMemset(mem, 0, off);
@@ -2997,6 +3264,9 @@ extern "C" int llmk_sampler_create(llmk_sampler** out, int device,
   s->ws.slow_p = (float*)(base + o_sp);
   s->ws.slow_idx = (uint32_t*)(base + o_si);
   s->ws.status = (uint32_t*)(base + o_status);
+  s->ws.cut = (u4v*)(base + o_cut);
+  s->ws.mtok = (uint32_t*)(base + o_mtok);
+  s->ws.zu = (float*)(base + o_zu);
   s->ws.max_vocab = max_vocab;
   s->ws.slow_slots = slots;
   *out = s;
@@ -3027,9 +3297,8 @@ extern "C" int llmk_sampler_status(llmk_sampler* s, void* stream,
   return LLMK_OK;
 }
 
-extern "C" int llmk_sample_batch(llmk_sampler* s,
-                                 const llmk_sample_batch_args* in,
-                                 void* stream) {
+static int sample_batch_impl(llmk_sampler* s, const llmk_sample_batch_args* in,
+                             void* stream, u4v* cut, uint32_t tp_clamp) {
   if (!s) return fail(LLMK_ERR_INVALID_ARGUMENT, "sampler is NULL");
   if (!in) return fail(LLMK_ERR_INVALID_ARGUMENT, "args is NULL");
   if (in->vocab == 0) return fail(LLMK_ERR_EMPTY_LOGITS, "Empty logits passed to sampler");
@@ -3076,6 +3345,8 @@ extern "C" int llmk_sample_batch(llmk_sampler* s,
   a.out_cnt = in->out_count;
   a.out_probs = in->out_probs;
   a.out_cap = in->out_cap;
+  a.cut = cut;
+  a.tp_clamp = tp_clamp;
   a.ntiles = (a.V + TILE - 1) / TILE;
   a.nchunks = (a.ntiles + CHUNK_TILES - 1) / CHUNK_TILES;
   // Segments per row: enough workgroups to cover the 256 CUs, whole 16-tile
@@ -3111,6 +3382,67 @@ extern "C" int llmk_sample_batch(llmk_sampler* s,
     hipLaunchKernelGGL(stream_kernel<LLMK_BF16>, grid, block, lds, st, a, s->ws);
   else
     hipLaunchKernelGGL(stream_kernel<LLMK_F16>, grid, block, lds, st, a, s->ws);
+  HIPCHK(hipGetLastError());
+  return LLMK_OK;
+}
+
+extern "C" int llmk_sample_batch(llmk_sampler* s, const llmk_sample_batch_args* in,
+                                 void* stream) {
+  return sample_batch_impl(s, in, stream, nullptr, 0u);
+}
+
+// Checks shared by the mask forms: in-place f32 rows.
+static int check_mask_rows(llmk_sampler* s, const float* logits, uint32_t vocab,
+                           uint64_t row_stride, const void* param) {
+  if (!s) return fail(LLMK_ERR_INVALID_ARGUMENT, "sampler is NULL");
+  if (!logits || !param) return fail(LLMK_ERR_INVALID_ARGUMENT, "logits and the parameter array are required");
+  if (row_stride < vocab) return fail(LLMK_ERR_INVALID_ARGUMENT, "row_stride < vocab");
+  if (((uintptr_t)logits % 4) != 0) return fail(LLMK_ERR_ALIGNMENT, "logits must be 4-byte aligned");
+  if (vocab > MAX_TILES * TILE) return fail(LLMK_ERR_CAPACITY, "vocab above 2^20");
+  return LLMK_OK;
+}
+
+extern "C" int llmk_apply_top_k(llmk_sampler* s, float* logits, uint32_t batch, uint32_t vocab,
+                                uint64_t row_stride, const int32_t* top_k, void* stream) {
+  const int rc = check_mask_rows(s, logits, vocab, row_stride, top_k);
+  if (rc != LLMK_OK) return rc;
+  if (batch == 0 || vocab == 0) return LLMK_OK;  // nothing to mask (sampler.rs:161)
+  HIPCHK(hipSetDevice(s->device));
+  hipLaunchKernelGGL(topk_mask_kernel, dim3(batch), dim3(NT), 4 * MK_LDS_WORDS,
+                     (hipStream_t)stream, logits, vocab, row_stride, top_k);
+  HIPCHK(hipGetLastError());
+  return LLMK_OK;
+}
+
+extern "C" int llmk_apply_top_p(llmk_sampler* s, float* logits, uint32_t batch, uint32_t vocab,
+                                uint64_t row_stride, const float* top_p, void* stream) {
+  const int rc = check_mask_rows(s, logits, vocab, row_stride, top_p);
+  if (rc != LLMK_OK) return rc;
+  if (batch == 0 || vocab == 0) return LLMK_OK;
+  if (batch > s->max_batch || vocab > s->max_vocab)
+    return fail(LLMK_ERR_CAPACITY, "batch or vocab above the sampler's maxima");
+  // the cut: the sampling kernel at temperature 1 with top_p alone
+  llmk_sample_batch_args in;
+  memset(&in, 0, sizeof(in));
+  in.logits = logits;
+  in.dtype = LLMK_F32;
+  in.batch = batch;
+  in.vocab = vocab;
+  in.row_stride = row_stride;
+  in.top_p = top_p;
+  in.uniforms = s->ws.zu;
+  in.out_tokens = s->ws.mtok;
+  const int rc2 = sample_batch_impl(s, &in, stream, s->ws.cut, 1u);
+  if (rc2 != LLMK_OK) return rc2;
+  // then the mask, in segments of whole 4096-element blocks, ~2048 workgroups
+  const uint32_t blocks = (vocab + 4 * NT - 1) / (4 * NT);
+  uint32_t want = (2048 + batch - 1) / batch;
+  if (want > blocks) want = blocks;
+  const uint32_t seg = (blocks + want - 1) / want * (4 * NT);
+  const uint32_t nseg = (vocab + seg - 1) / seg;
+  hipLaunchKernelGGL(topp_mask_kernel, dim3(batch * nseg), dim3(NT), 0, (hipStream_t)stream,
+                     logits, vocab, row_stride, top_p, (const u4v*)s->ws.cut, s->ws.mtok,
+                     nseg, seg);
   HIPCHK(hipGetLastError());
   return LLMK_OK;
 }

@@ -6,6 +6,8 @@ from .sampler import (  # noqa: F401
     HipSampler,
     SampleParams,
     SamplerError,
+    apply_top_k,
+    apply_top_p,
     device_batch_from_params,
     sample,
     sample_logits,

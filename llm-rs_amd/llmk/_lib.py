@@ -32,6 +32,8 @@ EXPORTED_SYMBOLS = (
     "llmk_sampler_status",
     "llmk_sampler_destroy",
     "llmk_last_error",
+    "llmk_apply_top_k",
+    "llmk_apply_top_p",
 )
 
 
@@ -87,6 +89,10 @@ def load():
     lib.llmk_sampler_status.restype = ctypes.c_int
     lib.llmk_sampler_destroy.argtypes = [vp]
     lib.llmk_sampler_destroy.restype = None
+    for fn, par in (("llmk_apply_top_k", vp), ("llmk_apply_top_p", vp)):
+        getattr(lib, fn).argtypes = [vp, vp, ctypes.c_uint32, ctypes.c_uint32,
+                                     ctypes.c_uint64, par, vp]
+        getattr(lib, fn).restype = ctypes.c_int
     lib.llmk_last_error.argtypes = []
     lib.llmk_last_error.restype = ctypes.c_char_p
     _lib = lib

@@ -174,6 +174,29 @@ class HipSampler:
             raise SamplerError(rc, _lib.last_error())
         return v.value
 
+    # ---- mask forms (sampler.rs:160-216), batched, in place --------------
+    def _mask(self, fn: str, logits: torch.Tensor, param: torch.Tensor,
+              stream: Optional[torch.cuda.Stream]) -> None:
+        if logits.dtype != torch.float32 or logits.dim() != 2 or logits.stride(1) != 1:
+            raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT,
+                               "logits must be a row-major float32 [batch, vocab] tensor")
+        st = stream if stream is not None else torch.cuda.current_stream()
+        rc = getattr(self._lib, fn)(self._h, logits.data_ptr(), logits.shape[0], logits.shape[1],
+                                    logits.stride(0), param.data_ptr(),
+                                    ctypes.c_void_p(st.cuda_stream))
+        if rc != 0:
+            raise SamplerError(rc, _lib.last_error())
+
+    def apply_top_k(self, logits: torch.Tensor, top_k: torch.Tensor,
+                    stream: Optional[torch.cuda.Stream] = None) -> None:
+        """sampler.rs:160-173 on every row: logits [B, V] float32, top_k [B] int32."""
+        self._mask("llmk_apply_top_k", logits, top_k.to(torch.int32).contiguous(), stream)
+
+    def apply_top_p(self, logits: torch.Tensor, top_p: torch.Tensor,
+                    stream: Optional[torch.cuda.Stream] = None) -> None:
+        """sampler.rs:176-216 on every row: logits [B, V] float32, top_p [B] float32."""
+        self._mask("llmk_apply_top_p", logits, top_p.to(torch.float32).contiguous(), stream)
+
     # ---- the per-row reference call (LlmBackend::sample) ------------------
     def sample(self, logits: torch.Tensor, params: SampleParams,
                token_history: Sequence[int], u: float) -> int:
@@ -222,3 +245,16 @@ def sample(sampler: HipSampler, logits: torch.Tensor, temperature: float, u: flo
         return sampler.sample(logits, SampleParams(temperature=temperature), [], u)
     except SamplerError:
         return 0
+
+
+def apply_top_k(sampler: HipSampler, logits: torch.Tensor, top_k: int) -> None:
+    """Free-function form of sampler.rs:160 apply_top_k for one row, in place."""
+    lg = logits.view(1, -1)
+    sampler.apply_top_k(lg, torch.tensor([min(int(top_k), 2**31 - 1)], dtype=torch.int32,
+                                         device=logits.device))
+
+
+def apply_top_p(sampler: HipSampler, logits: torch.Tensor, top_p: float) -> None:
+    """Free-function form of sampler.rs:176 apply_top_p for one row, in place."""
+    lg = logits.view(1, -1)
+    sampler.apply_top_p(lg, torch.tensor([top_p], dtype=torch.float32, device=logits.device))

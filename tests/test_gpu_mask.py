@@ -1,0 +1,217 @@
+"""GPU mask-form top-k and top-p (llmk_apply_top_k / llmk_apply_top_p, the
+batched in-place forms of sampler.rs:160-216) through the C ABI, compared bit
+for bit with the CPU oracle's apply_top_k and mirror-mode apply_top_p: the
+reference's known-answer vectors, the benchmark shapes, ties at the threshold,
+rows whose chosen radix digit holds more values than LDS gathers (so every
+digit level runs), -inf entries, signed zeros, padded rows, no-op parameters
+and tiny vocabularies.  NaN logits are left out (the reference's order is
+undefined there).  Marked gpu."""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import llmk
+from oracle import llmk_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+@pytest.fixture(scope="module")
+def sampler():
+    s = llmk.HipSampler(max_batch=64, max_vocab=256000)
+    yield s
+    s.close()
+
+
+def run_mask(sampler, op, rows, params, pad=0):
+    """rows [B, V] f32 (numpy); params [B]; returns the masked rows from the GPU."""
+    B, V = rows.shape
+    print(f"[case] {op} B={B} V={V} pad={pad} params={list(params)[:6]}", flush=True)
+    buf = np.full((B, V + pad), 7.0, np.float32)
+    buf[:, :V] = rows
+    t = torch.from_numpy(buf).cuda()
+    lg = t[:, :V] if pad else t
+    if op == "k":
+        sampler.apply_top_k(lg, torch.tensor(np.asarray(params, np.int64).clip(-2**31, 2**31 - 1)
+                                              .astype(np.int32)).cuda())
+    else:
+        sampler.apply_top_p(lg, torch.tensor(np.asarray(params, np.float32)).cuda())
+    out = t.cpu().numpy()
+    if pad:
+        assert np.all(out[:, V:] == 7.0), "padding was written"
+    return out[:, :V]
+
+
+def oracle_mask(op, rows, params):
+    out = np.empty_like(rows)
+    for i, (r, p) in enumerate(zip(rows, params)):
+        out[i] = O.apply_top_k(r, int(p)) if op == "k" else O.apply_top_p(O.MIRROR, r, float(p))
+    return out
+
+
+def check(sampler, op, rows, params, pad=0):
+    rows = np.ascontiguousarray(rows, np.float32)
+    gpu = run_mask(sampler, op, rows, params, pad)
+    orc = oracle_mask(op, rows, params)
+    bad = np.nonzero(np.any(gpu.view(np.uint32) != orc.view(np.uint32), axis=1))[0]
+    assert bad.size == 0, (
+        f"{op}: rows {bad[:8].tolist()} differ; row {bad[0]}: param {params[bad[0]]}, "
+        f"kept gpu {int(np.sum(gpu[bad[0]] > -np.inf))} oracle {int(np.sum(orc[bad[0]] > -np.inf))}")
+    assert sampler.status() == 0
+    return gpu
+
+
+def test_reference_kats(sampler):
+    with open(os.path.join(HERE, "golden", "reference_kats.json")) as f:
+        kats = [k for k in json.load(f)["kats"] if k["op"] in ("top_k", "top_p")]
+    assert len(kats) == 4
+    for k in kats:
+        lg = np.asarray(k["logits"], np.float32)[None, :]
+        op = "k" if k["op"] == "top_k" else "p"
+        out = check(sampler, op, lg, [k["k"] if op == "k" else k["top_p"]],
+                    pad=(-lg.shape[1]) % 4)[0]
+        if "expect" in k:
+            assert np.array_equal(out, np.asarray(k["expect"], np.float32))
+        fin = np.nonzero(out > -np.inf)[0].tolist()
+        if op == "k" and "expect_finite" in k:
+            assert fin == k["expect_finite"]
+            assert all(out[i] == -np.inf for i in k["expect_masked"])
+        if op == "p":
+            assert set(k["expect_finite"]) <= set(fin)
+            assert int(np.sum(out == -np.inf)) >= k["min_masked"]
+
+
+def c3_rows(B, V, seed):
+    rng = np.random.default_rng(seed)
+    x = rng.normal(0.0, 3.0, (B, V)).astype(np.float32)
+    hot = rng.random((B, V)) < 0.001
+    x[hot] = rng.normal(8.0, 2.0, int(hot.sum())).astype(np.float32)
+    return x
+
+
+@pytest.mark.parametrize("pad", [0, 12])
+def test_top_k_benchmark_shape(sampler, pad):
+    V = 151936
+    ks = [1, 2, 50, 200, 1000, 20000, 75968, V - 1, V, V + 5, 0, -3, 7, 40, 100, 5000]
+    check(sampler, "k", c3_rows(len(ks), V, 11), ks, pad)
+
+
+def test_top_k_ties_and_every_digit_level(sampler):
+    rng = np.random.default_rng(12)
+    V = 100000
+    rows = [
+        rng.integers(-5, 6, V).astype(np.float32),                       # ties: one key holds ~V/11
+        np.full(V, 2.5, np.float32),                                     # all equal
+        (1.0 + rng.random(V) * 2.0**-10).astype(np.float32),            # one top digit
+        (1.0 + rng.integers(0, 4096, V) * 2.0**-23).astype(np.float32),  # top two digits shared
+        np.where(rng.random(V) < 0.5, -np.inf, rng.normal(0, 1, V)).astype(np.float32),
+        np.where(rng.random(V) < 0.5, np.float32(-0.0), np.float32(0.0)),  # signed zeros only
+        np.concatenate([np.full(V - 10, -np.inf), np.arange(10)]).astype(np.float32),
+        np.where(rng.random(V) < 0.3, np.float32(0.0), rng.normal(0, 1, V)).astype(np.float32),
+    ]
+    for ks in ([1, 3, 50000, 99999, 17, 60000, 5, 40000], [9091, 50000, 33, 2, 99990, 30000, 10, 1]):
+        check(sampler, "k", np.stack(rows), ks)
+
+
+@pytest.mark.parametrize("V", [1, 2, 3, 5, 7, 64, 4097])
+def test_top_k_tiny_vocab(sampler, V):
+    rng = np.random.default_rng(V)
+    rows = np.stack([rng.normal(0, 1, V), rng.integers(0, 3, V)]).astype(np.float32)
+    for k in range(0, min(V, 6) + 1):
+        check(sampler, "k", rows, [k, k], pad=4 if V % 4 else 0)
+
+
+@pytest.mark.parametrize("pad", [0, 4])
+def test_top_p_benchmark_shape(sampler, pad):
+    V = 128256
+    tps = [0.9, 0.5, 0.95, 0.99, 0.999, 0.9999, 1e-6, 0.0, -1.0, -np.inf, np.nan, 1.0, 1.5,
+           np.inf, 0.3, 0.7]
+    rng = np.random.default_rng(13)
+    rows = rng.normal(0.0, 3.0, (len(tps), V)).astype(np.float32)
+    check(sampler, "p", rows, tps, pad)
+
+
+def test_top_p_ties_flat_and_masked_rows(sampler):
+    rng = np.random.default_rng(14)
+    V = 50000
+    rows = np.stack([
+        rng.integers(-3, 4, V).astype(np.float32),            # p ties at every cut
+        np.zeros(V, np.float32),                              # uniform
+        np.full(V, -np.inf, np.float32),                      # sum 0: untouched
+        np.where(rng.random(V) < 0.9, -np.inf, rng.normal(0, 2, V)).astype(np.float32),
+        (rng.normal(0, 2, V).astype(np.float32).view(np.uint32) & 0xFFFF0000).view(np.float32),
+        np.concatenate([[20.0], np.zeros(V - 1)]).astype(np.float32),  # one dominant
+        rng.normal(0, 0.01, V).astype(np.float32),            # nearly flat: a wide nucleus
+        np.where(rng.random(V) < 0.5, np.float32(-0.0), np.float32(0.0)),
+    ])
+    for tps in ([0.5, 0.5, 0.5, 0.5, 0.5, 0.5, 0.5, 0.5],
+                [0.9, 0.25, 0.9, 0.999, 0.95, 0.99, 0.99, 0.001],
+                [0.123, 0.9999, 0.1, 0.2, 0.6, 0.999999, 0.5, 0.75]):
+        check(sampler, "p", rows, tps)
+
+
+@pytest.mark.parametrize("V", [1, 2, 3, 5, 7, 64, 4097])
+def test_top_p_tiny_vocab(sampler, V):
+    rng = np.random.default_rng(100 + V)
+    rows = np.stack([rng.normal(0, 1, V), rng.integers(0, 3, V)]).astype(np.float32)
+    for tp in (0.0, 0.3, 0.6, 0.9, 0.99):
+        check(sampler, "p", rows, [tp, tp], pad=(-V) % 4 + 4 if V % 4 else 0)
+
+
+def test_mask_forms_agree_with_sampling(sampler):
+    """The kept set of apply_top_p is the kept list of a sampling call with
+    that top_p alone (sampler.rs:92-110 against sampler.rs:176-216)."""
+    V = 32000
+    rows = c3_rows(8, V, 15)
+    tps = np.asarray([0.5, 0.8, 0.9, 0.95, 0.99, 0.3, 0.7, 0.6], np.float32)
+    out = check(sampler, "p", rows, tps)
+    t = torch.from_numpy(rows).cuda()
+    db = llmk.DeviceBatch(logits=t, uniforms=torch.zeros(8, device="cuda"),
+                          top_p=torch.from_numpy(tps).cuda())
+    r = sampler.sample_batch(db, out_cap=V)
+    cnt = r.count.cpu().numpy()
+    ids = r.ids.cpu().numpy()
+    for i in range(8):
+        assert set(np.nonzero(out[i] > -np.inf)[0].tolist()) == set(ids[i, :cnt[i]].tolist())
+
+
+def test_invalid_arguments(sampler):
+    t = torch.zeros(2, 16, device="cuda")
+    k = torch.ones(2, dtype=torch.int32, device="cuda")
+    with pytest.raises(llmk.SamplerError):
+        sampler.apply_top_k(t.to(torch.bfloat16), k)
+    with pytest.raises(llmk.SamplerError):
+        sampler.apply_top_p(torch.zeros(2, 300000, device="cuda"), torch.ones(2, device="cuda"))
+    with pytest.raises(llmk.SamplerError):
+        sampler.apply_top_k(torch.zeros(16, device="cuda"), k)
+
+
+@pytest.mark.parametrize("op", ["k", "p"])
+def test_unaligned_rows(sampler, op):
+    """top-k takes rows at any f32 offset: a stride of 4099 and a view
+    starting one element in (scalar heads before the first 16-byte boundary).
+    top-p runs the sampling kernel first, whose rows are 16-byte aligned: it
+    refuses them."""
+    rng = np.random.default_rng(16)
+    B, V = 6, 4096
+    full = rng.normal(0, 3, (B, 4099)).astype(np.float32)
+    rows = full[:, 1:1 + V]
+    params = [1, 17, 400, 4095, 2048, 3] if op == "k" else [0.5, 0.9, 0.99, 0.1, 0.7, 0.95]
+    t = torch.from_numpy(full).cuda()
+    lg = t[:, 1:1 + V]
+    print(f"[case] unaligned {op}", flush=True)
+    if op == "k":
+        sampler.apply_top_k(lg, torch.tensor(params, dtype=torch.int32).cuda())
+    else:
+        with pytest.raises(llmk.SamplerError):
+            sampler.apply_top_p(lg, torch.tensor(params, dtype=torch.float32).cuda())
+        return
+    out = t.cpu().numpy()
+    assert np.array_equal(out[:, 0], full[:, 0]) and np.array_equal(out[:, 1 + V:], full[:, 1 + V:])
+    orc = oracle_mask(op, rows, params)
+    assert np.array_equal(out[:, 1:1 + V].view(np.uint32), orc.view(np.uint32))
