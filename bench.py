@@ -80,6 +80,48 @@ def time_config(llmk, synth, torch, name, steps=20, warmup=5):
             "frac_of_8TBps": gbps / HBM_PEAK_GBPS}
 
 
+def time_mask(llmk, synth, torch, op, steps=3):
+    """The mask forms in place: apply_top_k at C3's shape (k 50) and apply_top_p
+    at C4's (top-p 0.9).  Each launch masks a freshly restored copy of the
+    logits, restored before all timed launches of a round so that it has left
+    the MALL; event pairs on the launch stream around the call only."""
+    import numpy as np
+    w = synth.make("C3" if op == "top_k" else "C4")
+    src = torch.from_numpy(w.logits).to("cuda:0")
+    nbytes = src.numel() * 4
+    nsets = max(1, int(np.ceil(2 * MALL_BYTES / nbytes)) + 1)
+    bufs = [torch.empty_like(src) for _ in range(nsets)]
+    s = llmk.HipSampler(max_batch=w.B, max_vocab=w.V)
+    if op == "top_k":
+        par = torch.full((w.B,), 50, dtype=torch.int32, device="cuda:0")
+        call = lambda t: s.apply_top_k(t, par)
+    else:
+        par = torch.from_numpy(w.top_p).to("cuda:0")
+        call = lambda t: s.apply_top_p(t, par)
+    stream = torch.cuda.current_stream()
+    times = []
+    for r in range(steps + 1):
+        for b in bufs:
+            b.copy_(src)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in bufs]
+        for b, (e0, e1) in zip(bufs, ev):
+            e0.record(stream)
+            call(b)
+            e1.record(stream)
+        torch.cuda.synchronize()
+        if r:  # the first round warms up
+            times += [e0.elapsed_time(e1) for e0, e1 in ev]
+    masked = int((bufs[0] != src).sum().item())
+    us = float(np.mean(times)) * 1e3
+    alg = nbytes + 4 * masked + 4 * w.B
+    gbps = alg / (us * 1e-6) / 1e9
+    s.close()
+    return {"op": op, "B": w.B, "V": w.V, "param": 50 if op == "top_k" else float(w.top_p[0]),
+            "us_per_call": us, "masked_per_row": masked / w.B,
+            "algorithmic_bytes": alg, "achieved_GBps": gbps, "frac_of_8TBps": gbps / HBM_PEAK_GBPS}
+
+
 def stream_read_gbps(torch, nbytes=2 << 30, reps=5):
     """The box's achievable streaming-read bandwidth: llmk_read_probe (every
     lane reads 128-bit words with non-temporal loads, as the sampler does)
@@ -248,6 +290,9 @@ def main():
                 continue
             others[name] = time_config(llmk, synth, torch, name)
             log(f"[bench] {name}: {others[name]}")
+        for op in ("top_k", "top_p"):
+            others[f"apply_{op}"] = time_mask(llmk, synth, torch, op)
+            log(f"[bench] apply_{op}: {others[f'apply_{op}']}")
 
     cpu = None
     if not args.no_cpu_baseline:

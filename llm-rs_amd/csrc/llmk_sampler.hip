@@ -1454,7 +1454,7 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
       float v[8];
       processed(e0, v);
       float p[8];
-      uint32_t np = 0, nz = 0;
+      uint32_t np = 0, nz = 0, cm = 0;
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
         p[q] = -1.0f;  // not chosen
@@ -1462,8 +1462,34 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
         const bool chosen = fin && bin_of(v[q]) <= last;
         if (fin && !chosen) lkey = umax(lkey, fkey(v[q]));
         if (inr && !fin) p[q] = 0.0f;
-        // the exact p only where a lane of the wave needs one
-        if (__ballot(chosen) != 0 && chosen) p[q] = prob_of(v[q], P.T, m, S);
+        cm |= chosen ? 1u << q : 0u;
+      }
+      // the exact p of the wave's chosen values, packed in its 256 words of
+      // wcnt (free until the sort) so that each lane evaluates about
+      // chosen / 64 of them rather than a wave pass per slot holding one
+      LDS float* wz = (LDS float*)wcnt + wv * 256;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t hm = (cm >> (4 * h)) & 15u;
+        const uint32_t c = (uint32_t)__popc(hm);
+        const uint32_t incl = wave_incl_scan(c);
+        const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+        if (tot == 0) continue;
+        uint32_t at = incl - c;
+#pragma unroll
+        for (int q = 4 * h; q < 4 * h + 4; ++q)
+          if ((cm >> q) & 1u) wz[at++] = v[q];
+        WaveSync::sync();
+        for (uint32_t i = (uint32_t)lane; i < tot; i += WAVE) wz[i] = prob_of(wz[i], P.T, m, S);
+        WaveSync::sync();
+        at = incl - c;
+#pragma unroll
+        for (int q = 4 * h; q < 4 * h + 4; ++q)
+          if ((cm >> q) & 1u) p[q] = wz[at++];
+        WaveSync::sync();
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
         if (p[q] > 0.0f) ++np;
         else if (p[q] == 0.0f && !filt) ++nz;
       }
