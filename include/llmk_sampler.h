@@ -139,6 +139,20 @@ int llmk_apply_top_k(llmk_sampler* s, float* logits, uint32_t batch, uint32_t vo
 int llmk_apply_top_p(llmk_sampler* s, float* logits, uint32_t batch, uint32_t vocab,
                      uint64_t row_stride, const float* top_p, void* hip_stream);
 
+/* Logit bias (the OpenAI logit_bias map), batched and in place: no
+ * function of the reference has it; its formula is the one its test
+ * llm-tests/tests/mlc_parity.rs:1060-1072 applies, logits[idx] += bias (f32).
+ * Row b's pairs are bias_tokens[j], bias_values[j] for j in
+ * [bias_offsets[b], bias_offsets[b+1]) (device CSR, like the history); ids
+ * >= vocab are ignored.  The tokens of a row are the keys of a map: a token
+ * listed twice gets both biases in an unspecified order.  Run it before
+ * llmk_sample_batch on the same stream.  logits: device f32
+ * [batch][row_stride], any stride.  Allocates nothing. */
+int llmk_apply_logit_bias(llmk_sampler* s, float* logits, uint32_t batch, uint32_t vocab,
+                          uint64_t row_stride, const uint32_t* bias_offsets,
+                          const uint32_t* bias_tokens, const float* bias_values,
+                          void* hip_stream);
+
 /* Reads and clears the device status word (OR of LLMK_STATUS_* bits raised by
  * calls since the last read).  Synchronises `hip_stream`. */
 int llmk_sampler_status(llmk_sampler* s, void* hip_stream, uint32_t* status);

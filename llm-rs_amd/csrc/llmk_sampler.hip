@@ -3192,6 +3192,32 @@ __global__ __launch_bounds__(NT) void topp_mask_kernel(float* logits, uint32_t V
   });
 }
 
+
+// Logit bias in place (the formula of llm-tests/tests/mlc_parity.rs:1060-1072,
+// l += bias): one wave per row, lanes over the row's (token, bias) list.
+// The add is a compare-and-swap loop, an IEEE f32 addition (denormals kept)
+// that keeps both biases of a token listed twice; each round one of the
+// contending lanes succeeds, so the loop ends.
+__global__ __launch_bounds__(NT) void logit_bias_kernel(float* logits, uint32_t B, uint32_t V,
+                                                        uint64_t stride, const uint32_t* off,
+                                                        const uint32_t* tok, const float* val) {
+  const uint32_t b = blockIdx.x * NW + (threadIdx.x >> 6);
+  if (b >= B) return;
+  const uint32_t j0 = G(off)[b], j1 = G(off)[b + 1];
+  for (uint32_t j = j0 + (threadIdx.x & 63u); j < j1; j += WAVE) {
+    const uint32_t t = G(tok)[j];
+    if (t < V) {
+      uint32_t* p = (uint32_t*)(logits + (uint64_t)b * stride + t);
+      const float v = G(val)[j];
+      uint32_t old = G(p)[0], seen;
+      do {
+        seen = old;
+        old = atomicCAS(p, seen, __float_as_uint(__uint_as_float(seen) + v));
+      } while (old != seen);
+    }
+  }
+}
+
 }  // namespace llmk
 
 // ===========================================================================
@@ -3469,6 +3495,23 @@ extern "C" int llmk_apply_top_p(llmk_sampler* s, float* logits, uint32_t batch, 
   hipLaunchKernelGGL(topp_mask_kernel, dim3(batch * nseg), dim3(NT), 0, (hipStream_t)stream,
                      logits, vocab, row_stride, top_p, (const u4v*)s->ws.cut, s->ws.mtok,
                      nseg, seg);
+  HIPCHK(hipGetLastError());
+  return LLMK_OK;
+}
+
+extern "C" int llmk_apply_logit_bias(llmk_sampler* s, float* logits, uint32_t batch,
+                                     uint32_t vocab, uint64_t row_stride,
+                                     const uint32_t* bias_offsets, const uint32_t* bias_tokens,
+                                     const float* bias_values, void* stream) {
+  const int rc = check_mask_rows(s, logits, vocab, row_stride, bias_offsets);
+  if (rc != LLMK_OK) return rc;
+  if (!bias_tokens || !bias_values)
+    return fail(LLMK_ERR_INVALID_ARGUMENT, "bias_tokens and bias_values are required");
+  if (batch == 0 || vocab == 0) return LLMK_OK;
+  HIPCHK(hipSetDevice(s->device));
+  hipLaunchKernelGGL(logit_bias_kernel, dim3((batch + NW - 1) / NW), dim3(NT), 0,
+                     (hipStream_t)stream, logits, batch, vocab, row_stride, bias_offsets,
+                     bias_tokens, bias_values);
   HIPCHK(hipGetLastError());
   return LLMK_OK;
 }

@@ -34,6 +34,7 @@ EXPORTED_SYMBOLS = (
     "llmk_last_error",
     "llmk_apply_top_k",
     "llmk_apply_top_p",
+    "llmk_apply_logit_bias",
 )
 
 
@@ -93,6 +94,9 @@ def load():
         getattr(lib, fn).argtypes = [vp, vp, ctypes.c_uint32, ctypes.c_uint32,
                                      ctypes.c_uint64, par, vp]
         getattr(lib, fn).restype = ctypes.c_int
+    lib.llmk_apply_logit_bias.argtypes = [vp, vp, ctypes.c_uint32, ctypes.c_uint32,
+                                          ctypes.c_uint64, vp, vp, vp, vp]
+    lib.llmk_apply_logit_bias.restype = ctypes.c_int
     lib.llmk_last_error.argtypes = []
     lib.llmk_last_error.restype = ctypes.c_char_p
     _lib = lib

@@ -197,6 +197,25 @@ class HipSampler:
         """sampler.rs:176-216 on every row: logits [B, V] float32, top_p [B] float32."""
         self._mask("llmk_apply_top_p", logits, top_p.to(torch.float32).contiguous(), stream)
 
+    def apply_logit_bias(self, logits: torch.Tensor, offsets: torch.Tensor,
+                         tokens: torch.Tensor, values: torch.Tensor,
+                         stream: Optional[torch.cuda.Stream] = None) -> None:
+        """logits[b, tokens[j]] += values[j] for j in offsets[b]..offsets[b+1]
+        (the formula of mlc_parity.rs:1060-1072), in place on [B, V] float32."""
+        if logits.dtype != torch.float32 or logits.dim() != 2 or logits.stride(1) != 1:
+            raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT,
+                               "logits must be a row-major float32 [batch, vocab] tensor")
+        off = offsets.to(torch.int32).contiguous()
+        tok = tokens.to(torch.int32).contiguous()
+        val = values.to(torch.float32).contiguous()
+        st = stream if stream is not None else torch.cuda.current_stream()
+        rc = self._lib.llmk_apply_logit_bias(self._h, logits.data_ptr(), logits.shape[0],
+                                             logits.shape[1], logits.stride(0), off.data_ptr(),
+                                             tok.data_ptr(), val.data_ptr(),
+                                             ctypes.c_void_p(st.cuda_stream))
+        if rc != 0:
+            raise SamplerError(rc, _lib.last_error())
+
     # ---- the per-row reference call (LlmBackend::sample) ------------------
     def sample(self, logits: torch.Tensor, params: SampleParams,
                token_history: Sequence[int], u: float) -> int:

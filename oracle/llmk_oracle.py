@@ -198,6 +198,17 @@ def apply_top_p(mode, logits, top_p):
     return l
 
 
+def apply_logit_bias(logits, tokens, values):
+    """Logit bias, the formula of llm-tests/tests/mlc_parity.rs:1060-1072
+    (logits[idx] += bias, in f32), for each (token, bias) pair in list order;
+    ids >= len(logits) are ignored."""
+    l = _f32p(logits).copy()
+    for t, v in zip(tokens, values):
+        if int(t) < l.size:
+            l[int(t)] = np.float32(l[int(t)] + np.float32(v))
+    return l
+
+
 def sample_simple(mode, logits, t, u):
     l = _f32p(logits)
     return int(load().llmk_oracle_sample_simple(mode, _p(l), l.size, t, u))

@@ -85,6 +85,11 @@ KATS = [
          expect=[float(f32(3.7883238792419434) - (f32(1.09) + f32(2) * f32(0.94))),
                  float(f32(0.5029208660125732) - (f32(1.09) + f32(1) * f32(0.94))), 1.0],
          tol=0.0),
+    # logit bias (OpenAI logit_bias): logits[idx] += bias; the test's token
+    # ids 10 and 20 sit at positions 1 and 2 of its three-entry vector
+    dict(name="logit_bias", src=f"{P}:1060-1072", op="logit_bias",
+         logits=[1.0, 1.0, 1.0], bias_tokens=[1, 2], bias_values=[2.5, -5.0],
+         expect=[1.0, 3.5, -4.0], tol=0.0),
     # documented order: repetition before temperature
     dict(name="order_rep_then_temp_neg", src=f"{T}:760-791", op="rep_then_temp",
          logits=[-8.0, 0.0], history=[0], penalty=2.0, t=2.0, expect=[-8.0, 0.0], tol=1e-5),

@@ -215,3 +215,68 @@ def test_unaligned_rows(sampler, op):
     assert np.array_equal(out[:, 0], full[:, 0]) and np.array_equal(out[:, 1 + V:], full[:, 1 + V:])
     orc = oracle_mask(op, rows, params)
     assert np.array_equal(out[:, 1:1 + V].view(np.uint32), orc.view(np.uint32))
+
+
+def bias_case(B, V, seed, dup=False):
+    rng = np.random.default_rng(seed)
+    rows = rng.normal(0, 3, (B, V)).astype(np.float32)
+    rows[0, :5] = [-np.inf, 0.0, -0.0, 1e-40, -1e-40]  # -inf, signed zeros, denormals
+    n = rng.integers(0, 300, B)
+    n[0] = 8
+    off = np.concatenate([[0], np.cumsum(n)]).astype(np.uint32)
+    tok, val = [], []
+    for b in range(B):
+        t = rng.choice(V + 50, int(n[b]), replace=dup)  # some ids >= V (ignored)
+        if b == 0:
+            t = np.array([0, 1, 2, 3, 4, V + 1, 7, 7 if dup else 8])
+        tok.append(t)
+        val.append(rng.normal(0, 5, int(n[b])).astype(np.float32))
+    val[0][:5] = [3.0, 1e-40, -1e-40, 1e-40, 2e-40]
+    return rows, off, np.concatenate(tok).astype(np.uint32), np.concatenate(val).astype(np.float32)
+
+
+@pytest.mark.parametrize("dup", [False, True])
+def test_logit_bias(sampler, dup):
+    """llmk_apply_logit_bias against the oracle's restatement of the
+    formula of mlc_parity.rs:1060-1072, bit for bit: ids beyond the
+    vocabulary, -inf, signed zeros, denormal logits and biases, and (dup)
+    tokens listed twice, whose two f32 additions are checked in either order."""
+    B, V = 40, 32003
+    rows, off, tok, val = bias_case(B, V, 17, dup)
+    print(f"[case] logit_bias B={B} V={V} dup={dup}", flush=True)
+    t = torch.from_numpy(rows.copy()).cuda()
+    sampler.apply_logit_bias(t, torch.from_numpy(off.view(np.int32)).cuda(),
+                             torch.from_numpy(tok.view(np.int32)).cuda(), torch.from_numpy(val).cuda())
+    gpu = t.cpu().numpy()
+    for b in range(B):
+        tb, vb = tok[off[b]:off[b + 1]], val[off[b]:off[b + 1]]
+        want = O.apply_logit_bias(rows[b], tb, vb)
+        if not np.array_equal(gpu[b].view(np.uint32), want.view(np.uint32)):
+            # a token listed twice: its biases may land in the other order
+            alt = O.apply_logit_bias(rows[b], tb[::-1], vb[::-1])
+            diff = np.nonzero(gpu[b].view(np.uint32) != want.view(np.uint32))[0]
+            assert dup and np.array_equal(gpu[b][diff].view(np.uint32), alt[diff].view(np.uint32)), (b, diff[:5])
+
+
+def test_logit_bias_then_sample(sampler):
+    """Bias then sample on one stream equals the oracle sampling the biased
+    rows (C3's parameters and histories)."""
+    from llmk import synth
+    from gpu_util import assert_bit_exact, run_gpu
+    w = synth.make("C3", B=16)
+    rng = np.random.default_rng(18)
+    n = rng.integers(1, 50, w.B)
+    off = np.concatenate([[0], np.cumsum(n)]).astype(np.uint32)
+    tok = rng.choice(w.V, int(off[-1])).astype(np.uint32)
+    val = rng.normal(0, 8, int(off[-1])).astype(np.float32)
+    biased = np.stack([O.apply_logit_bias(w.logits[b], tok[off[b]:off[b + 1]], val[off[b]:off[b + 1]])
+                       for b in range(w.B)])
+    print("[case] logit_bias then C3 sampling B=16", flush=True)
+    db = w.to_device()
+    sampler.apply_logit_bias(db.logits, torch.from_numpy(off.view(np.int32)).cuda(),
+                             torch.from_numpy(tok.view(np.int32)).cuda(), torch.from_numpy(val).cuda())
+    assert np.array_equal(db.logits.cpu().numpy().view(np.uint32), biased.view(np.uint32))
+    w.logits = biased
+    gpu = run_gpu(sampler, w, 64)
+    orc = O.sample_workload(O.MIRROR, w, out_cap=64, nthreads=16)
+    assert_bit_exact(w, gpu, orc, 64, "bias+C3")

@@ -100,6 +100,9 @@ def test_reference_kat(kat, mode):
     elif op == "temp_then_rep":
         out = O.apply_repetition_penalty(O.apply_temperature(lg, kat["t"]), kat["history"], kat["penalty"])
         np.testing.assert_array_less(np.abs(out - np.asarray(kat["expect"], np.float32)), kat["tol"])
+    elif op == "logit_bias":
+        out = O.apply_logit_bias(lg, kat["bias_tokens"], kat["bias_values"])
+        assert np.array_equal(out, np.asarray(kat["expect"], np.float32))
     else:
         raise AssertionError(f"unknown op {op}")
 
