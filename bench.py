@@ -331,6 +331,8 @@ def main():
             "achievable_read_GBps": read_gbps,
             "frac_of_achievable": achieved / read_gbps,
             "kernel_avg_us": kern_avg_ms * 1e3,
+            "kernel_median_us": float(np.median(kern_ms)) * 1e3,
+            "kernel_launches_timed": len(kern_ms),
         },
         "other_configs": others,
         "cpu_baseline": cpu,
