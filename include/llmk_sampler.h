@@ -54,6 +54,9 @@ extern "C" {
  * without penalties. */
 #define LLMK_STATUS_HISTORY_OVERFLOW 0x2u
 #define LLMK_STATUS_SLOT_TIMEOUT 0x4u /* slow-path scratch slot not acquired */
+/* llmk_history_append found a row's history buffer full (its token was not
+ * appended). */
+#define LLMK_STATUS_HISTORY_FULL 0x8u
 
 typedef struct llmk_sampler llmk_sampler; /* opaque; owns device workspace */
 
@@ -98,6 +101,11 @@ typedef struct {
   float* out_probs;
   uint32_t out_cap;
   uint32_t* out_count;
+  /* Optional, [batch]: row b's history is hist_tokens[hist_offsets[b] ..
+   * hist_offsets[b] + hist_lengths[b]) (hist_offsets then needs [batch]
+   * entries).  This lets the history live in per-row buffers with room to
+   * grow, appended to on the device by llmk_history_append.  NULL = CSR. */
+  const uint32_t* hist_lengths;
 } llmk_sample_batch_args;
 
 /* Create a sampler on `device` able to serve batches up to max_batch rows of
@@ -152,6 +160,18 @@ int llmk_apply_logit_bias(llmk_sampler* s, float* logits, uint32_t batch, uint32
                           uint64_t row_stride, const uint32_t* bias_offsets,
                           const uint32_t* bias_tokens, const float* bias_values,
                           void* hip_stream);
+
+/* Appends each row's sampled token to its device-resident history, as the
+ * scheduler pushes it (llm-scheduler/src/scheduler.rs:147):
+ * hist_tokens[hist_offsets[b] + hist_lengths[b]] = tokens[b] and
+ * hist_lengths[b] += 1, for rows whose token is not LLMK_INVALID_TOKEN.  A
+ * row already holding `capacity` tokens is left as it is and raises
+ * LLMK_STATUS_HISTORY_FULL.  With hist_lengths in llmk_sample_batch_args
+ * the next step then reads the grown histories without a host round trip.
+ * Enqueued on hip_stream; allocates nothing. */
+int llmk_history_append(llmk_sampler* s, uint32_t batch, const uint32_t* hist_offsets,
+                        uint32_t* hist_lengths, uint32_t* hist_tokens, uint32_t capacity,
+                        const uint32_t* tokens, void* hip_stream);
 
 /* Reads and clears the device status word (OR of LLMK_STATUS_* bits raised by
  * calls since the last read).  Synchronises `hip_stream`. */

@@ -94,6 +94,7 @@ struct Args {
   const float *T, *top_p, *min_p, *rp, *pp, *fp;
   const int32_t* top_k;
   const uint32_t *hoff, *htok, *mask;
+  const uint32_t* hlen;  // optional: row b's history is htok[hoff[b] .. hoff[b] + hlen[b])
   uint32_t mask_words;
   const float* u;
   uint32_t *out_tok, *out_ids, *out_cnt;
@@ -433,7 +434,8 @@ __device__ __forceinline__ void build_history(const Args& a, const RowP& P, uint
   const uint32_t tid = threadIdx.x;
   const bool need_pen = P.rp != 1.0f || P.pp != 0.0f || P.fp != 0.0f;
   const bool have = need_pen && a.hoff;
-  const uint32_t h0 = have ? G(a.hoff)[b] : 0u, h1 = have ? G(a.hoff)[b + 1] : 0u;
+  const uint32_t h0 = have ? G(a.hoff)[b] : 0u;
+  const uint32_t h1 = have ? (a.hlen ? h0 + G(a.hlen)[b] : G(a.hoff)[b + 1]) : 0u;
   uint32_t tk[HTPT];
 #pragma unroll
   for (int q = 0; q < HTPT; ++q) {
@@ -2729,7 +2731,7 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   uint32_t h0 = 0, h1 = 0;
   if (a.hoff) {  // loaded unconditionally, in parallel with the parameters
     h0 = G(a.hoff)[b];
-    h1 = G(a.hoff)[b + 1];
+    h1 = a.hlen ? h0 + G(a.hlen)[b] : G(a.hoff)[b + 1];
   }
   if (!need_pen) h1 = h0;
   // history tokens exist: their positions are excluded from the vocabulary
@@ -3218,6 +3220,27 @@ __global__ __launch_bounds__(NT) void logit_bias_kernel(float* logits, uint32_t 
   }
 }
 
+
+// The scheduler's token push (scheduler.rs:147) on the device: row b appends
+// its sampled token to its history buffer, htok[hoff[b] + hlen[b]], while
+// hlen[b] < cap.  A full row keeps its history and raises a status bit.
+__global__ __launch_bounds__(256) void history_append_kernel(uint32_t B, const uint32_t* hoff,
+                                                             uint32_t* hlen, uint32_t* htok,
+                                                             uint32_t cap, const uint32_t* tok,
+                                                             uint32_t* status) {
+  const uint32_t b = blockIdx.x * 256 + threadIdx.x;
+  if (b >= B) return;
+  const uint32_t t = G(tok)[b];
+  if (t == LLMK_INVALID_TOKEN) return;
+  const uint32_t n = G(hlen)[b];
+  if (n >= cap) {
+    atomicOr(status, LLMK_STATUS_HISTORY_FULL);
+    return;
+  }
+  G(htok)[G(hoff)[b] + n] = t;
+  G(hlen)[b] = n + 1;
+}
+
 }  // namespace llmk
 
 // ===========================================================================
@@ -3365,6 +3388,8 @@ static int sample_batch_impl(llmk_sampler* s, const llmk_sample_batch_args* in,
     return fail(LLMK_ERR_INVALID_ARGUMENT, "row_stride < vocab");
   if ((in->hist_offsets == nullptr) != (in->hist_tokens == nullptr))
     return fail(LLMK_ERR_INVALID_ARGUMENT, "hist_offsets and hist_tokens go together");
+  if (in->hist_lengths && !in->hist_offsets)
+    return fail(LLMK_ERR_INVALID_ARGUMENT, "hist_lengths needs hist_offsets and hist_tokens");
   if (in->allow_mask && in->mask_words_per_row < (in->vocab + 31) / 32)
     return fail(LLMK_ERR_INVALID_ARGUMENT, "mask_words_per_row < ceil(vocab/32)");
   if (in->out_cap && !in->out_ids && !in->out_probs)
@@ -3389,6 +3414,7 @@ static int sample_batch_impl(llmk_sampler* s, const llmk_sample_batch_args* in,
   a.top_k = in->top_k;
   a.hoff = in->hist_offsets;
   a.htok = in->hist_tokens;
+  a.hlen = in->hist_lengths;
   a.mask = in->allow_mask;
   a.mask_words = in->mask_words_per_row;
   a.u = in->uniforms;
@@ -3512,6 +3538,21 @@ extern "C" int llmk_apply_logit_bias(llmk_sampler* s, float* logits, uint32_t ba
   hipLaunchKernelGGL(logit_bias_kernel, dim3((batch + NW - 1) / NW), dim3(NT), 0,
                      (hipStream_t)stream, logits, batch, vocab, row_stride, bias_offsets,
                      bias_tokens, bias_values);
+  HIPCHK(hipGetLastError());
+  return LLMK_OK;
+}
+
+extern "C" int llmk_history_append(llmk_sampler* s, uint32_t batch, const uint32_t* hist_offsets,
+                                   uint32_t* hist_lengths, uint32_t* hist_tokens,
+                                   uint32_t capacity, const uint32_t* tokens, void* stream) {
+  if (!s) return fail(LLMK_ERR_INVALID_ARGUMENT, "sampler is NULL");
+  if (!hist_offsets || !hist_lengths || !hist_tokens || !tokens)
+    return fail(LLMK_ERR_INVALID_ARGUMENT, "history arrays and tokens are required");
+  if (batch == 0) return LLMK_OK;
+  HIPCHK(hipSetDevice(s->device));
+  hipLaunchKernelGGL(history_append_kernel, dim3((batch + 255) / 256), dim3(256), 0,
+                     (hipStream_t)stream, batch, hist_offsets, hist_lengths, hist_tokens,
+                     capacity, tokens, s->ws.status);
   HIPCHK(hipGetLastError());
   return LLMK_OK;
 }

@@ -21,6 +21,7 @@ LLMK_INVALID_TOKEN = 0xFFFFFFFF
 LLMK_STATUS_INVALID_PARAMS = 0x1
 LLMK_STATUS_HISTORY_OVERFLOW = 0x2
 LLMK_STATUS_SLOT_TIMEOUT = 0x4
+LLMK_STATUS_HISTORY_FULL = 0x8
 LLMK_F32 = 0
 LLMK_BF16 = 1
 LLMK_F16 = 2
@@ -35,6 +36,7 @@ EXPORTED_SYMBOLS = (
     "llmk_apply_top_k",
     "llmk_apply_top_p",
     "llmk_apply_logit_bias",
+    "llmk_history_append",
 )
 
 
@@ -64,6 +66,7 @@ class SampleBatchArgs(ctypes.Structure):
         ("out_probs", ctypes.c_void_p),
         ("out_cap", ctypes.c_uint32),
         ("out_count", ctypes.c_void_p),
+        ("hist_lengths", ctypes.c_void_p),
     ]
 
 
@@ -97,6 +100,8 @@ def load():
     lib.llmk_apply_logit_bias.argtypes = [vp, vp, ctypes.c_uint32, ctypes.c_uint32,
                                           ctypes.c_uint64, vp, vp, vp, vp]
     lib.llmk_apply_logit_bias.restype = ctypes.c_int
+    lib.llmk_history_append.argtypes = [vp, ctypes.c_uint32, vp, vp, vp, ctypes.c_uint32, vp, vp]
+    lib.llmk_history_append.restype = ctypes.c_int
     lib.llmk_last_error.argtypes = []
     lib.llmk_last_error.restype = ctypes.c_char_p
     _lib = lib

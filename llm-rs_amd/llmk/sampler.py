@@ -76,6 +76,7 @@ class DeviceBatch:
     hist_offsets: Optional[torch.Tensor] = None  # int32/uint32 [B+1]
     hist_tokens: Optional[torch.Tensor] = None   # int32/uint32
     allow_mask: Optional[torch.Tensor] = None    # int32/uint32 [B, words]
+    hist_lengths: Optional[torch.Tensor] = None  # int32/uint32 [B]: per-row buffers
 
 
 class HipSampler:
@@ -150,6 +151,7 @@ class HipSampler:
             cap = out_probs.shape[1]
         a.out_cap = cap
         a.out_count = _ptr(out_count)
+        a.hist_lengths = _ptr(db.hist_lengths)
         st = stream if stream is not None else torch.cuda.current_stream()
         rc = self._lib.llmk_sample_batch(self._h, ctypes.byref(a), ctypes.c_void_p(st.cuda_stream))
         if rc != 0:
@@ -213,6 +215,23 @@ class HipSampler:
                                              logits.shape[1], logits.stride(0), off.data_ptr(),
                                              tok.data_ptr(), val.data_ptr(),
                                              ctypes.c_void_p(st.cuda_stream))
+        if rc != 0:
+            raise SamplerError(rc, _lib.last_error())
+
+    def history_append(self, hist_offsets: torch.Tensor, hist_lengths: torch.Tensor,
+                       hist_tokens: torch.Tensor, capacity: int, tokens: torch.Tensor,
+                       stream: Optional[torch.cuda.Stream] = None) -> None:
+        """scheduler.rs:147 on the device: append tokens[b] to row b's history
+        buffer (int32 tensors, updated in place)."""
+        for t in (hist_offsets, hist_lengths, hist_tokens, tokens):
+            if t.dtype != torch.int32 or not t.is_contiguous():
+                raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT,
+                                   "history arrays and tokens must be contiguous int32")
+        st = stream if stream is not None else torch.cuda.current_stream()
+        rc = self._lib.llmk_history_append(self._h, tokens.shape[0], hist_offsets.data_ptr(),
+                                           hist_lengths.data_ptr(), hist_tokens.data_ptr(),
+                                           capacity, tokens.data_ptr(),
+                                           ctypes.c_void_p(st.cuda_stream))
         if rc != 0:
             raise SamplerError(rc, _lib.last_error())
 

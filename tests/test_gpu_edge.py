@@ -249,3 +249,53 @@ def test_repeated_calls_are_stable(sampler):
         again = run_gpu(sampler, w, CAP)
         for a, b in zip(first, again):
             assert np.array_equal(a, b)
+
+
+def test_history_buffers_and_device_append(sampler):
+    """Per-row history buffers (hist_lengths) and llmk_history_append: two
+    decode steps of C3 rows whose histories live in buffers of capacity
+    2100, the sampled tokens appended on the device between the steps
+    (scheduler.rs:147), each step bit-exact against the oracle on the
+    compact CSR; a full row keeps its history and raises
+    LLMK_STATUS_HISTORY_FULL."""
+    import torch
+    w = synth.make("C3", B=24)
+    cap = 2100
+    B = w.B
+    lens = np.diff(w.hist_offsets.astype(np.int64)).astype(np.int64)
+    lens[3] = cap  # a full row: its history padded with repeats of its own tokens
+    buf = np.zeros(B * cap, np.uint32)
+    for b in range(B):
+        h = w.hist_tokens[w.hist_offsets[b]:w.hist_offsets[b + 1]]
+        hh = np.resize(h, int(lens[b])) if len(h) else np.zeros(int(lens[b]), np.uint32)
+        buf[b * cap:b * cap + lens[b]] = hh
+    offs = (np.arange(B) * cap).astype(np.uint32)
+    d_off = torch.from_numpy(offs.view(np.int32)).cuda()
+    d_len = torch.from_numpy(lens.astype(np.int32)).cuda()
+    d_buf = torch.from_numpy(buf.view(np.int32)).cuda()
+    assert sampler.status() == 0
+    for step in range(2):
+        # the compact CSR the oracle reads
+        cur = d_buf.cpu().numpy().view(np.uint32)
+        ln = d_len.cpu().numpy().astype(np.int64)
+        w.hist_offsets = np.concatenate([[0], np.cumsum(ln)]).astype(np.uint32)
+        w.hist_tokens = np.concatenate([cur[b * cap:b * cap + ln[b]] for b in range(B)]).astype(np.uint32)
+        w.uniforms = np.random.default_rng(40 + step).random(B).astype(np.float32)
+        print(f"[case] history buffers step {step}", flush=True)
+        db = w.to_device()
+        db.hist_offsets, db.hist_tokens, db.hist_lengths = d_off, d_buf, d_len
+        r = sampler.sample_batch(db, out_cap=CAP)
+        torch.cuda.synchronize()
+        gpu = (r.tokens.cpu().numpy().view(np.uint32), r.ids.cpu().numpy().view(np.uint32),
+               r.probs.cpu().numpy(), r.count.cpu().numpy().view(np.uint32))
+        orc = O.sample_workload(O.MIRROR, w, out_cap=CAP, nthreads=16)
+        assert_bit_exact(w, gpu, orc, CAP, f"history buffers step {step}")
+        sampler.history_append(d_off, d_len, d_buf, cap, r.tokens)
+        torch.cuda.synchronize()
+        ln2 = d_len.cpu().numpy().astype(np.int64)
+        full = ln >= cap
+        assert np.array_equal(ln2, np.where(full, ln, ln + 1))
+        nb = d_buf.cpu().numpy().view(np.uint32)
+        for b in np.nonzero(~full)[0]:
+            assert nb[b * cap + ln[b]] == gpu[0][b]
+        assert sampler.status() == _lib.LLMK_STATUS_HISTORY_FULL
