@@ -280,3 +280,40 @@ def test_logit_bias_then_sample(sampler):
     gpu = run_gpu(sampler, w, 64)
     orc = O.sample_workload(O.MIRROR, w, out_cap=64, nthreads=16)
     assert_bit_exact(w, gpu, orc, 64, "bias+C3")
+
+
+def random_rows(rng, B, V):
+    kind = rng.integers(0, 5)
+    if kind == 0:
+        x = rng.normal(0, rng.uniform(0.01, 6), (B, V))
+    elif kind == 1:
+        x = rng.integers(-4, 5, (B, V))  # heavy ties
+    elif kind == 2:
+        x = rng.normal(0, 3, (B, V)).astype(np.float32)
+        x = (x.view(np.uint32) & 0xFFFF0000).view(np.float32)  # bf16-valued
+    elif kind == 3:
+        x = rng.standard_cauchy((B, V)).clip(-1e4, 1e4)  # heavy tails
+    else:
+        x = rng.normal(0, 2, (B, V))
+        x[:, rng.integers(0, V, max(1, V // 100))] += rng.uniform(5, 15)  # spikes
+    x = np.asarray(x, np.float32)
+    if rng.random() < 0.4:
+        x[rng.random((B, V)) < rng.uniform(0, 0.95)] = -np.inf
+    return x
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_mask_forms_random(sampler, seed):
+    """Seeded random shapes, distributions, parameters and paddings, both
+    mask forms bit-exact against the oracle."""
+    rng = np.random.default_rng(1000 + seed)
+    B = int(rng.integers(1, 33))
+    V = int(rng.choice([int(rng.integers(1, 300)), int(rng.integers(300, 20000)),
+                        int(rng.integers(20000, 200000))]))
+    rows = random_rows(rng, B, V)
+    ks = [int(rng.choice([0, 1, 2, rng.integers(1, V + 2), V - 1, V, rng.integers(1, 64)]))
+          for _ in range(B)]
+    tps = [float(rng.choice([rng.uniform(0, 1), rng.uniform(0.9, 1.0), 0.0, 1.0,
+                             rng.uniform(0.99, 0.99999)])) for _ in range(B)]
+    check(sampler, "k", rows, ks, pad=int(rng.integers(0, 9)))
+    check(sampler, "p", rows, tps, pad=(-V) % 4 + 4 * int(rng.integers(0, 3)))
