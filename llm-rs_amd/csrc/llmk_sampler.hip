@@ -2980,9 +2980,17 @@ __device__ __forceinline__ void each4(const float* row, uint32_t e0, uint32_t e1
   uint32_t a0 = e0 + (mis ? 4u - mis : 0u);
   if (a0 > e1) a0 = e1;
   const uint32_t v4 = a0 + ((e1 - a0) & ~3u);
-  for (uint32_t e = a0 + 4 * threadIdx.x; e < v4; e += 4 * NT) {
-    const f4v x = *(const GLB f4v*)G(row + e);
-    f(e, x);
+  // four float4 loads in flight per lane before any is used: one workgroup
+  // per row needs the memory-level parallelism
+  constexpr uint32_t U = 4, STEP = 4 * NT;
+  for (uint32_t e = a0 + 4 * threadIdx.x; e < v4; e += U * STEP) {
+    f4v x[U];
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u)
+      if (e + u * STEP < v4) x[u] = *(const GLB f4v*)G(row + e + u * STEP);
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u)
+      if (e + u * STEP < v4) f(e + u * STEP, x[u]);
   }
   const uint32_t nh = a0 - e0, ns = nh + (e1 - v4);
   for (uint32_t i = threadIdx.x; i < ns; i += NT) {
