@@ -213,8 +213,8 @@ def main():
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py: this build measures one GPU only (rows shard with no communication; "
-              "see DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py: this build measures one GPU only: rows are independent, so N GPUs "
+              "each sample B/N rows with no communication; run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
