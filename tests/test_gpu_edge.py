@@ -257,7 +257,7 @@ def test_history_buffers_and_device_append(sampler):
     2100, the sampled tokens appended on the device between the steps
     (scheduler.rs:147), each step bit-exact against the oracle on the
     compact CSR; a full row keeps its history and raises
-    LLMK_STATUS_HISTORY_FULL."""
+    LLMK_STATUS_HISTORY_FULL; an invalid token is not pushed."""
     import torch
     w = synth.make("C3", B=24)
     cap = 2100
@@ -290,10 +290,13 @@ def test_history_buffers_and_device_append(sampler):
                r.probs.cpu().numpy(), r.count.cpu().numpy().view(np.uint32))
         orc = O.sample_workload(O.MIRROR, w, out_cap=CAP, nthreads=16)
         assert_bit_exact(w, gpu, orc, CAP, f"history buffers step {step}")
-        sampler.history_append(d_off, d_len, d_buf, cap, r.tokens)
+        toks = r.tokens.clone()
+        toks[5] = -1  # LLMK_INVALID_TOKEN: no push
+        sampler.history_append(d_off, d_len, d_buf, cap, toks)
         torch.cuda.synchronize()
         ln2 = d_len.cpu().numpy().astype(np.int64)
         full = ln >= cap
+        full[5] = True  # unchanged like a full row, without the status bit
         assert np.array_equal(ln2, np.where(full, ln, ln + 1))
         nb = d_buf.cpu().numpy().view(np.uint32)
         for b in np.nonzero(~full)[0]:
