@@ -210,6 +210,9 @@ def main():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run a plain device-to-device copy of BYTES, 10 times (the "
                          "reference kernel for scaling HBM traffic counters)")
+    ap.add_argument("--mask-probe", choices=["top_k", "top_p"], default=None,
+                    help="only time one mask form (apply_top_k at C3's shape, apply_top_p at "
+                         "C4's) and print its line")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -230,6 +233,9 @@ def main():
         return
     import llmk
     from llmk import synth
+    if args.mask_probe:
+        print(json.dumps(time_mask(llmk, synth, torch, args.mask_probe)), flush=True)
+        return
     w = synth.make(args.config)
     dev = torch.device("cuda:0")
     db0 = w.to_device(dev)
