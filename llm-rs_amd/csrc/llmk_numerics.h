@@ -10,55 +10,60 @@
 
 namespace llmk {
 
-// e^y for y <= 0, as used on the reference's candidate probabilities
-// (sampler.rs:61 `(l - max_logit).exp()`).  Cody–Waite reduction
-// y = k ln2 + r with ln2 split in two parts, e^r by its degree-13 Taylor
-// polynomial (|r| <= ln2/2, truncation < 5e-18) in double, one final rounding
-// to float.  Agrees with glibc expf on all but 1 in ~11500 inputs (1 ulp).
-__device__ __forceinline__ float exp_m(float y) {
-  const bool ok = y >= -110.0f;  // below: far under the smallest subnormal
-  const double yd = ok ? (double)y : 0.0;
-  const double kd = __builtin_rint(yd * 0x1.71547652b82fep+0);
-  double r = __builtin_fma(-kd, 0x1.62e42fee00000p-1, yd);
-  r = __builtin_fma(-kd, 0x1.a39ef35793c76p-33, r);
-  double p = 0x1.6124613a86d09p-33;
-  p = __builtin_fma(p, r, 0x1.1eed8eff8d898p-29);
-  p = __builtin_fma(p, r, 0x1.ae64567f544e4p-26);
-  p = __builtin_fma(p, r, 0x1.27e4fb7789f5cp-22);
-  p = __builtin_fma(p, r, 0x1.71de3a556c734p-19);
-  p = __builtin_fma(p, r, 0x1.a01a01a01a01ap-16);
-  p = __builtin_fma(p, r, 0x1.a01a01a01a01ap-13);
-  p = __builtin_fma(p, r, 0x1.6c16c16c16c17p-10);
-  p = __builtin_fma(p, r, 0x1.1111111111111p-7);
-  p = __builtin_fma(p, r, 0x1.5555555555555p-5);
-  p = __builtin_fma(p, r, 0x1.5555555555555p-3);
-  p = __builtin_fma(p, r, 0x1.0000000000000p-1);
-  p = __builtin_fma(p, r, 1.0);
-  p = __builtin_fma(p, r, 1.0);
-  const float res = (float)__builtin_amdgcn_ldexp(p, (int)kd);
-  return ok ? res : 0.0f;
+// e^x for x <= 0, bit for bit as glibc's expf computes it (glibc >= 2.28,
+// sysdeps/ieee754/flt-32/e_expf.c; the x86-64 FMA build that Rust's
+// f32::exp, sampler.rs:61, reaches): x*32/ln2 = k + r, k the nearest integer
+// (ties to even, through the 1.5*2^52 shift), 2^(k/32) = the table word of
+// k mod 32 with k >> 5 added to its exponent field, 2^(r/32) by a cubic, all
+// in double, one rounding to float.  The two reduction steps are fused
+// multiply-adds, as that build contracts them.  kExpTab[i] = bits(2^(i/32))
+// - (i << 47) with 2^(i/32) correctly rounded; the cubic is glibc's published
+// exp2f_data poly scaled by 32^-3, 32^-2, 32^-1.  The CPU tests scan every
+// float in [-104, 0] against the host's expf.  Below -0x1.9fe368p6 (e^x
+// rounds to 0) and at -inf the result is +0.
+constexpr uint64_t kExpTab[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull,
+    0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull,
+    0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull,
+    0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull,
+    0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull,
+    0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull,
+    0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull,
+    0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full,
+    0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
+};
+
+// The table in LDS (static, per workgroup): every kernel that evaluates
+// exp_ref calls exp_tab_init() before its first barrier.
+__shared__ uint64_t g_exptab[32];
+__device__ __forceinline__ void exp_tab_init() {
+  if (threadIdx.x < 32) g_exptab[threadIdx.x] = kExpTab[threadIdx.x];
 }
 
-// 2^d for d <= 0: the terms of the softmax normaliser.  d is clamped to
-// [-125, ...] (NaN and -inf give the clamp), rounded to k = rint(d) by adding
-// and subtracting 1.5*2^23, f = d - k in [-1/2, 1/2], 2^f by a degree-5
-// minimax polynomial (relative error 1.7e-7), and the scaling by 2^k is an
-// integer add of k to the exponent field (exact: the result stays normal).
-// Elements at or below the clamp contribute 2^-125 * 2^f.
-__device__ __forceinline__ float exp2_f(float d) {
-  const float dc = __builtin_fmaxf(d, -125.0f);
-  const float t = dc + 12582912.0f;
-  const float k = t - 12582912.0f;
-  const float f = dc - k;
-  float p = __builtin_fmaf(0x1.5bba14p-10f, f, 0x1.3cea88p-7f);
-  p = __builtin_fmaf(p, f, 0x1.c6b752p-5f);
-  p = __builtin_fmaf(p, f, 0x1.ebf9bcp-3f);
-  p = __builtin_fmaf(p, f, 0x1.62e42ap-1f);
-  p = __builtin_fmaf(p, f, 1.0f);
-  return __uint_as_float(__float_as_uint(p) + (__float_as_uint(t) << 23));
+__device__ __forceinline__ float exp_ref(float x) {
+  const bool live = x >= -0x1.9fe368p6f;  // false for -inf
+  const double xd = live ? (double)x : 0.0;
+  double kd = __builtin_fma(0x1.71547652b82fep+5, xd, 0x1.8p+52);
+  const uint32_t ki = (uint32_t)__double_as_longlong(kd);
+  kd = kd - 0x1.8p+52;
+  const double r = __builtin_fma(0x1.71547652b82fep+5, xd, -kd);
+  // (ki << 47) mod 2^64 touches only the high word: (ki << 15) << 32
+  const uint64_t t = g_exptab[ki & 31u] + ((uint64_t)(ki << 15) << 32);
+  const double s = __longlong_as_double((long long)t);
+  const double z = __builtin_fma(0x1.c6af84b912394p-20, r, 0x1.ebfce50fac4f3p-13);
+  const double r2 = r * r;
+  double y = __builtin_fma(0x1.62e42ff0c52d6p-6, r, 1.0);
+  y = __builtin_fma(z, r2, y);
+  y = y * s;
+  return live ? (float)y : 0.0f;
 }
-
-constexpr float LOG2E_F = 0x1.715476p+0f;
 
 // Order-preserving map float -> u32 (NaN excluded by callers).
 __device__ __forceinline__ uint32_t fkey(float v) {

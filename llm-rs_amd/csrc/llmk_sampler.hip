@@ -82,6 +82,11 @@ constexpr uint32_t SLOW_SLOTS = 512;  // most global scratch slots of the slow p
 constexpr uint32_t SLOW_BINS = 2048; // slow path: bins of the processed logits
 constexpr uint32_t EMPTY = 0xffffffffu;
 constexpr float NEG_INF = -__builtin_huge_valf();
+constexpr float LOG2E_F = 0x1.715476p+0f;  // the slow path's bins of (l - L)/T, in octaves
+
+// Words a workgroup passes from one phase to the next past the dynamic
+// shared memory, which each phase lays out afresh (static LDS).
+__shared__ uint32_t g_bcast[4];
 
 enum : uint32_t { MODE_INVALID = 0, MODE_GREEDY = 1, MODE_SAMPLE = 2 };
 enum : uint32_t { FLAG_OVERFLOW = 1u, FLAG_HIST_OVERFLOW = 2u };
@@ -662,10 +667,12 @@ __device__ __forceinline__ void unpack(const Raw& raw, float v[16]) {
 // Probabilities and the sequential semantics
 // ---------------------------------------------------------------------------
 // p of a (penalised, masked) logit v given the temperature, x_max = m and
-// the normaliser S: sampler.rs:53-70 with exp_m.
+// the normaliser S: sampler.rs:53-70, with glibc's expf (exp_ref).  S is
+// the reference's sequential sum, or 1 on a row that top-k renormalises
+// (where S cancels: p is then e itself).
 __device__ __forceinline__ float prob_of(float v, float T, float m, float S) {
   const float x = (T != 1.0f) ? v / T : v;
-  const float e = (x == NEG_INF) ? 0.0f : exp_m(x - m);
+  const float e = (x == NEG_INF) ? 0.0f : exp_ref(x - m);
   return (S > 0.0f) ? e / S : e;
 }
 
@@ -1254,6 +1261,207 @@ __host__ __device__ inline size_t slow_lds_words(uint32_t V) {
 }
 
 // ---------------------------------------------------------------------------
+// The reference's softmax normaliser, exactly (sampler.rs:56-66)
+// ---------------------------------------------------------------------------
+// Sixteen consecutive logits of a row from e0 (a multiple of 16), as f32;
+// positions past V read -inf.
+template <int DT>
+__device__ __forceinline__ void load16(const void* row, uint32_t e0, uint32_t V, float x[16]) {
+  if (e0 + 16 <= V) {
+    if (DT == LLMK_F32) {
+      const GLB f4v* r = (const GLB f4v*)((const GLB float*)row + e0);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const f4v a = r[k];
+        x[4 * k + 0] = a.x;
+        x[4 * k + 1] = a.y;
+        x[4 * k + 2] = a.z;
+        x[4 * k + 3] = a.w;
+      }
+    } else {
+      const GLB u2v* r = (const GLB u2v*)((const GLB uint16_t*)row + e0);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const u2v a = r[k];
+        x[4 * k + 0] = cvt16<DT>(a.x & 0xffffu);
+        x[4 * k + 1] = cvt16<DT>(a.x >> 16);
+        x[4 * k + 2] = cvt16<DT>(a.y & 0xffffu);
+        x[4 * k + 3] = cvt16<DT>(a.y >> 16);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < 16; ++q) x[q] = e0 + q < V ? load_logit<DT>(row, e0 + q) : NEG_INF;
+  }
+}
+
+// Inclusive scan of the pairs over the wave (shifted-in lanes read the
+// identity (0, 0)).
+__device__ __forceinline__ Par wave_par_incl(Par x) {
+  x = par_then(dpp_par<0x111, 0xf, true>(x), x);
+  x = par_then(dpp_par<0x112, 0xf, true>(x), x);
+  x = par_then(dpp_par<0x114, 0xf, true>(x), x);
+  x = par_then(dpp_par<0x118, 0xf, true>(x), x);
+  x = par_then(dpp_par<0x142, 0xa, false>(x), x);
+  x = par_then(dpp_par<0x143, 0xc, false>(x), x);
+  return x;
+}
+
+// The sequential f32 sum c = ((c + e_0) + e_1) + ... of the NT*16 values of
+// one window (thread t holds window entries 16t .. 16t+15, all >= 0),
+// continued from c and returned, exactly, by the whole workgroup.  The
+// running-sum argument of seq_scan over the block: while c lies in the
+// binade of quantum q = 2^(eb-23), each entry adds the integer r = p/q
+// rounded to nearest (a tie to the even sum), a pair of increments (from an
+// even, from an odd sum) per entry; the pairs of a thread compose in order,
+// the workgroup scans them (waves by DPP, then the sixteen wave totals), and
+// the first entry whose sum would reach 2^(eb+1) is added as one f32
+// addition, after which the scan resumes.  Entries p/q >= 2^25 are clamped
+// (they cross at once); every sum before the first crossing stays below
+// 2^24 + 2^25, so no count wraps where it is read.  A zero c takes the
+// first nonzero entry as it is (0 + p = p).  Each round's first event goes
+// through one of three LDS slots in turn (round it uses slot it % 3 and
+// clears slot (it + 1) % 3, read two rounds ago), so a round needs two
+// barriers; `it` carries the rotation from call to call, and the slots start
+// cleared (exact_normaliser).  sc: 6 + NW*2 words; uniform barriers only.
+__device__ __forceinline__ float block_seq_sum(const float (&e)[16], float c, uint32_t& it,
+                                               LDS uint32_t* sc) {
+  constexpr uint32_t Q = 16, TOP = 1u << 24;
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
+  LDS uint64_t* ev = (LDS uint64_t*)sc;  // [3]: first event (index << 32 | new sum bits)
+  LDS uint32_t* wt = sc + 6;             // [NW][2]: wave totals
+  uint32_t s = 0;                        // entries before s are summed
+  for (;; ++it) {
+    LDS uint64_t* slot = ev + it % 3u;
+    if (tid == 0) ev[(it + 1) % 3u] = ~0ull;
+    if (c == 0.0f) {
+      uint64_t best = ~0ull;
+#pragma unroll
+      for (int q = (int)Q - 1; q >= 0; --q) {
+        const uint32_t j = Q * tid + (uint32_t)q;
+        if (j >= s && e[q] != 0.0f) best = ((uint64_t)j << 32) | __float_as_uint(e[q]);
+      }
+      if (best != ~0ull) __atomic_fetch_min(slot, best, __ATOMIC_RELAXED);
+      __syncthreads();
+      const uint64_t r = *slot;
+      if (r == ~0ull) {  // every remaining entry is 0
+        ++it;
+        return 0.0f;
+      }
+      c = __uint_as_float((uint32_t)r);
+      s = (uint32_t)(r >> 32) + 1u;
+      if (s >= NT * Q) {
+        ++it;
+        return c;
+      }
+      continue;
+    }
+    const uint32_t cb = __float_as_uint(c);
+    const int eb = (int)umax((cb >> 23) & 255u, 1u) - 127;
+    const uint32_t C = (uint32_t)__builtin_ldexpf(c, 23 - eb);
+    uint32_t r[Q], tie = 0;
+#pragma unroll
+    for (uint32_t q = 0; q < Q; ++q) {
+      const float x = __builtin_fminf(__builtin_ldexpf(e[q], 23 - eb), 0x1p25f);  // exact below the clamp
+      const float k = __builtin_floorf(x);
+      const float fr = x - k;
+      const uint32_t ki = (uint32_t)k;
+      const bool live = Q * tid + q >= s;
+      r[q] = !live ? 0u : (fr > 0.5f ? ki + 1u : ki);
+      if (live && fr == 0.5f) tie |= 1u << q;
+    }
+    uint32_t s0 = 0, s1 = 1;
+#pragma unroll
+    for (uint32_t q = 0; q < Q; ++q) {
+      const uint32_t t = (tie >> q) & 1u;
+      s0 += r[q] + (t & ((s0 ^ r[q]) & 1u));
+      s1 += r[q] + (t & ((s1 ^ r[q]) & 1u));
+    }
+    const Par own{s0, s1 - 1u};
+    const Par inc = wave_par_incl(own);
+    if (lane == 63) {
+      wt[2 * wv] = inc.a0;
+      wt[2 * wv + 1] = inc.a1;
+    }
+    Par ex = dpp_par<0x138, 0xf, true>(inc);  // wave_shr:1, lane 0 reads (0, 0)
+    __syncthreads();
+    Par pre{0u, 0u}, tot{0u, 0u};
+#pragma unroll
+    for (uint32_t i = 0; i < NW; ++i) {
+      const Par wtot{wt[2 * i], wt[2 * i + 1]};
+      if (i < wv) pre = par_then(pre, wtot);
+      tot = par_then(tot, wtot);
+    }
+    ex = par_then(pre, ex);
+    uint32_t cur = C + ((C & 1u) ? ex.a1 : ex.a0);
+    uint64_t cand = ~0ull;
+#pragma unroll
+    for (uint32_t q = 0; q < Q; ++q) {
+      const uint32_t t = (tie >> q) & 1u;
+      const uint32_t nx = cur + r[q] + (t & ((cur ^ r[q]) & 1u));
+      if (cand == ~0ull && Q * tid + q >= s && nx >= TOP) {
+        // the addition that leaves the binade, as one f32 addition
+        const float before = __builtin_ldexpf((float)cur, eb - 23);
+        cand = ((uint64_t)(Q * tid + q) << 32) | __float_as_uint(before + e[q]);
+      }
+      cur = nx;
+    }
+    if (cand != ~0ull) __atomic_fetch_min(slot, cand, __ATOMIC_RELAXED);
+    __syncthreads();
+    const uint64_t res = *slot;
+    if (res == ~0ull) {
+      ++it;
+      return __builtin_ldexpf((float)(C + ((C & 1u) ? tot.a1 : tot.a0)), eb - 23);
+    }
+    c = __uint_as_float((uint32_t)res);
+    s = (uint32_t)(res >> 32) + 1u;
+    if (s >= NT * Q) {
+      ++it;
+      return c;
+    }
+  }
+}
+
+// S = the sequential f32 sum in index order of e_i = exp_ref(fl(l_i - m))
+// (0 for l_i = -inf), l_i = fl(v_i / T) the processed logit (penalties from
+// the history tables h if have_hist, the allow-mask, NaN read as -inf)
+// divided by T (sampler.rs:53, :57-66).  The whole workgroup, windows of
+// NT*16 consecutive elements; sc: 64 words of scratch.
+template <int DT>
+__device__ __forceinline__ float exact_normaliser(const Args& a, uint32_t b, const RowP& P,
+                                                  float m, const Hist& h, bool have_hist,
+                                                  LDS uint32_t* sc) {
+  const uint32_t tid = threadIdx.x, V = a.V;
+  const void* row = (const char*)a.logits + (uint64_t)b * a.stride * (DT == LLMK_F32 ? 4u : 2u);
+  const GLB uint32_t* mrow = a.mask ? G(a.mask) + (uint64_t)b * a.mask_words : nullptr;
+  constexpr uint32_t Q = 16, W = NT * Q;
+  if (tid < 3) ((LDS uint64_t*)sc)[tid] = ~0ull;
+  __syncthreads();
+  uint32_t it = 0;
+  float c = 0.0f;
+  for (uint32_t w0 = 0; w0 < V; w0 += W) {
+    const uint32_t e0 = w0 + Q * tid;
+    float v[Q];
+    load16<DT>(row, e0, V, v);
+    // the sixteen lie in one 32-bit word of the mask and of the bitmap
+    const uint32_t mw = (mrow && e0 < V) ? mrow[e0 >> 5] >> (e0 & 16u) : 0xffffffffu;
+    const uint32_t hw = (have_hist && e0 < V) ? h.bitmap[(e0 - h.lo) >> 5] >> (e0 & 16u) : 0u;
+    float e[Q];
+#pragma unroll
+    for (uint32_t q = 0; q < Q; ++q) {
+      float x = v[q];
+      if ((hw >> q) & 1u) x = h.pen[h.rank(e0 + q)];  // a kept rank (< U_MAX)
+      if (!((mw >> q) & 1u) || !(x > NEG_INF)) x = NEG_INF;
+      const float l = (P.T != 1.0f) ? x / P.T : x;
+      e[q] = (l == NEG_INF) ? 0.0f : exp_ref(l - m);
+    }
+    c = block_seq_sum(e, c, it, sc);
+  }
+  __syncthreads();  // the caller may reuse sc
+  return c;
+}
+
+// ---------------------------------------------------------------------------
 // Slow path (one workgroup, one row)
 // ---------------------------------------------------------------------------
 // Eight consecutive logits of a row from e0 (zeros past V).
@@ -1392,8 +1600,10 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
   if (wv == 0) {
     constexpr uint32_t PER = SLOW_BINS / WAVE;
     const bool topk = P.K > 0 && (uint32_t)P.K < V;
+    // the mass rule reads p = e / S, which needs the row's S: rows that top-k
+    // renormalises (S = 1) choose by count alone
     const float tm = (P.top_p < 1.0f ? P.top_p : u) + 0.002f;
-    const bool use_mass = tm < 1.0f && S > 0.0f;
+    const bool use_mass = !topk && tm < 1.0f && S > 0.0f;
     uint32_t cnt = 0;
     float mass = 0.0f;
     for (uint32_t k = 0; k < PER; ++k) {
@@ -2270,6 +2480,14 @@ __device__ __forceinline__ uint32_t candidate_fast(const Args& a, uint32_t b, co
 // seg_own: for a single-segment row, this workgroup's (count, beta, flags);
 // u: the row's uniform (loaded with the parameters, so that no global load
 // is outstanding at the finalize's barriers).
+//
+// The normaliser S: 1 on a row that top-k renormalises (0 < top_k < V,
+// sampler.rs:80-89: every probability is divided by the top-k sum before
+// any step reads it, so S cancels and none is computed), 0 for a row whose
+// logits are all -inf, else the reference's own sequential f32 sum in index
+// order (exact_normaliser; sampler.rs:66).  A single-segment row still holds
+// the whole row's history tables from its stream phase; a row of several
+// segments rebuilds them first.
 template <int DT>
 __device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_t b,
                                              const RowP& P, bool have_vt, u4v seg_own,
@@ -2278,40 +2496,20 @@ __device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_
   const int lane = (int)(tid & 63), wv = (int)(tid >> 6);
   const FinLds f = fin_carve(smem);
   const uint32_t nslots = a.ntiles + (have_vt ? a.nchunks : 0u);
-  uint32_t path = 2;  // 0 done, 1 workgroup candidate path, 2 slow path, 3 fast path
+  // ---- wave 0: the row maximum L (and the greedy token)
   if (wv == 0) {
-    // ---- partials: row maximum L, then the normaliser S as balanced trees
-    // of 64 slots and a tree over those (next_pow2(slots) >= 64, padding 0)
     const GLB f2v* part = G(w.tile_part) + (uint64_t)b * MAX_SLOTS;
     LDS const f2v* lpart = (LDS const f2v*)(smem + a.lds_part);
     float L = NEG_INF;
-    if (a.G == 1 && nslots <= 256) {
-      f2v q[4];
-#pragma unroll
-      for (uint32_t k = 0; k < 4; ++k) {
-        const uint32_t c = 64 * k + (uint32_t)lane;
-        q[k] = c < nslots ? lpart[c] : f2v{NEG_INF, 0.0f};
-      }
-#pragma unroll
-      for (uint32_t k = 0; k < 4; ++k) {
-        const uint32_t c = 64 * k + (uint32_t)lane;
-        if (c < nslots) {
-          f.tl[c] = q[k].x;
-          f.ts[c] = q[k].y;
-        }
-        L = fmaxf(L, q[k].x);
-      }
-    } else {
+    if (P.mode == MODE_GREEDY) {
       for (uint32_t c = (uint32_t)lane; c < nslots; c += WAVE) {
         const f2v q = a.G == 1 ? lpart[c] : part[c];
         f.tl[c] = q.x;
         f.ts[c] = q.y;
         L = fmaxf(L, q.x);
       }
-    }
-    L = wave_max(L);
-    WaveSync::sync();
-    if (P.mode == MODE_GREEDY) {
+      L = wave_max(L);
+      WaveSync::sync();
       // sampler.rs:40-50: the first index holding the maximum
       uint32_t bi = EMPTY;
       for (uint32_t c = (uint32_t)lane; c < nslots; c += WAVE)
@@ -2326,80 +2524,81 @@ __device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_
           if (a.out_probs) G(a.out_probs)[(uint64_t)b * a.out_cap] = 1.0f;
         }
       }
-      path = 0;
     } else {
-      const float c2 = LOG2E_F / P.T;
-      uint32_t ntp = 64;
-      while (ntp < nslots) ntp <<= 1;
-      const uint32_t nblk = ntp / 64;
-      float bsum = 0.0f;  // lane k: the tree of block k
-      if (nblk <= 4) {
-        // up to four blocks at once: the reads, the terms and the four trees
-        // are independent
-        float x[4];
-#pragma unroll
-        for (uint32_t k = 0; k < 4; ++k) {
-          const uint32_t c = 64 * k + (uint32_t)lane;
-          const bool in = k < nblk && c < nslots;
-          const float tl = in ? f.tl[c] : 0.0f, ts = in ? f.ts[c] : 0.0f;
-          x[k] = (in && L != NEG_INF) ? ts * exp2_f((tl - L) * c2) : 0.0f;
-        }
-#pragma unroll
-        for (uint32_t k = 0; k < 4; ++k) {
-          const float t = wave_tree_sum(x[k]);
-          if ((uint32_t)lane == k) bsum = t;
-        }
-      } else {
-        for (uint32_t k = 0; k < nblk; ++k) {
-          const uint32_t c = 64 * k + (uint32_t)lane;
-          float x = 0.0f;
-          if (c < nslots && L != NEG_INF) x = f.ts[c] * exp2_f((f.tl[c] - L) * c2);
-          x = wave_tree_sum(x);
-          if ((uint32_t)lane == k) bsum = x;
-        }
-      }
-      const float S = (L != NEG_INF) ? wave_tree_sum(bsum) : 0.0f;
-      const float m = (P.T != 1.0f) ? L / P.T : L;
-      // ---- segment table: counts, thresholds, flags
-      uint32_t cnt = 0, beta = 0, flg = 0;
-      if (a.G == 1) {
-        if (lane == 0) {
-          cnt = seg_own.x < CAND_CAP ? seg_own.x : CAND_CAP;
-          beta = seg_own.y;
-          flg = seg_own.z;
-        }
-      } else if ((uint32_t)lane < a.G) {
-        const u4v sm = G(w.seg_meta)[row_seg_to_wg(a, b, (uint32_t)lane)];
-        cnt = sm.x < CAND_CAP ? sm.x : CAND_CAP;
-        beta = sm.y;
-        flg = sm.z;
-      }
-      const uint32_t lam = wave_max_u32(beta << BIN_SHIFT);
-      const bool ovf = __ballot((flg & FLAG_OVERFLOW) != 0) != 0;
-      const uint32_t off_incl = wave_incl_scan(cnt);
-      const uint32_t total = bcast63u(off_incl);
-      if ((uint32_t)lane <= a.G) f.soff[lane] = off_incl - cnt;  // lane G: the total
-      WaveSync::sync();
-      // the bound on p of every element outside the candidate buffers, once
-      // (wave 0) rather than in every thread of the candidate path
-      const float plim = lam > 0x007fffffu ? prob_of(funkey(lam - 1), P.T, m, S) : 0.0f;
-      if (lane == 0) {
-        f.fm[F_S] = __float_as_uint(S);
-        f.fm[F_M] = __float_as_uint(m);
-        f.fm[F_L] = __float_as_uint(L);
-        f.fm[F_PLIM] = __float_as_uint(plim);
-        f.fm[F_TOTAL] = total;
-        f.fm[F_LAM] = lam;
-      }
-      if (!(L == NEG_INF || P.Kc == 0 || ovf))
-        path = (a.G == 1 && total <= LCAP) ? 3u : 1u;
+      for (uint32_t c = (uint32_t)lane; c < nslots; c += WAVE)
+        L = fmaxf(L, a.G == 1 ? lpart[c].x : part[c].x);
+      L = wave_max(L);
     }
+    if (lane == 0) g_bcast[0] = __float_as_uint(L);
+  }
+  __syncthreads();
+  if (P.mode == MODE_GREEDY) return;
+  const float L = __uint_as_float(g_bcast[0]);
+  const float m = (P.T != 1.0f) ? L / P.T : L;
+  const bool topk = P.K > 0 && (uint32_t)P.K < a.V;
+  float S = 1.0f;
+  if (L == NEG_INF) {
+    S = 0.0f;
+  } else if (!topk) {
+    Hist h;
+    bool have_hist = have_vt;
+    LDS uint32_t* sc = smem;  // below the tables in both layouts
+    if (a.G == 1) {
+      // the stream phase's tables: the stream layout's history words
+      hist_carve(h, smem + 64 + M_NMISC + NBINS + 64, a.ntiles * 32);
+      h.lo = 0;
+    } else {
+      LDS uint32_t* hb = smem + 128 + 256 + NW * 256 + SLOW_BINS;  // the slow path's layout
+      const uint32_t nwords = (a.V + 31) / 32;
+      hist_carve(h, hb, nwords);
+      h.lo = 0;
+      if (tid == 0) sc[64] = 0;
+      const void* row = (const char*)a.logits +
+                        (uint64_t)b * a.stride * (DT == LLMK_F32 ? 4u : 2u);
+      build_history<DT>(a, P, b, row, 0, a.V, nwords, h, sc + 128, &sc[64]);
+      have_hist = true;  // built (empty when the row has no penalised history)
+    }
+    S = exact_normaliser<DT>(a, b, P, m, h, have_hist, sc);
+  }
+  uint32_t path = 2;  // 0 done, 1 workgroup candidate path, 2 slow path, 3 fast path
+  if (wv == 0) {
+    // ---- segment table: counts, thresholds, flags
+    uint32_t cnt = 0, beta = 0, flg = 0;
+    if (a.G == 1) {
+      if (lane == 0) {
+        cnt = seg_own.x < CAND_CAP ? seg_own.x : CAND_CAP;
+        beta = seg_own.y;
+        flg = seg_own.z;
+      }
+    } else if ((uint32_t)lane < a.G) {
+      const u4v sm = G(w.seg_meta)[row_seg_to_wg(a, b, (uint32_t)lane)];
+      cnt = sm.x < CAND_CAP ? sm.x : CAND_CAP;
+      beta = sm.y;
+      flg = sm.z;
+    }
+    const uint32_t lam = wave_max_u32(beta << BIN_SHIFT);
+    const bool ovf = __ballot((flg & FLAG_OVERFLOW) != 0) != 0;
+    const uint32_t off_incl = wave_incl_scan(cnt);
+    const uint32_t total = bcast63u(off_incl);
+    if ((uint32_t)lane <= a.G) f.soff[lane] = off_incl - cnt;  // lane G: the total
+    WaveSync::sync();
+    // the bound on p of every element outside the candidate buffers, once
+    // (wave 0) rather than in every thread of the candidate path
+    const float plim = lam > 0x007fffffu ? prob_of(funkey(lam - 1), P.T, m, S) : 0.0f;
+    if (lane == 0) {
+      f.fm[F_S] = __float_as_uint(S);
+      f.fm[F_M] = __float_as_uint(m);
+      f.fm[F_L] = __float_as_uint(L);
+      f.fm[F_PLIM] = __float_as_uint(plim);
+      f.fm[F_TOTAL] = total;
+      f.fm[F_LAM] = lam;
+    }
+    if (!(L == NEG_INF || P.Kc == 0 || ovf))
+      path = (a.G == 1 && total <= LCAP) ? 3u : 1u;
     if (lane == 0) f.fm[F_DONE] = path;
   }
   __syncthreads();
   path = f.fm[F_DONE];
-  if (path == 0) return;
-  const float S = __uint_as_float(f.fm[F_S]), m = __uint_as_float(f.fm[F_M]);
   if (path == 3) {
     path = candidate_fast(a, b, P, S, m, u, f.fm[F_TOTAL], f.fm[F_LAM], f);
     if (path == 0) return;
@@ -2410,7 +2609,6 @@ __device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_
     path = candidate_path<BlockSync>(a, w, b, P, S, m, u, total, lam, f, EMPTY, SORT_CAP);
     if (path == 0) return;
   }
-  const float L = __uint_as_float(f.fm[F_L]);
   __syncthreads();
   slow_row<DT>(a, w, b, P, S, m, L, smem);
 }
@@ -2420,7 +2618,6 @@ __device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_
 // ---------------------------------------------------------------------------
 struct TileEnv {
   RowP P;
-  float c2;
   uint32_t V;
   bool collect;
   uint32_t recompute_at;
@@ -2475,27 +2672,7 @@ __device__ __forceinline__ void tile_reduce(const TileEnv& E, const float (&v)[1
     if (lane == 0) put_part(E, slot, f2v{lm, __uint_as_float(bi)});
     return;
   }
-  float s = 0.0f;
-  if (lm != NEG_INF) {
-    // per lane: ((run0 + run1) + (run2 + run3)), each run ((e0+e1)+(e2+e3));
-    // then a balanced tree over the 64 lanes
-    const float nb = -(lm * E.c2);
-    float sr[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      if ((uint32_t)r >= nr) {
-        sr[r] = 0x1p-123f;
-        continue;
-      }
-      const float e0 = exp2_f(__builtin_fmaf(v[4 * r + 0], E.c2, nb));
-      const float e1 = exp2_f(__builtin_fmaf(v[4 * r + 1], E.c2, nb));
-      const float e2 = exp2_f(__builtin_fmaf(v[4 * r + 2], E.c2, nb));
-      const float e3 = exp2_f(__builtin_fmaf(v[4 * r + 3], E.c2, nb));
-      sr[r] = (e0 + e1) + (e2 + e3);
-    }
-    s = wave_tree_sum((sr[0] + sr[1]) + (sr[2] + sr[3]));
-  }
-  if (lane == 0) put_part(E, slot, f2v{lm, s});
+  if (lane == 0) put_part(E, slot, f2v{lm, 0.0f});
   if (!E.collect) return;
   // ---- candidates above the rising histogram threshold
   uint32_t beta = __atomic_load_n(&E.misc[M_BETA], __ATOMIC_RELAXED);
@@ -2650,22 +2827,7 @@ __device__ __forceinline__ void vtile_chunk(const Args& a, uint32_t t0, uint32_t
     if (lane == 0) put_part(E, slot, f2v{lm, __uint_as_float(bi)});
     return;
   }
-  float s = 0.0f;
-  if (lm != NEG_INF) {
-    const float nbias = -(lm * E.c2);
-    float acc = 0.0f;
-    uint32_t r = (uint32_t)lane;
-    for (; r + 192u < n; r += 256u) {
-      const float y0 = pen[r], y1 = pen[r + 64u], y2 = pen[r + 128u], y3 = pen[r + 192u];
-      acc = acc + exp2_f(__builtin_fmaf(y0, E.c2, nbias));
-      acc = acc + exp2_f(__builtin_fmaf(y1, E.c2, nbias));
-      acc = acc + exp2_f(__builtin_fmaf(y2, E.c2, nbias));
-      acc = acc + exp2_f(__builtin_fmaf(y3, E.c2, nbias));
-    }
-    for (; r < n; r += 64u) acc = acc + exp2_f(__builtin_fmaf(pen[r], E.c2, nbias));
-    s = wave_tree_sum(acc);
-  }
-  if (lane == 0) put_part(E, slot, f2v{lm, s});
+  if (lane == 0) put_part(E, slot, f2v{lm, 0.0f});
   if (!E.collect || lm == NEG_INF) return;
   // ---- candidates: the chunk's history tokens at or above the threshold
   const float th = theta_of(__atomic_load_n(&E.misc[M_BETA], __ATOMIC_RELAXED));
@@ -2748,7 +2910,6 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   // before the tiles are requested (behind them they take microseconds).
   TileEnv E;
   E.P = P;
-  E.c2 = LOG2E_F / P.T;
   E.V = a.V;
   E.collect = collect;
   E.recompute_at = P.Kc / 4 > 8 ? P.Kc / 4 : 8;
@@ -2780,6 +2941,7 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
     if (tid < 64) hcoarse[tid] = 0;
   }
   if (tid < M_NMISC) misc[tid] = 0;
+  exp_tab_init();
   if (have) {
     for (uint32_t i = tid; i < nwords; i += NT) h.bitmap[i] = 0;
     if (need_cnt)
@@ -3146,6 +3308,8 @@ __global__ __launch_bounds__(NT) void topp_mask_kernel(float* logits, uint32_t V
   const uint32_t tid = threadIdx.x;
   const int lane = (int)(tid & 63);
   float* row = logits + (uint64_t)b * stride;
+  exp_tab_init();
+  __syncthreads();
   if (tid < WAVE) {
     const float tp = G(top_p)[b];
     const u4v r = G(cut)[b];
@@ -3283,6 +3447,10 @@ extern "C" const char* llmk_last_error(void) { return g_last_error.c_str(); }
 
 static size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+// Dynamic LDS of one workgroup: the CU's 160 KiB less the kernels' static
+// tables (the expf table and the phase words, under 512 bytes).
+static constexpr size_t LDS_DYN_MAX = 160 * 1024 - 512;
+
 extern "C" int llmk_sampler_create(llmk_sampler** out, int device,
                                    uint32_t max_batch, uint32_t max_vocab) {
   if (!out) return fail(LLMK_ERR_INVALID_ARGUMENT, "out is NULL");
@@ -3291,16 +3459,16 @@ extern "C" int llmk_sampler_create(llmk_sampler** out, int device,
     return fail(LLMK_ERR_INVALID_ARGUMENT, "max_batch and max_vocab must be > 0");
   if (max_vocab > MAX_TILES * TILE)
     return fail(LLMK_ERR_CAPACITY, "max_vocab above 2^20");
-  if (4 * slow_lds_words(max_vocab) > 160 * 1024)
+  if (4 * slow_lds_words(max_vocab) > LDS_DYN_MAX)
     return fail(LLMK_ERR_CAPACITY, "max_vocab too large for the slow path's LDS tables");
   HIPCHK(hipSetDevice(device));
   // Dynamic LDS above 64 KiB must be allowed explicitly.
   HIPCHK(hipFuncSetAttribute((const void*)stream_kernel<LLMK_F32>,
-                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+                             hipFuncAttributeMaxDynamicSharedMemorySize, LDS_DYN_MAX));
   HIPCHK(hipFuncSetAttribute((const void*)stream_kernel<LLMK_BF16>,
-                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+                             hipFuncAttributeMaxDynamicSharedMemorySize, LDS_DYN_MAX));
   HIPCHK(hipFuncSetAttribute((const void*)stream_kernel<LLMK_F16>,
-                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+                             hipFuncAttributeMaxDynamicSharedMemorySize, LDS_DYN_MAX));
   HIPCHK(hipFuncSetAttribute((const void*)topk_mask_kernel,
                              hipFuncAttributeMaxDynamicSharedMemorySize, 4 * MK_LDS_WORDS));
   const uint32_t pool = max_batch > MAX_WGS ? max_batch : MAX_WGS;
@@ -3459,7 +3627,7 @@ static int sample_batch_impl(llmk_sampler* s, const llmk_sample_batch_args* in,
   if (a.G == 1) words = a.lds_cand + 2 * LCAP;
   if (slow_lds_words(a.V) > words) words = slow_lds_words(a.V);
   const size_t lds = 4 * words;
-  if (lds > 160 * 1024)
+  if (lds > LDS_DYN_MAX)
     return fail(LLMK_ERR_CAPACITY, "vocabulary too large for one workgroup's LDS tables");
   const dim3 grid(a.B * a.G), block(NT);
   if (a.dtype == LLMK_F32)

@@ -22,179 +22,67 @@
 #include <stdlib.h>
 #include <string.h>
 
-#define TILE 1024u
-
 /* ------------------------------------------------------------------------ */
 /* Numerics                                                                  */
 /* ------------------------------------------------------------------------ */
 
-/* ln 2 split for Cody–Waite reduction (hi has 32 significant bits), 1/ln 2,
- * and 1/n! for the degree-13 Taylor polynomial of e^r on |r| <= ln2/2
- * (truncation error < 5e-18 relative).  Derived in oracle/gen_constants.py. */
-static const double LN2_HI = 0x1.62e42fee00000p-1;
-static const double LN2_LO = 0x1.a39ef35793c76p-33;
-static const double INV_LN2 = 0x1.71547652b82fep+0;
-static const double INV_FACT[14] = {
-    0x1.0000000000000p+0, 0x1.0000000000000p+0, 0x1.0000000000000p-1,
-    0x1.5555555555555p-3, 0x1.5555555555555p-5, 0x1.1111111111111p-7,
-    0x1.6c16c16c16c17p-10, 0x1.a01a01a01a01ap-13, 0x1.a01a01a01a01ap-16,
-    0x1.71de3a556c734p-19, 0x1.27e4fb7789f5cp-22, 0x1.ae64567f544e4p-26,
-    0x1.1eed8eff8d898p-29, 0x1.6124613a86d09p-33};
+/* e^x as glibc's expf computes it (glibc >= 2.28, sysdeps/ieee754/flt-32/
+ * e_expf.c, the ARM optimized-routines method by Szabolcs Nagy): x*32/ln2 =
+ * k + r with k the nearest integer (ties to even), 2^(k/32) from a table of
+ * 2^(i/32) (the exponent of 2^(k>>5) added to its bits), 2^(r/32) by a cubic,
+ * all in double, one rounding to float.  The x86-64 build that Rust's
+ * f32::exp reaches on this platform (the FMA variant) fuses the two
+ * reduction steps kd = x*InvLn2N + SHIFT and r = x*InvLn2N - kd; written out
+ * with fma() here.  EXP_TAB[i] = bits(2^(i/32)) - (i << 47), 2^(i/32)
+ * correctly rounded (oracle/gen_constants.py recomputes it); the cubic's
+ * coefficients are glibc's published exp2f_data poly, scaled by 32^-3,
+ * 32^-2, 32^-1.  tests/test_oracle_math.py checks every float in [-104, 0]
+ * against the host's expf.  Inputs below -0x1.9fe368p6 (where e^x rounds
+ * to 0) and -inf give +0. */
+static const uint64_t EXP_TAB[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull,
+    0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull,
+    0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull,
+    0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull,
+    0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull,
+    0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull,
+    0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull,
+    0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full,
+    0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
+};
+static const double EXP_C0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
+static const double EXP_C1 = 0x1.ebfce50fac4f3p-3 / 32 / 32;
+static const double EXP_C2 = 0x1.62e42ff0c52d6p-1 / 32;
+static const double EXP_INVLN2N = 0x1.71547652b82fep+0 * 32;
+static const double EXP_SHIFT = 0x1.8p+52;
 
-/* 2^f on [-1/2, 1/2], constant term 1, degree 5, minimax relative error
- * 1.7e-7 after fp32 rounding of the coefficients (gen_constants.py). */
-static const float E2C1 = 0x1.62e42ap-1f;
-static const float E2C2 = 0x1.ebf9bcp-3f;
-static const float E2C3 = 0x1.c6b752p-5f;
-static const float E2C4 = 0x1.3cea88p-7f;
-static const float E2C5 = 0x1.5bba14p-10f;
-static const float LOG2E_F = 0x1.715476p+0f;
-
-float llmk_oracle_exp_m(float y) {
-  /* e^y evaluated in double, rounded once to float.  Below -110 the result
-   * is far under the smallest subnormal (2^-149 ~ e^-103.3). */
-  if (!(y >= -110.0f)) return 0.0f;
-  double yd = (double)y;
-  double kd = rint(yd * INV_LN2);
-  double r = fma(-kd, LN2_HI, yd);
-  r = fma(-kd, LN2_LO, r);
-  double p = INV_FACT[13];
-  for (int n = 12; n >= 0; --n) p = fma(p, r, INV_FACT[n]);
-  return (float)ldexp(p, (int)kd);
-}
-
-float llmk_oracle_exp2_f(float d) {
-  /* Terms of the softmax normaliser: 2^d for d <= 0.  d is clamped at -125
-   * (fmaxf also maps NaN there), k = rint(d) through +/- 1.5*2^23, f = d - k,
-   * degree-5 polynomial for 2^f, exact scaling by adding k to the exponent
-   * bits. */
-  const float dc = fmaxf(d, -125.0f);
-  const float t = dc + 12582912.0f;
-  const float k = t - 12582912.0f;
-  const float f = dc - k;
-  float p = fmaf(E2C5, f, E2C4);
-  p = fmaf(p, f, E2C3);
-  p = fmaf(p, f, E2C2);
-  p = fmaf(p, f, E2C1);
-  p = fmaf(p, f, 1.0f);
-  uint32_t pb, tb;
-  memcpy(&pb, &p, 4);
-  memcpy(&tb, &t, 4);
-  const uint32_t rb = pb + (tb << 23);
-  float r;
-  memcpy(&r, &rb, 4);
-  return r;
+float llmk_oracle_exp_ref(float x) {
+  if (!(x >= -0x1.9fe368p6f)) return 0.0f;
+  const double xd = (double)x;
+  double kd = fma(EXP_INVLN2N, xd, EXP_SHIFT);
+  uint64_t ki;
+  memcpy(&ki, &kd, 8);
+  kd -= EXP_SHIFT;
+  const double r = fma(EXP_INVLN2N, xd, -kd);
+  const uint64_t t = EXP_TAB[ki % 32] + (ki << 47);
+  double s;
+  memcpy(&s, &t, 8);
+  const double z = fma(EXP_C0, r, EXP_C1);
+  const double r2 = r * r;
+  double y = fma(EXP_C2, r, 1.0);
+  y = fma(z, r2, y);
+  y = y * s;
+  return (float)y;
 }
 
 float llmk_oracle_libm_expf(float y) { return expf(y); }
-
-static void tree_sum_inplace(float* buf, uint32_t len) {
-  /* Balanced pairwise tree over contiguous indices: node = left + right. */
-  for (; len > 1; len >>= 1)
-    for (uint32_t i = 0; i < len / 2; ++i) buf[i] = buf[2 * i] + buf[2 * i + 1];
-}
-
-/* Partial of one 1024-value tile x[0..1023] (excluded positions already
- * -inf): its max lc and, relative to lc, the tree sum of the 2^ terms. */
-static void tile_partial(const float* x, float c2, float* lc_out, float* s_out) {
-  float m = -INFINITY;
-  for (uint32_t i = 0; i < TILE; ++i)
-    if (x[i] > m) m = x[i];
-  *lc_out = m;
-  if (m == -INFINITY) {
-    *s_out = 0.0f;
-    return;
-  }
-  const float nb = -(m * c2);
-  float lanes[64];
-  for (uint32_t L = 0; L < 64; ++L) {
-    float run[4];
-    for (uint32_t r = 0; r < 4; ++r) {
-      float e[4];
-      for (uint32_t q = 0; q < 4; ++q)
-        e[q] = llmk_oracle_exp2_f(fmaf(x[256 * r + 4 * L + q], c2, nb));
-      run[r] = (e[0] + e[1]) + (e[2] + e[3]);
-    }
-    lanes[L] = (run[0] + run[1]) + (run[2] + run[3]);
-  }
-  tree_sum_inplace(lanes, 64);
-  *s_out = lanes[0];
-}
-
-float llmk_oracle_normalizer(const float* lp, const uint8_t* is_hist, uint32_t V,
-                             float temperature) {
-  /* Two-level log-sum-exp over fixed partial slots.
-   *   c2 = fl(log2(e) / T).
-   *   Real tile c (1024 tokens; positions past V and history tokens count
-   *   as -inf): lc = max; if lc = -inf the sum is 0, else with
-   *   nb = -fl(lc*c2) each position gives e = exp2_f(fma(x, c2, nb));
-   *   position 256r + 4L + q belongs to lane L, run r; a run sums
-   *   ((e0+e1)+(e2+e3)), a lane ((run0+run1)+(run2+run3)), the tile is the
-   *   balanced tree over the 64 lanes.
-   *   Virtual tile k holds the history tokens of chunk k (16 real tiles,
-   *   tokens 16384k ..): lc = their max (-inf if none, sum 0); numbered
-   *   0, 1, 2, ... in increasing token order, token j goes to lane j mod 64,
-   *   which sums its terms exp2_f(fma(x, c2, nb)) sequentially in that
-   *   order (0 if none); the tile is the balanced tree over the 64 lanes.
-   *   Slots: real tiles 0..nt-1, then virtual tile k at nt + k.  Row:
-   *   L = max lc; S = balanced tree over the next power of two >= slots of
-   *   s_c * exp2_f((lc_c - L)*c2) (padding 0).
-   * Mathematically S = sum_i e^{(lp_i - L)/T}, the reference's softmax
-   * denominator (sampler.rs:57-66); the order of operations is fixed. */
-  const float c2 = LOG2E_F / temperature;
-  const uint32_t nt = (V + TILE - 1) / TILE;
-  const uint32_t nch = (nt + 15) / 16;
-  const uint32_t P = nt + nch;
-  uint32_t ntp = 1;
-  while (ntp < P) ntp <<= 1;
-  float* lc = (float*)malloc(sizeof(float) * P);
-  float* w = (float*)calloc(ntp, sizeof(float));
-  float buf[TILE];
-  for (uint32_t c = 0; c < nt; ++c) {
-    for (uint32_t i = 0; i < TILE; ++i) {
-      const uint32_t e = c * TILE + i;
-      buf[i] = (e < V && !(is_hist && is_hist[e])) ? lp[e] : -INFINITY;
-    }
-    tile_partial(buf, c2, &lc[c], &w[c]);
-  }
-  for (uint32_t k = 0; k < nch; ++k) {
-    const uint32_t slot = nt + k;
-    const uint32_t lo = k * 16 * TILE;
-    const uint32_t hi = (lo + 16 * TILE < V) ? lo + 16 * TILE : V;
-    float m = -INFINITY;
-    if (is_hist)
-      for (uint32_t e = lo; e < hi; ++e)
-        if (is_hist[e] && lp[e] > m) m = lp[e];
-    lc[slot] = m;
-    if (m == -INFINITY) {
-      w[slot] = 0.0f;
-      continue;
-    }
-    const float nb = -(m * c2);
-    float lanes[64] = {0.0f};
-    uint32_t j = 0;
-    for (uint32_t e = lo; e < hi; ++e)
-      if (is_hist[e]) {
-        lanes[j & 63] = lanes[j & 63] + llmk_oracle_exp2_f(fmaf(lp[e], c2, nb));
-        ++j;
-      }
-    tree_sum_inplace(lanes, 64);
-    w[slot] = lanes[0];
-  }
-  float L = -INFINITY;
-  for (uint32_t c = 0; c < P; ++c)
-    if (lc[c] > L) L = lc[c];
-  float S = 0.0f;
-  if (L != -INFINITY) {
-    for (uint32_t c = 0; c < P; ++c)
-      w[c] = w[c] * llmk_oracle_exp2_f((lc[c] - L) * c2);
-    tree_sum_inplace(w, ntp);
-    S = w[0];
-  }
-  free(lc);
-  free(w);
-  return S;
-}
 
 /* ------------------------------------------------------------------------ */
 /* Sorting helpers (in-place introsort on u64 / u32 keys, ascending)         */
@@ -483,36 +371,26 @@ int llmk_oracle_sample_row(int mode, const float* logits, uint32_t V,
     return 0;
   }
 
-  /* The mirror normaliser works on the penalised, masked, unscaled logits;
-   * when a penalty is on, the distinct in-vocabulary history tokens sit in
-   * its virtual tiles. */
-  float S_mirror = 0.0f;
-  if (mode == LLMK_ORACLE_MIRROR) {
-    uint8_t* is_hist = NULL;
-    if (H > 0 && (prm->repetition_penalty != 1.0f || prm->presence_penalty != 0.0f ||
-                  prm->frequency_penalty != 0.0f)) {
-      is_hist = (uint8_t*)calloc(V, 1);
-      for (uint32_t i = 0; i < H; ++i)
-        if (hist[i] < V) is_hist[hist[i]] = 1;
-    }
-    S_mirror = llmk_oracle_normalizer(l, is_hist, V, prm->temperature);
-    free(is_hist);
-  }
-
   apply_temperature(l, V, prm->temperature); /* :53 */
 
-  /* Softmax, :56-71 */
+  /* Softmax, :56-71.  The exp is glibc's expf in both modes (exp_ref
+   * restates it bit for bit).  S is the sequential f32 sum in index order
+   * (:66), except in mirror mode on rows where top-k renormalises
+   * (0 < top_k < V, :80-89): there every probability is divided by the
+   * top-k sum before any step reads it, S cancels in exact arithmetic, and
+   * mirror takes S = 1 (the engine computes no normaliser for such rows). */
   float m = -INFINITY;
   for (uint32_t i = 0; i < V; ++i) m = fmaxf(m, l[i]);
   float* e = (float*)malloc(sizeof(float) * V);
   for (uint32_t i = 0; i < V; ++i) {
     if (l[i] == -INFINITY) e[i] = 0.0f;
     else
-      e[i] = (mode == LLMK_ORACLE_MIRROR) ? llmk_oracle_exp_m(l[i] - m)
+      e[i] = (mode == LLMK_ORACLE_MIRROR) ? llmk_oracle_exp_ref(l[i] - m)
                                           : expf(l[i] - m);
   }
+  const int topk_on = prm->top_k > 0 && (uint32_t)prm->top_k < V;
   float S;
-  if (mode == LLMK_ORACLE_MIRROR) S = S_mirror;
+  if (mode == LLMK_ORACLE_MIRROR && topk_on) S = 1.0f;
   else {
     S = 0.0f;
     for (uint32_t i = 0; i < V; ++i) S += e[i];
@@ -718,20 +596,14 @@ void llmk_oracle_apply_top_p(int mode, float* logits, uint32_t V, float top_p) {
   float* e = (float*)malloc(sizeof(float) * V);
   for (uint32_t i = 0; i < V; ++i) {
     if (logits[i] == -INFINITY) e[i] = 0.0f;
+    else if (mode == LLMK_ORACLE_MIRROR)  /* NaN acts as -inf, as on the GPU */
+      e[i] = isnan(logits[i]) ? 0.0f : llmk_oracle_exp_ref(logits[i] - m);
     else
-      e[i] = (mode == LLMK_ORACLE_MIRROR) ? llmk_oracle_exp_m(logits[i] - m)
-                                          : expf(logits[i] - m);
+      e[i] = expf(logits[i] - m);
   }
-  float S;
-  if (mode == LLMK_ORACLE_MIRROR) {
-    float* lp = (float*)malloc(sizeof(float) * V);
-    for (uint32_t i = 0; i < V; ++i) lp[i] = isnan(logits[i]) ? -INFINITY : logits[i];
-    S = llmk_oracle_normalizer(lp, NULL, V, 1.0f);
-    free(lp);
-  } else {
-    S = 0.0f;
-    for (uint32_t i = 0; i < V; ++i) S += e[i];
-  }
+  /* the sequential f32 sum in index order, :190 (top-k is off here) */
+  float S = 0.0f;
+  for (uint32_t i = 0; i < V; ++i) S += e[i];
   if (!(S > 0.0f)) {
     free(e);
     return;
@@ -769,7 +641,7 @@ uint32_t llmk_oracle_sample_simple(int mode, const float* logits, uint32_t V,
 }
 
 /* ------------------------------------------------------------------------ */
-/* exp_m exhaustive scan                                                     */
+/* exp_ref exhaustive scan                                                     */
 /* ------------------------------------------------------------------------ */
 
 void llmk_oracle_exp_scan(uint32_t lo_bits, uint32_t hi_bits,
@@ -781,7 +653,7 @@ void llmk_oracle_exp_scan(uint32_t lo_bits, uint32_t hi_bits,
   int have_prev = 0;
   for (uint64_t b = lo_bits; b <= hi_bits; ++b) {
     float y = u2f((uint32_t)b);
-    float a = llmk_oracle_exp_m(y);
+    float a = llmk_oracle_exp_ref(y);
     float r = expf(y);
     ++chk;
     if (f2u(a) != f2u(r)) {

@@ -13,11 +13,16 @@
  *                        helpers :128-228: glibc expf (what Rust's f32::exp
  *                        lowers to on Linux), sequential f32 sums in index /
  *                        sorted order, a full sort of (p, idx) pairs.
- *   LLMK_ORACLE_MIRROR — the same algorithm with the two numeric choices the
- *                        GPU engine fixes: its own exp (llmk_oracle_exp_m) and
- *                        its own softmax normaliser (llmk_oracle_normalizer,
- *                        tiled two-level log-sum-exp in a fixed tree order).
- *                        The HIP engine must reproduce this mode bit for bit.
+ *   LLMK_ORACLE_MIRROR — what the GPU engine computes, bit for bit.  It is
+ *                        the same algorithm with the same glibc expf
+ *                        (llmk_oracle_exp_ref restates it bit for bit), and
+ *                        differs from REF in one place: on rows where top-k
+ *                        renormalises (0 < top_k < V, sampler.rs:80-89) the
+ *                        softmax normaliser S, which cancels there in exact
+ *                        arithmetic, is taken as 1 instead of the sequential
+ *                        sum (sampler.rs:66).  Every other row is computed
+ *                        exactly as REF (NaN logits aside: mirror reads them
+ *                        as -inf).
  *
  * Both modes: ties in probability are ordered by index ascending (the
  * reference's sort_unstable_by leaves tie order unspecified, sampler.rs:77),
@@ -112,20 +117,16 @@ void llmk_oracle_apply_top_p(int mode, float* logits, uint32_t V, float top_p);
 uint32_t llmk_oracle_sample_simple(int mode, const float* logits, uint32_t V,
                                    float temperature, float u);
 
-/* Numerics of the mirror mode. */
-float llmk_oracle_exp_m(float y);          /* e^y, y <= 0 */
-float llmk_oracle_exp2_f(float d);         /* 2^d, d <= 0 (normaliser terms) */
-float llmk_oracle_libm_expf(float y);      /* glibc expf, for comparisons */
-/* Mirror softmax normaliser over penalised+masked logits lp[0..V); is_hist
- * (NULL = none) flags the distinct history tokens, which the engine reduces
- * in virtual tiles when a penalty is on. */
-float llmk_oracle_normalizer(const float* lp, const uint8_t* is_hist, uint32_t V,
-                             float temperature);
+/* Numerics. */
+/* e^x exactly as glibc's expf (>= 2.28, x86-64 FMA build) computes it, for
+ * x <= 0 (-inf and x < -0x1.9fe368p6 give +0). */
+float llmk_oracle_exp_ref(float x);
+float llmk_oracle_libm_expf(float y); /* the host's expf, for comparisons */
 
-/* Exhaustive checks of exp_m over the float bit patterns [lo, hi] of
+/* Exhaustive check of exp_ref over the float bit patterns [lo, hi] of
  * non-positive inputs (sign bit set, ascending magnitude): counts inputs
- * where exp_m differs from glibc expf, and adjacent pairs where exp_m is not
- * monotone.  max_ulp receives the largest |exp_m - expf| in ulps. */
+ * where exp_ref differs from the host's expf, and adjacent pairs where it is
+ * not monotone.  max_ulp receives the largest difference in ulps. */
 void llmk_oracle_exp_scan(uint32_t lo_bits, uint32_t hi_bits,
                           uint64_t* n_checked, uint64_t* n_mismatch,
                           uint64_t* n_nonmono, uint32_t* max_ulp);

@@ -40,14 +40,10 @@ def load():
     lib.llmk_oracle_process_logits.restype = ctypes.c_int
     lib.llmk_oracle_semantics.argtypes = [P, P, u32, P, f32, P, P, P, u32, P]
     lib.llmk_oracle_semantics.restype = ctypes.c_int
-    lib.llmk_oracle_exp_m.argtypes = [f32]
-    lib.llmk_oracle_exp_m.restype = f32
-    lib.llmk_oracle_exp2_f.argtypes = [f32]
-    lib.llmk_oracle_exp2_f.restype = f32
+    lib.llmk_oracle_exp_ref.argtypes = [f32]
+    lib.llmk_oracle_exp_ref.restype = f32
     lib.llmk_oracle_libm_expf.argtypes = [f32]
     lib.llmk_oracle_libm_expf.restype = f32
-    lib.llmk_oracle_normalizer.argtypes = [P, P, u32, f32]
-    lib.llmk_oracle_normalizer.restype = f32
     lib.llmk_oracle_apply_repetition_penalty.argtypes = [P, u32, P, u32, f32]
     lib.llmk_oracle_apply_temperature.argtypes = [P, u32, f32]
     lib.llmk_oracle_apply_top_k.argtypes = [P, u32, ctypes.c_int64]
@@ -214,18 +210,8 @@ def sample_simple(mode, logits, t, u):
     return int(load().llmk_oracle_sample_simple(mode, _p(l), l.size, t, u))
 
 
-def normalizer(lp, temperature, is_hist=None):
-    l = _f32p(lp)
-    h = None if is_hist is None else np.ascontiguousarray(is_hist, dtype=np.uint8)
-    return float(load().llmk_oracle_normalizer(_p(l), _p(h), l.size, temperature))
-
-
-def exp_m(y):
-    return np.float32(load().llmk_oracle_exp_m(float(y)))
-
-
-def exp2_f(d):
-    return np.float32(load().llmk_oracle_exp2_f(float(d)))
+def exp_ref(y):
+    return np.float32(load().llmk_oracle_exp_ref(float(y)))
 
 
 def libm_expf(y):
