@@ -1295,6 +1295,19 @@ __device__ __forceinline__ void load16(const void* row, uint32_t e0, uint32_t V,
   }
 }
 
+// The smallest of the lanes' keys (~0 = none), whose high words (entry
+// indices) differ between lanes that hold one: the minimum high word over
+// the wave, then its lane's key.  One LDS atomic per wave then suffices
+// (after a crossing every later entry of the window also reports one).
+__device__ __forceinline__ uint64_t wave_min_key(uint64_t k) {
+  const uint32_t hi = wave_min_u32((uint32_t)(k >> 32));
+  const uint64_t owner = __ballot(k != ~0ull && (uint32_t)(k >> 32) == hi);
+  if (!owner) return ~0ull;
+  const int l = __ffsll((unsigned long long)owner) - 1;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)k, l);
+  return ((uint64_t)hi << 32) | lo;
+}
+
 // Inclusive scan of the pairs over the wave (shifted-in lanes read the
 // identity (0, 0)).
 __device__ __forceinline__ Par wave_par_incl(Par x) {
@@ -1307,25 +1320,28 @@ __device__ __forceinline__ Par wave_par_incl(Par x) {
   return x;
 }
 
-// The sequential f32 sum c = ((c + e_0) + e_1) + ... of the NT*16 values of
-// one window (thread t holds window entries 16t .. 16t+15, all >= 0),
-// continued from c and returned, exactly, by the whole workgroup.  The
-// running-sum argument of seq_scan over the block: while c lies in the
-// binade of quantum q = 2^(eb-23), each entry adds the integer r = p/q
-// rounded to nearest (a tie to the even sum), a pair of increments (from an
-// even, from an odd sum) per entry; the pairs of a thread compose in order,
-// the workgroup scans them (waves by DPP, then the sixteen wave totals), and
-// the first entry whose sum would reach 2^(eb+1) is added as one f32
-// addition, after which the scan resumes.  Entries p/q >= 2^25 are clamped
-// (they cross at once); every sum before the first crossing stays below
-// 2^24 + 2^25, so no count wraps where it is read.  A zero c takes the
-// first nonzero entry as it is (0 + p = p).  Each round's first event goes
-// through one of three LDS slots in turn (round it uses slot it % 3 and
-// clears slot (it + 1) % 3, read two rounds ago), so a round needs two
-// barriers; `it` carries the rotation from call to call, and the slots start
-// cleared (exact_normaliser).  sc: 6 + NW*2 words; uniform barriers only.
-__device__ __forceinline__ float block_seq_sum(const float (&e)[16], float c, uint32_t& it,
-                                               LDS uint32_t* sc) {
+// The sequential f32 sum c = ((c + e_0) + e_1) + ... of one window's
+// entries (all >= 0), continued from c and returned, exactly, by the whole
+// workgroup.  Thread t holds entries 16t .. 16t+nq-1 (nq 16, or 4 for a wave
+// whose window part was compacted; wave-uniform), so entry j = 16t + q of
+// the window comes before entry j' exactly when j < j'.  The running-sum
+// argument of seq_scan over the block: while c lies in the binade of quantum
+// q = 2^(eb-23), each entry adds the integer r = p/q rounded to nearest (a
+// tie to the even sum), a pair of increments (from an even, from an odd sum)
+// per entry; the pairs of a thread compose in order, the workgroup scans
+// them (waves by DPP, then the sixteen wave totals), and the first entry
+// whose sum would reach 2^(eb+1) is added as one f32 addition, after which
+// the scan resumes.  Entries p/q >= 2^25 are clamped (they cross at once);
+// every sum before the first crossing stays below 2^24 + 2^25, so no count
+// wraps where it is read.  A zero c takes the first nonzero entry as it is
+// (0 + p = p).  A wave whose entries all lie before the resume point adds
+// the identity.  Each round's first event goes through one of three LDS
+// slots in turn (round it uses slot it % 3 and clears slot (it + 1) % 3,
+// read two rounds ago), so a round needs two barriers; `it` carries the
+// rotation from call to call, and the slots start cleared
+// (exact_normaliser).  sc: 6 + NW*2 words; uniform barriers only.
+__device__ __forceinline__ float block_seq_sum(const float (&e)[16], uint32_t nq, float c,
+                                               uint32_t& it, LDS uint32_t* sc) {
   constexpr uint32_t Q = 16, TOP = 1u << 24;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
   LDS uint64_t* ev = (LDS uint64_t*)sc;  // [3]: first event (index << 32 | new sum bits)
@@ -1334,14 +1350,20 @@ __device__ __forceinline__ float block_seq_sum(const float (&e)[16], float c, ui
   for (;; ++it) {
     LDS uint64_t* slot = ev + it % 3u;
     if (tid == 0) ev[(it + 1) % 3u] = ~0ull;
+    // every entry of this wave lies before s
+    const bool wave_done = Q * (64u * wv + 63u) + Q - 1u < s;
     if (c == 0.0f) {
       uint64_t best = ~0ull;
+      if (!wave_done) {
 #pragma unroll
-      for (int q = (int)Q - 1; q >= 0; --q) {
-        const uint32_t j = Q * tid + (uint32_t)q;
-        if (j >= s && e[q] != 0.0f) best = ((uint64_t)j << 32) | __float_as_uint(e[q]);
+        for (int q = (int)Q - 1; q >= 0; --q) {
+          const uint32_t j = Q * tid + (uint32_t)q;
+          if ((uint32_t)q < nq && j >= s && e[q] != 0.0f)
+            best = ((uint64_t)j << 32) | __float_as_uint(e[q]);
+        }
       }
-      if (best != ~0ull) __atomic_fetch_min(slot, best, __ATOMIC_RELAXED);
+      best = wave_min_key(best);
+      if (lane == 0 && best != ~0ull) __atomic_fetch_min(slot, best, __ATOMIC_RELAXED);
       __syncthreads();
       const uint64_t r = *slot;
       if (r == ~0ull) {  // every remaining entry is 0
@@ -1360,24 +1382,32 @@ __device__ __forceinline__ float block_seq_sum(const float (&e)[16], float c, ui
     const int eb = (int)umax((cb >> 23) & 255u, 1u) - 127;
     const uint32_t C = (uint32_t)__builtin_ldexpf(c, 23 - eb);
     uint32_t r[Q], tie = 0;
+    Par own{0u, 0u};
+    if (!wave_done) {
 #pragma unroll
-    for (uint32_t q = 0; q < Q; ++q) {
-      const float x = __builtin_fminf(__builtin_ldexpf(e[q], 23 - eb), 0x1p25f);  // exact below the clamp
-      const float k = __builtin_floorf(x);
-      const float fr = x - k;
-      const uint32_t ki = (uint32_t)k;
-      const bool live = Q * tid + q >= s;
-      r[q] = !live ? 0u : (fr > 0.5f ? ki + 1u : ki);
-      if (live && fr == 0.5f) tie |= 1u << q;
-    }
-    uint32_t s0 = 0, s1 = 1;
+      for (uint32_t q = 0; q < Q; ++q) {
+        r[q] = 0u;
+        if (q < nq) {
+          const float x = __builtin_fminf(__builtin_ldexpf(e[q], 23 - eb), 0x1p25f);  // exact below the clamp
+          const float k = __builtin_floorf(x);
+          const float fr = x - k;
+          const uint32_t ki = (uint32_t)k;
+          const bool live = Q * tid + q >= s;
+          r[q] = !live ? 0u : (fr > 0.5f ? ki + 1u : ki);
+          if (live && fr == 0.5f) tie |= 1u << q;
+        }
+      }
+      uint32_t s0 = 0, s1 = 1;
 #pragma unroll
-    for (uint32_t q = 0; q < Q; ++q) {
-      const uint32_t t = (tie >> q) & 1u;
-      s0 += r[q] + (t & ((s0 ^ r[q]) & 1u));
-      s1 += r[q] + (t & ((s1 ^ r[q]) & 1u));
+      for (uint32_t q = 0; q < Q; ++q) {
+        if (q < nq) {
+          const uint32_t t = (tie >> q) & 1u;
+          s0 += r[q] + (t & ((s0 ^ r[q]) & 1u));
+          s1 += r[q] + (t & ((s1 ^ r[q]) & 1u));
+        }
+      }
+      own = Par{s0, s1 - 1u};
     }
-    const Par own{s0, s1 - 1u};
     const Par inc = wave_par_incl(own);
     if (lane == 63) {
       wt[2 * wv] = inc.a0;
@@ -1392,21 +1422,26 @@ __device__ __forceinline__ float block_seq_sum(const float (&e)[16], float c, ui
       if (i < wv) pre = par_then(pre, wtot);
       tot = par_then(tot, wtot);
     }
-    ex = par_then(pre, ex);
-    uint32_t cur = C + ((C & 1u) ? ex.a1 : ex.a0);
     uint64_t cand = ~0ull;
+    if (!wave_done) {
+      ex = par_then(pre, ex);
+      uint32_t cur = C + ((C & 1u) ? ex.a1 : ex.a0);
 #pragma unroll
-    for (uint32_t q = 0; q < Q; ++q) {
-      const uint32_t t = (tie >> q) & 1u;
-      const uint32_t nx = cur + r[q] + (t & ((cur ^ r[q]) & 1u));
-      if (cand == ~0ull && Q * tid + q >= s && nx >= TOP) {
-        // the addition that leaves the binade, as one f32 addition
-        const float before = __builtin_ldexpf((float)cur, eb - 23);
-        cand = ((uint64_t)(Q * tid + q) << 32) | __float_as_uint(before + e[q]);
+      for (uint32_t q = 0; q < Q; ++q) {
+        if (q < nq) {
+          const uint32_t t = (tie >> q) & 1u;
+          const uint32_t nx = cur + r[q] + (t & ((cur ^ r[q]) & 1u));
+          if (cand == ~0ull && Q * tid + q >= s && nx >= TOP) {
+            // the addition that leaves the binade, as one f32 addition
+            const float before = __builtin_ldexpf((float)cur, eb - 23);
+            cand = ((uint64_t)(Q * tid + q) << 32) | __float_as_uint(before + e[q]);
+          }
+          cur = nx;
+        }
       }
-      cur = nx;
     }
-    if (cand != ~0ull) __atomic_fetch_min(slot, cand, __ATOMIC_RELAXED);
+    cand = wave_min_key(cand);
+    if (lane == 0 && cand != ~0ull) __atomic_fetch_min(slot, cand, __ATOMIC_RELAXED);
     __syncthreads();
     const uint64_t res = *slot;
     if (res == ~0ull) {
@@ -1426,36 +1461,136 @@ __device__ __forceinline__ float block_seq_sum(const float (&e)[16], float c, ui
 // (0 for l_i = -inf), l_i = fl(v_i / T) the processed logit (penalties from
 // the history tables h if have_hist, the allow-mask, NaN read as -inf)
 // divided by T (sampler.rs:53, :57-66).  The whole workgroup, windows of
-// NT*16 consecutive elements; sc: 64 words of scratch.
+// NT*16 consecutive elements, the next window's logits requested before the
+// current one is summed.  Most entries cannot change the sum: zeros (-inf
+// logits), and, once the sum is positive, every e below half its quantum at
+// the window's start (the sum only grows, so such an e adds 0 wherever it
+// falls).  A cheap bound on l finds them (the product with 1/T is within a
+// few ulps of l, far inside the margin), and a wave whose window part keeps
+// at most 256 entries packs them in order into LDS, four per lane, so that
+// the exact division and exp run on those alone.  A window whose entries
+// are all packed and number at most SERIAL_MAX is then summed by one lane,
+// entry after entry (a few cycles each, against microseconds for a round of
+// the workgroup scan); any other window goes through block_seq_sum.
+// sc: 96 + NW*256 words of scratch.
+// A function of its own (not inlined, scalars only across the call): its
+// registers are then allocated apart from the stream loop's, which an
+// inlined copy crowds into spilling.
+constexpr uint32_t SERIAL_MAX = 2048;
 template <int DT>
-__device__ __forceinline__ float exact_normaliser(const Args& a, uint32_t b, const RowP& P,
-                                                  float m, const Hist& h, bool have_hist,
-                                                  LDS uint32_t* sc) {
-  const uint32_t tid = threadIdx.x, V = a.V;
-  const void* row = (const char*)a.logits + (uint64_t)b * a.stride * (DT == LLMK_F32 ? 4u : 2u);
-  const GLB uint32_t* mrow = a.mask ? G(a.mask) + (uint64_t)b * a.mask_words : nullptr;
-  constexpr uint32_t Q = 16, W = NT * Q;
+__device__ __attribute__((noinline)) float exact_normaliser(
+    const void* row, const uint32_t* mask_row, uint32_t V, float T, float m,
+    LDS uint32_t* bitmap, LDS uint16_t* pre, LDS float* pen, bool have_hist, LDS uint32_t* sc) {
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
+  const GLB uint32_t* mrow = mask_row ? G(mask_row) : nullptr;
+  Hist h;
+  h.bitmap = bitmap;
+  h.pre = pre;
+  h.pen = pen;
+  h.tokr = nullptr;
+  h.lo = 0;
+  RowP P;
+  P.T = T;
+  constexpr uint32_t Q = 16, W = NT * Q, CW = 256;
+  LDS uint32_t* nwv = sc + 64;                         // [NW]: packed entries per wave (~0: not packed)
+  LDS float* cbc = (LDS float*)(sc + 80);              // the serial sum's result
+  LDS float* comp0 = (LDS float*)(sc + 96);            // [NW][CW]
+  LDS float* comp = comp0 + CW * wv;                   // this wave's packed entries
+  const float rT = 1.0f / P.T;
+  auto exact_e = [&](float x) __attribute__((always_inline)) {
+    const float l = (P.T != 1.0f) ? x / P.T : x;
+    return (l == NEG_INF) ? 0.0f : exp_ref(l - m);
+  };
   if (tid < 3) ((LDS uint64_t*)sc)[tid] = ~0ull;
   __syncthreads();
   uint32_t it = 0;
   float c = 0.0f;
+  float xn[Q];
+  load16<DT>(row, Q * tid, V, xn);
   for (uint32_t w0 = 0; w0 < V; w0 += W) {
     const uint32_t e0 = w0 + Q * tid;
-    float v[Q];
-    load16<DT>(row, e0, V, v);
+    float x[Q];
+#pragma unroll
+    for (uint32_t q = 0; q < Q; ++q) x[q] = xn[q];
     // the sixteen lie in one 32-bit word of the mask and of the bitmap
     const uint32_t mw = (mrow && e0 < V) ? mrow[e0 >> 5] >> (e0 & 16u) : 0xffffffffu;
     const uint32_t hw = (have_hist && e0 < V) ? h.bitmap[(e0 - h.lo) >> 5] >> (e0 & 16u) : 0u;
-    float e[Q];
+    // entries below lim (on l - m) add nothing to a sum of binade eb or above
+    float lim = NEG_INF;
+    if (c > 0.0f) {
+      const int eb = (int)umax((__float_as_uint(c) >> 23) & 255u, 1u) - 127;
+      lim = (float)(eb - 24) * 0.693147f - (0.01f + 1e-6f * fabsf(m));
+    }
+    uint32_t live = 0;
 #pragma unroll
     for (uint32_t q = 0; q < Q; ++q) {
-      float x = v[q];
-      if ((hw >> q) & 1u) x = h.pen[h.rank(e0 + q)];  // a kept rank (< U_MAX)
-      if (!((mw >> q) & 1u) || !(x > NEG_INF)) x = NEG_INF;
-      const float l = (P.T != 1.0f) ? x / P.T : x;
-      e[q] = (l == NEG_INF) ? 0.0f : exp_ref(l - m);
+      float v = x[q];
+      if ((hw >> q) & 1u) v = h.pen[h.rank(e0 + q)];  // a kept rank (< U_MAX)
+      if (!((mw >> q) & 1u) || !(v > NEG_INF)) v = NEG_INF;
+      x[q] = v;
+      if (v > NEG_INF && v * rT - m >= lim) live |= 1u << q;
     }
-    c = block_seq_sum(e, c, it, sc);
+    // the next window's logits, while this one is summed
+    if (w0 + W < V) load16<DT>(row, e0 + W, V, xn);
+    const uint32_t n = (uint32_t)__popc(live);
+    const uint32_t incl = wave_incl_scan(n);
+    const uint32_t nw = bcast63u(incl);
+    float e[Q];
+    uint32_t nq = Q;
+    if (nw <= CW) {
+      // pack this wave's entries in order, four per lane
+      uint32_t at = incl - n;
+#pragma unroll
+      for (uint32_t q = 0; q < Q; ++q)
+        if ((live >> q) & 1u) comp[at++] = x[q];
+      WaveSync::sync();
+#pragma unroll
+      for (uint32_t q = 0; q < 4; ++q) {
+        const uint32_t k = 4u * lane + q;
+        e[q] = k < nw ? exact_e(comp[k]) : 0.0f;
+      }
+#pragma unroll
+      for (uint32_t q = 4; q < Q; ++q) e[q] = 0.0f;
+      nq = 4;
+      WaveSync::sync();
+      // the exact terms, in the same order
+#pragma unroll
+      for (uint32_t q = 0; q < 4; ++q)
+        if (4u * lane + q < nw) comp[4u * lane + q] = e[q];
+    } else {
+#pragma unroll
+      for (uint32_t q = 0; q < Q; ++q) e[q] = ((live >> q) & 1u) ? exact_e(x[q]) : 0.0f;
+    }
+    if (lane == 0) nwv[wv] = nw <= CW ? nw : EMPTY;
+    __syncthreads();
+    uint32_t tot = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < NW; ++i) tot += umin(nwv[i], SERIAL_MAX + 1u);
+    if (tot <= SERIAL_MAX) {
+      // every wave packed, few entries: one lane sums them in order
+      if (tid == 0) {
+        float cc = c;
+        for (uint32_t i = 0; i < NW; ++i) {
+          LDS const float* L = comp0 + CW * i;
+          const uint32_t ni = nwv[i];
+          uint32_t k = 0;
+          for (; k + 4u <= ni; k += 4u) {
+            const f4v y = *(LDS const f4v*)(L + k);
+            cc = cc + y.x;
+            cc = cc + y.y;
+            cc = cc + y.z;
+            cc = cc + y.w;
+          }
+          for (; k < ni; ++k) cc = cc + L[k];
+        }
+        *cbc = cc;
+      }
+      __syncthreads();
+      c = *cbc;
+      __syncthreads();  // nwv, comp and cbc are rewritten next window
+    } else {
+      c = block_seq_sum(e, nq, c, it, sc);
+    }
   }
   __syncthreads();  // the caller may reuse sc
   return c;
@@ -2558,7 +2693,10 @@ __device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_
       build_history<DT>(a, P, b, row, 0, a.V, nwords, h, sc + 128, &sc[64]);
       have_hist = true;  // built (empty when the row has no penalised history)
     }
-    S = exact_normaliser<DT>(a, b, P, m, h, have_hist, sc);
+    const void* row = (const char*)a.logits +
+                      (uint64_t)b * a.stride * (DT == LLMK_F32 ? 4u : 2u);
+    S = exact_normaliser<DT>(row, a.mask ? a.mask + (uint64_t)b * a.mask_words : nullptr, a.V,
+                             P.T, m, h.bitmap, h.pre, h.pen, have_hist, sc);
   }
   uint32_t path = 2;  // 0 done, 1 workgroup candidate path, 2 slow path, 3 fast path
   if (wv == 0) {
