@@ -26,22 +26,64 @@ HBM_PEAK_GBPS = 8000.0
 MALL_BYTES = 256 << 20
 
 
+def kernel_source_digest():
+    """sha256 of the sampling kernel's source: a traffic summary applies to the
+    kernel it was measured on and to no later edit."""
+    import hashlib
+    with open(os.path.join(ROOT, "llm-rs_amd", "csrc", "llmk_sampler.hip"), "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()
+
+
 def measured_traffic(config):
     """HBM bytes per launch of the stream kernel from the committed counter
-    summary (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy), or None."""
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy), or None when
+    there is none or it was measured on another version of the kernel."""
     import re
     path = os.path.join(ROOT, "profiles", f"stream_kernel_{config}_hbm_traffic.md")
     try:
         with open(path) as f:
-            m = re.search(r"^traffic_bytes_per_launch = (\d+)$", f.read(), re.M)
-        return int(m.group(1)) if m else None
+            text = f.read()
     except OSError:
-        return None
+        return None, "no counter summary"
+    m = re.search(r"^traffic_bytes_per_launch = (\d+)$", text, re.M)
+    d = re.search(r"^kernel_source_sha256 = ([0-9a-f]{64})$", text, re.M)
+    if not m:
+        return None, "no traffic line in " + os.path.basename(path)
+    if not d or d.group(1) != kernel_source_digest():
+        return None, "counter summary measured on another version of llmk_sampler.hip"
+    return int(m.group(1)), os.path.basename(path)
+
+
+def rotated_sets(llmk, db0, logit_bytes, sets=0):
+    """db0 and clones of its logits, enough that consecutive steps do not
+    find the previous step's logits in the 256 MB MALL."""
+    import numpy as np
+    nsets = sets or max(1, int(np.ceil(2 * MALL_BYTES / logit_bytes)) + 1)
+    dbs = [db0]
+    for _ in range(nsets - 1):
+        d = llmk.DeviceBatch(**{k: getattr(db0, k) for k in db0.__dataclass_fields__})
+        d.logits = db0.logits.clone()
+        dbs.append(d)
+    return dbs
+
+
+def back_to_back(torch, s, prepared, K, stream):
+    """K launches of llmk_sample_batch, rotating over the prepared argument
+    sets, between two events on the launch stream: the time per launch."""
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for i in range(K):
+        s.launch_prepared(prepared[i % len(prepared)], stream)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / K
 
 
 def time_config(llmk, synth, torch, name, steps=20, warmup=5):
-    """Mean kernel time (event pairs on the launch stream) of one config, its
-    logits rotated over enough copies to leave the 256 MB MALL."""
+    """Time per launch of one config (back-to-back launches between two
+    events), its logits rotated over enough copies to leave the MALL."""
     import numpy as np
     if name.endswith("-f16"):
         # the config with its logits rounded to f16 (a half-precision lm_head
@@ -53,26 +95,13 @@ def time_config(llmk, synth, torch, name, steps=20, warmup=5):
     else:
         w = synth.make(name)
     db0 = w.to_device()
-    nbytes = db0.logits.numel() * db0.logits.element_size()
-    nsets = max(1, int(np.ceil(2 * MALL_BYTES / nbytes)) + 1)
-    dbs = [db0]
-    for _ in range(nsets - 1):
-        d = llmk.DeviceBatch(**{k: getattr(db0, k) for k in db0.__dataclass_fields__})
-        d.logits = db0.logits.clone()
-        dbs.append(d)
+    dbs = rotated_sets(llmk, db0, db0.logits.numel() * db0.logits.element_size())
     s = llmk.HipSampler(max_batch=w.B, max_vocab=w.V)
     tok = torch.empty(w.B, dtype=torch.int32, device="cuda:0")
+    prepared = [s.prepare(d, tok) for d in dbs]
     stream = torch.cuda.current_stream()
-    for i in range(warmup):
-        s.launch(dbs[i % nsets], tok, stream=stream)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(steps)]
-    for i in range(steps):
-        ev[i][0].record(stream)
-        s.launch(dbs[i % nsets], tok, stream=stream)
-        ev[i][1].record(stream)
-    torch.cuda.synchronize()
-    us = float(np.mean([a.elapsed_time(b) for a, b in ev])) * 1e3
+    back_to_back(torch, s, prepared, warmup, stream)
+    us = back_to_back(torch, s, prepared, steps, stream) * 1e3
     gbps = w.algorithmic_bytes() / (us * 1e-6) / 1e9
     s.close()
     return {"B": w.B, "V": w.V, "dtype": w.dtype, "us_per_step": us,
@@ -84,7 +113,8 @@ def time_mask(llmk, synth, torch, op, steps=3):
     """The mask forms in place: apply_top_k at C3's shape (k 50) and apply_top_p
     at C4's (top-p 0.9).  Each launch masks a freshly restored copy of the
     logits, restored before all timed launches of a round so that it has left
-    the MALL; event pairs on the launch stream around the call only."""
+    the MALL; the launches of a round run back to back between two events on
+    the launch stream."""
     import numpy as np
     w = synth.make("C3" if op == "top_k" else "C4")
     src = torch.from_numpy(w.logits).to("cuda:0")
@@ -103,15 +133,15 @@ def time_mask(llmk, synth, torch, op, steps=3):
     for r in range(steps + 1):
         for b in bufs:
             b.copy_(src)
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for _ in bufs]
-        for b, (e0, e1) in zip(bufs, ev):
-            e0.record(stream)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for b in bufs:
             call(b)
-            e1.record(stream)
+        e1.record(stream)
         torch.cuda.synchronize()
         if r:  # the first round warms up
-            times += [e0.elapsed_time(e1) for e0, e1 in ev]
+            times.append(e0.elapsed_time(e1) / len(bufs))
     masked = int((bufs[0] != src).sum().item())
     us = float(np.mean(times)) * 1e3
     alg = nbytes + 4 * masked + 4 * w.B
@@ -241,50 +271,26 @@ def main():
     db0 = w.to_device(dev)
     step_bytes = w.algorithmic_bytes()
     logit_bytes = db0.logits.numel() * db0.logits.element_size()
-    nsets = args.sets or max(1, int(np.ceil(2 * MALL_BYTES / logit_bytes)) + 1)
-    dbs = [db0]
-    for _ in range(nsets - 1):
-        d = llmk.DeviceBatch(**{k: getattr(db0, k) for k in db0.__dataclass_fields__})
-        d.logits = db0.logits.clone()
-        dbs.append(d)
+    dbs = rotated_sets(llmk, db0, logit_bytes, args.sets)
+    nsets = len(dbs)
     s = llmk.HipSampler(max_batch=w.B, max_vocab=w.V)
     B = w.B
     tok = torch.empty(B, dtype=torch.int32, device=dev)
     cnt = torch.empty(B, dtype=torch.int32, device=dev)
+    prepared = [s.prepare(d, tok, out_count=cnt) for d in dbs]
     stream = torch.cuda.current_stream()
 
-    for i in range(args.warmup):
-        s.launch(dbs[i % nsets], tok, out_count=cnt, stream=stream)
-    torch.cuda.synchronize()
-
+    back_to_back(torch, s, prepared, args.warmup, stream)
     K = args.steps
-    # timed steps: K back-to-back launches between two events (the job rate)
-    t_start = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t_start.record(stream)
-    for i in range(K):
-        s.launch(dbs[i % nsets], tok, out_count=cnt, stream=stream)
-    t_end.record(stream)
-    torch.cuda.synchronize()
-    total_ms = t_start.elapsed_time(t_end)
-    ms_per_step = total_ms / K
+    # timed steps: K back-to-back launches between two events on the launch
+    # stream; the time per step is also the stream kernel's average duration
+    # (one launch per step, nothing between launches)
+    ms_per_step = back_to_back(torch, s, prepared, K, stream)
     value = B / (ms_per_step * 1e-3)
-    # the kernel's own duration: K more launches, each between two events on
-    # the launch stream
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
-    for i in range(K):
-        ev[i][0].record(stream)
-        s.launch(dbs[i % nsets], tok, out_count=cnt, stream=stream)
-        ev[i][1].record(stream)
-    torch.cuda.synchronize()
-    kern_ms = [a.elapsed_time(b) for a, b in ev]
-    kern_avg_ms = float(np.mean(kern_ms))
-    achieved = step_bytes / (kern_avg_ms * 1e-3) / 1e9
-
-    log(f"[bench] {w.name}: {ms_per_step*1e3:.2f} us/step (kernel avg {kern_avg_ms*1e3:.2f} us, "
-        f"min {min(kern_ms)*1e3:.2f}, max {max(kern_ms)*1e3:.2f}), "
-        f"{achieved:.0f} GB/s algorithmic, sets {nsets}")
+    achieved = step_bytes / (ms_per_step * 1e-3) / 1e9
+    traffic, traffic_src = measured_traffic(args.config)
+    log(f"[bench] {w.name}: {ms_per_step*1e3:.2f} us/step, {achieved:.0f} GB/s algorithmic, "
+        f"sets {nsets}; traffic {traffic} ({traffic_src})")
 
     read_gbps = stream_read_gbps(torch)
     log(f"[bench] streaming read probe (2 GiB): {read_gbps:.0f} GB/s")
@@ -332,13 +338,12 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBPS,
-            "traffic": measured_traffic(args.config),
+            "traffic": traffic,
+            "traffic_source": traffic_src,
             "kernel": "llmk::stream_kernel",
+            "kernel_avg_us": ms_per_step * 1e3,
             "achievable_read_GBps": read_gbps,
             "frac_of_achievable": achieved / read_gbps,
-            "kernel_avg_us": kern_avg_ms * 1e3,
-            "kernel_median_us": float(np.median(kern_ms)) * 1e3,
-            "kernel_launches_timed": len(kern_ms),
         },
         "other_configs": others,
         "cpu_baseline": cpu,

@@ -57,6 +57,12 @@ extern "C" {
 /* llmk_history_append found a row's history buffer full (its token was not
  * appended). */
 #define LLMK_STATUS_HISTORY_FULL 0x8u
+/* A sampling row held a logit that makes the reference's probabilities NaN
+ * (NaN itself, or +inf: l - max = inf - inf), outside the allow-mask's
+ * disallowed tokens: the device analogue of sampler.rs's NAN_WARNED
+ * warn-once flag (sampler.rs:7-9, :74-76).  The engine reads NaN as -inf
+ * and samples on; results for such rows are outside the parity contract. */
+#define LLMK_STATUS_NAN_LOGITS 0x10u
 
 typedef struct llmk_sampler llmk_sampler; /* opaque; owns device workspace */
 

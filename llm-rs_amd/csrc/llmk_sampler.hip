@@ -89,7 +89,7 @@ constexpr float LOG2E_F = 0x1.715476p+0f;  // the slow path's bins of (l - L)/T,
 __shared__ uint32_t g_bcast[4];
 
 enum : uint32_t { MODE_INVALID = 0, MODE_GREEDY = 1, MODE_SAMPLE = 2 };
-enum : uint32_t { FLAG_OVERFLOW = 1u, FLAG_HIST_OVERFLOW = 2u };
+enum : uint32_t { FLAG_OVERFLOW = 1u, FLAG_HIST_OVERFLOW = 2u, FLAG_NAN = 4u };
 
 struct Args {
   const void* logits;
@@ -2900,7 +2900,8 @@ constexpr int VB = 8;  // gathers in flight per thread
 template <int DT>
 __device__ __forceinline__ void gather_penalised(const Args& a, const RowP& P, uint32_t b,
                                                  const void* row, uint32_t U, const Hist& h,
-                                                 bool need_cnt, uint32_t nw) {
+                                                 bool need_cnt, uint32_t nw,
+                                                 LDS uint32_t* flags) {
   const uint32_t tid = threadIdx.x, step = nw * WAVE;
   const GLB uint32_t* mrow = a.mask ? G(a.mask) + (uint64_t)b * a.mask_words : nullptr;
   LDS const uint32_t* cnt = (LDS const uint32_t*)h.pen;
@@ -2926,9 +2927,12 @@ __device__ __forceinline__ void gather_penalised(const Args& a, const RowP& P, u
     for (int i = 0; i < VB; ++i) {
       const uint32_t r = r0 + i * step + tid;
       if ((uint32_t)i < nr && tk[i] != EMPTY) {
+        const bool allowed = (mw[i] >> (tk[i] & 31)) & 1u;
+        if (allowed && !(x[i] < __builtin_huge_valf()) && P.mode == MODE_SAMPLE)
+          __atomic_fetch_or(flags, FLAG_NAN, __ATOMIC_RELAXED);
         float y = (x[i] > NEG_INF) ? x[i] : NEG_INF;  // NaN acts as -inf
         y = penalize(y, P, need_cnt ? cnt[r] : 1u);
-        if (!((mw[i] >> (tk[i] & 31)) & 1u)) y = NEG_INF;
+        if (!allowed) y = NEG_INF;
         h.pen[r] = y;
       }
     }
@@ -3160,7 +3164,7 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
         if (tb2 != EMPTY) load_tile<DT>(a, row, mrow, h, tb2, lane, rb);
 #pragma unroll
         for (int q = 0; q < TQ; ++q) asm volatile("" ::"v"(pf[q]));  // the prefetch is done
-        gather_penalised<DT>(a, P, b, row, U, h, need_cnt, TW);
+        gather_penalised<DT>(a, P, b, row, U, h, need_cnt, TW, &misc[M_FLAGS]);
         gs();
         for (uint32_t k = (uint32_t)wv; k < nch; k += TW) vtile_chunk(a, t0, nwords, k, U, h, E, lane);
       }
@@ -3171,7 +3175,7 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
         if (tok_wave) counts();
         __syncthreads();
       }
-      gather_penalised<DT>(a, P, b, row, U, h, need_cnt, NW);
+      gather_penalised<DT>(a, P, b, row, U, h, need_cnt, NW, &misc[M_FLAGS]);
       __syncthreads();
       for (uint32_t k = (uint32_t)wv; k < nch; k += NW) vtile_chunk(a, t0, nwords, k, U, h, E, lane);
     }
@@ -3200,6 +3204,16 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) v[4 * r + q] = exclude(v[4 * r + q], x, sh4 + q);
       }
+    }
+    // a logit that makes the reference's probabilities NaN: NaN, or +inf
+    // (whose l - max is inf - inf); masked ones are -inf by now.  Sampling
+    // rows only: the reference's greedy branch returns first (sampler.rs:40-50,
+    // :74-76)
+    if (P.mode == MODE_SAMPLE) {
+      uint64_t bad = 0;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) bad |= __ballot(!(v[j] < __builtin_huge_valf()));
+      if (bad && lane == 0) __atomic_fetch_or(&misc[M_FLAGS], FLAG_NAN, __ATOMIC_RELAXED);
     }
     tile_reduce(E, v, t, [&](int j) -> uint32_t {
       return tb + 256u * (j >> 2) + 4u * (uint32_t)lane + (j & 3);
@@ -3237,6 +3251,7 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   if (tid == 0) {
     const uint32_t fl = misc[M_FLAGS];
     if (fl & FLAG_HIST_OVERFLOW) atomicOr(w.status, LLMK_STATUS_HISTORY_OVERFLOW);
+    if (fl & FLAG_NAN) atomicOr(w.status, LLMK_STATUS_NAN_LOGITS);
     uint32_t last = 1;
     if (a.G > 1) {  // a single-segment row passes its table in registers
       G(w.seg_meta)[blockIdx.x] = u4v{misc[M_CCOUNT], misc[M_BETA], fl, have ? 1u : 0u};
@@ -3583,11 +3598,67 @@ extern "C" const char* llmk_last_error(void) { return g_last_error.c_str(); }
                                     hipGetErrorString(e_));                 \
   } while (0)
 
-static size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+static constexpr size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
 // Dynamic LDS of one workgroup: the CU's 160 KiB less the kernels' static
 // tables (the expf table and the phase words, under 512 bytes).
 static constexpr size_t LDS_DYN_MAX = 160 * 1024 - 512;
+
+// The workspace of the sampling kernel for batches up to mb rows of up to mv
+// logits, pool workgroup entries and `slots` slow-path slots: byte offsets
+// of its arrays in one 256-byte aligned block.
+struct WsLayout {
+  size_t arrive, part, meta, cand, lock, skeys, sp, si, status, cut, mtok, zu, total;
+};
+static constexpr WsLayout ws_layout(uint32_t mb, uint32_t mv, uint32_t pool, uint32_t slots) {
+  WsLayout L{};
+  size_t off = 0;
+  L.arrive = off; off = align_up(off + 4ull * mb, 256);
+  L.part = off; off = align_up(off + 8ull * mb * MAX_SLOTS, 256);
+  L.meta = off; off = align_up(off + 16ull * pool, 256);
+  L.cand = off; off = align_up(off + 8ull * pool * CAND_CAP, 256);
+  L.lock = off; off = align_up(off + 4ull * slots, 256);
+  L.skeys = off; off = align_up(off + 8ull * slots * 3 * mv, 256);
+  L.sp = off; off = align_up(off + 4ull * slots * mv, 256);
+  L.si = off; off = align_up(off + 4ull * slots * mv, 256);
+  L.status = off; off = align_up(off + 256, 256);
+  L.cut = off; off = align_up(off + 16ull * mb, 256);
+  L.mtok = off; off = align_up(off + 4ull * mb, 256);
+  L.zu = off; off = align_up(off + 4ull * mb, 256);
+  L.total = off;
+  return L;
+}
+static Ws ws_carve(char* base, const WsLayout& L, uint32_t mv, uint32_t slots) {
+  Ws w;
+  w.row_arrive = (uint32_t*)(base + L.arrive);
+  w.tile_part = (f2v*)(base + L.part);
+  w.seg_meta = (u4v*)(base + L.meta);
+  w.cand = (u2v*)(base + L.cand);
+  w.slow_lock = (uint32_t*)(base + L.lock);
+  w.slow_keys = (uint64_t*)(base + L.skeys);
+  w.slow_p = (float*)(base + L.sp);
+  w.slow_idx = (uint32_t*)(base + L.si);
+  w.status = (uint32_t*)(base + L.status);
+  w.cut = (u4v*)(base + L.cut);
+  w.mtok = (uint32_t*)(base + L.mtok);
+  w.zu = (float*)(base + L.zu);
+  w.max_vocab = mv;
+  w.slow_slots = slots;
+  return w;
+}
+// Dynamic LDS above 64 KiB must be allowed explicitly (per device; no
+// allocation).
+static int set_kernel_attributes() {
+  HIPCHK(hipFuncSetAttribute((const void*)stream_kernel<LLMK_F32>,
+                             hipFuncAttributeMaxDynamicSharedMemorySize, LDS_DYN_MAX));
+  HIPCHK(hipFuncSetAttribute((const void*)stream_kernel<LLMK_BF16>,
+                             hipFuncAttributeMaxDynamicSharedMemorySize, LDS_DYN_MAX));
+  HIPCHK(hipFuncSetAttribute((const void*)stream_kernel<LLMK_F16>,
+                             hipFuncAttributeMaxDynamicSharedMemorySize, LDS_DYN_MAX));
+  HIPCHK(hipFuncSetAttribute((const void*)topk_mask_kernel,
+                             hipFuncAttributeMaxDynamicSharedMemorySize, 4 * MK_LDS_WORDS));
+  return LLMK_OK;
+}
 
 extern "C" int llmk_sampler_create(llmk_sampler** out, int device,
                                    uint32_t max_batch, uint32_t max_vocab) {
@@ -3600,64 +3671,26 @@ extern "C" int llmk_sampler_create(llmk_sampler** out, int device,
   if (4 * slow_lds_words(max_vocab) > LDS_DYN_MAX)
     return fail(LLMK_ERR_CAPACITY, "max_vocab too large for the slow path's LDS tables");
   HIPCHK(hipSetDevice(device));
-  // Dynamic LDS above 64 KiB must be allowed explicitly.
-  HIPCHK(hipFuncSetAttribute((const void*)stream_kernel<LLMK_F32>,
-                             hipFuncAttributeMaxDynamicSharedMemorySize, LDS_DYN_MAX));
-  HIPCHK(hipFuncSetAttribute((const void*)stream_kernel<LLMK_BF16>,
-                             hipFuncAttributeMaxDynamicSharedMemorySize, LDS_DYN_MAX));
-  HIPCHK(hipFuncSetAttribute((const void*)stream_kernel<LLMK_F16>,
-                             hipFuncAttributeMaxDynamicSharedMemorySize, LDS_DYN_MAX));
-  HIPCHK(hipFuncSetAttribute((const void*)topk_mask_kernel,
-                             hipFuncAttributeMaxDynamicSharedMemorySize, 4 * MK_LDS_WORDS));
+  const int rc = set_kernel_attributes();
+  if (rc != LLMK_OK) return rc;
   const uint32_t pool = max_batch > MAX_WGS ? max_batch : MAX_WGS;
-  size_t off = 0;
-  auto take = [&](size_t bytes) {
-    const size_t o = off;
-    off = align_up(off + bytes, 256);
-    return o;
-  };
-  const size_t o_arrive = take(4ull * max_batch);
-  const size_t o_part = take(8ull * max_batch * MAX_SLOTS);
-  const size_t o_meta = take(16ull * pool);
-  const size_t o_cand = take(8ull * pool * CAND_CAP);
   const uint32_t slots = max_batch < SLOW_SLOTS ? max_batch : SLOW_SLOTS;
-  const size_t o_lock = take(4ull * slots);
-  const size_t o_skeys = take(8ull * slots * 3 * max_vocab);
-  const size_t o_sp = take(4ull * slots * max_vocab);
-  const size_t o_si = take(4ull * slots * max_vocab);
-  const size_t o_status = take(256);
-  const size_t o_cut = take(16ull * max_batch);
-  const size_t o_mtok = take(4ull * max_batch);
-  const size_t o_zu = take(4ull * max_batch);
+  const WsLayout L = ws_layout(max_batch, max_vocab, pool, slots);
   void* mem = nullptr;
-  HIPCHK(hipMalloc(&mem, off));
-  hipError_t e = hipMemset(mem, 0, off);
+  HIPCHK(hipMalloc(&mem, L.total));
+  hipError_t e = hipMemset(mem, 0, L.total);
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) {
     (void)hipFree(mem);
     return fail(LLMK_ERR_HIP, std::string("workspace init failed: ") + hipGetErrorString(e));
   }
-  char* base = (char*)mem;
   llmk_sampler* s = new llmk_sampler();
   s->device = device;
   s->max_batch = max_batch;
   s->max_vocab = max_vocab;
   s->mem = mem;
-  s->mem_bytes = off;
-  s->ws.row_arrive = (uint32_t*)(base + o_arrive);
-  s->ws.tile_part = (f2v*)(base + o_part);
-  s->ws.seg_meta = (u4v*)(base + o_meta);
-  s->ws.cand = (u2v*)(base + o_cand);
-  s->ws.slow_lock = (uint32_t*)(base + o_lock);
-  s->ws.slow_keys = (uint64_t*)(base + o_skeys);
-  s->ws.slow_p = (float*)(base + o_sp);
-  s->ws.slow_idx = (uint32_t*)(base + o_si);
-  s->ws.status = (uint32_t*)(base + o_status);
-  s->ws.cut = (u4v*)(base + o_cut);
-  s->ws.mtok = (uint32_t*)(base + o_mtok);
-  s->ws.zu = (float*)(base + o_zu);
-  s->ws.max_vocab = max_vocab;
-  s->ws.slow_slots = slots;
+  s->mem_bytes = L.total;
+  s->ws = ws_carve((char*)mem, L, max_vocab, slots);
   *out = s;
   g_last_error.clear();
   return LLMK_OK;
@@ -3686,9 +3719,12 @@ extern "C" int llmk_sampler_status(llmk_sampler* s, void* stream,
   return LLMK_OK;
 }
 
-static int sample_batch_impl(llmk_sampler* s, const llmk_sample_batch_args* in,
-                             void* stream, u4v* cut, uint32_t tp_clamp) {
-  if (!s) return fail(LLMK_ERR_INVALID_ARGUMENT, "sampler is NULL");
+// One sampling launch on workspace ws, sized for batches up to max_batch rows
+// of up to max_vocab logits with `pool` workgroup entries, on the current
+// device.
+static int sample_batch_run(const Ws& ws, uint32_t max_batch, uint32_t max_vocab, uint32_t pool,
+                            const llmk_sample_batch_args* in, void* stream, u4v* cut,
+                            uint32_t tp_clamp) {
   if (!in) return fail(LLMK_ERR_INVALID_ARGUMENT, "args is NULL");
   if (in->vocab == 0) return fail(LLMK_ERR_EMPTY_LOGITS, "Empty logits passed to sampler");
   if (in->batch == 0) return fail(LLMK_ERR_INVALID_ARGUMENT, "batch is 0");
@@ -3696,7 +3732,7 @@ static int sample_batch_impl(llmk_sampler* s, const llmk_sample_batch_args* in,
     return fail(LLMK_ERR_INVALID_ARGUMENT, "logits, uniforms and out_tokens are required");
   if (in->dtype != LLMK_F32 && in->dtype != LLMK_BF16 && in->dtype != LLMK_F16)
     return fail(LLMK_ERR_INVALID_ARGUMENT, "dtype must be LLMK_F32, LLMK_BF16 or LLMK_F16");
-  if (in->batch > s->max_batch || in->vocab > s->max_vocab)
+  if (in->batch > max_batch || in->vocab > max_vocab)
     return fail(LLMK_ERR_CAPACITY, "batch or vocab above the sampler's maxima");
   if (in->row_stride < in->vocab)
     return fail(LLMK_ERR_INVALID_ARGUMENT, "row_stride < vocab");
@@ -3743,7 +3779,6 @@ static int sample_batch_impl(llmk_sampler* s, const llmk_sample_batch_args* in,
   a.nchunks = (a.ntiles + CHUNK_TILES - 1) / CHUNK_TILES;
   // Segments per row: enough workgroups to cover the 256 CUs, whole 16-tile
   // chunks per segment, at most MAX_SEG segments.
-  const uint32_t pool = s->max_batch > MAX_WGS ? s->max_batch : MAX_WGS;
   uint32_t G = (256 + a.B - 1) / a.B;
   if (G > a.nchunks) G = a.nchunks;
   if (G > MAX_SEG) G = MAX_SEG;
@@ -3754,7 +3789,6 @@ static int sample_batch_impl(llmk_sampler* s, const llmk_sample_batch_args* in,
   a.G = (a.nchunks + cps - 1) / cps;
   a.xcd_map = (a.G > 1 && (a.B % 8) == 0) ? 1u : 0u;
 
-  HIPCHK(hipSetDevice(s->device));
   hipStream_t st = (hipStream_t)stream;
   size_t words = stream_lds_words(a.tps);
   if (finalize_lds_words() > words) words = finalize_lds_words();
@@ -3769,13 +3803,21 @@ static int sample_batch_impl(llmk_sampler* s, const llmk_sample_batch_args* in,
     return fail(LLMK_ERR_CAPACITY, "vocabulary too large for one workgroup's LDS tables");
   const dim3 grid(a.B * a.G), block(NT);
   if (a.dtype == LLMK_F32)
-    hipLaunchKernelGGL(stream_kernel<LLMK_F32>, grid, block, lds, st, a, s->ws);
+    hipLaunchKernelGGL(stream_kernel<LLMK_F32>, grid, block, lds, st, a, ws);
   else if (a.dtype == LLMK_BF16)
-    hipLaunchKernelGGL(stream_kernel<LLMK_BF16>, grid, block, lds, st, a, s->ws);
+    hipLaunchKernelGGL(stream_kernel<LLMK_BF16>, grid, block, lds, st, a, ws);
   else
-    hipLaunchKernelGGL(stream_kernel<LLMK_F16>, grid, block, lds, st, a, s->ws);
+    hipLaunchKernelGGL(stream_kernel<LLMK_F16>, grid, block, lds, st, a, ws);
   HIPCHK(hipGetLastError());
   return LLMK_OK;
+}
+
+static int sample_batch_impl(llmk_sampler* s, const llmk_sample_batch_args* in,
+                             void* stream, u4v* cut, uint32_t tp_clamp) {
+  if (!s) return fail(LLMK_ERR_INVALID_ARGUMENT, "sampler is NULL");
+  HIPCHK(hipSetDevice(s->device));
+  const uint32_t pool = s->max_batch > MAX_WGS ? s->max_batch : MAX_WGS;
+  return sample_batch_run(s->ws, s->max_batch, s->max_vocab, pool, in, stream, cut, tp_clamp);
 }
 
 extern "C" int llmk_sample_batch(llmk_sampler* s, const llmk_sample_batch_args* in,

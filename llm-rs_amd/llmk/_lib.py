@@ -22,6 +22,7 @@ LLMK_STATUS_INVALID_PARAMS = 0x1
 LLMK_STATUS_HISTORY_OVERFLOW = 0x2
 LLMK_STATUS_SLOT_TIMEOUT = 0x4
 LLMK_STATUS_HISTORY_FULL = 0x8
+LLMK_STATUS_NAN_LOGITS = 0x10
 LLMK_F32 = 0
 LLMK_BF16 = 1
 LLMK_F16 = 2

@@ -79,6 +79,98 @@ class DeviceBatch:
     hist_lengths: Optional[torch.Tensor] = None  # int32/uint32 [B]: per-row buffers
 
 
+def _on_device(dev: torch.device, **tensors) -> None:
+    """Every tensor handed to the C ABI must live on the logits' GPU: a host
+    pointer or another device's pointer would reach a kernel."""
+    if dev.type != "cuda":
+        raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT, "logits must be a CUDA (HIP) tensor")
+    for name, t in tensors.items():
+        if t is not None and t.device != dev:
+            raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT,
+                               f"{name} is on {t.device}, the logits on {dev}")
+
+
+def _flat(name: str, t: Optional[torch.Tensor], dtypes) -> None:
+    """Per-row arrays are read as dense vectors of one element type."""
+    if t is not None and (t.dtype not in dtypes or not t.is_contiguous()):
+        raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT,
+                           f"{name} must be a contiguous {' or '.join(map(str, dtypes))} tensor")
+
+
+_I32 = (torch.int32,)
+_F32 = (torch.float32,)
+
+
+def _batch_args(db: DeviceBatch, out_tokens: torch.Tensor,
+                out_ids: Optional[torch.Tensor], out_probs: Optional[torch.Tensor],
+                out_count: Optional[torch.Tensor]) -> "_lib.SampleBatchArgs":
+    """llmk_sample_batch_args for db, after checking every tensor's device,
+    element type and layout (nothing is converted, so nothing temporary has
+    to outlive the call)."""
+    lg = db.logits
+    if lg.dtype == torch.float32:
+        dt = _lib.LLMK_F32
+    elif lg.dtype == torch.bfloat16:
+        dt = _lib.LLMK_BF16
+    elif lg.dtype == torch.float16:
+        dt = _lib.LLMK_F16
+    else:
+        raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT,
+                           "logits must be float32, bfloat16 or float16")
+    if lg.dim() != 2 or lg.stride(1) != 1:
+        raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT,
+                           "logits must be [batch, >= vocab] with unit stride along the vocabulary")
+    fields = dict(uniforms=db.uniforms, temperature=db.temperature, top_k=db.top_k,
+                  top_p=db.top_p, min_p=db.min_p, repetition_penalty=db.repetition_penalty,
+                  presence_penalty=db.presence_penalty, frequency_penalty=db.frequency_penalty,
+                  hist_offsets=db.hist_offsets, hist_tokens=db.hist_tokens,
+                  allow_mask=db.allow_mask, hist_lengths=db.hist_lengths,
+                  out_tokens=out_tokens, out_ids=out_ids, out_probs=out_probs,
+                  out_count=out_count)
+    _on_device(lg.device, **fields)
+    if db.uniforms is None:
+        raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT, "uniforms are required")
+    for name in ("uniforms", "temperature", "top_p", "min_p", "repetition_penalty",
+                 "presence_penalty", "frequency_penalty", "out_probs"):
+        _flat(name, fields[name], _F32)
+    for name in ("top_k", "out_tokens", "out_ids", "out_count"):
+        _flat(name, fields[name], _I32)
+    for name in ("hist_offsets", "hist_tokens", "allow_mask", "hist_lengths"):
+        _flat(name, fields[name], _I32 + (getattr(torch, "uint32", torch.int32),))
+    B = lg.shape[0]
+    V = db.vocab if db.vocab is not None else lg.shape[1]
+    a = _lib.SampleBatchArgs()
+    a.logits = lg.data_ptr()
+    a.dtype = dt
+    a.batch = B
+    a.vocab = V
+    a.row_stride = lg.stride(0)
+    a.temperature = _ptr(db.temperature)
+    a.top_k = _ptr(db.top_k)
+    a.top_p = _ptr(db.top_p)
+    a.min_p = _ptr(db.min_p)
+    a.repetition_penalty = _ptr(db.repetition_penalty)
+    a.presence_penalty = _ptr(db.presence_penalty)
+    a.frequency_penalty = _ptr(db.frequency_penalty)
+    a.hist_offsets = _ptr(db.hist_offsets)
+    a.hist_tokens = _ptr(db.hist_tokens)
+    a.allow_mask = _ptr(db.allow_mask)
+    a.mask_words_per_row = 0 if db.allow_mask is None else db.allow_mask.shape[1]
+    a.uniforms = _ptr(db.uniforms)
+    a.out_tokens = _ptr(out_tokens)
+    a.out_ids = _ptr(out_ids)
+    a.out_probs = _ptr(out_probs)
+    cap = 0
+    if out_ids is not None:
+        cap = out_ids.shape[1]
+    elif out_probs is not None:
+        cap = out_probs.shape[1]
+    a.out_cap = cap
+    a.out_count = _ptr(out_count)
+    a.hist_lengths = _ptr(db.hist_lengths)
+    return a
+
+
 class HipSampler:
     """Owns an llmk_sampler handle (device workspace) on one GPU."""
 
@@ -111,49 +203,22 @@ class HipSampler:
                out_count: Optional[torch.Tensor] = None,
                stream: Optional[torch.cuda.Stream] = None) -> None:
         """Enqueue one batched sampling call; no allocation, no sync."""
-        lg = db.logits
-        if lg.dtype == torch.float32:
-            dt = _lib.LLMK_F32
-        elif lg.dtype == torch.bfloat16:
-            dt = _lib.LLMK_BF16
-        elif lg.dtype == torch.float16:
-            dt = _lib.LLMK_F16
-        else:
-            raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT,
-                               "logits must be float32, bfloat16 or float16")
-        B = lg.shape[0]
-        V = db.vocab if db.vocab is not None else lg.shape[1]
-        a = _lib.SampleBatchArgs()
-        a.logits = lg.data_ptr()
-        a.dtype = dt
-        a.batch = B
-        a.vocab = V
-        a.row_stride = lg.stride(0)
-        a.temperature = _ptr(db.temperature)
-        a.top_k = _ptr(db.top_k)
-        a.top_p = _ptr(db.top_p)
-        a.min_p = _ptr(db.min_p)
-        a.repetition_penalty = _ptr(db.repetition_penalty)
-        a.presence_penalty = _ptr(db.presence_penalty)
-        a.frequency_penalty = _ptr(db.frequency_penalty)
-        a.hist_offsets = _ptr(db.hist_offsets)
-        a.hist_tokens = _ptr(db.hist_tokens)
-        a.allow_mask = _ptr(db.allow_mask)
-        a.mask_words_per_row = 0 if db.allow_mask is None else db.allow_mask.shape[1]
-        a.uniforms = _ptr(db.uniforms)
-        a.out_tokens = _ptr(out_tokens)
-        a.out_ids = _ptr(out_ids)
-        a.out_probs = _ptr(out_probs)
-        cap = 0
-        if out_ids is not None:
-            cap = out_ids.shape[1]
-        elif out_probs is not None:
-            cap = out_probs.shape[1]
-        a.out_cap = cap
-        a.out_count = _ptr(out_count)
-        a.hist_lengths = _ptr(db.hist_lengths)
-        st = stream if stream is not None else torch.cuda.current_stream()
-        rc = self._lib.llmk_sample_batch(self._h, ctypes.byref(a), ctypes.c_void_p(st.cuda_stream))
+        a = _batch_args(db, out_tokens, out_ids, out_probs, out_count)
+        self.launch_prepared(a, self._stream(db.logits, stream))
+
+    def prepare(self, db: DeviceBatch, out_tokens: torch.Tensor,
+                out_ids: Optional[torch.Tensor] = None,
+                out_probs: Optional[torch.Tensor] = None,
+                out_count: Optional[torch.Tensor] = None) -> "_lib.SampleBatchArgs":
+        """The checked llmk_sample_batch_args of a call, for a caller that
+        launches the same buffers many times (launch_prepared)."""
+        return _batch_args(db, out_tokens, out_ids, out_probs, out_count)
+
+    def launch_prepared(self, a: "_lib.SampleBatchArgs", stream: torch.cuda.Stream) -> None:
+        """llmk_sample_batch on arguments from prepare(); the tensors they
+        point at must still be alive."""
+        rc = self._lib.llmk_sample_batch(self._h, ctypes.byref(a),
+                                         ctypes.c_void_p(stream.cuda_stream))
         if rc != 0:
             raise SamplerError(rc, _lib.last_error())
 
@@ -171,33 +236,49 @@ class HipSampler:
 
     def status(self) -> int:
         v = ctypes.c_uint32()
-        rc = self._lib.llmk_sampler_status(self._h, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream), ctypes.byref(v))
+        st = torch.cuda.current_stream(self.device)
+        rc = self._lib.llmk_sampler_status(self._h, ctypes.c_void_p(st.cuda_stream), ctypes.byref(v))
         if rc != 0:
             raise SamplerError(rc, _lib.last_error())
         return v.value
 
     # ---- mask forms (sampler.rs:160-216), batched, in place --------------
-    def _mask(self, fn: str, logits: torch.Tensor, param: torch.Tensor,
+    def _stream(self, logits: torch.Tensor, stream: Optional[torch.cuda.Stream]):
+        return stream if stream is not None else torch.cuda.current_stream(logits.device)
+
+    @staticmethod
+    def _keep(st, *tmps: torch.Tensor) -> None:
+        """Converted copies are freed when the wrapper returns, while the
+        kernel may still be queued on `st`: tell the caching allocator."""
+        for t in tmps:
+            t.record_stream(st)
+
+    def _mask(self, fn: str, logits: torch.Tensor, param: torch.Tensor, dtype: torch.dtype,
               stream: Optional[torch.cuda.Stream]) -> None:
         if logits.dtype != torch.float32 or logits.dim() != 2 or logits.stride(1) != 1:
             raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT,
                                "logits must be a row-major float32 [batch, vocab] tensor")
-        st = stream if stream is not None else torch.cuda.current_stream()
+        _on_device(logits.device, param=param)
+        if param.numel() != logits.shape[0]:
+            raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT, "one parameter per row")
+        st = self._stream(logits, stream)
+        p = param.to(dtype).contiguous()
         rc = getattr(self._lib, fn)(self._h, logits.data_ptr(), logits.shape[0], logits.shape[1],
-                                    logits.stride(0), param.data_ptr(),
+                                    logits.stride(0), p.data_ptr(),
                                     ctypes.c_void_p(st.cuda_stream))
         if rc != 0:
             raise SamplerError(rc, _lib.last_error())
+        self._keep(st, p)
 
     def apply_top_k(self, logits: torch.Tensor, top_k: torch.Tensor,
                     stream: Optional[torch.cuda.Stream] = None) -> None:
         """sampler.rs:160-173 on every row: logits [B, V] float32, top_k [B] int32."""
-        self._mask("llmk_apply_top_k", logits, top_k.to(torch.int32).contiguous(), stream)
+        self._mask("llmk_apply_top_k", logits, top_k, torch.int32, stream)
 
     def apply_top_p(self, logits: torch.Tensor, top_p: torch.Tensor,
                     stream: Optional[torch.cuda.Stream] = None) -> None:
         """sampler.rs:176-216 on every row: logits [B, V] float32, top_p [B] float32."""
-        self._mask("llmk_apply_top_p", logits, top_p.to(torch.float32).contiguous(), stream)
+        self._mask("llmk_apply_top_p", logits, top_p, torch.float32, stream)
 
     def apply_logit_bias(self, logits: torch.Tensor, offsets: torch.Tensor,
                          tokens: torch.Tensor, values: torch.Tensor,
@@ -207,16 +288,21 @@ class HipSampler:
         if logits.dtype != torch.float32 or logits.dim() != 2 or logits.stride(1) != 1:
             raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT,
                                "logits must be a row-major float32 [batch, vocab] tensor")
+        _on_device(logits.device, offsets=offsets, tokens=tokens, values=values)
+        if offsets.numel() != logits.shape[0] + 1 or tokens.numel() != values.numel():
+            raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT,
+                               "offsets must hold batch + 1 entries, tokens and values one per pair")
         off = offsets.to(torch.int32).contiguous()
         tok = tokens.to(torch.int32).contiguous()
         val = values.to(torch.float32).contiguous()
-        st = stream if stream is not None else torch.cuda.current_stream()
+        st = self._stream(logits, stream)
         rc = self._lib.llmk_apply_logit_bias(self._h, logits.data_ptr(), logits.shape[0],
                                              logits.shape[1], logits.stride(0), off.data_ptr(),
                                              tok.data_ptr(), val.data_ptr(),
                                              ctypes.c_void_p(st.cuda_stream))
         if rc != 0:
             raise SamplerError(rc, _lib.last_error())
+        self._keep(st, off, tok, val)
 
     def history_append(self, hist_offsets: torch.Tensor, hist_lengths: torch.Tensor,
                        hist_tokens: torch.Tensor, capacity: int, tokens: torch.Tensor,
@@ -227,7 +313,13 @@ class HipSampler:
             if t.dtype != torch.int32 or not t.is_contiguous():
                 raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT,
                                    "history arrays and tokens must be contiguous int32")
-        st = stream if stream is not None else torch.cuda.current_stream()
+        _on_device(tokens.device, hist_offsets=hist_offsets, hist_lengths=hist_lengths,
+                   hist_tokens=hist_tokens)
+        B = tokens.shape[0]
+        if hist_offsets.numel() < B or hist_lengths.numel() < B:
+            raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT,
+                               "hist_offsets and hist_lengths need one entry per row")
+        st = self._stream(tokens, stream)
         rc = self._lib.llmk_history_append(self._h, tokens.shape[0], hist_offsets.data_ptr(),
                                            hist_lengths.data_ptr(), hist_tokens.data_ptr(),
                                            capacity, tokens.data_ptr(),

@@ -302,3 +302,48 @@ def test_history_buffers_and_device_append(sampler):
         for b in np.nonzero(~full)[0]:
             assert nb[b * cap + ln[b]] == gpu[0][b]
         assert sampler.status() == _lib.LLMK_STATUS_HISTORY_FULL
+
+
+def test_nan_logits_raise_the_status_bit(sampler):
+    """NaN logits are read as -inf (as the mirror oracle does) and raise
+    LLMK_STATUS_NAN_LOGITS, the device form of sampler.rs's NAN_WARNED
+    (sampler.rs:7-9, :74-76): on the fast candidate path (top-k 50), the
+    general one (top-k 600 over flat logits), the slow path (top-k off, a
+    nucleus of ~10^4 tokens) and for a penalised history token.  A greedy row
+    (whose reference branch returns before the warning) and a NaN under a
+    disallowed mask bit raise nothing; +inf raises the bit too."""
+    V = 30000
+    rng = np.random.default_rng(21)
+    cases = {
+        "fast": dict(sd=3.0, T=0.8, K=50, P=0.95),
+        "general": dict(sd=0.5, T=1.0, K=600, P=1.0),
+        "slow": dict(sd=0.5, T=1.0, K=0, P=0.99),
+        "history": dict(sd=3.0, T=0.8, K=40, P=0.9, R=1.3, hist=True),
+    }
+    for name, c in cases.items():
+        lg = rng.normal(0, c["sd"], (3, V)).astype(np.float32)
+        lg[:, [5, 999, 20001]] = np.nan
+        hists = [[999, 3, 3, 20001] for _ in range(3)] if c.get("hist") else None
+        w = workload(lg, T=c["T"], K=c["K"], P=c["P"], R=c.get("R", 1.0), hists=hists,
+                     u=rng.random(3).astype(np.float32))
+        sampler.status()
+        check(sampler, w, cap=CAP, label=f"NaN {name}")
+        assert sampler.status() & _lib.LLMK_STATUS_NAN_LOGITS, name
+    # greedy rows: no warning (the reference returns before it); the token
+    # is the first maximum, NaN read as -inf
+    lg = rng.normal(0, 3, (2, V)).astype(np.float32)
+    lg[:, 17] = np.nan
+    sampler.status()
+    check(sampler, workload(lg, T=0.0), cap=4, label="NaN greedy")
+    assert not sampler.status() & _lib.LLMK_STATUS_NAN_LOGITS
+    # a NaN at a disallowed token is -inf before anything reads it
+    mask = np.full((2, (V + 31) // 32), 0xFFFFFFFF, np.uint32)
+    mask[:, 17 >> 5] &= ~np.uint32(1 << (17 & 31))
+    check(sampler, workload(lg, T=0.9, K=30, mask=mask), cap=8, label="NaN masked")
+    assert not sampler.status() & _lib.LLMK_STATUS_NAN_LOGITS
+    # +inf: l - max is inf - inf for the reference
+    lg2 = lg.copy()
+    lg2[:, 17] = np.inf
+    print("[case] +inf logit", flush=True)
+    run_gpu(sampler, workload(lg2, T=0.9, K=30), 8)
+    assert sampler.status() & _lib.LLMK_STATUS_NAN_LOGITS
