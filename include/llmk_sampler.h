@@ -128,6 +128,21 @@ int llmk_sampler_create(llmk_sampler** out, int device, uint32_t max_batch,
 int llmk_sample_batch(llmk_sampler* s, const llmk_sample_batch_args* args,
                       void* hip_stream);
 
+/* llmk_sample_batch with no handle and no allocation of any kind.  It has no
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments, semantics and results as
+ * llmk_sample_batch, on the current device; its workspace is a static
+ * device array of 98 MiB that each GPU the library runs on holds
+ * until the process ends, sized for batch <= 256 and vocab <= 262144 (larger
+ * calls fail with LLMK_ERR_CAPACITY).  `status`: optional device u32 into
+ * which the call ORs its LLMK_STATUS_* bits (the caller clears it); NULL =
+ * the bits are dropped.  Every call on one GPU shares that workspace: calls
+ * that overlap on one GPU (two streams, or two threads) race and give wrong
+ * results; calls in one stream's order are safe. */
+int llmk_sample_batch_static(const llmk_sample_batch_args* args, uint32_t* status,
+                             void* hip_stream);
+
 /* Mask-form top-k, batched and in place: replaces apply_top_k
  * (llm-core/src/sampler.rs:160-173) called on each row.  In row b every
  * logit below the top_k[b]-th largest value becomes -inf; values equal to

@@ -36,6 +36,7 @@
 
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "llmk_numerics.h"
@@ -3823,6 +3824,81 @@ static int sample_batch_impl(llmk_sampler* s, const llmk_sample_batch_args* in,
 extern "C" int llmk_sample_batch(llmk_sampler* s, const llmk_sample_batch_args* in,
                                  void* stream) {
   return sample_batch_impl(s, in, stream, nullptr, 0u);
+}
+
+// ---- llmk_sample_batch_static: the sampling call with no allocation ------
+// Limits of the static workspace: batches up to 256 rows of up to 2^18
+// logits, 512 workgroup entries (B x G stays below 256 + B <= 512 for every
+// B <= 256, so the launch shape is that of a handle) and 8 slow-path slots
+// (rows b, b + 8, ... share one; a row waits for its slot's holder).
+constexpr uint32_t STATIC_MAX_BATCH = 256;
+constexpr uint32_t STATIC_MAX_VOCAB = 1u << 18;
+constexpr uint32_t STATIC_POOL = 512;
+constexpr uint32_t STATIC_SLOTS = 8;
+constexpr WsLayout STATIC_LAYOUT =
+    ws_layout(STATIC_MAX_BATCH, STATIC_MAX_VOCAB, STATIC_POOL, STATIC_SLOTS);
+static_assert(STATIC_LAYOUT.total <= (160ull << 20), "static workspace above 160 MiB");
+
+// One copy per GPU, held until the process ends.  Host code must not use
+// this name as an address: it is a host-side stand-in for the symbol; the
+// device address comes from hipGetSymbolAddress.
+static __device__ __align__(256) uint8_t scratch[STATIC_LAYOUT.total];
+
+constexpr int STATIC_MAX_DEVICES = 64;
+static std::mutex g_static_mu;
+static char* g_static_ptr[STATIC_MAX_DEVICES];  // device address of scratch, per device
+
+// Clears what every call must find at zero: the rows' arrival counters, the
+// slow-path slot locks and the status word (a fill kernel, so the call can
+// be captured in a HIP graph).
+__global__ __launch_bounds__(256) void static_clear_kernel(uint32_t* arrive, uint32_t n_arrive,
+                                                           uint32_t* lock, uint32_t n_lock,
+                                                           uint32_t* status) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n_arrive) arrive[i] = 0;
+  if (i < n_lock) lock[i] = 0;
+  if (i == 0) status[0] = 0;
+}
+
+// Device address of this device's scratch array, looked up (and the
+// kernels' LDS limits set) on the first call on each device.
+static int static_scratch(int dev, char** out) {
+  if (dev < 0 || dev >= STATIC_MAX_DEVICES)
+    return fail(LLMK_ERR_UNSUPPORTED, "device ordinal above 63");
+  std::lock_guard<std::mutex> g(g_static_mu);
+  if (!g_static_ptr[dev]) {
+    const int rc = set_kernel_attributes();
+    if (rc != LLMK_OK) return rc;
+    void* ptr = nullptr;
+    HIPCHK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    if (!ptr) return fail(LLMK_ERR_HIP, "hipGetSymbolAddress(scratch) returned NULL");
+    g_static_ptr[dev] = (char*)ptr;
+  }
+  *out = g_static_ptr[dev];
+  return LLMK_OK;
+}
+
+extern "C" int llmk_sample_batch_static(const llmk_sample_batch_args* in, uint32_t* status,
+                                        void* stream) {
+  if (!in) return fail(LLMK_ERR_INVALID_ARGUMENT, "args is NULL");
+  if (in->batch > STATIC_MAX_BATCH || in->vocab > STATIC_MAX_VOCAB)
+    return fail(LLMK_ERR_CAPACITY,
+                "llmk_sample_batch_static serves batch <= 256 and vocab <= 262144 (got batch " +
+                    std::to_string(in->batch) + ", vocab " + std::to_string(in->vocab) +
+                    "); use a handle from llmk_sampler_create");
+  int dev = 0;
+  HIPCHK(hipGetDevice(&dev));
+  char* base = nullptr;
+  const int rc = static_scratch(dev, &base);
+  if (rc != LLMK_OK) return rc;
+  Ws ws = ws_carve(base, STATIC_LAYOUT, STATIC_MAX_VOCAB, STATIC_SLOTS);
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(static_clear_kernel, dim3((STATIC_MAX_BATCH + 255) / 256), dim3(256), 0, st,
+                     ws.row_arrive, STATIC_MAX_BATCH, ws.slow_lock, STATIC_SLOTS, ws.status);
+  HIPCHK(hipGetLastError());
+  if (status) ws.status = status;
+  return sample_batch_run(ws, STATIC_MAX_BATCH, STATIC_MAX_VOCAB, STATIC_POOL, in, stream,
+                          nullptr, 0u);
 }
 
 // Checks shared by the mask forms: in-place f32 rows.

@@ -10,5 +10,6 @@ from .sampler import (  # noqa: F401
     apply_top_p,
     device_batch_from_params,
     sample,
+    sample_batch_static,
     sample_logits,
 )

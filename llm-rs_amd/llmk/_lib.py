@@ -38,6 +38,7 @@ EXPORTED_SYMBOLS = (
     "llmk_apply_top_p",
     "llmk_apply_logit_bias",
     "llmk_history_append",
+    "llmk_sample_batch_static",
 )
 
 
@@ -90,6 +91,8 @@ def load():
     lib.llmk_sampler_create.restype = ctypes.c_int
     lib.llmk_sample_batch.argtypes = [vp, ctypes.POINTER(SampleBatchArgs), vp]
     lib.llmk_sample_batch.restype = ctypes.c_int
+    lib.llmk_sample_batch_static.argtypes = [ctypes.POINTER(SampleBatchArgs), vp, vp]
+    lib.llmk_sample_batch_static.restype = ctypes.c_int
     lib.llmk_sampler_status.argtypes = [vp, vp, ctypes.POINTER(ctypes.c_uint32)]
     lib.llmk_sampler_status.restype = ctypes.c_int
     lib.llmk_sampler_destroy.argtypes = [vp]

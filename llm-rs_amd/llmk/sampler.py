@@ -171,6 +171,28 @@ def _batch_args(db: DeviceBatch, out_tokens: torch.Tensor,
     return a
 
 
+def sample_batch_static(db: DeviceBatch, out_tokens: torch.Tensor,
+                        out_ids: Optional[torch.Tensor] = None,
+                        out_probs: Optional[torch.Tensor] = None,
+                        out_count: Optional[torch.Tensor] = None,
+                        status: Optional[torch.Tensor] = None,
+                        stream: Optional[torch.cuda.Stream] = None) -> None:
+    """llmk_sample_batch_static: the batched call without a handle and without
+    allocating (batch <= 256, vocab <= 262144), on the logits' device.
+    `status`: optional int32 [1] device tensor the call ORs its status bits
+    into.  Calls that overlap on one GPU race on its static workspace."""
+    lib = _lib.load()
+    a = _batch_args(db, out_tokens, out_ids, out_probs, out_count)
+    _on_device(db.logits.device, status=status)
+    _flat("status", status, _I32)
+    st = stream if stream is not None else torch.cuda.current_stream(db.logits.device)
+    with torch.cuda.device(db.logits.device):
+        rc = lib.llmk_sample_batch_static(ctypes.byref(a), _ptr(status),
+                                          ctypes.c_void_p(st.cuda_stream))
+    if rc != 0:
+        raise SamplerError(rc, _lib.last_error())
+
+
 class HipSampler:
     """Owns an llmk_sampler handle (device workspace) on one GPU."""
 
