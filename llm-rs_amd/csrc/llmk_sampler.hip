@@ -2793,9 +2793,27 @@ __device__ __forceinline__ void tile_reduce(const TileEnv& E, const float (&v)[1
                                             uint32_t slot, const IDX& idx,
                                             uint32_t& since, int lane, uint32_t nr = 4) {
   float lm = NEG_INF;
+  if (E.P.mode == MODE_SAMPLE) {
+    // v_maximum3_f32 propagates NaN at the cost of v_max3_f32, so one
+    // compare per lane finds a logit that makes the reference's
+    // probabilities NaN: NaN, or +inf (whose l - max is inf - inf).
+    // Masked logits are -inf by now.  Greedy rows return before the
+    // reference's NaN check (sampler.rs:40-50, :74-76).
 #pragma unroll
-  for (int j = 0; j < 16; ++j)
-    if ((uint32_t)(j >> 2) < nr) lm = fmaxf(lm, v[j]);
+    for (int j = 0; j < 16; ++j)
+      if ((uint32_t)(j >> 2) < nr) lm = __builtin_elementwise_maximum(lm, v[j]);
+    if (__ballot(!(lm < __builtin_huge_valf()))) {
+      if (lane == 0) __atomic_fetch_or(&E.misc[M_FLAGS], FLAG_NAN, __ATOMIC_RELAXED);
+      lm = NEG_INF;  // the tile's maximum with NaN read as -inf
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if ((uint32_t)(j >> 2) < nr) lm = fmaxf(lm, v[j]);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if ((uint32_t)(j >> 2) < nr) lm = fmaxf(lm, v[j]);
+  }
   lm = wave_max(lm);
   if (E.P.mode == MODE_GREEDY) {
     uint32_t bi = EMPTY;
@@ -3205,16 +3223,6 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) v[4 * r + q] = exclude(v[4 * r + q], x, sh4 + q);
       }
-    }
-    // a logit that makes the reference's probabilities NaN: NaN, or +inf
-    // (whose l - max is inf - inf); masked ones are -inf by now.  Sampling
-    // rows only: the reference's greedy branch returns first (sampler.rs:40-50,
-    // :74-76)
-    if (P.mode == MODE_SAMPLE) {
-      uint64_t bad = 0;
-#pragma unroll
-      for (int j = 0; j < 16; ++j) bad |= __ballot(!(v[j] < __builtin_huge_valf()));
-      if (bad && lane == 0) __atomic_fetch_or(&misc[M_FLAGS], FLAG_NAN, __ATOMIC_RELAXED);
     }
     tile_reduce(E, v, t, [&](int j) -> uint32_t {
       return tb + 256u * (j >> 2) + 4u * (uint32_t)lane + (j & 3);
