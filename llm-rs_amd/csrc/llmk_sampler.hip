@@ -144,16 +144,49 @@ struct RowP {
 
 __device__ __forceinline__ bool finitef(float x) { return __builtin_isfinite(x); }
 
-__device__ __forceinline__ RowP row_params(const Args& a, uint32_t b) {
+// Defaults of absent per-row arrays (SampleParams, llm-core/src/types.rs:
+// 186-195), read in place of the array: every load is then unconditional.
+__constant__ float kOneF = 1.0f;
+__constant__ uint32_t kZeroU = 0u;
+template <class T>
+__device__ __forceinline__ const T* row_or(const T* p, uint32_t b, const void* dflt) {
+  return p ? p + b : (const T*)dflt;
+}
+
+// The row's parameters, uniform, history extent and uniform as loaded: all
+// requested together, before anything branches on one of them, so that they
+// cost one round trip.
+struct RowIn {
+  float T, top_p, min_p, rp, pp, fp, u;
+  int32_t K;
+  uint32_t h0, hn, hl;
+};
+__device__ __forceinline__ RowIn load_row(const Args& a, uint32_t b) {
+  RowIn r;
+  r.T = *G(row_or(a.T, b, &kOneF));
+  r.top_p = *G(row_or(a.top_p, b, &kOneF));
+  r.min_p = *G((const float*)row_or(a.min_p, b, &kZeroU));
+  r.rp = *G(row_or(a.rp, b, &kOneF));
+  r.pp = *G((const float*)row_or(a.pp, b, &kZeroU));
+  r.fp = *G((const float*)row_or(a.fp, b, &kZeroU));
+  r.K = *G((const int32_t*)row_or(a.top_k, b, &kZeroU));
+  r.u = *G(a.u + b);
+  r.h0 = *G(row_or(a.hoff, b, &kZeroU));
+  r.hn = *G(row_or(a.hoff, b + 1, &kZeroU));
+  r.hl = *G(row_or(a.hlen, b, &kZeroU));
+  return r;
+}
+
+__device__ __forceinline__ RowP row_params(const Args& a, const RowIn& in) {
   RowP r;
-  r.T = a.T ? a.T[b] : 1.0f;
-  r.top_p = a.top_p ? a.top_p[b] : 1.0f;
+  r.T = in.T;
+  r.top_p = in.top_p;
   if (a.tp_clamp) r.top_p = r.top_p < 0.0f ? 0.0f : (r.top_p < 1.0f ? r.top_p : 1.0f);
-  r.min_p = a.min_p ? a.min_p[b] : 0.0f;
-  r.rp = a.rp ? a.rp[b] : 1.0f;
-  r.pp = a.pp ? a.pp[b] : 0.0f;
-  r.fp = a.fp ? a.fp[b] : 0.0f;
-  r.K = a.top_k ? a.top_k[b] : 0;
+  r.min_p = in.min_p;
+  r.rp = in.rp;
+  r.pp = in.pp;
+  r.fp = in.fp;
+  r.K = in.K;
   const bool bad = !finitef(r.T) || r.K < 0 || !finitef(r.top_p) ||
                    !finitef(r.min_p) || !(r.min_p >= 0.0f) || !finitef(r.rp) ||
                    !finitef(r.pp) || !finitef(r.fp);
@@ -3023,19 +3056,17 @@ template <int DT>
 __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   extern __shared__ __align__(16) uint32_t smem[];
   const uint32_t tid = threadIdx.x;
-  const int lane = (int)(tid & 63), wv = (int)(tid >> 6);
+  const int lane = (int)(tid & 63);
+  const int wv = __builtin_amdgcn_readfirstlane((int)(tid >> 6));  // wave-uniform
   uint32_t b, g;
   wg_to_row_seg(a, blockIdx.x, b, g);
-  const RowP P = row_params(a, b);
-  const float u_row = G(a.u)[b];
-  if (P.mode == MODE_INVALID) {
-    if (g == 0 && tid == 0) {
-      a.out_tok[b] = LLMK_INVALID_TOKEN;
-      if (a.out_cnt) a.out_cnt[b] = 0;
-      atomicOr(w.status, LLMK_STATUS_INVALID_PARAMS);
-    }
-    return;
-  }
+  // The row's parameters and history extent, ahead of every tile request
+  // (behind them they would take microseconds).
+  const RowIn rin = load_row(a, b);
+  const RowP P = row_params(a, rin);
+  const float u_row = rin.u;
+  const uint32_t h0 = rin.h0;
+  uint32_t h1 = a.hlen ? h0 + rin.hl : rin.hn;
   const uint32_t t0 = g * a.tps;
   const uint32_t t1 = min(t0 + a.tps, a.ntiles);
   const uint32_t lo = t0 * TILE, hi = min(a.V, t1 * TILE);
@@ -3050,12 +3081,27 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   hist_carve(h, hb, nwords);
   LDS uint32_t* btot = hb + hist_lds_words(nwords);  // NW words
   h.lo = lo;
-  const bool need_pen = P.rp != 1.0f || P.pp != 0.0f || P.fp != 0.0f;
-  uint32_t h0 = 0, h1 = 0;
-  if (a.hoff) {  // loaded unconditionally, in parallel with the parameters
-    h0 = G(a.hoff)[b];
-    h1 = a.hlen ? h0 + G(a.hlen)[b] : G(a.hoff)[b + 1];
+  // Waves 0..TW-1 load the history tokens (TQ per lane per pass); every
+  // wave then requests its first two tiles.
+  constexpr uint32_t TW = 8;
+  constexpr int TQ = 4;  // tokens per lane per pass
+  const void* row = (const char*)a.logits +
+                    (uint64_t)b * a.stride * (DT == LLMK_F32 ? 4u : 2u);
+  const uint32_t* mrow = a.mask ? a.mask + (uint64_t)b * a.mask_words : nullptr;
+  Raw ra, rb;
+  uint32_t ta = t0 + (uint32_t)wv, tb2 = t0 + (uint32_t)wv + NW;
+  ta = ta < t1 ? ta : EMPTY;
+  tb2 = tb2 < t1 ? tb2 : EMPTY;
+  const bool tok_wave = (uint32_t)wv < TW;
+  if (P.mode == MODE_INVALID) {
+    if (g == 0 && tid == 0) {
+      a.out_tok[b] = LLMK_INVALID_TOKEN;
+      if (a.out_cnt) a.out_cnt[b] = 0;
+      atomicOr(w.status, LLMK_STATUS_INVALID_PARAMS);
+    }
+    return;
   }
+  const bool need_pen = P.rp != 1.0f || P.pp != 0.0f || P.fp != 0.0f;
   if (!need_pen) h1 = h0;
   // history tokens exist: their positions are excluded from the vocabulary
   // tiles and reduced in virtual tiles, one per 16-tile chunk
@@ -3064,11 +3110,6 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   // no more distinct history tokens than ranks: no token can be dropped
   const bool early = h1 - h0 <= U_MAX;
   const bool collect = P.mode == MODE_SAMPLE && P.Kc > 0;
-  const void* row = (const char*)a.logits +
-                    (uint64_t)b * a.stride * (DT == LLMK_F32 ? 4u : 2u);
-  const uint32_t* mrow = a.mask ? a.mask + (uint64_t)b * a.mask_words : nullptr;
-  // The tile environment first: its kernel-argument loads then complete
-  // before the tiles are requested (behind them they take microseconds).
   TileEnv E;
   E.P = P;
   E.V = a.V;
@@ -3082,20 +3123,15 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   E.lpart = a.G == 1 ? (LDS f2v*)(smem + a.lds_part) : nullptr;
   E.lcand = a.G == 1 ? (LDS u2v*)(smem + a.lds_cand) : nullptr;
   const uint32_t nch = (nwords + 511) / 512;  // chunks of this segment
-  // Waves 0..TW-1 load the history tokens (TQ per lane per pass); every
-  // wave then requests its first two tiles.
-  constexpr uint32_t TW = 8;
-  constexpr int TQ = 4;  // tokens per lane per pass
-  Raw ra, rb;
-  uint32_t ta = t0 + (uint32_t)wv, tb2 = t0 + (uint32_t)wv + NW;
-  ta = ta < t1 ? ta : EMPTY;
-  tb2 = tb2 < t1 ? tb2 : EMPTY;
-  const bool tok_wave = (uint32_t)wv < TW;
   uint32_t tk[TQ];
 #pragma unroll
-  for (int q = 0; q < TQ; ++q) {
-    const uint32_t i = h0 + q * (TW * WAVE) + tid;
-    tk[q] = (tok_wave && i < h1) ? G(a.htok)[i] : EMPTY;
+  for (int q = 0; q < TQ; ++q) tk[q] = EMPTY;
+  if (tok_wave && have) {
+#pragma unroll
+    for (int q = 0; q < TQ; ++q) {
+      const uint32_t i = h0 + q * (TW * WAVE) + tid;
+      tk[q] = i < h1 ? G(a.htok)[i] : EMPTY;
+    }
   }
   if (collect) {
     for (uint32_t i = tid; i < NBINS; i += NT) hf[i] = 0;
@@ -3110,20 +3146,19 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   }
   // The history tokens arrive before any tile is requested: behind the first
   // tiles of every workgroup they would take several microseconds, and no
-  // tile can be reduced before the tables are built.  (Unconditional, so that
-  // no path reaches the insertion below with the tokens still in flight.)
+  // tile can be reduced before the tables are built.
+  if (tok_wave) {
 #pragma unroll
-  for (int q = 0; q < TQ; ++q) asm volatile("" ::"v"(tk[q]));
+    for (int q = 0; q < TQ; ++q) asm volatile("" ::"v"(tk[q]));
+  }
   __syncthreads();
-  // the logits of the first pass's history tokens, requested ahead of the
-  // tiles so that the gather after the rank tables finds them in L2
   float pf[TQ];
 #pragma unroll
-  for (int q = 0; q < TQ; ++q)
-    pf[q] = (have && tk[q] >= lo && tk[q] < hi) ? load_logit<DT>(row, tk[q]) : 0.0f;
-  // With history, the tiles are requested after the bitmap barrier: a wave
-  // whose requests fill the memory pipeline stalls at its next request for
-  // microseconds, and every wave waits at that barrier.
+  for (int q = 0; q < TQ; ++q) pf[q] = 0.0f;
+  // Without history, the tiles now.  With history, they are requested after
+  // the bitmap barrier: requests queued ahead of the history tokens and
+  // their logits would delay them by microseconds, and the tables cannot be
+  // built without them.
   if (!have) {
     if (ta != EMPTY) load_tile<DT>(a, row, mrow, h, ta, lane, ra);
     if (tb2 != EMPTY) load_tile<DT>(a, row, mrow, h, tb2, lane, rb);
@@ -3148,10 +3183,19 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
         }
       }
     };
-    if (tok_wave)
+    if (tok_wave) {
       each_token([&](uint32_t t) {
         __atomic_fetch_or(&h.bitmap[(t - lo) >> 5], 1u << (t & 31), __ATOMIC_RELAXED);
       });
+      // the logits of the first pass's history tokens, requested now (after
+      // the insertions, which must not wait for them) so that the gather
+      // after the rank tables finds them in L2; token waves only: a wait
+      // that the others executed, even with no lane loading, would wait for
+      // their tiles
+#pragma unroll
+      for (int q = 0; q < TQ; ++q)
+        if (tk[q] >= lo && tk[q] < hi) pf[q] = load_logit<DT>(row, tk[q]);
+    }
     __syncthreads();
     // the token waves of the early path request theirs after the tables
     if (!(early && tok_wave)) {
