@@ -194,6 +194,36 @@ int llmk_history_append(llmk_sampler* s, uint32_t batch, const uint32_t* hist_of
                         uint32_t* hist_lengths, uint32_t* hist_tokens, uint32_t capacity,
                         const uint32_t* tokens, void* hip_stream);
 
+/* Speculative-decoding verification, batched: the residual resampling that
+ * docs/mlc-contracts.md:83-84 describes (BatchVerifyDraftTokensWithProb-
+ * AfterTopP) at the hook the reference leaves for it (llm-core/src/
+ * backend.rs:20-22, "so the scheduler can apply speculative decoding"); the
+ * reference itself has no implementation.  Row b verifies draft token
+ * draft_tokens[b] against the target distribution p that llmk_sample_batch
+ * returned for the row: its kept list ids/probs[b * list_cap ..] (in
+ * (p desc, idx asc) order) and counts[b], i.e. out_ids/out_probs/out_count
+ * with out_cap = list_cap; p is 0 outside the list.  draft_probs[b *
+ * draft_stride + t] is the draft model's probability of token t (an id >= vocab
+ * in a list, which the sampler never writes, reads q = 0).
+ *   accept iff u_accept[b] * q(d) < p(d)  (the contract's reject when
+ *   r >= p/q): out_tokens[b] = d, out_accepted[b] = 1;
+ *   else out_accepted[b] = 0 and out_tokens[b] is drawn from the residual
+ *   max(p - q, 0) over the kept list (one f32 subtraction each): R = its
+ *   sequential f32 sum in list order; the first entry whose running sum of
+ *   residual/R reaches u_resample[b] (the reference's `r <= cumulative`,
+ *   sampler.rs:113-124), else the last entry with a positive residual; when
+ *   R = 0, the same draw over p itself.
+ * A chain of k draft tokens is k rows, one per position; the caller keeps
+ * the accepted prefix and the first resampled token.  A row whose count is 0
+ * or above list_cap (the list was cut) or whose draft token is >= vocab gets
+ * LLMK_INVALID_TOKEN and raises LLMK_STATUS_INVALID_PARAMS.  Device arrays;
+ * enqueued on hip_stream; allocates nothing. */
+int llmk_verify_batch(llmk_sampler* s, uint32_t batch, uint32_t vocab, const uint32_t* ids,
+                      const float* probs, uint32_t list_cap, const uint32_t* counts,
+                      const uint32_t* draft_tokens, const float* draft_probs,
+                      uint64_t draft_stride, const float* u_accept, const float* u_resample,
+                      uint32_t* out_tokens, uint32_t* out_accepted, void* hip_stream);
+
 /* Reads and clears the device status word (OR of LLMK_STATUS_* bits raised by
  * calls since the last read).  Synchronises `hip_stream`. */
 int llmk_sampler_status(llmk_sampler* s, void* hip_stream, uint32_t* status);

@@ -862,7 +862,8 @@ __device__ __forceinline__ float pickf(const float (&x)[Q], uint32_t k) {
   for (int q = 1; q < Q; ++q) r = (k == (uint32_t)q) ? x[q] : r;
   return r;
 }
-__device__ __forceinline__ uint32_t seq_scan(const List& list, uint32_t n, int mode, float thr,
+template <class L>
+__device__ __forceinline__ uint32_t seq_scan(const L& list, uint32_t n, int mode, float thr,
                                              float& cum_out, LDS uint32_t* sh, LDS float* z) {
   if (threadIdx.x < WAVE) {
     constexpr uint32_t Q = 8, W = Q * WAVE;
@@ -3619,6 +3620,105 @@ __global__ __launch_bounds__(256) void history_append_kernel(uint32_t B, const u
   G(hlen)[b] = n + 1;
 }
 
+// ---------------------------------------------------------------------------
+// Speculative-decoding verification (docs/mlc-contracts.md:83-84: accept the
+// draft token unless r >= p/q, else resample from max(p - q, 0))
+// ---------------------------------------------------------------------------
+struct VerifyArgs {
+  uint32_t B, V, cap;      // rows, vocabulary, list stride (the sampler's out_cap)
+  const uint32_t* ids;     // [B][cap]: the target's kept ids, (p desc, idx asc)
+  const float* probs;      // [B][cap]: their processed probabilities
+  const uint32_t* cnt;     // [B]: kept counts
+  const uint32_t* draft;   // [B]: draft tokens
+  const float* q;          // [B][qstride]: the draft distribution over the vocabulary
+  uint64_t qstride;
+  const float* ua;         // [B]: uniforms of the acceptance test
+  const float* ur;         // [B]: uniforms of the residual draw
+  uint32_t* out_tok;       // [B]
+  uint32_t* out_acc;       // [B]: 1 accepted, 0 resampled
+};
+
+// The residual max(p_i - q[id_i], 0) of kept entry i (one f32 subtraction),
+// through the divisor chain: the list the residual draw scans, in the
+// target's (p desc, idx asc) order.
+struct ResidualList {
+  const float* p;
+  const uint32_t* idx;
+  const float* q;
+  uint32_t V;  // an id at or above V (not one the sampler writes) reads q = 0
+  Chain c;
+  __device__ float raw(uint32_t i) const {
+    const uint32_t t = G(idx)[i];
+    const float r = G(p)[i] - (t < V ? G(q)[t] : 0.0f);
+    return r > 0.0f ? r : 0.0f;
+  }
+  __device__ float get(uint32_t i) const { return c.apply(raw(i)); }
+};
+
+// One wave per row.  Accept when u_a * q(d) < p(d) (the draft token d's
+// target probability p(d) is 0 outside the kept list).  Otherwise the
+// residual sum R is the sequential f32 sum of the residuals in list order,
+// and the token is the reference's draw (sampler.rs:113-124) over the
+// residuals divided by R: the first entry whose running sum reaches u_r, else
+// the last entry with a positive residual.  R = 0 (p <= q on every kept
+// entry) draws from p itself.  A row whose list is empty or was cut short
+// (count > cap), or whose draft token is not below V, is invalid.
+__global__ __launch_bounds__(WAVE) void verify_kernel(VerifyArgs v, uint32_t* status) {
+  __shared__ uint32_t sh_[2];
+  __shared__ float z_[2 * WAVE];
+  LDS uint32_t* sh = (LDS uint32_t*)sh_;
+  LDS float* z = (LDS float*)z_;
+  const uint32_t b = blockIdx.x, lane = threadIdx.x;
+  const uint32_t n = G(v.cnt)[b], d = G(v.draft)[b];
+  if (n == 0 || n > v.cap || d >= v.V) {
+    if (lane == 0) {
+      G(v.out_tok)[b] = LLMK_INVALID_TOKEN;
+      G(v.out_acc)[b] = 0u;
+      atomicOr(status, LLMK_STATUS_INVALID_PARAMS);
+    }
+    return;
+  }
+  const uint32_t* ids = v.ids + (uint64_t)b * v.cap;
+  const float* probs = v.probs + (uint64_t)b * v.cap;
+  const float* q = v.q + (uint64_t)b * v.qstride;
+  uint32_t jd = EMPTY;  // ids are distinct: at most one entry holds d
+  for (uint32_t j = lane; j < n; j += WAVE)
+    if (G(ids)[j] == d) jd = j;
+  jd = wave_min_u32(jd);
+  const float pd = jd < n ? G(probs)[jd] : 0.0f;
+  const float qd = G(q)[d];
+  const float ua = G(v.ua)[b], ur = G(v.ur)[b];
+  uint32_t tok = d, acc = 1u;
+  if (!(ua * qd < pd)) {
+    acc = 0u;
+    ResidualList rl{probs, ids, q, v.V, Chain{0.0f, 0.0f, 0.0f, 0}};
+    float R;
+    seq_scan(rl, n, 0, 0.0f, R, sh, z);
+    float c;
+    if (R > 0.0f) {
+      rl.c.push(R);
+      const uint32_t j = seq_scan(rl, n, 2, ur, c, sh, z);
+      if (j < n) {
+        tok = G(ids)[j];
+      } else {
+        uint32_t jl = 0;  // the last entry with a positive residual (R > 0: one exists)
+        for (uint32_t i = lane; i < n; i += WAVE)
+          if (rl.raw(i) > 0.0f) jl = i + 1;
+        jl = wave_max_u32(jl);
+        tok = G(ids)[jl - 1];
+      }
+    } else {
+      List pl{probs, ids, Chain{0.0f, 0.0f, 0.0f, 0}, nullptr};
+      const uint32_t j = seq_scan(pl, n, 2, ur, c, sh, z);
+      tok = G(ids)[j < n ? j : n - 1];
+    }
+  }
+  if (lane == 0) {
+    G(v.out_tok)[b] = tok;
+    G(v.out_acc)[b] = acc;
+  }
+}
+
 }  // namespace llmk
 
 // ===========================================================================
@@ -4022,6 +4122,29 @@ extern "C" int llmk_apply_logit_bias(llmk_sampler* s, float* logits, uint32_t ba
   hipLaunchKernelGGL(logit_bias_kernel, dim3((batch + NW - 1) / NW), dim3(NT), 0,
                      (hipStream_t)stream, logits, batch, vocab, row_stride, bias_offsets,
                      bias_tokens, bias_values);
+  HIPCHK(hipGetLastError());
+  return LLMK_OK;
+}
+
+extern "C" int llmk_verify_batch(llmk_sampler* s, uint32_t batch, uint32_t vocab,
+                                 const uint32_t* ids, const float* probs, uint32_t list_cap,
+                                 const uint32_t* counts, const uint32_t* draft_tokens,
+                                 const float* draft_probs, uint64_t draft_stride,
+                                 const float* u_accept, const float* u_resample,
+                                 uint32_t* out_tokens, uint32_t* out_accepted, void* stream) {
+  if (!s) return fail(LLMK_ERR_INVALID_ARGUMENT, "sampler is NULL");
+  if (vocab == 0) return fail(LLMK_ERR_EMPTY_LOGITS, "Empty logits passed to sampler");
+  if (!ids || !probs || !counts || !draft_tokens || !draft_probs || !u_accept || !u_resample ||
+      !out_tokens || !out_accepted)
+    return fail(LLMK_ERR_INVALID_ARGUMENT, "every array of llmk_verify_batch is required");
+  if (list_cap == 0) return fail(LLMK_ERR_INVALID_ARGUMENT, "list_cap is 0");
+  if (draft_stride < vocab) return fail(LLMK_ERR_INVALID_ARGUMENT, "draft_stride < vocab");
+  if (batch == 0) return LLMK_OK;
+  HIPCHK(hipSetDevice(s->device));
+  VerifyArgs v{batch, vocab, list_cap, ids, probs, counts, draft_tokens, draft_probs,
+               draft_stride, u_accept, u_resample, out_tokens, out_accepted};
+  hipLaunchKernelGGL(verify_kernel, dim3(batch), dim3(WAVE), 0, (hipStream_t)stream, v,
+                     s->ws.status);
   HIPCHK(hipGetLastError());
   return LLMK_OK;
 }

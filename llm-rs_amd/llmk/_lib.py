@@ -39,6 +39,7 @@ EXPORTED_SYMBOLS = (
     "llmk_apply_logit_bias",
     "llmk_history_append",
     "llmk_sample_batch_static",
+    "llmk_verify_batch",
 )
 
 
@@ -106,6 +107,10 @@ def load():
     lib.llmk_apply_logit_bias.restype = ctypes.c_int
     lib.llmk_history_append.argtypes = [vp, ctypes.c_uint32, vp, vp, vp, ctypes.c_uint32, vp, vp]
     lib.llmk_history_append.restype = ctypes.c_int
+    u32, u64 = ctypes.c_uint32, ctypes.c_uint64
+    lib.llmk_verify_batch.argtypes = [vp, u32, u32, vp, vp, u32, vp, vp, vp, u64, vp, vp, vp, vp,
+                                      vp]
+    lib.llmk_verify_batch.restype = ctypes.c_int
     lib.llmk_last_error.argtypes = []
     lib.llmk_last_error.restype = ctypes.c_char_p
     _lib = lib

@@ -349,6 +349,43 @@ class HipSampler:
         if rc != 0:
             raise SamplerError(rc, _lib.last_error())
 
+    # ---- speculative-decoding verification (docs/mlc-contracts.md:83-84) --
+    def verify_batch(self, ids: torch.Tensor, probs: torch.Tensor, counts: torch.Tensor,
+                     draft_tokens: torch.Tensor, draft_probs: torch.Tensor,
+                     u_accept: torch.Tensor, u_resample: torch.Tensor,
+                     vocab: Optional[int] = None,
+                     stream: Optional[torch.cuda.Stream] = None):
+        """llmk_verify_batch: row b accepts draft_tokens[b] against the target
+        distribution given by the kept list ids/probs[b, :counts[b]] (what
+        sample_batch returns with out_cap = ids.shape[1]), or resamples from
+        max(p - q, 0) with q = draft_probs[b].  Returns (tokens, accepted)."""
+        B, cap = ids.shape
+        V = vocab if vocab is not None else draft_probs.shape[1]
+        _on_device(ids.device, probs=probs, counts=counts, draft_tokens=draft_tokens,
+                   draft_probs=draft_probs, u_accept=u_accept, u_resample=u_resample)
+        for name, t, dts in (("ids", ids, _I32), ("probs", probs, _F32), ("counts", counts, _I32),
+                             ("draft_tokens", draft_tokens, _I32), ("u_accept", u_accept, _F32),
+                             ("u_resample", u_resample, _F32)):
+            _flat(name, t, dts)
+        if (draft_probs.dtype != torch.float32 or draft_probs.dim() != 2
+                or draft_probs.stride(1) != 1):
+            raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT,
+                               "draft_probs must be a row-major float32 [batch, >= vocab] tensor")
+        if probs.shape != ids.shape or draft_probs.shape[0] != B or counts.numel() != B:
+            raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT, "inconsistent shapes")
+        tok = torch.empty(B, dtype=torch.int32, device=ids.device)
+        acc = torch.empty(B, dtype=torch.int32, device=ids.device)
+        st = self._stream(ids, stream)
+        rc = self._lib.llmk_verify_batch(self._h, B, V, ids.data_ptr(), probs.data_ptr(), cap,
+                                         counts.data_ptr(), draft_tokens.data_ptr(),
+                                         draft_probs.data_ptr(), draft_probs.stride(0),
+                                         u_accept.data_ptr(), u_resample.data_ptr(),
+                                         tok.data_ptr(), acc.data_ptr(),
+                                         ctypes.c_void_p(st.cuda_stream))
+        if rc != 0:
+            raise SamplerError(rc, _lib.last_error())
+        return tok, acc
+
     # ---- the per-row reference call (LlmBackend::sample) ------------------
     def sample(self, logits: torch.Tensor, params: SampleParams,
                token_history: Sequence[int], u: float) -> int:

@@ -12,6 +12,7 @@
  *   apply_top_k              :160-173  -> llmk_oracle_apply_top_k()
  *   apply_top_p              :176-216  -> llmk_oracle_apply_top_p()
  *   sample                   :219-228  -> llmk_oracle_sample_simple()
+ * Speculative verification (docs/mlc-contracts.md:83-84) -> llmk_oracle_verify_row().
  * Presence/frequency formula: llm-tests/tests/mlc_parity.rs:1074-1089.
  */
 #define _GNU_SOURCE
@@ -638,6 +639,67 @@ uint32_t llmk_oracle_sample_simple(int mode, const float* logits, uint32_t V,
                              NULL, 0, &cnt) != 0)
     return 0; /* sampler.rs:227 unwrap_or(0) */
   return tok;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Speculative-decoding verification                                          */
+/* ------------------------------------------------------------------------ */
+
+/* One row of the verification docs/mlc-contracts.md:83-84 describes (the
+ * reference leaves the hook, llm-core/src/backend.rs:20-22, and no
+ * implementation), over the target's processed kept list (ids/probs in
+ * (p desc, idx asc) order, n entries; p = 0 outside it) and the draft
+ * distribution q[0..V): accept d iff u_a * q[d] < p(d); otherwise draw from
+ * max(p - q, 0) with sampler.rs:113-124's loop over the residuals divided by
+ * their sequential sum R, falling back to the last positive residual; R = 0
+ * draws from p with the same loop.  Returns 1 (token LLMK_INVALID) for an
+ * empty list or d >= V. */
+int llmk_oracle_verify_row(uint32_t n, const uint32_t* ids, const float* probs,
+                           uint32_t d, const float* q, uint32_t V, float u_a,
+                           float u_r, uint32_t* tok, uint32_t* accepted) {
+  *accepted = 0;
+  if (n == 0 || d >= V) {
+    *tok = 0xffffffffu;
+    return 1;
+  }
+  float pd = 0.0f;
+  for (uint32_t j = 0; j < n; ++j)
+    if (ids[j] == d) pd = probs[j];
+  if (u_a * q[d] < pd) {
+    *tok = d;
+    *accepted = 1;
+    return 0;
+  }
+  float R = 0.0f;
+  for (uint32_t j = 0; j < n; ++j) {
+    const float r = probs[j] - (ids[j] < V ? q[ids[j]] : 0.0f);
+    R += r > 0.0f ? r : 0.0f;
+  }
+  float c = 0.0f;
+  if (R > 0.0f) {
+    uint32_t last = 0;
+    for (uint32_t j = 0; j < n; ++j) {
+      float r = probs[j] - (ids[j] < V ? q[ids[j]] : 0.0f);
+      r = r > 0.0f ? r : 0.0f;
+      if (r > 0.0f) last = j;
+      c += r / R;
+      if (u_r <= c) {
+        *tok = ids[j];
+        return 0;
+      }
+    }
+    *tok = ids[last];
+    return 0;
+  }
+  for (uint32_t j = 0; j < n; ++j) {
+    c += probs[j];
+    if (u_r <= c) {
+      *tok = ids[j];
+      return 0;
+    }
+  }
+  *tok = ids[n - 1];
+  return 0;
 }
 
 /* ------------------------------------------------------------------------ */

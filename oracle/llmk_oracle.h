@@ -117,6 +117,12 @@ void llmk_oracle_apply_top_p(int mode, float* logits, uint32_t V, float top_p);
 uint32_t llmk_oracle_sample_simple(int mode, const float* logits, uint32_t V,
                                    float temperature, float u);
 
+/* Speculative-decoding verification of one row (docs/mlc-contracts.md:
+ * 83-84) over the target's kept list and the draft distribution q[0..V). */
+int llmk_oracle_verify_row(uint32_t n, const uint32_t* ids, const float* probs,
+                           uint32_t d, const float* q, uint32_t V, float u_a,
+                           float u_r, uint32_t* tok, uint32_t* accepted);
+
 /* Numerics. */
 /* e^x exactly as glibc's expf (>= 2.28, x86-64 FMA build) computes it, for
  * x <= 0 (-inf and x < -0x1.9fe368p6 give +0). */

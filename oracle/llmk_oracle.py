@@ -50,6 +50,9 @@ def load():
     lib.llmk_oracle_apply_top_p.argtypes = [ctypes.c_int, P, u32, f32]
     lib.llmk_oracle_sample_simple.argtypes = [ctypes.c_int, P, u32, f32, f32]
     lib.llmk_oracle_sample_simple.restype = u32
+    lib.llmk_oracle_verify_row.argtypes = [u32, P, P, u32, P, u32, f32, f32,
+                                           ctypes.POINTER(u32), ctypes.POINTER(u32)]
+    lib.llmk_oracle_verify_row.restype = ctypes.c_int
     u64p = ctypes.POINTER(ctypes.c_uint64)
     lib.llmk_oracle_exp_scan.argtypes = [u32, u32, u64p, u64p, u64p, ctypes.POINTER(u32)]
     _lib = lib
@@ -223,3 +226,17 @@ def exp_scan(lo_bits, hi_bits):
     d = ctypes.c_uint32()
     load().llmk_oracle_exp_scan(lo_bits, hi_bits, ctypes.byref(a), ctypes.byref(b), ctypes.byref(c), ctypes.byref(d))
     return a.value, b.value, c.value, d.value
+
+
+def verify_row(ids, probs, d, q, u_a, u_r):
+    """Speculative verification of one row (docs/mlc-contracts.md:83-84):
+    the target's kept list (ids, probs), draft token d, draft distribution q
+    over the vocabulary; returns (token, accepted), token 0xffffffff for an
+    invalid row."""
+    i = np.ascontiguousarray(ids, dtype=np.uint32)
+    p = np.ascontiguousarray(probs, dtype=np.float32)
+    qq = np.ascontiguousarray(q, dtype=np.float32)
+    tok, acc = ctypes.c_uint32(), ctypes.c_uint32()
+    load().llmk_oracle_verify_row(i.size, _p(i), _p(p), int(d), _p(qq), qq.size, float(u_a),
+                                  float(u_r), ctypes.byref(tok), ctypes.byref(acc))
+    return tok.value, acc.value
