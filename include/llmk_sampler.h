@@ -112,6 +112,13 @@ typedef struct {
    * entries).  This lets the history live in per-row buffers with room to
    * grow, appended to on the device by llmk_history_append.  NULL = CSR. */
   const uint32_t* hist_lengths;
+  /* final_logit_softcapping (candle.rs:1803-1807, models whose metadata sets
+   * it, candle.rs:606): > 0 = the logits are the lm_head output before the
+   * cap, and each is read as cap * tanh(l / cap) evaluated as candle's CPU
+   * ops do in the logits' dtype (l * (1/cap) + 0, glibc's tanhf, * cap + 0,
+   * each rounded to the dtype); 0 = off.  Fused into the sampling pass: the
+   * capped logits are never written. */
+  float softcap;
 } llmk_sample_batch_args;
 
 /* Create a sampler on `device` able to serve batches up to max_batch rows of

@@ -65,6 +65,100 @@ __device__ __forceinline__ float exp_ref(float x) {
   return live ? (float)y : 0.0f;
 }
 
+// tanh(x) bit for bit as glibc's tanhf computes it (glibc 2.35, sysdeps/
+// ieee754/flt-32/s_tanhf.c and s_expm1f.c: Sun's fdlibm method, all in
+// float, no fused operations): tanh|x| = 1 - 2/(expm1(2|x|) + 2) for
+// |x| >= 1, -t/(t + 2) with t = expm1(-2|x|) below, x(1 + x) below 2^-55,
+// 1 from 22 on; the sign restored last.  expm1 reduces x = k ln2 + r with ln2
+// split into a head of 16 significant bits and a tail (k = +-1 directly
+// between 0.5 ln2 and 1.5 ln2, else k = trunc(x/ln2 +- 1/2) and the
+// rounding error of the reduction kept in c), approximates expm1 on
+// [-ln2/2, ln2/2] through the rational form of fdlibm with its quintic in
+// (x^2/2) (coefficients Q1..Q5), and rebuilds 2^k (expm1(r) + 1) - 1 by the
+// case on k.  The CPU tests compare every float against the host's tanhf and
+// expm1f.
+__device__ __forceinline__ float f_of(uint32_t b) { return __uint_as_float(b); }
+__device__ __forceinline__ float expm1_ref(float x) {
+  const float ln2_head = f_of(0x3f317180u), ln2_tail = f_of(0x3717f7d1u);
+  const float inv_ln2 = f_of(0x3fb8aa3bu);
+  const float q1 = f_of(0xbd088889u), q2 = f_of(0x3ad00d01u), q3 = f_of(0xb8a670cdu),
+              q4 = f_of(0x36867e54u), q5 = f_of(0xb457edbbu);
+  const uint32_t bits = __float_as_uint(x);
+  const bool neg = (bits >> 31) != 0;
+  const uint32_t mag = bits & 0x7fffffffu;
+  if (mag >= 0x4195b844u) {  // |x| >= 27 ln2: the result is -1 or overflows
+    if (mag >= 0x42b17218u) {
+      if (mag > 0x7f800000u) return x + x;  // NaN
+      if (mag == 0x7f800000u) return neg ? -1.0f : x;
+      if (x > f_of(0x42b17180u)) return __builtin_huge_valf();
+    }
+    if (neg) return -1.0f;
+  }
+  int k = 0;
+  float c = 0.0f;
+  if (mag > 0x3eb17218u) {  // |x| > ln2/2: reduce
+    float head, tail;
+    if (mag < 0x3f851592u) {  // |x| < 1.5 ln2
+      k = neg ? -1 : 1;
+      head = neg ? x + ln2_head : x - ln2_head;
+      tail = neg ? -ln2_tail : ln2_tail;
+    } else {
+      k = (int)(inv_ln2 * x + (neg ? -0.5f : 0.5f));
+      const float kf = (float)k;
+      head = x - kf * ln2_head;
+      tail = kf * ln2_tail;
+    }
+    x = head - tail;
+    c = (head - x) - tail;
+  } else if (mag < 0x33000000u) {  // |x| < 2^-25
+    return x;
+  }
+  const float half_x = 0.5f * x;
+  const float hx2 = x * half_x;
+  const float r1 = 1.0f + hx2 * (q1 + hx2 * (q2 + hx2 * (q3 + hx2 * (q4 + hx2 * q5))));
+  float t = 3.0f - r1 * half_x;
+  float e = hx2 * ((r1 - t) / (6.0f - x * t));
+  if (k == 0) return x - (x * e - hx2);
+  e = x * (e - c) - c;
+  e = e - hx2;
+  if (k == -1) return 0.5f * (x - e) - 0.5f;
+  if (k == 1) return x < -0.25f ? -2.0f * (e - (x + 0.5f)) : 1.0f + 2.0f * (x - e);
+  float y;
+  if (k <= -2 || k > 56) {
+    y = 1.0f - (e - x);
+    return f_of(__float_as_uint(y) + ((uint32_t)k << 23)) - 1.0f;
+  }
+  if (k < 23) {
+    t = f_of(0x3f800000u - (0x1000000u >> k));  // 1 - 2^-k
+    y = t - (e - x);
+  } else {
+    t = f_of((uint32_t)(0x7f - k) << 23);  // 2^-k
+    y = x - (e + t);
+    y = y + 1.0f;
+  }
+  return f_of(__float_as_uint(y) + ((uint32_t)k << 23));
+}
+__device__ __forceinline__ float tanh_ref(float x) {
+  const uint32_t bits = __float_as_uint(x), mag = bits & 0x7fffffffu;
+  const bool neg = (bits >> 31) != 0;
+  if (mag >= 0x7f800000u) return neg ? 1.0f / x - 1.0f : 1.0f / x + 1.0f;  // +-1, NaN
+  float z;
+  if (mag >= 0x41b00000u) {  // |x| >= 22
+    z = 1.0f;
+  } else if (mag == 0) {
+    return x;
+  } else if (mag < 0x24000000u) {  // |x| < 2^-55
+    return x * (1.0f + x);
+  } else if (mag >= 0x3f800000u) {
+    const float t = expm1_ref(2.0f * __builtin_fabsf(x));
+    z = 1.0f - 2.0f / (t + 2.0f);
+  } else {
+    const float t = expm1_ref(-2.0f * __builtin_fabsf(x));
+    z = -t / (t + 2.0f);
+  }
+  return neg ? -z : z;
+}
+
 // Order-preserving map float -> u32 (NaN excluded by callers).
 __device__ __forceinline__ uint32_t fkey(float v) {
   const uint32_t b = __float_as_uint(v);

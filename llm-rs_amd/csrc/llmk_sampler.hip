@@ -34,6 +34,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -95,6 +96,7 @@ enum : uint32_t { FLAG_OVERFLOW = 1u, FLAG_HIST_OVERFLOW = 2u, FLAG_NAN = 4u };
 struct Args {
   const void* logits;
   int32_t dtype;
+  float sc_m1, sc_cap;  // softcap: 1/cap and cap in the logits' dtype (DT & SOFTCAP)
   uint32_t B, V;
   uint64_t stride;
   const float *T, *top_p, *min_p, *rp, *pp, *fp;
@@ -338,13 +340,51 @@ __device__ __forceinline__ float penalize(float x, const RowP& P,
 // A 16-bit logit (bf16 or f16 bits) as f32, exactly.
 template <int DT>
 __device__ __forceinline__ float cvt16(uint32_t h) {
-  if (DT == LLMK_BF16) return __uint_as_float(h << 16);
+  if ((DT & 3) == LLMK_BF16) return __uint_as_float(h << 16);
   return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
+
+// Template flag on the dtype: the logits are the lm_head output before
+// final_logit_softcapping, capped as they are read.  1/cap and cap (in the
+// logits' dtype) sit in LDS, written before the kernel's first barrier.
+constexpr int SOFTCAP = 4;
+__shared__ float g_softcap[2];
+// f32 -> the logits' dtype, round to nearest even (NaN stays NaN)
+template <int DT>
+__device__ __forceinline__ float round_dt(float x) {
+  if ((DT & 3) == LLMK_BF16) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return __uint_as_float((u | 0x00400000u) & 0xffff0000u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return __uint_as_float(u & 0xffff0000u);
+  }
+  if ((DT & 3) == LLMK_F16) return (float)(_Float16)x;
+  return x;
+}
+// final_logit_softcapping as candle evaluates it on the logits tensor
+// (candle.rs:1803-1807): (x / cap).tanh() * cap, where dividing or
+// multiplying a tensor by a scalar is its affine map x * m + 0 (m = 1/cap or
+// cap, as the dtype) and tanh is glibc's tanhf; in a 16-bit dtype every
+// operation rounds to it.
+template <int DT>
+__device__ __forceinline__ float softcap(float x) {
+  if (!(DT & SOFTCAP)) return x;
+  float y = round_dt<DT>(x * g_softcap[0]);
+  y = round_dt<DT>(y + 0.0f);
+  float t = round_dt<DT>(tanh_ref(y));
+  t = round_dt<DT>(t * g_softcap[1]);
+  return round_dt<DT>(t + 0.0f);
+}
+template <int DT>
+__device__ __forceinline__ void softcap_init(const Args& a) {
+  if (DT & SOFTCAP)
+    if (threadIdx.x < 2) g_softcap[threadIdx.x] = threadIdx.x ? a.sc_cap : a.sc_m1;
+}
+
 template <int DT>
 __device__ __forceinline__ float load_logit(const void* row, uint32_t e) {
-  if (DT == LLMK_F32) return G((const float*)row)[e];
-  return cvt16<DT>(G((const uint16_t*)row)[e]);
+  if ((DT & 3) == LLMK_F32) return softcap<DT>(G((const float*)row)[e]);
+  return softcap<DT>(cvt16<DT>(G((const uint16_t*)row)[e]));
 }
 
 struct Hist {
@@ -628,7 +668,7 @@ __device__ __forceinline__ void load_tile(const Args& a, const void* row,
   const uint32_t tb = t * TILE;
   (void)h;
   if (tb + TILE <= a.V) {
-    if (DT == LLMK_F32) {
+    if ((DT & 3) == LLMK_F32) {
       const GLB f4v* p = (const GLB f4v*)G((const float*)row + tb) + lane;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -653,12 +693,12 @@ __device__ __forceinline__ void load_tile(const Args& a, const void* row,
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const uint32_t e = tb + 256u * r + 4u * lane + q;
-        if (DT == LLMK_F32) {
+        if ((DT & 3) == LLMK_F32) {
           raw.d[4 * r + q] = e < a.V ? G((const uint32_t*)row)[e] : 0xff800000u;  // -inf past V
         } else {
           // the raw 16-bit value, -inf past V
           const uint32_t hv = e < a.V ? (uint32_t)G((const uint16_t*)row)[e]
-                                      : (DT == LLMK_BF16 ? 0xff80u : 0xfc00u);
+                                      : ((DT & 3) == LLMK_BF16 ? 0xff80u : 0xfc00u);
           const int w = 2 * r + (q >> 1);
           if ((q & 1) == 0) raw.d[w] = hv;
           else raw.d[w] |= hv << 16;
@@ -676,13 +716,13 @@ __device__ __forceinline__ void load_tile(const Args& a, const void* row,
 
 template <int DT>
 __device__ __forceinline__ void unpack(const Raw& raw, float v[16]) {
-  if (DT == LLMK_F32) {
+  if ((DT & 3) == LLMK_F32) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) v[j] = __uint_as_float(raw.d[j]);
   } else {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      if (DT == LLMK_BF16) {
+      if ((DT & 3) == LLMK_BF16) {
         v[4 * r + 0] = __uint_as_float(raw.d[2 * r] << 16);
         v[4 * r + 1] = __uint_as_float(raw.d[2 * r] & 0xffff0000u);
         v[4 * r + 2] = __uint_as_float(raw.d[2 * r + 1] << 16);
@@ -694,6 +734,10 @@ __device__ __forceinline__ void unpack(const Raw& raw, float v[16]) {
         v[4 * r + 3] = cvt16<DT>(raw.d[2 * r + 1] >> 16);
       }
     }
+  }
+  if (DT & SOFTCAP) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = softcap<DT>(v[j]);
   }
 }
 
@@ -1303,7 +1347,7 @@ __host__ __device__ inline size_t slow_lds_words(uint32_t V) {
 template <int DT>
 __device__ __forceinline__ void load16(const void* row, uint32_t e0, uint32_t V, float x[16]) {
   if (e0 + 16 <= V) {
-    if (DT == LLMK_F32) {
+    if ((DT & 3) == LLMK_F32) {
       const GLB f4v* r = (const GLB f4v*)((const GLB float*)row + e0);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
@@ -1323,6 +1367,10 @@ __device__ __forceinline__ void load16(const void* row, uint32_t e0, uint32_t V,
         x[4 * k + 2] = cvt16<DT>(a.y & 0xffffu);
         x[4 * k + 3] = cvt16<DT>(a.y >> 16);
       }
+    }
+    if (DT & SOFTCAP) {
+#pragma unroll
+      for (int q = 0; q < 16; ++q) x[q] = softcap<DT>(x[q]);
     }
   } else {
 #pragma unroll
@@ -1638,7 +1686,7 @@ __device__ __attribute__((noinline)) float exact_normaliser(
 template <int DT>
 __device__ __forceinline__ void load8(const void* row, uint32_t e0, uint32_t V, float x[8]) {
   if (e0 + 8 <= V) {
-    if (DT == LLMK_F32) {
+    if ((DT & 3) == LLMK_F32) {
       const GLB f4v* r = (const GLB f4v*)((const GLB float*)row + e0);
       const f4v a = r[0], b = r[1];
       x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
@@ -1652,6 +1700,10 @@ __device__ __forceinline__ void load8(const void* row, uint32_t e0, uint32_t V, 
         x[2 * q] = cvt16<DT>(w[q] & 0xffffu);
         x[2 * q + 1] = cvt16<DT>(w[q] >> 16);
       }
+    }
+    if (DT & SOFTCAP) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) x[q] = softcap<DT>(x[q]);
     }
   } else {
 #pragma unroll
@@ -1720,7 +1772,7 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
     return;
   }
   const void* row = (const char*)a.logits +
-                    (uint64_t)b * a.stride * (DT == LLMK_F32 ? 4u : 2u);
+                    (uint64_t)b * a.stride * ((DT & 3) == LLMK_F32 ? 4u : 2u);
   if (tid == 0) sh[10] = 0;
   build_history<DT>(a, P, b, row, 0, V, nwords, h, red, &sh[10]);
   if (tid == 0 && (sh[10] & FLAG_HIST_OVERFLOW))
@@ -2724,12 +2776,12 @@ __device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_
       h.lo = 0;
       if (tid == 0) sc[64] = 0;
       const void* row = (const char*)a.logits +
-                        (uint64_t)b * a.stride * (DT == LLMK_F32 ? 4u : 2u);
+                        (uint64_t)b * a.stride * ((DT & 3) == LLMK_F32 ? 4u : 2u);
       build_history<DT>(a, P, b, row, 0, a.V, nwords, h, sc + 128, &sc[64]);
       have_hist = true;  // built (empty when the row has no penalised history)
     }
     const void* row = (const char*)a.logits +
-                      (uint64_t)b * a.stride * (DT == LLMK_F32 ? 4u : 2u);
+                      (uint64_t)b * a.stride * ((DT & 3) == LLMK_F32 ? 4u : 2u);
     S = exact_normaliser<DT>(row, a.mask ? a.mask + (uint64_t)b * a.mask_words : nullptr, a.V,
                              P.T, m, h.bitmap, h.pre, h.pen, have_hist, sc);
   }
@@ -3087,7 +3139,7 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   constexpr uint32_t TW = 8;
   constexpr int TQ = 4;  // tokens per lane per pass
   const void* row = (const char*)a.logits +
-                    (uint64_t)b * a.stride * (DT == LLMK_F32 ? 4u : 2u);
+                    (uint64_t)b * a.stride * ((DT & 3) == LLMK_F32 ? 4u : 2u);
   const uint32_t* mrow = a.mask ? a.mask + (uint64_t)b * a.mask_words : nullptr;
   Raw ra, rb;
   uint32_t ta = t0 + (uint32_t)wv, tb2 = t0 + (uint32_t)wv + NW;
@@ -3140,6 +3192,7 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   }
   if (tid < M_NMISC) misc[tid] = 0;
   exp_tab_init();
+  softcap_init<DT>(a);
   if (have) {
     for (uint32_t i = tid; i < nwords; i += NT) h.bitmap[i] = 0;
     if (need_cnt)
@@ -3251,6 +3304,12 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
     float v[16];
     unpack<DT>(raw, v);
     const uint32_t tb = t * TILE;
+    if ((DT & SOFTCAP) && tb + TILE > a.V) {
+      // positions past V hold -inf, which the cap would have made -cap
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (tb + 256u * (j >> 2) + 4u * (uint32_t)lane + (j & 3) >= a.V) v[j] = NEG_INF;
+    }
     // history tokens and disallowed tokens become -inf (a uniform branch per
     // case, so a row without a mask spends nothing on one)
     if (mrow) {
@@ -3802,12 +3861,12 @@ static Ws ws_carve(char* base, const WsLayout& L, uint32_t mv, uint32_t slots) {
 // Dynamic LDS above 64 KiB must be allowed explicitly (per device; no
 // allocation).
 static int set_kernel_attributes() {
-  HIPCHK(hipFuncSetAttribute((const void*)stream_kernel<LLMK_F32>,
-                             hipFuncAttributeMaxDynamicSharedMemorySize, LDS_DYN_MAX));
-  HIPCHK(hipFuncSetAttribute((const void*)stream_kernel<LLMK_BF16>,
-                             hipFuncAttributeMaxDynamicSharedMemorySize, LDS_DYN_MAX));
-  HIPCHK(hipFuncSetAttribute((const void*)stream_kernel<LLMK_F16>,
-                             hipFuncAttributeMaxDynamicSharedMemorySize, LDS_DYN_MAX));
+  const void* kernels[] = {
+      (const void*)stream_kernel<LLMK_F32>,           (const void*)stream_kernel<LLMK_BF16>,
+      (const void*)stream_kernel<LLMK_F16>,           (const void*)stream_kernel<LLMK_F32 | SOFTCAP>,
+      (const void*)stream_kernel<LLMK_BF16 | SOFTCAP>, (const void*)stream_kernel<LLMK_F16 | SOFTCAP>};
+  for (const void* k : kernels)
+    HIPCHK(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_DYN_MAX));
   HIPCHK(hipFuncSetAttribute((const void*)topk_mask_kernel,
                              hipFuncAttributeMaxDynamicSharedMemorySize, 4 * MK_LDS_WORDS));
   return LLMK_OK;
@@ -3872,6 +3931,24 @@ extern "C" int llmk_sampler_status(llmk_sampler* s, void* stream,
   return LLMK_OK;
 }
 
+// x rounded to nearest even into f32 (fmt 0), bf16 (1) or f16 (2), as a
+// float: the scalar operand candle makes of an f64 for a tensor of that
+// dtype (T::from_f64).  Subnormal results keep the format's fixed quantum;
+// past the largest finite value the result is infinite.
+static float dtype_round(double x, int fmt) {
+  if (fmt == 0) return (float)x;
+  if (x == 0.0 || !(x == x) || x - x != 0.0) return (float)x;
+  const int p = fmt == 1 ? 8 : 11, emin = fmt == 1 ? -126 : -14, emax = fmt == 1 ? 127 : 15;
+  int e = 0;
+  (void)std::frexp(x, &e);  // x = f 2^e, 1/2 <= |f| < 1: the leading bit is 2^(e-1)
+  const int lead = e - 1 < emin ? emin : e - 1;
+  const double quantum = std::ldexp(1.0, lead - p + 1);
+  const double r = std::nearbyint(x / quantum) * quantum;  // x / quantum is exact
+  const double maxf = std::ldexp(2.0 - std::ldexp(1.0, 1 - p), emax);
+  if (std::fabs(r) > maxf) return r > 0 ? __builtin_huge_valf() : -__builtin_huge_valf();
+  return (float)r;
+}
+
 // One sampling launch on workspace ws, sized for batches up to max_batch rows
 // of up to max_vocab logits with `pool` workgroup entries, on the current
 // device.
@@ -3897,6 +3974,8 @@ static int sample_batch_run(const Ws& ws, uint32_t max_batch, uint32_t max_vocab
     return fail(LLMK_ERR_INVALID_ARGUMENT, "mask_words_per_row < ceil(vocab/32)");
   if (in->out_cap && !in->out_ids && !in->out_probs)
     return fail(LLMK_ERR_INVALID_ARGUMENT, "out_cap without out_ids/out_probs");
+  if (!(in->softcap >= 0.0f) || !(in->softcap < __builtin_huge_valf()))
+    return fail(LLMK_ERR_INVALID_ARGUMENT, "softcap must be finite and >= 0 (0 = off)");
   const size_t esz = in->dtype == LLMK_F32 ? 4 : 2;
   const size_t align = in->dtype == LLMK_F32 ? 16 : 8;
   if (((uintptr_t)in->logits % align) != 0 || ((in->row_stride * esz) % align) != 0)
@@ -3905,6 +3984,13 @@ static int sample_batch_run(const Ws& ws, uint32_t max_batch, uint32_t max_vocab
   Args a;
   a.logits = in->logits;
   a.dtype = in->dtype;
+  a.sc_m1 = a.sc_cap = 0.0f;
+  if (in->softcap > 0.0f) {
+    // candle's scalar operands: 1/cap in f64, then the tensor's dtype
+    const int fmt = in->dtype == LLMK_F32 ? 0 : (in->dtype == LLMK_BF16 ? 1 : 2);
+    a.sc_m1 = dtype_round(1.0 / (double)in->softcap, fmt);
+    a.sc_cap = dtype_round((double)in->softcap, fmt);
+  }
   a.B = in->batch;
   a.V = in->vocab;
   a.stride = in->row_stride;
@@ -3955,12 +4041,17 @@ static int sample_batch_run(const Ws& ws, uint32_t max_batch, uint32_t max_vocab
   if (lds > LDS_DYN_MAX)
     return fail(LLMK_ERR_CAPACITY, "vocabulary too large for one workgroup's LDS tables");
   const dim3 grid(a.B * a.G), block(NT);
-  if (a.dtype == LLMK_F32)
-    hipLaunchKernelGGL(stream_kernel<LLMK_F32>, grid, block, lds, st, a, ws);
-  else if (a.dtype == LLMK_BF16)
-    hipLaunchKernelGGL(stream_kernel<LLMK_BF16>, grid, block, lds, st, a, ws);
-  else
-    hipLaunchKernelGGL(stream_kernel<LLMK_F16>, grid, block, lds, st, a, ws);
+  const bool sc = in->softcap > 0.0f;
+  if (a.dtype == LLMK_F32) {
+    if (sc) hipLaunchKernelGGL(stream_kernel<LLMK_F32 | SOFTCAP>, grid, block, lds, st, a, ws);
+    else hipLaunchKernelGGL(stream_kernel<LLMK_F32>, grid, block, lds, st, a, ws);
+  } else if (a.dtype == LLMK_BF16) {
+    if (sc) hipLaunchKernelGGL(stream_kernel<LLMK_BF16 | SOFTCAP>, grid, block, lds, st, a, ws);
+    else hipLaunchKernelGGL(stream_kernel<LLMK_BF16>, grid, block, lds, st, a, ws);
+  } else {
+    if (sc) hipLaunchKernelGGL(stream_kernel<LLMK_F16 | SOFTCAP>, grid, block, lds, st, a, ws);
+    else hipLaunchKernelGGL(stream_kernel<LLMK_F16>, grid, block, lds, st, a, ws);
+  }
   HIPCHK(hipGetLastError());
   return LLMK_OK;
 }

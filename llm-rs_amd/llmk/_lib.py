@@ -70,6 +70,7 @@ class SampleBatchArgs(ctypes.Structure):
         ("out_cap", ctypes.c_uint32),
         ("out_count", ctypes.c_void_p),
         ("hist_lengths", ctypes.c_void_p),
+        ("softcap", ctypes.c_float),
     ]
 
 

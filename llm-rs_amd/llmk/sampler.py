@@ -77,6 +77,7 @@ class DeviceBatch:
     hist_tokens: Optional[torch.Tensor] = None   # int32/uint32
     allow_mask: Optional[torch.Tensor] = None    # int32/uint32 [B, words]
     hist_lengths: Optional[torch.Tensor] = None  # int32/uint32 [B]: per-row buffers
+    softcap: float = 0.0  # > 0: the logits are the lm_head output before final_logit_softcapping
 
 
 def _on_device(dev: torch.device, **tensors) -> None:
@@ -168,6 +169,7 @@ def _batch_args(db: DeviceBatch, out_tokens: torch.Tensor,
     a.out_cap = cap
     a.out_count = _ptr(out_count)
     a.hist_lengths = _ptr(db.hist_lengths)
+    a.softcap = float(db.softcap or 0.0)
     return a
 
 

@@ -642,6 +642,161 @@ uint32_t llmk_oracle_sample_simple(int mode, const float* logits, uint32_t V,
 }
 
 /* ------------------------------------------------------------------------ */
+/* final_logit_softcapping (candle.rs:1803-1807)                              */
+/* ------------------------------------------------------------------------ */
+
+static inline float f_bits(uint32_t b) {
+  float x;
+  memcpy(&x, &b, 4);
+  return x;
+}
+static inline uint32_t bits_f(float x) {
+  uint32_t b;
+  memcpy(&b, &x, 4);
+  return b;
+}
+
+/* expm1 and tanh as glibc 2.35's expm1f / tanhf compute them (sysdeps/
+ * ieee754/flt-32/s_expm1f.c, s_tanhf.c: Sun's fdlibm method in float, no
+ * fused operations).  expm1: x = k ln2 + r, ln2 as a 16-bit head plus a
+ * tail; k = +-1 between 0.5 ln2 and 1.5 ln2, else trunc(x/ln2 +- 1/2), the
+ * reduction's rounding error carried in c; expm1(r) by fdlibm's rational form
+ * with the quintic Q1..Q5 in r^2/2; 2^k (1 + expm1(r)) - 1 rebuilt per case
+ * of k.  tanh: 1 - 2/(expm1(2|x|) + 2) from |x| = 1, -t/(t + 2) with
+ * t = expm1(-2|x|) below, x(1 + x) below 2^-55, 1 from 22, sign last.
+ * llmk_oracle_tanh_scan checks both against the host's functions. */
+float llmk_oracle_expm1_ref(float x) {
+  const float ln2_head = f_bits(0x3f317180u), ln2_tail = f_bits(0x3717f7d1u);
+  const float inv_ln2 = f_bits(0x3fb8aa3bu);
+  const float q1 = f_bits(0xbd088889u), q2 = f_bits(0x3ad00d01u), q3 = f_bits(0xb8a670cdu),
+              q4 = f_bits(0x36867e54u), q5 = f_bits(0xb457edbbu);
+  const uint32_t b = bits_f(x), mag = b & 0x7fffffffu;
+  const int neg = (int)(b >> 31);
+  if (mag >= 0x4195b844u) {
+    if (mag >= 0x42b17218u) {
+      if (mag > 0x7f800000u) return x + x;
+      if (mag == 0x7f800000u) return neg ? -1.0f : x;
+      if (x > f_bits(0x42b17180u)) return INFINITY;
+    }
+    if (neg) return -1.0f;
+  }
+  int k = 0;
+  float c = 0.0f;
+  if (mag > 0x3eb17218u) {
+    float head, tail;
+    if (mag < 0x3f851592u) {
+      k = neg ? -1 : 1;
+      head = neg ? x + ln2_head : x - ln2_head;
+      tail = neg ? -ln2_tail : ln2_tail;
+    } else {
+      k = (int)(inv_ln2 * x + (neg ? -0.5f : 0.5f));
+      const float kf = (float)k;
+      head = x - kf * ln2_head;
+      tail = kf * ln2_tail;
+    }
+    x = head - tail;
+    c = (head - x) - tail;
+  } else if (mag < 0x33000000u) {
+    return x;
+  }
+  const float half_x = 0.5f * x, hx2 = x * half_x;
+  const float r1 = 1.0f + hx2 * (q1 + hx2 * (q2 + hx2 * (q3 + hx2 * (q4 + hx2 * q5))));
+  float t = 3.0f - r1 * half_x;
+  float e = hx2 * ((r1 - t) / (6.0f - x * t));
+  if (k == 0) return x - (x * e - hx2);
+  e = x * (e - c) - c;
+  e = e - hx2;
+  if (k == -1) return 0.5f * (x - e) - 0.5f;
+  if (k == 1) return x < -0.25f ? -2.0f * (e - (x + 0.5f)) : 1.0f + 2.0f * (x - e);
+  float y;
+  if (k <= -2 || k > 56) {
+    y = 1.0f - (e - x);
+    return f_bits(bits_f(y) + ((uint32_t)k << 23)) - 1.0f;
+  }
+  if (k < 23) {
+    t = f_bits(0x3f800000u - (0x1000000u >> k));
+    y = t - (e - x);
+  } else {
+    t = f_bits((uint32_t)(0x7f - k) << 23);
+    y = x - (e + t);
+    y = y + 1.0f;
+  }
+  return f_bits(bits_f(y) + ((uint32_t)k << 23));
+}
+
+float llmk_oracle_tanh_ref(float x) {
+  const uint32_t b = bits_f(x), mag = b & 0x7fffffffu;
+  const int neg = (int)(b >> 31);
+  if (mag >= 0x7f800000u) return neg ? 1.0f / x - 1.0f : 1.0f / x + 1.0f;
+  float z;
+  if (mag >= 0x41b00000u) {
+    z = 1.0f;
+  } else if (mag == 0) {
+    return x;
+  } else if (mag < 0x24000000u) {
+    return x * (1.0f + x);
+  } else if (mag >= 0x3f800000u) {
+    const float t = llmk_oracle_expm1_ref(2.0f * fabsf(x));
+    z = 1.0f - 2.0f / (t + 2.0f);
+  } else {
+    const float t = llmk_oracle_expm1_ref(-2.0f * fabsf(x));
+    z = -t / (t + 2.0f);
+  }
+  return neg ? -z : z;
+}
+
+/* x rounded to nearest even into the dtype (0 f32, 1 bf16, 2 f16), as a
+ * float: a 16-bit dtype keeps p = 8 or 11 significant bits, its subnormals a
+ * fixed quantum, and overflows to infinity past its largest finite value. */
+static double round_fmt(double x, int fmt) {
+  if (fmt == 0) return (double)(float)x;
+  if (x == 0.0 || isnan(x) || isinf(x)) return x;
+  const int p = fmt == 1 ? 8 : 11, emin = fmt == 1 ? -126 : -14, emax = fmt == 1 ? 127 : 15;
+  int e = 0;
+  (void)frexp(x, &e);
+  const int lead = e - 1 < emin ? emin : e - 1;
+  const double quantum = ldexp(1.0, lead - p + 1);
+  const double r = nearbyint(x / quantum) * quantum;
+  const double maxf = ldexp(2.0 - ldexp(1.0, 1 - p), emax);
+  if (fabs(r) > maxf) return r > 0 ? INFINITY : -INFINITY;
+  return r;
+}
+
+/* candle.rs:1803-1807, (x / cap).tanh() * cap on the logits tensor, as
+ * candle's CPU ops evaluate it: each scalar operation is the tensor's affine
+ * map v * m + 0 with m = 1/cap or cap (an f64 made the dtype's value), tanh
+ * is glibc's tanhf, and in a 16-bit dtype every operation rounds to it.
+ * logits: the dtype's values as floats; rewritten in place. */
+void llmk_oracle_softcap(int dtype, float* logits, uint32_t n, float cap) {
+  const int fmt = dtype;
+  const float m = (float)round_fmt(1.0 / (double)cap, fmt);
+  const float c = (float)round_fmt((double)cap, fmt);
+  for (uint32_t i = 0; i < n; ++i) {
+    float y = (float)round_fmt((double)(logits[i] * m), fmt);
+    y = (float)round_fmt((double)(y + 0.0f), fmt);
+    float t = (float)round_fmt((double)llmk_oracle_tanh_ref(y), fmt);
+    t = (float)round_fmt((double)(t * c), fmt);
+    logits[i] = (float)round_fmt((double)(t + 0.0f), fmt);
+  }
+}
+
+/* Every float bit pattern in [lo, hi]: mismatches of tanh_ref against the
+ * host's tanhf and of expm1_ref against its expm1f (NaN results match any
+ * NaN). */
+void llmk_oracle_tanh_scan(uint32_t lo, uint32_t hi, uint64_t* n_tanh, uint64_t* n_expm1) {
+  uint64_t a = 0, b = 0;
+  for (uint64_t u = lo; u <= hi; ++u) {
+    const float x = f_bits((uint32_t)u);
+    const float r1 = tanhf(x), m1 = llmk_oracle_tanh_ref(x);
+    if (bits_f(r1) != bits_f(m1) && !(isnan(r1) && isnan(m1))) ++a;
+    const float r2 = expm1f(x), m2 = llmk_oracle_expm1_ref(x);
+    if (bits_f(r2) != bits_f(m2) && !(isnan(r2) && isnan(m2))) ++b;
+  }
+  *n_tanh = a;
+  *n_expm1 = b;
+}
+
+/* ------------------------------------------------------------------------ */
 /* Speculative-decoding verification                                          */
 /* ------------------------------------------------------------------------ */
 

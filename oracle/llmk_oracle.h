@@ -117,6 +117,15 @@ void llmk_oracle_apply_top_p(int mode, float* logits, uint32_t V, float top_p);
 uint32_t llmk_oracle_sample_simple(int mode, const float* logits, uint32_t V,
                                    float temperature, float u);
 
+/* final_logit_softcapping (candle.rs:1803-1807) as candle's CPU ops evaluate
+ * it in the logits' dtype (0 f32, 1 bf16, 2 f16; values as floats), in
+ * place; and the glibc-exact tanhf / expm1f it uses, with an exhaustive
+ * comparison against the host's. */
+void llmk_oracle_softcap(int dtype, float* logits, uint32_t n, float cap);
+float llmk_oracle_tanh_ref(float x);
+float llmk_oracle_expm1_ref(float x);
+void llmk_oracle_tanh_scan(uint32_t lo, uint32_t hi, uint64_t* n_tanh, uint64_t* n_expm1);
+
 /* Speculative-decoding verification of one row (docs/mlc-contracts.md:
  * 83-84) over the target's kept list and the draft distribution q[0..V). */
 int llmk_oracle_verify_row(uint32_t n, const uint32_t* ids, const float* probs,

@@ -53,6 +53,13 @@ def load():
     lib.llmk_oracle_verify_row.argtypes = [u32, P, P, u32, P, u32, f32, f32,
                                            ctypes.POINTER(u32), ctypes.POINTER(u32)]
     lib.llmk_oracle_verify_row.restype = ctypes.c_int
+    lib.llmk_oracle_softcap.argtypes = [ctypes.c_int, P, u32, f32]
+    lib.llmk_oracle_tanh_ref.argtypes = [f32]
+    lib.llmk_oracle_tanh_ref.restype = f32
+    lib.llmk_oracle_expm1_ref.argtypes = [f32]
+    lib.llmk_oracle_expm1_ref.restype = f32
+    lib.llmk_oracle_tanh_scan.argtypes = [u32, u32, ctypes.POINTER(ctypes.c_uint64),
+                                          ctypes.POINTER(ctypes.c_uint64)]
     u64p = ctypes.POINTER(ctypes.c_uint64)
     lib.llmk_oracle_exp_scan.argtypes = [u32, u32, u64p, u64p, u64p, ctypes.POINTER(u32)]
     _lib = lib
@@ -240,3 +247,24 @@ def verify_row(ids, probs, d, q, u_a, u_r):
     load().llmk_oracle_verify_row(i.size, _p(i), _p(p), int(d), _p(qq), qq.size, float(u_a),
                                   float(u_r), ctypes.byref(tok), ctypes.byref(acc))
     return tok.value, acc.value
+
+
+DTYPES = {"f32": 0, "bf16": 1, "f16": 2}
+
+
+def softcap(dtype, logits, cap):
+    """final_logit_softcapping (candle.rs:1803-1807) in the logits' dtype
+    ("f32", "bf16", "f16"; values given as float32), as a new array."""
+    l = np.ascontiguousarray(logits, dtype=np.float32).copy()
+    load().llmk_oracle_softcap(DTYPES[dtype], _p(l), l.size, float(cap))
+    return l
+
+
+def tanh_ref(x):
+    return np.float32(load().llmk_oracle_tanh_ref(float(x)))
+
+
+def tanh_scan(lo_bits, hi_bits):
+    a, b = ctypes.c_uint64(), ctypes.c_uint64()
+    load().llmk_oracle_tanh_scan(lo_bits, hi_bits, ctypes.byref(a), ctypes.byref(b))
+    return a.value, b.value
