@@ -371,3 +371,52 @@ def test_mirror_equals_ref_without_top_k():
         b = O.sample_row(O.MIRROR, lg, prm, hist, mask, u)
         assert a[1] == b[1] and a[4] == b[4] and np.array_equal(a[2], b[2])
         assert np.array_equal(a[3].view(np.uint32), b[3].view(np.uint32))
+
+
+# ---------------------------------------------------------------------------
+# The mask-form apply_top_p (sampler.rs:176-216), on its own cut loop
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("mode", [O.REF, O.MIRROR])
+def test_apply_top_p_against_fp64_kept_set(mode):
+    """Random rows and thresholds: the kept set is the shortest prefix of the
+    (p desc, idx asc) order whose fp64 running sum reaches top_p, on every
+    row whose cut is decided by more than 3e-4 (an f32 sequential sum of at
+    most 3000 probabilities drifts by less than 3000 * 2^-24 = 1.8e-4); kept
+    logits are unchanged, the others -inf."""
+    rng = np.random.default_rng(11)
+    checked = 0
+    for _ in range(200):
+        V = int(rng.integers(50, 3000))
+        lg = (rng.normal(0, rng.choice([0.5, 2.0, 4.0]), V)).astype(np.float32)
+        tp = float(np.float32(rng.uniform(0.05, 0.995)))
+        p = np.exp(lg.astype(np.float64) - lg.max())
+        p /= p.sum()
+        order = sorted(range(V), key=lambda i: (-p[i], i))
+        cum = np.cumsum(p[order])
+        j = int(np.searchsorted(cum, tp))  # first j with cum[j] >= tp
+        lo = cum[j - 1] if j > 0 else 0.0
+        if abs(cum[j] - tp) < 3e-4 or abs(lo - tp) < 3e-4:
+            continue
+        out = O.apply_top_p(mode, lg, tp)
+        kept = set(np.nonzero(out > -np.inf)[0].tolist())
+        assert kept == set(order[:j + 1]), (V, tp, len(kept), j + 1)
+        assert np.array_equal(out[sorted(kept)], lg[sorted(kept)])
+        checked += 1
+    assert checked >= 100
+
+
+@pytest.mark.parametrize("mode", [O.REF, O.MIRROR])
+def test_apply_top_p_cut_is_at_or_above(mode):
+    """sampler.rs:98: the cut is the first running sum >= top_p.  With top_p
+    equal to the first probability itself, exactly one token stays; one f32
+    step above it, two.  A `>` in the cut loop keeps two in the first case."""
+    lg = np.array([3.0, 1.0, 0.5, -1.0, 0.25], np.float32)
+    exp = O.exp_ref if mode == O.MIRROR else O.libm_expf
+    e = np.array([exp(np.float32(x - lg.max())) for x in lg], np.float32)
+    S = np.float32(0)
+    for x in e:  # the sequential f32 sum in index order
+        S = np.float32(S + x)
+    p0 = np.float32(e[0] / S)
+    assert np.count_nonzero(O.apply_top_p(mode, lg, float(p0)) > -np.inf) == 1
+    above = float(np.nextafter(p0, np.float32(1)))
+    assert np.count_nonzero(O.apply_top_p(mode, lg, above) > -np.inf) == 2
