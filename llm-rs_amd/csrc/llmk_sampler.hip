@@ -482,6 +482,48 @@ __device__ __forceinline__ uint32_t build_ranks(const Hist& h, uint32_t nwords,
   return total < U_MAX ? total : U_MAX;
 }
 
+// pre[w] = history tokens in the bitmap words before w, built by the first nw
+// waves from contiguous runs of words (a popcount per run, an exclusive scan
+// over the threads), which call sync() together twice.  Returns the number
+// of tokens, which the caller knows to be at most U_MAX.  wtot: nw words.
+template <class Sync>
+__device__ __forceinline__ uint32_t build_pre(const Hist& h, uint32_t nwords,
+                                              LDS uint32_t* wtot, uint32_t nw, Sync& sync) {
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
+  const uint32_t per = (nwords + 64u * nw - 1u) / (64u * nw);
+  const uint32_t w0 = tid * per < nwords ? tid * per : nwords;
+  const uint32_t w1 = w0 + per < nwords ? w0 + per : nwords;
+  uint32_t c = 0;
+  for (uint32_t b0 = w0; b0 < w1; b0 += 8) {
+    uint32_t x[8];
+#pragma unroll
+    for (uint32_t q = 0; q < 8; ++q) x[q] = b0 + q < w1 ? h.bitmap[b0 + q] : 0u;
+#pragma unroll
+    for (uint32_t q = 0; q < 8; ++q) c += (uint32_t)__popc(x[q]);
+  }
+  const uint32_t incl = wave_incl_scan(c);
+  if (lane == 63) wtot[wv] = incl;
+  sync();
+  uint32_t r = incl - c, total = 0;
+  for (uint32_t i = 0; i < nw; ++i) {
+    const uint32_t t = wtot[i];
+    r += i < wv ? t : 0u;
+    total += t;
+  }
+  for (uint32_t b0 = w0; b0 < w1; b0 += 8) {
+    uint32_t x[8];
+#pragma unroll
+    for (uint32_t q = 0; q < 8; ++q) x[q] = b0 + q < w1 ? h.bitmap[b0 + q] : 0u;
+#pragma unroll
+    for (uint32_t q = 0; q < 8; ++q) {
+      if (b0 + q < w1) h.pre[b0 + q] = (uint16_t)r;
+      r += (uint32_t)__popc(x[q]);
+    }
+  }
+  sync();
+  return total;
+}
+
 // A barrier among waves 0 .. n-1 while the others run on: an arrival count
 // in LDS that the waiting waves poll.  Every one of the n waves makes every
 // call, and none of them waits on the other waves in between, so each wait
@@ -3135,16 +3177,19 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   LDS uint32_t* btot = hb + hist_lds_words(nwords);  // NW words
   h.lo = lo;
   // Waves 0..TW-1 load the history tokens (TQ per lane per pass); every
-  // wave then requests its first two tiles.
+  // wave then requests its first tile.
   constexpr uint32_t TW = 8;
   constexpr int TQ = 4;  // tokens per lane per pass
   const void* row = (const char*)a.logits +
                     (uint64_t)b * a.stride * ((DT & 3) == LLMK_F32 ? 4u : 2u);
   const uint32_t* mrow = a.mask ? a.mask + (uint64_t)b * a.mask_words : nullptr;
-  Raw ra, rb;
-  uint32_t ta = t0 + (uint32_t)wv, tb2 = t0 + (uint32_t)wv + NW;
+  // One tile in flight per wave: 16 waves per CU already keep HBM busy, and
+  // a deeper queue only adds latency to every other load (the history
+  // tokens and their logits, instruction fetches) and to the last tiles
+  // (measured: C3 40.1 -> 38.7 us, C5 165 -> 159 us against two per wave).
+  Raw ra;
+  uint32_t ta = t0 + (uint32_t)wv;
   ta = ta < t1 ? ta : EMPTY;
-  tb2 = tb2 < t1 ? tb2 : EMPTY;
   const bool tok_wave = (uint32_t)wv < TW;
   if (P.mode == MODE_INVALID) {
     if (g == 0 && tid == 0) {
@@ -3207,15 +3252,18 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   }
   __syncthreads();
   float pf[TQ];
+  uint32_t pm[TQ];
 #pragma unroll
-  for (int q = 0; q < TQ; ++q) pf[q] = 0.0f;
+  for (int q = 0; q < TQ; ++q) {
+    pf[q] = 0.0f;
+    pm[q] = 0xffffffffu;
+  }
   // Without history, the tiles now.  With history, they are requested after
   // the bitmap barrier: requests queued ahead of the history tokens and
   // their logits would delay them by microseconds, and the tables cannot be
   // built without them.
   if (!have) {
     if (ta != EMPTY) load_tile<DT>(a, row, mrow, h, ta, lane, ra);
-    if (tb2 != EMPTY) load_tile<DT>(a, row, mrow, h, tb2, lane, rb);
   }
   // The history tables: the bitmap of the segment's history tokens, their
   // ranks, for the frequency penalty occurrence counts by rank, and the
@@ -3237,24 +3285,31 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
         }
       }
     };
+    // Every history token held in tk[] (one pass): the token waves keep
+    // their tokens' logits in registers and place them by rank themselves.
+    const bool one_pass = early && h1 - h0 <= step;
     if (tok_wave) {
       each_token([&](uint32_t t) {
         __atomic_fetch_or(&h.bitmap[(t - lo) >> 5], 1u << (t & 31), __ATOMIC_RELAXED);
       });
-      // the logits of the first pass's history tokens, requested now (after
-      // the insertions, which must not wait for them) so that the gather
-      // after the rank tables finds them in L2; token waves only: a wait
-      // that the others executed, even with no lane loading, would wait for
-      // their tiles
+      // the logits (and allow-mask words) of the first pass's history
+      // tokens, requested now, ahead of every tile (after the insertions,
+      // which must not wait for them); token waves only: a wait that the
+      // others executed, even with no lane loading, would wait for their
+      // tiles
 #pragma unroll
       for (int q = 0; q < TQ; ++q)
-        if (tk[q] >= lo && tk[q] < hi) pf[q] = load_logit<DT>(row, tk[q]);
+        if (tk[q] >= lo && tk[q] < hi) {
+          pf[q] = load_logit<DT>(row, tk[q]);
+          if (one_pass && mrow) pm[q] = G(mrow)[tk[q] >> 5];
+        }
     }
     __syncthreads();
-    // the token waves of the early path request theirs after the tables
-    if (!(early && tok_wave)) {
+    // the token waves of the early multi-pass path request theirs after the
+    // tables; in one pass the loads of the tokens' logits come first in
+    // every token wave, so waiting for them does not wait for its tiles
+    if (!(early && tok_wave) || one_pass) {
       if (ta != EMPTY) load_tile<DT>(a, row, mrow, h, ta, lane, ra);
-      if (tb2 != EMPTY) load_tile<DT>(a, row, mrow, h, tb2, lane, rb);
     }
     auto counts = [&]() __attribute__((always_inline)) {
       each_token([&](uint32_t t) {
@@ -3270,7 +3325,46 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
       // waves go on to their tiles while the token waves build the tables
       // and reduce the virtual tiles (the gathers' latency hidden behind
       // the streaming waves).
-      if (tok_wave) {
+      if (tok_wave && one_pass) {
+        // pre[] by word runs; each thread ranks its own tokens, counts them,
+        // penalises their logits (already in registers) and writes them by
+        // rank (a token held twice writes the same values twice)
+        GroupSync gs{&misc[M_GSYNC], TW, 0};
+        const uint32_t U = build_pre(h, nwords, btot, TW, gs);
+        LDS uint32_t* cnt = (LDS uint32_t*)h.pen;
+        uint32_t rk[TQ];
+#pragma unroll
+        for (int q = 0; q < TQ; ++q) rk[q] = (tk[q] >= lo && tk[q] < hi) ? h.rank(tk[q]) : EMPTY;
+        if (need_cnt) {
+#pragma unroll
+          for (int q = 0; q < TQ; ++q)
+            if (rk[q] != EMPTY) __atomic_fetch_add(&cnt[rk[q]], 1u, __ATOMIC_RELAXED);
+          gs();
+        }
+        float y[TQ];
+#pragma unroll
+        for (int q = 0; q < TQ; ++q) {
+          y[q] = NEG_INF;
+          if (rk[q] != EMPTY) {
+            const bool allowed = (pm[q] >> (tk[q] & 31)) & 1u;
+            const float x = pf[q];
+            if (allowed && !(x < __builtin_huge_valf()) && P.mode == MODE_SAMPLE)
+              __atomic_fetch_or(&misc[M_FLAGS], FLAG_NAN, __ATOMIC_RELAXED);
+            float v = (x > NEG_INF) ? x : NEG_INF;  // NaN acts as -inf
+            v = penalize(v, P, need_cnt ? cnt[rk[q]] : 1u);
+            y[q] = allowed ? v : NEG_INF;
+          }
+        }
+        if (need_cnt) gs();  // every count is read before pen[] (which holds them) is written
+#pragma unroll
+        for (int q = 0; q < TQ; ++q)
+          if (rk[q] != EMPTY) {
+            h.pen[rk[q]] = y[q];
+            h.tokr[rk[q]] = tk[q];
+          }
+        gs();
+        for (uint32_t k = (uint32_t)wv; k < nch; k += TW) vtile_chunk(a, t0, nwords, k, U, h, E, lane);
+      } else if (tok_wave) {
         GroupSync gs{&misc[M_GSYNC], TW, 0};
         const uint32_t U = build_ranks(h, nwords, btot, &misc[M_FLAGS], TW, gs);
         if (need_cnt) {
@@ -3278,7 +3372,6 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
           gs();
         }
         if (ta != EMPTY) load_tile<DT>(a, row, mrow, h, ta, lane, ra);
-        if (tb2 != EMPTY) load_tile<DT>(a, row, mrow, h, tb2, lane, rb);
 #pragma unroll
         for (int q = 0; q < TQ; ++q) asm volatile("" ::"v"(pf[q]));  // the prefetch is done
         gather_penalised<DT>(a, P, b, row, U, h, need_cnt, TW, &misc[M_FLAGS]);
@@ -3337,26 +3430,13 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
     uint32_t k = 0;
     if (lane == 0) k = __atomic_fetch_add(&misc[M_NEXT], 1u, __ATOMIC_RELAXED);
     k = (uint32_t)__builtin_amdgcn_readfirstlane((int)k);
-    const uint32_t t = t0 + 2u * NW + k;
+    const uint32_t t = t0 + NW + k;
     return t < t1 ? t : EMPTY;
   };
-  if (ta != EMPTY) {
+  while (ta != EMPTY) {
     process(ra, ta);
     ta = grab();
     if (ta != EMPTY) load_tile<DT>(a, row, mrow, h, ta, lane, ra);
-  }
-  for (;;) {
-    if (ta == EMPTY && tb2 == EMPTY) break;
-    if (tb2 != EMPTY) {
-      process(rb, tb2);
-      tb2 = grab();
-      if (tb2 != EMPTY) load_tile<DT>(a, row, mrow, h, tb2, lane, rb);
-    }
-    if (ta != EMPTY) {
-      process(ra, ta);
-      ta = grab();
-      if (ta != EMPTY) load_tile<DT>(a, row, mrow, h, ta, lane, ra);
-    }
   }
   // ---- publish the segment; the row's last workgroup finalizes
   wait_stores();
