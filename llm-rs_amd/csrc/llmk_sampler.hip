@@ -1694,11 +1694,25 @@ __device__ __attribute__((noinline)) float exact_normaliser(
     if (tot <= SERIAL_MAX) {
       // every wave packed, few entries: one lane sums them in order
       if (tid == 0) {
+        // eight 16-byte reads in flight, then their 32 additions in order
+        // (a read per four additions would wait on the LDS each time)
         float cc = c;
         for (uint32_t i = 0; i < NW; ++i) {
           LDS const float* L = comp0 + CW * i;
           const uint32_t ni = nwv[i];
           uint32_t k = 0;
+          for (; k + 32u <= ni; k += 32u) {
+            f4v y[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) y[j] = *(LDS const f4v*)(L + k + 4 * j);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              cc = cc + y[j].x;
+              cc = cc + y[j].y;
+              cc = cc + y[j].z;
+              cc = cc + y[j].w;
+            }
+          }
           for (; k + 4u <= ni; k += 4u) {
             const f4v y = *(LDS const f4v*)(L + k);
             cc = cc + y.x;
@@ -2353,11 +2367,19 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
     }
     if (id == 0) f.fm[F_SCR + 2] = 0;
   };
+  // the largest binned p: a running maximum per thread, one atomic per wave
+  // after the pass (an atomic per candidate on one word serialises)
+  uint32_t pmx = 0;
   auto hist_add = [&](float pv) __attribute__((always_inline)) {
     const uint32_t bi = __float_as_uint(pv) >> 19;
     __atomic_fetch_add(&bcnt[bi], 1u, __ATOMIC_RELAXED);
     __atomic_fetch_add(&bmass[bi], pv, __ATOMIC_RELAXED);
-    __atomic_fetch_max(&f.fm[F_SCR + 2], __float_as_uint(pv), __ATOMIC_RELAXED);
+    pmx = umax(pmx, __float_as_uint(pv));
+  };
+  auto hist_flush = [&]() __attribute__((always_inline)) {
+    const uint32_t x = wave_max_u32(pmx);
+    if ((id & 63u) == 0 && x) __atomic_fetch_max(&f.fm[F_SCR + 2], x, __ATOMIC_RELAXED);
+    pmx = 0;
   };
   // pv of candidate e if it is at or above lam (0 otherwise), where a lane
   // of the wave needs one
@@ -2427,6 +2449,7 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
       }
     n0 += tot;
   }
+  if (!topk) hist_flush();
   SY::sync();
   uint32_t n = 0;
   if (!topk || n0 > SORT_CAP) {
@@ -2437,6 +2460,7 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
       each([&](bool k, float pv, uint32_t) __attribute__((always_inline)) {
         if (k) hist_add(pv);
       });
+      hist_flush();
       SY::sync();
     }
     if (threadIdx.x < WAVE) {
