@@ -54,6 +54,26 @@ def measured_traffic(config):
     return int(m.group(1)), os.path.basename(path)
 
 
+def with_count_history(w, db):
+    """db with each row's history in the count-table form (hist_counts): its
+    distinct tokens, ascending, with their occurrences, as the device push
+    llmk_history_count_append keeps them."""
+    import numpy as np
+    import torch
+    toks, cnts = [], []
+    for b in range(w.B):
+        u, c = np.unique(w.hist_tokens[w.hist_offsets[b]:w.hist_offsets[b + 1]],
+                         return_counts=True)
+        toks.append(u.astype(np.uint32))
+        cnts.append(c.astype(np.uint32))
+    offs = np.concatenate([[0], np.cumsum([len(u) for u in toks])]).astype(np.uint32)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int32)).to(db.logits.device)
+    db.hist_offsets = T(offs)
+    db.hist_tokens = T(np.concatenate(toks))
+    db.hist_counts = T(np.concatenate(cnts))
+    return db, int(offs[-1])
+
+
 def rotated_sets(llmk, db0, logit_bytes, sets=0):
     """db0 and clones of its logits, enough that consecutive steps do not
     find the previous step's logits in the 256 MB MALL."""
@@ -85,6 +105,9 @@ def time_config(llmk, synth, torch, name, steps=20, warmup=5):
     """Time per launch of one config (back-to-back launches between two
     events), its logits rotated over enough copies to leave the MALL."""
     import numpy as np
+    counts = name.endswith("-counts")
+    if counts:
+        name = name[:-7]
     if name.endswith("-f16"):
         # the config with its logits rounded to f16 (a half-precision lm_head
         # output handed over as it is)
@@ -95,6 +118,11 @@ def time_config(llmk, synth, torch, name, steps=20, warmup=5):
     else:
         w = synth.make(name)
     db0 = w.to_device()
+    alg = w.algorithmic_bytes()
+    if counts:
+        # the history read as (token, count) pairs: 8 bytes per distinct token
+        db0, nd = with_count_history(w, db0)
+        alg += 8 * nd - 4 * int(w.hist_tokens.size)
     dbs = rotated_sets(llmk, db0, db0.logits.numel() * db0.logits.element_size())
     s = llmk.HipSampler(max_batch=w.B, max_vocab=w.V)
     tok = torch.empty(w.B, dtype=torch.int32, device="cuda:0")
@@ -102,7 +130,7 @@ def time_config(llmk, synth, torch, name, steps=20, warmup=5):
     stream = torch.cuda.current_stream()
     back_to_back(torch, s, prepared, warmup, stream)
     us = back_to_back(torch, s, prepared, steps, stream) * 1e3
-    gbps = w.algorithmic_bytes() / (us * 1e-6) / 1e9
+    gbps = alg / (us * 1e-6) / 1e9
     s.close()
     return {"B": w.B, "V": w.V, "dtype": w.dtype, "us_per_step": us,
             "tokens_per_s": w.B / (us * 1e-6), "achieved_GBps": gbps,
@@ -297,7 +325,7 @@ def main():
     others = None
     if not args.no_other_configs:
         others = {}
-        for name in ("C1", "C2", "C3", "C4", "C5", "C3-f16"):
+        for name in ("C1", "C2", "C3", "C4", "C5", "C3-f16", "C3-counts", "C5-counts"):
             if name == args.config:
                 continue
             others[name] = time_config(llmk, synth, torch, name)

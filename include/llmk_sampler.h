@@ -119,6 +119,16 @@ typedef struct {
    * each rounded to the dtype); 0 = off.  Fused into the sampling pass: the
    * capped logits are never written. */
   float softcap;
+  /* Optional: the count-table form of the history (the per-row counts the
+   * scheduler's token push, scheduler.rs:147, accumulates), indexed like
+   * hist_tokens: entry i stands for hist_counts[i] occurrences of token
+   * hist_tokens[i] (0 is read as 1).  Penalties are those of the history that
+   * lists each token that many times (sampler.rs:128-147; the frequency
+   * penalty's count).  Entries may come in any order; a token listed twice
+   * has the sum of its counts.  llmk_history_count_append keeps such tables
+   * sorted and distinct on the device, so a step reads each distinct token
+   * once instead of every occurrence.  NULL = one occurrence per entry. */
+  const uint32_t* hist_counts;
 } llmk_sample_batch_args;
 
 /* Create a sampler on `device` able to serve batches up to max_batch rows of
@@ -200,6 +210,20 @@ int llmk_apply_logit_bias(llmk_sampler* s, float* logits, uint32_t batch, uint32
 int llmk_history_append(llmk_sampler* s, uint32_t batch, const uint32_t* hist_offsets,
                         uint32_t* hist_lengths, uint32_t* hist_tokens, uint32_t capacity,
                         const uint32_t* tokens, void* hip_stream);
+
+/* The token push of scheduler.rs:147 on a count-table history: row b's
+ * entries hist_tokens/hist_counts[hist_offsets[b] .. + hist_lengths[b]) hold
+ * its distinct tokens in ascending order with their occurrences.  A token
+ * already listed gets count + 1; a new token is inserted in order with count
+ * 1 (hist_lengths[b] += 1), or, when the row already holds `capacity`
+ * entries, the row is left as it is and LLMK_STATUS_HISTORY_FULL is raised.
+ * Rows whose token is LLMK_INVALID_TOKEN are left as they are.  Pass the same
+ * arrays as hist_offsets / hist_tokens / hist_lengths / hist_counts of
+ * llmk_sample_batch_args.  Enqueued on hip_stream; allocates nothing. */
+int llmk_history_count_append(llmk_sampler* s, uint32_t batch, const uint32_t* hist_offsets,
+                              uint32_t* hist_lengths, uint32_t* hist_tokens,
+                              uint32_t* hist_counts, uint32_t capacity,
+                              const uint32_t* tokens, void* hip_stream);
 
 /* Speculative-decoding verification, batched: the residual resampling that
  * docs/mlc-contracts.md:83-84 describes (BatchVerifyDraftTokensWithProb-

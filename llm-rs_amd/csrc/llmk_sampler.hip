@@ -103,6 +103,7 @@ struct Args {
   const int32_t* top_k;
   const uint32_t *hoff, *htok, *mask;
   const uint32_t* hlen;  // optional: row b's history is htok[hoff[b] .. hoff[b] + hlen[b])
+  const uint32_t* hcnt;  // optional: occurrences of each htok entry (the count-table form)
   uint32_t mask_words;
   const float* u;
   uint32_t *out_tok, *out_ids, *out_cnt;
@@ -546,6 +547,12 @@ struct BarrierSync {
 // Builds the history tables for tokens in [lo, hi) of row b.  All threads.
 // Global round trips: the row's history (held in registers, HTPT tokens per
 // thread per pass) and one gather of the logits of the distinct tokens.
+// Occurrences of history entry i: its count in the count-table form (read
+// as at least 1: a listed token is in the history), else 1 per entry.
+__device__ __forceinline__ uint32_t hist_weight(const Args& a, uint32_t i) {
+  return a.hcnt ? umax(G(a.hcnt)[i], 1u) : 1u;
+}
+
 constexpr int HTPT = 8;
 template <int DT>
 __device__ __forceinline__ void build_history(const Args& a, const RowP& P, uint32_t b,
@@ -612,13 +619,11 @@ __device__ __forceinline__ void build_history(const Args& a, const RowP& P, uint
 #pragma unroll
       for (int q = 0; q < HTPT; ++q) {
         uint32_t t = tk[q];
-        if (!one_pass) {
-          const uint32_t i = c0 + q * NT + tid;
-          t = (i < h1) ? G(a.htok)[i] : EMPTY;
-        }
+        const uint32_t i = c0 + q * NT + tid;
+        if (!one_pass) t = (i < h1) ? G(a.htok)[i] : EMPTY;
         if (t >= lo && t < hi) {
           const uint32_t r = h.rank(t);
-          if (r < U_MAX) __atomic_fetch_add(&cnt[r], 1u, __ATOMIC_RELAXED);
+          if (r < U_MAX) __atomic_fetch_add(&cnt[r], hist_weight(a, i), __ATOMIC_RELAXED);
         }
       }
     }
@@ -3245,14 +3250,18 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   E.lpart = a.G == 1 ? (LDS f2v*)(smem + a.lds_part) : nullptr;
   E.lcand = a.G == 1 ? (LDS u2v*)(smem + a.lds_cand) : nullptr;
   const uint32_t nch = (nwords + 511) / 512;  // chunks of this segment
-  uint32_t tk[TQ];
+  uint32_t tk[TQ], hc[TQ];
 #pragma unroll
-  for (int q = 0; q < TQ; ++q) tk[q] = EMPTY;
+  for (int q = 0; q < TQ; ++q) {
+    tk[q] = EMPTY;
+    hc[q] = 1u;
+  }
   if (tok_wave && have) {
 #pragma unroll
     for (int q = 0; q < TQ; ++q) {
       const uint32_t i = h0 + q * (TW * WAVE) + tid;
       tk[q] = i < h1 ? G(a.htok)[i] : EMPTY;
+      if (need_cnt && a.hcnt) hc[q] = i < h1 ? G(a.hcnt)[i] : 1u;
     }
   }
   if (collect) {
@@ -3294,18 +3303,19 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   // penalised logits by rank; then the virtual tiles (one per 16-tile chunk).
   if (have) {
     const uint32_t step = TQ * TW * WAVE;
+    // fn(token, history index)
     auto each_token = [&](auto&& fn) __attribute__((always_inline)) {
       // the first pass from registers (no load in flight but the tiles'),
       // the rest loaded here
 #pragma unroll
       for (int q = 0; q < TQ; ++q)
-        if (tk[q] >= lo && tk[q] < hi) fn(tk[q]);
+        if (tk[q] >= lo && tk[q] < hi) fn(tk[q], h0 + q * (TW * WAVE) + tid);
       for (uint32_t c0 = h0 + step; c0 < h1; c0 += step) {
 #pragma unroll
         for (int q = 0; q < TQ; ++q) {
           const uint32_t i = c0 + q * (TW * WAVE) + tid;
           const uint32_t t = (i < h1) ? G(a.htok)[i] : EMPTY;
-          if (t >= lo && t < hi) fn(t);
+          if (t >= lo && t < hi) fn(t, i);
         }
       }
     };
@@ -3313,7 +3323,7 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
     // their tokens' logits in registers and place them by rank themselves.
     const bool one_pass = early && h1 - h0 <= step;
     if (tok_wave) {
-      each_token([&](uint32_t t) {
+      each_token([&](uint32_t t, uint32_t) {
         __atomic_fetch_or(&h.bitmap[(t - lo) >> 5], 1u << (t & 31), __ATOMIC_RELAXED);
       });
       // the logits (and allow-mask words) of the first pass's history
@@ -3336,11 +3346,11 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
       if (ta != EMPTY) load_tile<DT>(a, row, mrow, h, ta, lane, ra);
     }
     auto counts = [&]() __attribute__((always_inline)) {
-      each_token([&](uint32_t t) {
+      each_token([&](uint32_t t, uint32_t i) {
         const uint32_t o = t - lo, wd = h.bitmap[o >> 5], bit = 1u << (o & 31);
         if (wd & bit) {  // not dropped by the rank limit
           const uint32_t r = h.pre[o >> 5] + (uint32_t)__popc(wd & (bit - 1u));
-          __atomic_fetch_add(&((LDS uint32_t*)h.pen)[r], 1u, __ATOMIC_RELAXED);
+          __atomic_fetch_add(&((LDS uint32_t*)h.pen)[r], hist_weight(a, i), __ATOMIC_RELAXED);
         }
       });
     };
@@ -3362,7 +3372,7 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
         if (need_cnt) {
 #pragma unroll
           for (int q = 0; q < TQ; ++q)
-            if (rk[q] != EMPTY) __atomic_fetch_add(&cnt[rk[q]], 1u, __ATOMIC_RELAXED);
+            if (rk[q] != EMPTY) __atomic_fetch_add(&cnt[rk[q]], umax(hc[q], 1u), __ATOMIC_RELAXED);
           gs();
         }
         float y[TQ];
@@ -3783,6 +3793,94 @@ __global__ __launch_bounds__(256) void history_append_kernel(uint32_t B, const u
   G(hlen)[b] = n + 1;
 }
 
+// The count-table form of the same push: row b's history is its distinct
+// tokens htok[hoff[b] .. hoff[b] + hlen[b]) in ascending order, with their
+// occurrences in hcnt at the same positions.  A token already listed has its
+// count raised by one; a new one is inserted in order with count 1 (the
+// entries above it move up by one) while hlen[b] < cap, else the row keeps
+// its table and raises a status bit.  One workgroup per row: its entries are
+// read HCA_Q per thread, below-t counted and an equal entry looked for, then
+// the entries from the insertion point up are moved, the highest chunk
+// first, every read of a chunk before any of its writes.
+constexpr uint32_t HCA_T = 256, HCA_Q = 8, HCA_CH = HCA_T * HCA_Q;
+__global__ __launch_bounds__(HCA_T) void history_count_append_kernel(
+    const uint32_t* hoff, uint32_t* hlen, uint32_t* htok, uint32_t* hcnt, uint32_t cap,
+    const uint32_t* tok, uint32_t* status) {
+  __shared__ uint32_t red[2 * (HCA_T / WAVE)];
+  const uint32_t b = blockIdx.x, tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
+  const uint32_t t = G(tok)[b];
+  if (t == LLMK_INVALID_TOKEN) return;
+  const uint32_t off = G(hoff)[b], n = G(hlen)[b];
+  GLB uint32_t* T = G(htok) + off;
+  GLB uint32_t* C = G(hcnt) + off;
+  uint32_t below = 0, eq = EMPTY;
+  for (uint32_t c0 = 0; c0 < n; c0 += HCA_CH) {
+    uint32_t x[HCA_Q];
+#pragma unroll
+    for (uint32_t q = 0; q < HCA_Q; ++q) {
+      const uint32_t i = c0 + q * HCA_T + tid;
+      x[q] = i < n ? T[i] : EMPTY;
+    }
+#pragma unroll
+    for (uint32_t q = 0; q < HCA_Q; ++q) {
+      const uint32_t i = c0 + q * HCA_T + tid;
+      if (i < n) {
+        below += x[q] < t ? 1u : 0u;
+        if (x[q] == t) eq = umin(eq, i);
+      }
+    }
+  }
+  below = bcast63u(wave_incl_scan(below));
+  eq = wave_min_u32(eq);
+  if (lane == 0) {
+    red[wv] = below;
+    red[HCA_T / WAVE + wv] = eq;
+  }
+  __syncthreads();
+  below = 0;
+  eq = EMPTY;
+#pragma unroll
+  for (uint32_t i = 0; i < HCA_T / WAVE; ++i) {
+    below += red[i];
+    eq = umin(eq, red[HCA_T / WAVE + i]);
+  }
+  if (eq != EMPTY) {
+    if (tid == 0) C[eq] = C[eq] + 1u;
+    return;
+  }
+  if (n >= cap) {
+    if (tid == 0) atomicOr(status, LLMK_STATUS_HISTORY_FULL);
+    return;
+  }
+  const uint32_t pos = below;
+  for (uint32_t hi = n; hi > pos;) {
+    const uint32_t lo = hi - pos > HCA_CH ? hi - HCA_CH : pos;
+    uint32_t xt[HCA_Q], xc[HCA_Q];
+#pragma unroll
+    for (uint32_t q = 0; q < HCA_Q; ++q) {
+      const uint32_t i = lo + q * HCA_T + tid;
+      xt[q] = i < hi ? T[i] : 0u;
+      xc[q] = i < hi ? C[i] : 0u;
+    }
+    __syncthreads();  // the chunk's reads before its writes (the next chunk's reads lie below lo)
+#pragma unroll
+    for (uint32_t q = 0; q < HCA_Q; ++q) {
+      const uint32_t i = lo + q * HCA_T + tid;
+      if (i < hi) {
+        T[i + 1] = xt[q];
+        C[i + 1] = xc[q];
+      }
+    }
+    hi = lo;
+  }
+  __syncthreads();  // entry pos was read by the first chunk before it is rewritten
+  if (tid == 0) {
+    T[pos] = t;
+    C[pos] = 1u;
+    G(hlen)[b] = n + 1u;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Speculative-decoding verification (docs/mlc-contracts.md:83-84: accept the
 // draft token unless r >= p/q, else resample from max(p - q, 0))
@@ -4074,6 +4172,8 @@ static int sample_batch_run(const Ws& ws, uint32_t max_batch, uint32_t max_vocab
     return fail(LLMK_ERR_INVALID_ARGUMENT, "hist_offsets and hist_tokens go together");
   if (in->hist_lengths && !in->hist_offsets)
     return fail(LLMK_ERR_INVALID_ARGUMENT, "hist_lengths needs hist_offsets and hist_tokens");
+  if (in->hist_counts && !in->hist_offsets)
+    return fail(LLMK_ERR_INVALID_ARGUMENT, "hist_counts needs hist_offsets and hist_tokens");
   if (in->allow_mask && in->mask_words_per_row < (in->vocab + 31) / 32)
     return fail(LLMK_ERR_INVALID_ARGUMENT, "mask_words_per_row < ceil(vocab/32)");
   if (in->out_cap && !in->out_ids && !in->out_probs)
@@ -4108,6 +4208,7 @@ static int sample_batch_run(const Ws& ws, uint32_t max_batch, uint32_t max_vocab
   a.hoff = in->hist_offsets;
   a.htok = in->hist_tokens;
   a.hlen = in->hist_lengths;
+  a.hcnt = in->hist_counts;
   a.mask = in->allow_mask;
   a.mask_words = in->mask_words_per_row;
   a.u = in->uniforms;
@@ -4340,6 +4441,23 @@ extern "C" int llmk_verify_batch(llmk_sampler* s, uint32_t batch, uint32_t vocab
                draft_stride, u_accept, u_resample, out_tokens, out_accepted};
   hipLaunchKernelGGL(verify_kernel, dim3(batch), dim3(WAVE), 0, (hipStream_t)stream, v,
                      s->ws.status);
+  HIPCHK(hipGetLastError());
+  return LLMK_OK;
+}
+
+extern "C" int llmk_history_count_append(llmk_sampler* s, uint32_t batch,
+                                         const uint32_t* hist_offsets, uint32_t* hist_lengths,
+                                         uint32_t* hist_tokens, uint32_t* hist_counts,
+                                         uint32_t capacity, const uint32_t* tokens,
+                                         void* stream) {
+  if (!s) return fail(LLMK_ERR_INVALID_ARGUMENT, "sampler is NULL");
+  if (!hist_offsets || !hist_lengths || !hist_tokens || !hist_counts || !tokens)
+    return fail(LLMK_ERR_INVALID_ARGUMENT, "history arrays, counts and tokens are required");
+  if (batch == 0) return LLMK_OK;
+  HIPCHK(hipSetDevice(s->device));
+  hipLaunchKernelGGL(history_count_append_kernel, dim3(batch), dim3(HCA_T), 0,
+                     (hipStream_t)stream, hist_offsets, hist_lengths, hist_tokens, hist_counts,
+                     capacity, tokens, s->ws.status);
   HIPCHK(hipGetLastError());
   return LLMK_OK;
 }

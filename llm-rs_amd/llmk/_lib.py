@@ -38,6 +38,7 @@ EXPORTED_SYMBOLS = (
     "llmk_apply_top_p",
     "llmk_apply_logit_bias",
     "llmk_history_append",
+    "llmk_history_count_append",
     "llmk_sample_batch_static",
     "llmk_verify_batch",
 )
@@ -71,6 +72,7 @@ class SampleBatchArgs(ctypes.Structure):
         ("out_count", ctypes.c_void_p),
         ("hist_lengths", ctypes.c_void_p),
         ("softcap", ctypes.c_float),
+        ("hist_counts", ctypes.c_void_p),
     ]
 
 
@@ -108,6 +110,9 @@ def load():
     lib.llmk_apply_logit_bias.restype = ctypes.c_int
     lib.llmk_history_append.argtypes = [vp, ctypes.c_uint32, vp, vp, vp, ctypes.c_uint32, vp, vp]
     lib.llmk_history_append.restype = ctypes.c_int
+    lib.llmk_history_count_append.argtypes = [vp, ctypes.c_uint32, vp, vp, vp, vp,
+                                              ctypes.c_uint32, vp, vp]
+    lib.llmk_history_count_append.restype = ctypes.c_int
     u32, u64 = ctypes.c_uint32, ctypes.c_uint64
     lib.llmk_verify_batch.argtypes = [vp, u32, u32, vp, vp, u32, vp, vp, vp, u64, vp, vp, vp, vp,
                                       vp]

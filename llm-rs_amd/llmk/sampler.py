@@ -78,6 +78,7 @@ class DeviceBatch:
     allow_mask: Optional[torch.Tensor] = None    # int32/uint32 [B, words]
     hist_lengths: Optional[torch.Tensor] = None  # int32/uint32 [B]: per-row buffers
     softcap: float = 0.0  # > 0: the logits are the lm_head output before final_logit_softcapping
+    hist_counts: Optional[torch.Tensor] = None  # int32/uint32, like hist_tokens: occurrences
 
 
 def _on_device(dev: torch.device, **tensors) -> None:
@@ -126,7 +127,7 @@ def _batch_args(db: DeviceBatch, out_tokens: torch.Tensor,
                   presence_penalty=db.presence_penalty, frequency_penalty=db.frequency_penalty,
                   hist_offsets=db.hist_offsets, hist_tokens=db.hist_tokens,
                   allow_mask=db.allow_mask, hist_lengths=db.hist_lengths,
-                  out_tokens=out_tokens, out_ids=out_ids, out_probs=out_probs,
+                  hist_counts=db.hist_counts, out_tokens=out_tokens, out_ids=out_ids, out_probs=out_probs,
                   out_count=out_count)
     _on_device(lg.device, **fields)
     if db.uniforms is None:
@@ -136,7 +137,7 @@ def _batch_args(db: DeviceBatch, out_tokens: torch.Tensor,
         _flat(name, fields[name], _F32)
     for name in ("top_k", "out_tokens", "out_ids", "out_count"):
         _flat(name, fields[name], _I32)
-    for name in ("hist_offsets", "hist_tokens", "allow_mask", "hist_lengths"):
+    for name in ("hist_offsets", "hist_tokens", "allow_mask", "hist_lengths", "hist_counts"):
         _flat(name, fields[name], _I32 + (getattr(torch, "uint32", torch.int32),))
     B = lg.shape[0]
     V = db.vocab if db.vocab is not None else lg.shape[1]
@@ -170,6 +171,7 @@ def _batch_args(db: DeviceBatch, out_tokens: torch.Tensor,
     a.out_count = _ptr(out_count)
     a.hist_lengths = _ptr(db.hist_lengths)
     a.softcap = float(db.softcap or 0.0)
+    a.hist_counts = _ptr(db.hist_counts)
     return a
 
 
@@ -348,6 +350,34 @@ class HipSampler:
                                            hist_lengths.data_ptr(), hist_tokens.data_ptr(),
                                            capacity, tokens.data_ptr(),
                                            ctypes.c_void_p(st.cuda_stream))
+        if rc != 0:
+            raise SamplerError(rc, _lib.last_error())
+
+    def history_count_append(self, hist_offsets: torch.Tensor, hist_lengths: torch.Tensor,
+                             hist_tokens: torch.Tensor, hist_counts: torch.Tensor,
+                             capacity: int, tokens: torch.Tensor,
+                             stream: Optional[torch.cuda.Stream] = None) -> None:
+        """scheduler.rs:147 on a count-table history: token b joins row b's
+        sorted distinct tokens (count 1) or raises its count (int32 tensors,
+        updated in place)."""
+        for t in (hist_offsets, hist_lengths, hist_tokens, hist_counts, tokens):
+            if t.dtype != torch.int32 or not t.is_contiguous():
+                raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT,
+                                   "history arrays, counts and tokens must be contiguous int32")
+        _on_device(tokens.device, hist_offsets=hist_offsets, hist_lengths=hist_lengths,
+                   hist_tokens=hist_tokens, hist_counts=hist_counts)
+        B = tokens.shape[0]
+        if hist_offsets.numel() < B or hist_lengths.numel() < B:
+            raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT,
+                               "hist_offsets and hist_lengths need one entry per row")
+        if hist_counts.numel() < hist_tokens.numel():
+            raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT,
+                               "hist_counts needs an entry per hist_tokens entry")
+        st = self._stream(tokens, stream)
+        rc = self._lib.llmk_history_count_append(
+            self._h, B, hist_offsets.data_ptr(), hist_lengths.data_ptr(),
+            hist_tokens.data_ptr(), hist_counts.data_ptr(), capacity, tokens.data_ptr(),
+            ctypes.c_void_p(st.cuda_stream))
         if rc != 0:
             raise SamplerError(rc, _lib.last_error())
 

@@ -80,6 +80,8 @@ def test_host_argument_checks_without_device():
     assert "NULL" in _lib.last_error()
     st = ctypes.c_uint32()
     assert lib.llmk_sampler_status(None, None, ctypes.byref(st)) == _lib.LLMK_ERR_INVALID_ARGUMENT
+    assert lib.llmk_history_count_append(None, 1, None, None, None, None, 8, None,
+                                         None) == _lib.LLMK_ERR_INVALID_ARGUMENT
     lib.llmk_sampler_destroy(None)  # no-op
 
 
