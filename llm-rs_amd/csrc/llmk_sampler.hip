@@ -3544,6 +3544,159 @@ __device__ __forceinline__ void each4(const float* row, uint32_t e0, uint32_t e1
   }
 }
 
+// apply_top_k in one read of the row (top_k <= MK1_KMAX, V <= MK1_VMAX):
+// every value at or above a rising threshold is gathered into LDS as it is
+// read, the threshold being the lower edge of the top_k-th largest fine bin
+// (key >> 20) of what has been counted so far -- the first round of the
+// workgroup (16 values per thread) is counted whole before any is gathered,
+// later gathers count themselves -- so it only rises and never passes the
+// true top_k-th largest value tau: every value
+// >= tau is gathered, and the top_k-th largest gathered value is tau.  The
+// kept positions (values >= tau, and NaN, which `v < threshold` never
+// masks) go into an LDS bitmap, and a second pass only writes: -inf over
+// every position not kept.  Returns false, having written nothing, when the
+// gathered values overflow the buffer (then the radix select runs).
+constexpr uint32_t MK1_CAP = 8192;       // gathered values
+constexpr uint32_t MK1_NAN = 256;        // gathered NaN positions
+constexpr uint32_t MK1_KMAX = 1024;
+constexpr uint32_t MK1_VMAX = 1u << 18;  // the kept bitmap's reach
+constexpr uint32_t MK1_LDS_WORDS = NBINS + 64 + 64 + MK1_VMAX / 32 + 2 * MK1_CAP + MK1_NAN;
+static_assert(MK1_LDS_WORDS <= MK_LDS_WORDS, "the one-read path fits the kernel's shared memory");
+__device__ __forceinline__ bool topk_one_read(float* row, uint32_t V, uint32_t K,
+                                              LDS uint32_t* smem) {
+  const uint32_t tid = threadIdx.x;
+  const int lane = (int)(tid & 63u);
+  LDS uint32_t* hf = smem;             // NBINS fine bins (key >> 20)
+  LDS uint32_t* hc = hf + NBINS;       // 64 coarse bins (key >> 26)
+  LDS uint32_t* sc = hc + 64;          // [0] gathered, [1] beta, [2] NaNs, [3] flags
+  LDS uint32_t* bm = sc + 64;          // kept bitmap, (V + 31) / 32 words
+  LDS float* cval = (LDS float*)(bm + MK1_VMAX / 32);
+  LDS uint32_t* cidx = (LDS uint32_t*)(cval + MK1_CAP);
+  LDS uint32_t* nidx = cidx + MK1_CAP;
+  const uint32_t nwords = (V + 31) / 32;
+  for (uint32_t i = tid; i < NBINS; i += NT) hf[i] = 0;
+  for (uint32_t i = tid; i < nwords; i += NT) bm[i] = 0;
+  if (tid < 64) hc[tid] = 0;
+  if (tid < 4) sc[tid] = 0;
+  __syncthreads();
+  // the float4-aligned body [a0, v4) in rounds of U float4 per thread, and
+  // the single elements before and after it
+  const uint32_t mis = (uint32_t)(((uintptr_t)row >> 2) & 3u);
+  const uint32_t a0 = umin(mis ? 4u - mis : 0u, V);
+  const uint32_t v4 = a0 + ((V - a0) & ~3u);
+  constexpr uint32_t U = 4, STEP = 4 * NT;
+  const uint32_t nrounds = (v4 - a0 + U * STEP - 1) / (U * STEP);
+  auto gather = [&](float v, uint32_t e, uint32_t thr, bool count) __attribute__((always_inline)) {
+    if (v != v) {
+      const uint32_t at = __atomic_fetch_add(&sc[2], 1u, __ATOMIC_RELAXED);
+      if (at < MK1_NAN) nidx[at] = e;
+      return;
+    }
+    const uint32_t key = ckey(v);
+    if (key < thr) return;
+    const uint32_t at = __atomic_fetch_add(&sc[0], 1u, __ATOMIC_RELAXED);
+    if (at < MK1_CAP) {
+      cval[at] = v == 0.0f ? 0.0f : v;
+      cidx[at] = e;
+    }
+    if (count) {
+      __atomic_fetch_add(&hf[key >> BIN_SHIFT], 1u, __ATOMIC_RELAXED);
+      __atomic_fetch_add(&hc[key >> CBIN_SHIFT], 1u, __ATOMIC_RELAXED);
+    }
+  };
+  // the singles first (gathered at threshold 0, counted in the fine bins:
+  // the first round's coarse sums include them)
+  const uint32_t ns = a0 + (V - v4);
+  for (uint32_t i = tid; i < ns; i += NT) {
+    const uint32_t e = i < a0 ? i : v4 + (i - a0);
+    const float v = G(row)[e];
+    gather(v, e, 0u, false);
+    if (v > NEG_INF && v == v) __atomic_fetch_add(&hf[ckey(v) >> BIN_SHIFT], 1u, __ATOMIC_RELAXED);
+  }
+  __syncthreads();
+  for (uint32_t r = 0; r < nrounds; ++r) {
+    f4v x[U];
+    const uint32_t eb = a0 + 4 * tid + r * U * STEP;
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u)
+      x[u] = eb + u * STEP < v4 ? __builtin_nontemporal_load((const GLB f4v*)G(row + eb + u * STEP))
+                                : f4v{NEG_INF, NEG_INF, NEG_INF, NEG_INF};
+    if (r == 0) {
+      // the first round: every value counted in the fine bins, the coarse
+      // bins summed from them, the threshold raised; the round is then
+      // gathered without counting again
+#pragma unroll
+      for (uint32_t u = 0; u < U; ++u) {
+        const float vv[4] = {x[u].x, x[u].y, x[u].z, x[u].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (vv[q] > NEG_INF && vv[q] == vv[q])
+            __atomic_fetch_add(&hf[ckey(vv[q]) >> BIN_SHIFT], 1u, __ATOMIC_RELAXED);
+      }
+      __syncthreads();
+      if (tid < 64) {
+        uint32_t c = 0;
+        for (uint32_t i = 0; i < 64; ++i) c += hf[64 * tid + i];
+        hc[tid] = c;
+      }
+      __syncthreads();
+      if (tid < 64) {
+        const uint32_t nb = compute_beta(hc, hf, K, lane);
+        if (lane == 0) sc[1] = nb;
+      }
+      __syncthreads();
+    }
+    uint32_t beta = __atomic_load_n(&sc[1], __ATOMIC_RELAXED);
+    const uint32_t thr = beta << BIN_SHIFT;
+    bool any = false;
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u) {
+      const uint32_t e = eb + u * STEP;
+      if (e >= v4) continue;
+      const float vv[4] = {x[u].x, x[u].y, x[u].z, x[u].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const bool hit = !(ckey(vv[q]) < thr) || vv[q] != vv[q];
+        any |= hit;
+        if (hit) gather(vv[q], e + q, thr, r > 0);
+      }
+    }
+    if (r > 0 && __ballot(any)) {
+      const uint32_t nb = compute_beta(hc, hf, K, lane);
+      if (nb > beta && lane == 0) __atomic_fetch_max(&sc[1], nb, __ATOMIC_RELAXED);
+    }
+  }
+  __syncthreads();
+  const uint32_t n = sc[0], nn = sc[2];
+  if (n > MK1_CAP || nn > MK1_NAN || n < K) return false;
+  __syncthreads();  // every thread has read the counts before sc is reused
+  const uint32_t tau = kth_largest_key<BlockSync>(cval, n, K, hf, sc + 8);
+  for (uint32_t i = tid; i < n; i += NT)
+    if (ckey(cval[i]) >= tau) __atomic_fetch_or(&bm[cidx[i] >> 5], 1u << (cidx[i] & 31u), __ATOMIC_RELAXED);
+  for (uint32_t i = tid; i < nn; i += NT)
+    __atomic_fetch_or(&bm[nidx[i] >> 5], 1u << (nidx[i] & 31u), __ATOMIC_RELAXED);
+  __syncthreads();
+  // write only: -inf wherever nothing is kept (kept values stay as they are)
+  for (uint32_t i = tid; i < ns; i += NT) {
+    const uint32_t e = i < a0 ? i : v4 + (i - a0);
+    if (!((bm[e >> 5] >> (e & 31u)) & 1u)) G(row)[e] = NEG_INF;
+  }
+  for (uint32_t e = a0 + 4 * tid; e < v4; e += STEP) {
+    // the four positions' bits (e is 16-byte aligned in memory, not a
+    // multiple of 4 when the row is not: they may straddle two words)
+    const uint32_t w = e >> 5, sh = e & 31u;
+    const uint32_t kb = (uint32_t)((((uint64_t)(sh > 28u ? bm[w + 1] : 0u) << 32) | bm[w]) >> sh) & 15u;
+    if (kb == 0) {
+      __builtin_nontemporal_store(f4v{NEG_INF, NEG_INF, NEG_INF, NEG_INF}, (GLB f4v*)G(row + e));
+    } else {
+#pragma unroll
+      for (uint32_t q = 0; q < 4; ++q)
+        if (!((kb >> q) & 1u)) G(row)[e + q] = NEG_INF;
+    }
+  }
+  return true;
+}
+
 // apply_top_k (sampler.rs:160-173) for one row per workgroup: the key of
 // the top_k-th largest value by a radix select over the row (11-bit digits
 // counted in per-wave LDS histograms), stopping once the chosen digit holds
@@ -3558,6 +3711,10 @@ __global__ __launch_bounds__(NT) void topk_mask_kernel(float* logits, uint32_t V
   const int32_t k = G(top_k)[b];
   if (k <= 0 || (uint32_t)k >= V) return;  // sampler.rs:161-163
   float* row = logits + (uint64_t)b * stride;
+  if ((uint32_t)k <= MK1_KMAX && V <= MK1_VMAX &&
+      topk_one_read(row, V, (uint32_t)k, (LDS uint32_t*)smem))
+    return;
+  __syncthreads();  // the radix select reuses the shared memory
   LDS uint32_t* hist = (LDS uint32_t*)smem;  // NW * MK_BINS
   LDS uint32_t* sh = hist + NW * MK_BINS;     // 512: select histogram, scalars
   uint32_t pbits = 0, pref = 0, need = (uint32_t)k, cnt = V;

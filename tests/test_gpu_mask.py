@@ -23,7 +23,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 
 @pytest.fixture(scope="module")
 def sampler():
-    s = llmk.HipSampler(max_batch=64, max_vocab=256000)
+    s = llmk.HipSampler(max_batch=64, max_vocab=270000)
     yield s
     s.close()
 
@@ -116,6 +116,21 @@ def test_top_k_ties_and_every_digit_level(sampler):
     ]
     for ks in ([1, 3, 50000, 99999, 17, 60000, 5, 40000], [9091, 50000, 33, 2, 99990, 30000, 10, 1]):
         check(sampler, "k", np.stack(rows), ks)
+
+
+def test_top_k_one_read_and_its_fallbacks(sampler):
+    """apply_top_k's one-read path (top_k <= 1024, V <= 2^18: values gathered
+    above a rising threshold, then a write-only mask pass) and each way back
+    to the radix select: an ascending row whose every value passes the rising
+    threshold (the gather buffer overflows), top_k 1025, and V above 2^18."""
+    rng = np.random.default_rng(21)
+    V = 151936
+    asc = np.sort(rng.normal(0, 3, V)).astype(np.float32)
+    rows = np.stack([asc, asc[::-1].copy(), c3_rows(1, V, 22)[0], c3_rows(1, V, 23)[0]])
+    check(sampler, "k", rows, [1024, 1024, 1024, 1025])
+    check(sampler, "k", rows, [1, 1000, 50, 1])
+    for V in (1 << 18, (1 << 18) + 8):
+        check(sampler, "k", c3_rows(2, V, V), [50, 1024])
 
 
 @pytest.mark.parametrize("V", [1, 2, 3, 5, 7, 64, 4097])
