@@ -2456,6 +2456,43 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
   }
   if (!topk) hist_flush();
   SY::sync();
+  // ---- min-p first (top-k rows): an entry below fl(min_p * p_max) is cut
+  // by the semantics' first step and never read after it, so the gathered
+  // entries below it are dropped now, in order; the largest dropped p then
+  // bounds everything past the list from below the threshold, which tells
+  // the semantics that the cut lies at the list's end.
+  float pdrop = 0.0f;
+  if (topk && P.min_p > 0.0f && n0 <= SORT_CAP) {
+    float pm = 0.0f;
+    for (uint32_t i = id; i < n0; i += SY::N) pm = fmaxf(pm, prob_of(cval[i], P.T, m, S));
+    pm = block_max(pm, (LDS float*)f.red);
+    const float t = P.min_p * pm;
+    uint32_t nk = 0;
+    for (uint32_t i0 = 0; i0 < n0; i0 += SY::N) {
+      const uint32_t i = i0 + id;
+      float v = 0.0f;
+      uint32_t ix = 0;
+      bool keep = false;
+      if (i < n0) {
+        v = cval[i];
+        ix = cidx[i];
+        const float pv = prob_of(v, P.T, m, S);
+        keep = pv >= t;
+        if (!keep) pdrop = fmaxf(pdrop, pv);
+      }
+      // every read of this round precedes the scan's barriers; the writes
+      // land below the next round's entries
+      uint32_t tot;
+      const uint32_t pos = nk + SY::excl_scan(keep, f.red, tot);
+      if (keep) {
+        cval[pos] = v;
+        cidx[pos] = ix;
+      }
+      nk += tot;
+    }
+    pdrop = block_max(pdrop, (LDS float*)f.red);
+    n0 = nk;
+  }
   uint32_t n = 0;
   if (!topk || n0 > SORT_CAP) {
     if (topk) {
@@ -2581,6 +2618,7 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
   }
   }
   SY::sync();
+  plim_e = fmaxf(plim_e, pdrop);  // also bounds the entries min-p dropped
   if (n > keep_cap) return 1;
   sort_keys<SY>(f, n);
   for (uint32_t i = id; i < n; i += SY::N) {
