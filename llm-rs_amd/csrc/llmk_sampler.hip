@@ -1928,11 +1928,12 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
     if (hm) last = umin(last, bin_in((uint32_t)__ffsll((unsigned long long)hm) - 1, true));
     if (hk) last = umin(last, bin_in((uint32_t)__ffsll((unsigned long long)hk) - 1, false));
     // min-p: the chosen bins reach below p_max * min_p (d = log2(min_p)),
-    // so that its cut is seen or lies past every chosen entry
-    if (P.min_p > 0.0f && last < SLOW_BINS - 1) {
+    // so that its cut is seen or lies past every chosen entry; the later
+    // steps read only what it keeps, so the count and mass rules do not
+    // apply to such a row
+    if (P.min_p > 0.0f) {
       const float bm = __builtin_ceilf(-16.0f * __builtin_log2f(P.min_p)) + 2.0f;
-      last = umax(last, (uint32_t)__builtin_fminf(__builtin_fmaxf(bm, 0.0f),
-                                                   (float)(SLOW_BINS - 1)));
+      last = (uint32_t)__builtin_fminf(__builtin_fmaxf(bm, 0.0f), (float)(SLOW_BINS - 1));
     }
     if (lane == 0) sh[11] = last;
   }
@@ -2541,11 +2542,14 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
           }
         }
       }
-      // min-p: the kept bins reach below the threshold, so that its cut is
-      // seen (or lies past every kept entry)
+      // min-p: the semantics' first step keeps p >= min_p * p_max and
+      // renormalises by the sum of exactly those, and every later step reads
+      // only them, so the kept bins are those down to the one below the
+      // threshold's (its cut seen, or lying past every kept entry) whatever
+      // the count or mass rule asks
       if (P.min_p > 0.0f) {
         const uint32_t tk = __float_as_uint(P.min_p * __uint_as_float(f.fm[F_SCR + 2])) >> 19;
-        tb = umin(tb, tk > 0 ? tk - 1 : 0u);
+        tb = tk > 0 ? tk - 1 : 0u;
       }
       uint32_t nk = 0;
       for (uint32_t k = (uint32_t)lane; k < 2048; k += WAVE) nk += k >= tb ? bcnt[k] : 0u;
