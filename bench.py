@@ -268,6 +268,9 @@ def main():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run a plain device-to-device copy of BYTES, 10 times (the "
                          "reference kernel for scaling HBM traffic counters)")
+    ap.add_argument("--cpu-configs", action="store_true",
+                    help="only time the CPU baseline (oracle ref mode) on a bounded sample of "
+                         "every config and print one JSON line (no GPU)")
     ap.add_argument("--mask-probe", choices=["top_k", "top_p"], default=None,
                     help="only time one mask form (apply_top_k at C3's shape, apply_top_p at "
                          "C4's) and print its line")
@@ -278,6 +281,15 @@ def main():
               "each sample B/N rows with no communication; run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
+    if args.cpu_configs:
+        from llmk import synth
+        out = {}
+        for name in ("C1", "C2", "C3", "C4", "C5"):
+            w = synth.make(name)
+            out[name] = cpu_baseline(w, budget_s=4.0)
+            log(f"[bench] cpu {name}: {out[name]}")
+        print(json.dumps(out), flush=True)
+        return
     import numpy as np
     import torch
     if args.copy_probe:
