@@ -2059,51 +2059,65 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
       }
     }
     __syncthreads();
-    // stable scatter, RE slots of 1024 keys per step, the slot's keys loaded
-    // together: ranks among equal digits within a wave (ballots), then
-    // across waves (a prefix per digit, written over the counts); each wave
-    // clears its own row after its scatter, so two barriers per slot suffice
+    // stable scatter, RE * NT keys per step: wave w ranks its own run of
+    // RE * 64 consecutive keys slot after slot (equal digits found by
+    // ballots, counted on in the wave's row of wcnt), then one prefix per
+    // digit across the waves (written over the counts) places every key;
+    // each wave reads only its own row when it scatters and clears it
+    // after, so two barriers per step
     for (uint32_t b0 = 0; b0 < npos; b0 += RE * NT) {
+      const uint32_t wb = b0 + (uint32_t)wv * (RE * WAVE);
       uint64_t ky[RE];
+      uint32_t pw[RE];
 #pragma unroll
       for (int q = 0; q < RE; ++q) {
-        const uint32_t i = b0 + q * NT + tid;
+        const uint32_t i = wb + q * WAVE + lane;
         ky[q] = i < npos ? src[i] : 0ull;
       }
 #pragma unroll
       for (int q = 0; q < RE; ++q) {
-        if (b0 + q * NT >= npos) break;
-        const bool valid = b0 + q * NT + tid < npos;
-        const uint64_t key = ky[q];
-        const uint32_t d = (uint32_t)(key >> sh_bits) & 255u;
+        const bool valid = wb + q * WAVE + lane < npos;
+        const uint32_t d = (uint32_t)(ky[q] >> sh_bits) & 255u;
         uint64_t peers = __ballot(valid);
+        pw[q] = 0;
+        if (peers == 0) continue;  // wave-uniform: this slot is past the keys
 #pragma unroll
         for (int bit = 0; bit < 8; ++bit) {
           const uint64_t bb = __ballot(((d >> bit) & 1u) != 0);
           peers &= ((d >> bit) & 1u) ? bb : ~bb;
         }
         const uint32_t rank = lanes_below(peers);
-        if (valid && rank == 0) wcnt[wv * 256 + d] = __popcll(peers);
-        __syncthreads();
-        if (tid < 256) {
-          // the sixteen counts read at once, then the prefix
-          uint32_t c[NW];
-#pragma unroll
-          for (int w2 = 0; w2 < NW; ++w2) c[w2] = wcnt[w2 * 256 + tid];
-          uint32_t acc = digit_off[tid];
-#pragma unroll
-          for (int w2 = 0; w2 < NW; ++w2) {
-            wcnt[w2 * 256 + tid] = acc;
-            acc += c[w2];
-          }
-          digit_off[tid] = acc;
-        }
-        __syncthreads();
-        if (valid) dst[wcnt[wv * 256 + d] + rank] = key;
-        WaveSync::sync();  // this wave's reads of its row are done
-#pragma unroll
-        for (int w2 = 0; w2 < 4; ++w2) wcnt[wv * 256 + 64 * w2 + lane] = 0;
+        const uint32_t base = valid ? wcnt[wv * 256 + d] : 0u;
+        pw[q] = base + rank;
+        WaveSync::sync();  // every lane has read the count before it moves on
+        if (valid && rank == 0) wcnt[wv * 256 + d] = base + (uint32_t)__popcll(peers);
+        WaveSync::sync();  // the next slot reads the new counts
       }
+      __syncthreads();
+      if (tid < 256) {
+        // the sixteen counts read at once, then the prefix
+        uint32_t c[NW];
+#pragma unroll
+        for (int w2 = 0; w2 < NW; ++w2) c[w2] = wcnt[w2 * 256 + tid];
+        uint32_t acc = digit_off[tid];
+#pragma unroll
+        for (int w2 = 0; w2 < NW; ++w2) {
+          wcnt[w2 * 256 + tid] = acc;
+          acc += c[w2];
+        }
+        digit_off[tid] = acc;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int q = 0; q < RE; ++q) {
+        if (wb + q * WAVE + lane < npos) {
+          const uint32_t d = (uint32_t)(ky[q] >> sh_bits) & 255u;
+          dst[wcnt[wv * 256 + d] + pw[q]] = ky[q];
+        }
+      }
+      WaveSync::sync();  // this wave's reads of its row are done
+#pragma unroll
+      for (int w2 = 0; w2 < 4; ++w2) wcnt[wv * 256 + 64 * w2 + lane] = 0;
     }
     wait_stores();
     __syncthreads();
