@@ -1587,6 +1587,51 @@ __device__ __forceinline__ float block_seq_sum(const float (&e)[16], uint32_t nq
   }
 }
 
+// A wave-uniform 64-bit value in scalar registers.
+__device__ __forceinline__ uint64_t sgpr_u64(uint64_t x) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)x);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(x >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// A window that the serial sum cannot take, as a call of its own: the exact
+// terms of an unpacked wave (x, the processed logits, where `live`) or the
+// packed terms of a packed wave (comp, its nw entries), then block_seq_sum.
+// Its registers (sixteen exps in flight, the scan's pairs) are allocated
+// apart from the window loop of exact_normaliser, which with them inlined
+// spilled the row's pointers, and every reload waited for the next window's
+// logits in flight.  Returns (sum bits, slot rotation).
+__device__ __attribute__((noinline)) u2v window_scan(f4v x0, f4v x1, f4v x2, f4v x3,
+                                                     uint32_t live, uint32_t nw, float T,
+                                                     float m, float c, uint32_t it,
+                                                     LDS uint32_t* sc, LDS const float* comp) {
+  constexpr uint32_t Q = 16, CW = 256;
+  const uint32_t lane = threadIdx.x & 63u;
+  float e[Q];
+  uint32_t nq = Q;
+  if (nw <= CW) {
+    // thread entries 4 lane .. 4 lane + 3, in order
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q) {
+      const uint32_t k = 4u * lane + q;
+      e[q] = k < nw ? comp[k] : 0.0f;
+    }
+#pragma unroll
+    for (uint32_t q = 4; q < Q; ++q) e[q] = 0.0f;
+    nq = 4;
+  } else {
+    const float x[Q] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w,
+                        x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+#pragma unroll
+    for (uint32_t q = 0; q < Q; ++q) {
+      const float l = (T != 1.0f) ? x[q] / T : x[q];
+      e[q] = ((live >> q) & 1u) && l != NEG_INF ? exp_ref(l - m) : 0.0f;
+    }
+  }
+  const float r = block_seq_sum(e, nq, c, it, sc);
+  return u2v{__float_as_uint(r), it};
+}
+
 // S = the sequential f32 sum in index order of e_i = exp_ref(fl(l_i - m))
 // (0 for l_i = -inf), l_i = fl(v_i / T) the processed logit (penalties from
 // the history tables h if have_hist, the allow-mask, NaN read as -inf)
@@ -1611,7 +1656,21 @@ template <int DT>
 __device__ __attribute__((noinline)) float exact_normaliser(
     const void* row, const uint32_t* mask_row, uint32_t V, float T, float m,
     LDS uint32_t* bitmap, LDS uint16_t* pre, LDS float* pen, bool have_hist, LDS uint32_t* sc) {
-  const uint32_t tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  // the arguments arrive in vector registers; the row's pointers, the LDS
+  // tables and the scalars are moved to scalar ones, which the window loop
+  // then does not spill (a reload from scratch waits for every load in
+  // flight, the next window's logits among them)
+  const uint32_t wv = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));
+  sc = (LDS uint32_t*)(uintptr_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)sc);
+  bitmap = (LDS uint32_t*)(uintptr_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)bitmap);
+  pre = (LDS uint16_t*)(uintptr_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)pre);
+  pen = (LDS float*)(uintptr_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)pen);
+  row = (const void*)sgpr_u64((uint64_t)row);
+  mask_row = (const uint32_t*)sgpr_u64((uint64_t)mask_row);
+  T = __uint_as_float((uint32_t)__builtin_amdgcn_readfirstlane((int)__float_as_uint(T)));
+  m = __uint_as_float((uint32_t)__builtin_amdgcn_readfirstlane((int)__float_as_uint(m)));
+  V = (uint32_t)__builtin_amdgcn_readfirstlane((int)V);
   const GLB uint32_t* mrow = mask_row ? G(mask_row) : nullptr;
   Hist h;
   h.bitmap = bitmap;
@@ -1637,13 +1696,15 @@ __device__ __attribute__((noinline)) float exact_normaliser(
   float c = 0.0f;
   float xn[Q];
   load16<DT>(row, Q * tid, V, xn);
+  // the mask word of the next window, requested with its logits
+  uint32_t mwn = (mrow && Q * tid < V) ? mrow[(Q * tid) >> 5] : 0xffffffffu;
   for (uint32_t w0 = 0; w0 < V; w0 += W) {
     const uint32_t e0 = w0 + Q * tid;
     float x[Q];
 #pragma unroll
     for (uint32_t q = 0; q < Q; ++q) x[q] = xn[q];
     // the sixteen lie in one 32-bit word of the mask and of the bitmap
-    const uint32_t mw = (mrow && e0 < V) ? mrow[e0 >> 5] >> (e0 & 16u) : 0xffffffffu;
+    const uint32_t mw = mwn >> (e0 & 16u);
     const uint32_t hw = (have_hist && e0 < V) ? h.bitmap[(e0 - h.lo) >> 5] >> (e0 & 16u) : 0u;
     // entries below lim (on l - m) add nothing to a sum of binade eb or above
     float lim = NEG_INF;
@@ -1660,36 +1721,39 @@ __device__ __attribute__((noinline)) float exact_normaliser(
       x[q] = v;
       if (v > NEG_INF && v * rT - m >= lim) live |= 1u << q;
     }
-    // the next window's logits, while this one is summed
-    if (w0 + W < V) load16<DT>(row, e0 + W, V, xn);
+    // the next window's logits and mask word, while this one is summed
+    if (w0 + W < V) {
+      load16<DT>(row, e0 + W, V, xn);
+      if (mrow && e0 + W < V) mwn = mrow[(e0 + W) >> 5];
+    }
     const uint32_t n = (uint32_t)__popc(live);
     const uint32_t incl = wave_incl_scan(n);
     const uint32_t nw = bcast63u(incl);
-    float e[Q];
-    uint32_t nq = Q;
     if (nw <= CW) {
-      // pack this wave's entries in order, four per lane
+      // pack this wave's entries in order; their exact terms one per lane
+      // per 64 entries (a wave with 40 entries computes one exp, not four)
       uint32_t at = incl - n;
 #pragma unroll
       for (uint32_t q = 0; q < Q; ++q)
         if ((live >> q) & 1u) comp[at++] = x[q];
       WaveSync::sync();
+      float e[4];
 #pragma unroll
       for (uint32_t q = 0; q < 4; ++q) {
-        const uint32_t k = 4u * lane + q;
-        e[q] = k < nw ? exact_e(comp[k]) : 0.0f;
+        const uint32_t k = (uint32_t)lane + WAVE * q;
+        e[q] = 0.0f;
+        if (WAVE * q < nw && k < nw) e[q] = exact_e(comp[k]);
       }
-#pragma unroll
-      for (uint32_t q = 4; q < Q; ++q) e[q] = 0.0f;
-      nq = 4;
       WaveSync::sync();
-      // the exact terms, in the same order
+      // the exact terms, in the same order, then zeros up to a multiple of
+      // 32 (the serial sum adds whole chunks of 32; +0 leaves a sum >= 0
+      // unchanged)
 #pragma unroll
-      for (uint32_t q = 0; q < 4; ++q)
-        if (4u * lane + q < nw) comp[4u * lane + q] = e[q];
-    } else {
-#pragma unroll
-      for (uint32_t q = 0; q < Q; ++q) e[q] = ((live >> q) & 1u) ? exact_e(x[q]) : 0.0f;
+      for (uint32_t q = 0; q < 4; ++q) {
+        const uint32_t k = (uint32_t)lane + WAVE * q;
+        if (k < nw) comp[k] = e[q];
+      }
+      if (nw + (uint32_t)lane < ((nw + 31u) & ~31u)) comp[nw + lane] = 0.0f;
     }
     if (lane == 0) nwv[wv] = nw <= CW ? nw : EMPTY;
     __syncthreads();
@@ -1697,43 +1761,55 @@ __device__ __attribute__((noinline)) float exact_normaliser(
 #pragma unroll
     for (uint32_t i = 0; i < NW; ++i) tot += umin(nwv[i], SERIAL_MAX + 1u);
     if (tot <= SERIAL_MAX) {
-      // every wave packed, few entries: one lane sums them in order
-      if (tid == 0) {
-        // eight 16-byte reads in flight, then their 32 additions in order
-        // (a read per four additions would wait on the LDS each time)
-        float cc = c;
+      // every wave packed, few entries: wave 0 sums them in order, in every
+      // lane alike (the reads are broadcasts), in chunks of 32: eight 16-byte
+      // reads, then their 32 additions (a read per four additions, or per
+      // wave's short list, would wait on the LDS each time)
+      if (wv == 0) {
+        // chunk j (j = lane, lane + 64) of the waves' lists in order: its
+        // offset in comp0
+        const uint32_t nl = (uint32_t)lane < NW ? (nwv[lane] + 31u) >> 5 : 0u;
+        const uint32_t ci = wave_incl_scan(nl);
+        const uint32_t nchk = bcast63u(ci);
+        uint32_t ad0 = 0, ad1 = 0;
+#pragma unroll
         for (uint32_t i = 0; i < NW; ++i) {
-          LDS const float* L = comp0 + CW * i;
-          const uint32_t ni = nwv[i];
-          uint32_t k = 0;
-          for (; k + 32u <= ni; k += 32u) {
-            f4v y[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) y[j] = *(LDS const f4v*)(L + k + 4 * j);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              cc = cc + y[j].x;
-              cc = cc + y[j].y;
-              cc = cc + y[j].z;
-              cc = cc + y[j].w;
-            }
-          }
-          for (; k + 4u <= ni; k += 4u) {
-            const f4v y = *(LDS const f4v*)(L + k);
-            cc = cc + y.x;
-            cc = cc + y.y;
-            cc = cc + y.z;
-            cc = cc + y.w;
-          }
-          for (; k < ni; ++k) cc = cc + L[k];
+          const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)ci, (int)i);
+          const uint32_t lo = hi - (uint32_t)__builtin_amdgcn_readlane((int)nl, (int)i);
+          const uint32_t j0 = (uint32_t)lane, j1 = (uint32_t)lane + WAVE;
+          if (j0 >= lo && j0 < hi) ad0 = CW * i + 32u * (j0 - lo);
+          if (j1 >= lo && j1 < hi) ad1 = CW * i + 32u * (j1 - lo);
         }
-        *cbc = cc;
+        auto fetch = [&](uint32_t j, f4v (&d)[8]) __attribute__((always_inline)) {
+          const uint32_t ad = j < WAVE ? (uint32_t)__builtin_amdgcn_readlane((int)ad0, (int)j)
+                                       : (uint32_t)__builtin_amdgcn_readlane((int)ad1, (int)(j - WAVE));
+          LDS const f4v* p = (LDS const f4v*)(comp0 + ad);
+#pragma unroll
+          for (int t = 0; t < 8; ++t) d[t] = p[t];
+        };
+        float cc = c;
+        for (uint32_t j = 0; j < nchk; ++j) {
+          f4v y[8];
+          fetch(j, y);
+#pragma unroll
+          for (int t = 0; t < 8; ++t) {
+            cc = cc + y[t].x;
+            cc = cc + y[t].y;
+            cc = cc + y[t].z;
+            cc = cc + y[t].w;
+          }
+        }
+        if (lane == 0) *cbc = cc;
       }
       __syncthreads();
       c = *cbc;
       __syncthreads();  // nwv, comp and cbc are rewritten next window
     } else {
-      c = block_seq_sum(e, nq, c, it, sc);
+      const u2v r = window_scan(f4v{x[0], x[1], x[2], x[3]}, f4v{x[4], x[5], x[6], x[7]},
+                                f4v{x[8], x[9], x[10], x[11]}, f4v{x[12], x[13], x[14], x[15]},
+                                live, nw, P.T, m, c, it, sc, comp);
+      c = __uint_as_float(r.x);
+      it = r.y;
     }
   }
   __syncthreads();  // the caller may reuse sc
