@@ -1848,6 +1848,142 @@ __device__ __forceinline__ void load8(const void* row, uint32_t e0, uint32_t V, 
   }
 }
 
+// Stable LSD radix sort of src[0..npos) on bits 32..63 of the keys, four
+// passes of 8 bits through dst (src holds the sorted keys after the even
+// number of passes), by the whole workgroup.  Inlined: as a call of its
+// own it measured C5 1.5 us slower (the stream kernel's code moves).
+// wcnt: NW*256 words, digit_off: 256, red: 64.
+__device__ __forceinline__ void radix_sort_keys(GLB uint64_t* src, GLB uint64_t* dst,
+                                                         uint32_t npos, LDS uint32_t* wcnt,
+                                                         LDS uint32_t* digit_off,
+                                                         LDS uint32_t* red) {
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  const uint32_t wv = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));
+  src = (GLB uint64_t*)sgpr_u64((uint64_t)src);
+  dst = (GLB uint64_t*)sgpr_u64((uint64_t)dst);
+  npos = (uint32_t)__builtin_amdgcn_readfirstlane((int)npos);
+  for (uint32_t j = tid; j < NW * 256; j += NT) wcnt[j] = 0;
+  for (int pass = 0; pass < 4; ++pass) {
+    const int sh_bits = 32 + 8 * pass;
+    if (tid < 256) digit_off[tid] = 0;
+    __syncthreads();
+    // the digit histogram, RE keys per thread loaded at once: a wave whose
+    // keys share one digit (the top digits of p keys are few and equal, and
+    // per-element atomics on one address serialise) adds its count once
+    constexpr int RE = 8;
+    for (uint32_t b0 = 0; b0 < npos; b0 += RE * NT) {
+      uint32_t dg[RE];
+#pragma unroll
+      for (int q = 0; q < RE; ++q) {
+        const uint32_t i = b0 + q * NT + tid;
+        dg[q] = i < npos ? (uint32_t)(src[i] >> sh_bits) & 255u : 256u;
+      }
+#pragma unroll
+      for (int q = 0; q < RE; ++q) {
+        if (b0 + q * NT >= npos) break;
+        // the valid lanes are a prefix of the wave: lane 0 holds one if any
+        // does; a wave of one digit (the high digits of p keys) adds its
+        // count once, any other adds per lane (spread digits rarely collide)
+        const bool valid = dg[q] < 256u;
+        const uint32_t d0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)dg[q]);
+        const uint64_t vm = __ballot(valid);
+        if (__ballot(valid && dg[q] != d0) == 0) {
+          if (lane == 0 && vm) __atomic_fetch_add(&digit_off[d0 & 255u], (uint32_t)__popcll(vm), __ATOMIC_RELAXED);
+        } else if (valid) {
+          __atomic_fetch_add(&digit_off[dg[q]], 1u, __ATOMIC_RELAXED);
+        }
+      }
+    }
+    __syncthreads();
+    // exclusive prefix of the 256 digit counts: waves 0..3, one digit a lane
+    {
+      const uint32_t c = tid < 256 ? digit_off[tid] : 0u;
+      const uint32_t incl = wave_incl_scan(c);
+      if (tid < 256 && lane == 63) red[wv] = incl;
+      __syncthreads();
+      if (tid < 256) {
+        uint32_t base = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) base += q < wv ? red[q] : 0u;
+        digit_off[tid] = base + incl - c;
+      }
+    }
+    __syncthreads();
+    // stable scatter, RE * NT keys per step: wave w ranks its own run of
+    // RE * 64 consecutive keys slot after slot (equal digits found by
+    // ballots, counted on in the wave's row of wcnt), then one prefix per
+    // digit across the waves (written over the counts) places every key;
+    // each wave reads only its own row when it scatters and clears it
+    // after, so two barriers per step
+    for (uint32_t b0 = 0; b0 < npos; b0 += RE * NT) {
+      const uint32_t wb = b0 + (uint32_t)wv * (RE * WAVE);
+      uint64_t ky[RE];
+      uint32_t pw[RE];
+#pragma unroll
+      for (int q = 0; q < RE; ++q) {
+        const uint32_t i = wb + q * WAVE + lane;
+        ky[q] = i < npos ? src[i] : 0ull;
+      }
+#pragma unroll
+      for (int q = 0; q < RE; ++q) {
+        const bool valid = wb + q * WAVE + lane < npos;
+        const uint32_t d = (uint32_t)(ky[q] >> sh_bits) & 255u;
+        uint64_t peers = __ballot(valid);
+        pw[q] = 0;
+        if (peers == 0) continue;  // wave-uniform: this slot is past the keys
+        // the lanes holding this lane's digit: all valid lanes when the wave
+        // holds one digit, else matched bit by bit
+        const uint32_t d0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)d);
+        if (__ballot(valid && d != d0) != 0) {
+#pragma unroll
+          for (int bit = 0; bit < 8; ++bit) {
+            const uint64_t bb = __ballot(((d >> bit) & 1u) != 0);
+            peers &= ((d >> bit) & 1u) ? bb : ~bb;
+          }
+        }
+        const uint32_t rank = lanes_below(peers);
+        const uint32_t base = valid ? wcnt[wv * 256 + d] : 0u;
+        pw[q] = base + rank;
+        WaveSync::sync();  // every lane has read the count before it moves on
+        if (valid && rank == 0) wcnt[wv * 256 + d] = base + (uint32_t)__popcll(peers);
+        WaveSync::sync();  // the next slot reads the new counts
+      }
+      __syncthreads();
+      if (tid < 256) {
+        // the sixteen counts read at once, then the prefix
+        uint32_t c[NW];
+#pragma unroll
+        for (int w2 = 0; w2 < NW; ++w2) c[w2] = wcnt[w2 * 256 + tid];
+        uint32_t acc = digit_off[tid];
+#pragma unroll
+        for (int w2 = 0; w2 < NW; ++w2) {
+          wcnt[w2 * 256 + tid] = acc;
+          acc += c[w2];
+        }
+        digit_off[tid] = acc;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int q = 0; q < RE; ++q) {
+        if (wb + q * WAVE + lane < npos) {
+          const uint32_t d = (uint32_t)(ky[q] >> sh_bits) & 255u;
+          dst[wcnt[wv * 256 + d] + pw[q]] = ky[q];
+        }
+      }
+      WaveSync::sync();  // this wave's reads of its row are done
+#pragma unroll
+      for (int w2 = 0; w2 < 4; ++w2) wcnt[wv * 256 + 64 * w2 + lane] = 0;
+    }
+    wait_stores();
+    __syncthreads();
+    if (tid == 0) __threadfence();
+    __syncthreads();
+    GLB uint64_t* tmp = src;
+    src = dst;
+    dst = tmp;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Slow path (one workgroup, one row).  Rows the candidate path cannot prove:
 //   A  every processed logit l falls in a bin of d = (l - L) log2(e)/T (1/16
@@ -2087,122 +2223,10 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
     if (tid == 0) __threadfence();  // drop stale vector-L1 lines before re-reads
     __syncthreads();
     // ---- D: sort, then the semantics
-  // stable LSD radix sort of kA[0..npos) on bits 32..63, 4 passes of 8 bits
+  // stable LSD radix sort of kA[0..npos) on bits 32..63 (kA again holds
+  // the sorted keys after its four passes)
+  radix_sort_keys(kA, kB, npos, wcnt, digit_off, red);
   GLB uint64_t* src = kA;
-  GLB uint64_t* dst = kB;
-  for (uint32_t j = tid; j < NW * 256; j += NT) wcnt[j] = 0;
-  for (int pass = 0; pass < 4; ++pass) {
-    const int sh_bits = 32 + 8 * pass;
-    if (tid < 256) digit_off[tid] = 0;
-    __syncthreads();
-    // the digit histogram: one atomic per distinct digit per wave and slot
-    // (the top digits of p keys are few and equal, and per-element atomics
-    // on one address serialise); RE keys per thread loaded at once
-    constexpr int RE = 8;
-    for (uint32_t b0 = 0; b0 < npos; b0 += RE * NT) {
-      uint32_t dg[RE];
-#pragma unroll
-      for (int q = 0; q < RE; ++q) {
-        const uint32_t i = b0 + q * NT + tid;
-        dg[q] = i < npos ? (uint32_t)(src[i] >> sh_bits) & 255u : 256u;
-      }
-#pragma unroll
-      for (int q = 0; q < RE; ++q) {
-        if (b0 + q * NT >= npos) break;
-        const uint32_t d = dg[q] & 255u;
-        uint64_t peers = __ballot(dg[q] < 256u);
-#pragma unroll
-        for (int bit = 0; bit < 8; ++bit) {
-          const uint64_t bb = __ballot(((d >> bit) & 1u) != 0);
-          peers &= ((d >> bit) & 1u) ? bb : ~bb;
-        }
-        if (dg[q] < 256u && lanes_below(peers) == 0)
-          __atomic_fetch_add(&digit_off[d], (uint32_t)__popcll(peers), __ATOMIC_RELAXED);
-      }
-    }
-    __syncthreads();
-    // exclusive prefix of the 256 digit counts: waves 0..3, one digit a lane
-    {
-      const uint32_t c = tid < 256 ? digit_off[tid] : 0u;
-      const uint32_t incl = wave_incl_scan(c);
-      if (tid < 256 && lane == 63) red[wv] = incl;
-      __syncthreads();
-      if (tid < 256) {
-        uint32_t base = 0;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) base += q < wv ? red[q] : 0u;
-        digit_off[tid] = base + incl - c;
-      }
-    }
-    __syncthreads();
-    // stable scatter, RE * NT keys per step: wave w ranks its own run of
-    // RE * 64 consecutive keys slot after slot (equal digits found by
-    // ballots, counted on in the wave's row of wcnt), then one prefix per
-    // digit across the waves (written over the counts) places every key;
-    // each wave reads only its own row when it scatters and clears it
-    // after, so two barriers per step
-    for (uint32_t b0 = 0; b0 < npos; b0 += RE * NT) {
-      const uint32_t wb = b0 + (uint32_t)wv * (RE * WAVE);
-      uint64_t ky[RE];
-      uint32_t pw[RE];
-#pragma unroll
-      for (int q = 0; q < RE; ++q) {
-        const uint32_t i = wb + q * WAVE + lane;
-        ky[q] = i < npos ? src[i] : 0ull;
-      }
-#pragma unroll
-      for (int q = 0; q < RE; ++q) {
-        const bool valid = wb + q * WAVE + lane < npos;
-        const uint32_t d = (uint32_t)(ky[q] >> sh_bits) & 255u;
-        uint64_t peers = __ballot(valid);
-        pw[q] = 0;
-        if (peers == 0) continue;  // wave-uniform: this slot is past the keys
-#pragma unroll
-        for (int bit = 0; bit < 8; ++bit) {
-          const uint64_t bb = __ballot(((d >> bit) & 1u) != 0);
-          peers &= ((d >> bit) & 1u) ? bb : ~bb;
-        }
-        const uint32_t rank = lanes_below(peers);
-        const uint32_t base = valid ? wcnt[wv * 256 + d] : 0u;
-        pw[q] = base + rank;
-        WaveSync::sync();  // every lane has read the count before it moves on
-        if (valid && rank == 0) wcnt[wv * 256 + d] = base + (uint32_t)__popcll(peers);
-        WaveSync::sync();  // the next slot reads the new counts
-      }
-      __syncthreads();
-      if (tid < 256) {
-        // the sixteen counts read at once, then the prefix
-        uint32_t c[NW];
-#pragma unroll
-        for (int w2 = 0; w2 < NW; ++w2) c[w2] = wcnt[w2 * 256 + tid];
-        uint32_t acc = digit_off[tid];
-#pragma unroll
-        for (int w2 = 0; w2 < NW; ++w2) {
-          wcnt[w2 * 256 + tid] = acc;
-          acc += c[w2];
-        }
-        digit_off[tid] = acc;
-      }
-      __syncthreads();
-#pragma unroll
-      for (int q = 0; q < RE; ++q) {
-        if (wb + q * WAVE + lane < npos) {
-          const uint32_t d = (uint32_t)(ky[q] >> sh_bits) & 255u;
-          dst[wcnt[wv * 256 + d] + pw[q]] = ky[q];
-        }
-      }
-      WaveSync::sync();  // this wave's reads of its row are done
-#pragma unroll
-      for (int w2 = 0; w2 < 4; ++w2) wcnt[wv * 256 + 64 * w2 + lane] = 0;
-    }
-    wait_stores();
-    __syncthreads();
-    if (tid == 0) __threadfence();
-    __syncthreads();
-    GLB uint64_t* tmp = src;
-    src = dst;
-    dst = tmp;
-  }
     // unpack into p / idx lists (sorted positives, then zeros by index)
     for (uint32_t i = tid; i < npos; i += NT) {
       const uint64_t k = src[i];
