@@ -862,6 +862,7 @@ struct List {
   const uint32_t* idx;
   Chain c;
   float* wp;  // p, writable (an LDS list): renormalisations rewrite it
+  __device__ float raw(uint32_t i) const { return p[i]; }
   __device__ float get(uint32_t i) const { return c.apply(p[i]); }
   __device__ uint32_t id(uint32_t i) const { return idx[i]; }
 };
@@ -991,11 +992,22 @@ __device__ __forceinline__ uint32_t seq_scan(const L& list, uint32_t n, int mode
         j0 += h;
       }
     }
+    // the raw entries of the window at jj (the divisor chain is applied when
+    // it is scanned); the next window's are requested before a window is
+    // scanned, so that a list in global memory is not waited for window by
+    // window
+    float pr[Q];
+    auto fetch = [&](uint32_t jj) __attribute__((always_inline)) {
+#pragma unroll
+      for (uint32_t q = 0; q < Q; ++q) pr[q] = jj + l0 + q < n ? list.raw(jj + l0 + q) : 0.0f;
+    };
+    if (j0 < n && stop == n) fetch(j0);
     for (uint32_t j = j0; j < n && stop == n; j += W) {
       const uint32_t lim = umin(n - j, W);
       float p[Q];
 #pragma unroll
-      for (uint32_t q = 0; q < Q; ++q) p[q] = (l0 + q < lim) ? list.get(j + l0 + q) : 0.0f;
+      for (uint32_t q = 0; q < Q; ++q) p[q] = (l0 + q < lim) ? list.c.apply(pr[q]) : 0.0f;
+      if (j + W < n) fetch(j + W);
       uint32_t s = 0;  // window entries before s are summed
       while (s < lim) {
         if (c == 0.0f) {
