@@ -1156,10 +1156,18 @@ __device__ __forceinline__ uint32_t first_below(const List& list, uint32_t n, fl
   return r;
 }
 
+// Lists at least this long are scanned by the whole workgroup
+// (block_list_scan), shorter ones by wave 0 (seq_scan); only the slow path's
+// lists get that long (the candidate path keeps at most SORT_CAP).
+constexpr uint32_t BLOCK_SCAN_MIN = 4096;
+__device__ __attribute__((noinline)) u2v block_list_scan(List list, uint32_t n, int mode,
+                                                        float thr, LDS uint32_t* sc);
+
 // min-p / top-k / top-p / draw (sampler.rs:77-124 + min-p) over a sorted list
 // of full_len entries whose first E are exact; every entry past E has
 // p <= ptail.  Every thread of the workgroup.  Returns false if an entry
 // beyond E would be needed.  The four steps share one running-sum call.
+template <bool LONG>
 __device__ __forceinline__ bool run_semantics(const RowP& P, float u, uint32_t E,
                                               uint32_t full_len, float ptail, List& list,
                                               LDS uint32_t* sh, LDS float* z,
@@ -1203,7 +1211,14 @@ __device__ __forceinline__ bool run_semantics(const RowP& P, float u, uint32_t E
       thr = step == 2 ? P.top_p : u;
     }
     float s;
-    const uint32_t j = seq_scan(list, n, mode, thr, s, sh, z);
+    uint32_t j;
+    if (LONG && n >= BLOCK_SCAN_MIN) {
+      const u2v r = block_list_scan(list, n, mode, thr, (LDS uint32_t*)z);
+      j = r.x;
+      s = __uint_as_float(r.y);
+    } else {
+      j = seq_scan(list, n, mode, thr, s, sh, z);
+    }
     if (step == 3) {
       uint32_t tok;
       if (j < n) tok = list.id(j);
@@ -1482,9 +1497,17 @@ __device__ __forceinline__ Par wave_par_incl(Par x) {
 // read two rounds ago), so a round needs two barriers; `it` carries the
 // rotation from call to call, and the slots start cleared
 // (exact_normaliser).  sc: 6 + NW*2 words; uniform barriers only.
-__device__ __forceinline__ float block_seq_sum(const float (&e)[16], uint32_t nq, float c,
-                                               uint32_t& it, LDS uint32_t* sc) {
+//
+// block_seq_scan<true> also stops at the first entry whose running sum
+// reaches thr (stop_at: its index in the window, EMPTY if none) and returns
+// that sum: a stop is an event like a crossing, the first event in index
+// order taken, and a crossing's sum is compared with thr after its addition.
+template <bool STOPS>
+__device__ __forceinline__ float block_seq_scan(const float (&e)[16], uint32_t nq, float c,
+                                                uint32_t& it, LDS uint32_t* sc, float thr,
+                                                uint32_t& stop_at) {
   constexpr uint32_t Q = 16, TOP = 1u << 24;
+  stop_at = EMPTY;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
   LDS uint64_t* ev = (LDS uint64_t*)sc;  // [3]: first event (index << 32 | new sum bits)
   LDS uint32_t* wt = sc + 6;             // [NW][2]: wave totals
@@ -1514,6 +1537,11 @@ __device__ __forceinline__ float block_seq_sum(const float (&e)[16], uint32_t nq
       }
       c = __uint_as_float((uint32_t)r);
       s = (uint32_t)(r >> 32) + 1u;
+      if (STOPS && c >= thr) {
+        stop_at = s - 1u;
+        ++it;
+        return c;
+      }
       if (s >= NT * Q) {
         ++it;
         return c;
@@ -1573,10 +1601,15 @@ __device__ __forceinline__ float block_seq_sum(const float (&e)[16], uint32_t nq
         if (q < nq) {
           const uint32_t t = (tie >> q) & 1u;
           const uint32_t nx = cur + r[q] + (t & ((cur ^ r[q]) & 1u));
-          if (cand == ~0ull && Q * tid + q >= s && nx >= TOP) {
-            // the addition that leaves the binade, as one f32 addition
-            const float before = __builtin_ldexpf((float)cur, eb - 23);
-            cand = ((uint64_t)(Q * tid + q) << 32) | __float_as_uint(before + e[q]);
+          if (cand == ~0ull && Q * tid + q >= s) {
+            if (nx >= TOP) {
+              // the addition that leaves the binade, as one f32 addition
+              const float before = __builtin_ldexpf((float)cur, eb - 23);
+              cand = ((uint64_t)(Q * tid + q) << 32) | __float_as_uint(before + e[q]);
+            } else if (STOPS) {
+              const float cv = __builtin_ldexpf((float)nx, eb - 23);  // exact
+              if (cv >= thr) cand = ((uint64_t)(Q * tid + q) << 32) | __float_as_uint(cv);
+            }
           }
           cur = nx;
         }
@@ -1592,18 +1625,69 @@ __device__ __forceinline__ float block_seq_sum(const float (&e)[16], uint32_t nq
     }
     c = __uint_as_float((uint32_t)res);
     s = (uint32_t)(res >> 32) + 1u;
+    if (STOPS && c >= thr) {
+      stop_at = s - 1u;
+      ++it;
+      return c;
+    }
     if (s >= NT * Q) {
       ++it;
       return c;
     }
   }
 }
+__device__ __forceinline__ float block_seq_sum(const float (&e)[16], uint32_t nq, float c,
+                                               uint32_t& it, LDS uint32_t* sc) {
+  uint32_t st;
+  return block_seq_scan<false>(e, nq, c, it, sc, 0.0f, st);
+}
 
-// A wave-uniform 64-bit value in scalar registers.
+// seq_scan's running sums of list[0..n) (mode 0: the total; 1 and 2: the
+// first j whose running sum reaches thr) by the whole workgroup, for long
+// lists (the slow path's nuclei): windows of NT*16 entries, thread t holding
+// entries 16t .. 16t+15 of a window, each window through block_seq_scan.
+// Returns (the stop index, n if none; the running sum there, the total if
+// none).  sc: 6 + NW*2 words.  A call of its own, its registers apart from
+// the kernel's.
+__device__ __attribute__((noinline)) u2v block_list_scan(List list, uint32_t n, int mode,
+                                                        float thr, LDS uint32_t* sc) {
+  constexpr uint32_t Q = 16;
+  const uint32_t tid = threadIdx.x;
+  const bool stops = mode != 0;
+  if (n > 0 && stops && thr <= 0.0f) return u2v{0u, __float_as_uint(0.0f + list.get(0))};
+  if (tid < 3) ((LDS uint64_t*)sc)[tid] = ~0ull;  // the event slots start cleared
+  __syncthreads();
+  uint32_t it = 0, stop = n;
+  float c = 0.0f;
+  for (uint32_t w0 = 0; w0 < n; w0 += NT * Q) {
+    float e[Q];
+#pragma unroll
+    for (uint32_t q = 0; q < Q; ++q) {
+      const uint32_t i = w0 + Q * tid + q;
+      e[q] = i < n ? list.get(i) : 0.0f;
+    }
+    uint32_t st;
+    c = stops ? block_seq_scan<true>(e, Q, c, it, sc, thr, st)
+              : block_seq_scan<false>(e, Q, c, it, sc, 0.0f, st);
+    if (st != EMPTY) {
+      stop = w0 + st;
+      break;
+    }
+  }
+  __syncthreads();  // the caller may reuse sc
+  return u2v{stop, __float_as_uint(c)};
+}
+
+// A wave-uniform 64-bit value, or LDS pointer, in scalar registers.
 __device__ __forceinline__ uint64_t sgpr_u64(uint64_t x) {
   const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)x);
   const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(x >> 32));
   return ((uint64_t)hi << 32) | lo;
+}
+template <class T>
+__device__ __forceinline__ LDS T* sgpr_lds(LDS T* p) {
+  const uint32_t a = (uint32_t)(uintptr_t)p;
+  return (LDS T*)(uintptr_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)a);
 }
 
 // A window that the serial sum cannot take, as a call of its own: the exact
@@ -1674,10 +1758,10 @@ __device__ __attribute__((noinline)) float exact_normaliser(
   // then does not spill (a reload from scratch waits for every load in
   // flight, the next window's logits among them)
   const uint32_t wv = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));
-  sc = (LDS uint32_t*)(uintptr_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)sc);
-  bitmap = (LDS uint32_t*)(uintptr_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)bitmap);
-  pre = (LDS uint16_t*)(uintptr_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)pre);
-  pen = (LDS float*)(uintptr_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)pen);
+  sc = sgpr_lds(sc);
+  bitmap = sgpr_lds(bitmap);
+  pre = sgpr_lds(pre);
+  pen = sgpr_lds(pen);
   row = (const void*)sgpr_u64((uint64_t)row);
   mask_row = (const uint32_t*)sgpr_u64((uint64_t)mask_row);
   T = __uint_as_float((uint32_t)__builtin_amdgcn_readfirstlane((int)__float_as_uint(T)));
@@ -1793,8 +1877,9 @@ __device__ __attribute__((noinline)) float exact_normaliser(
           if (j1 >= lo && j1 < hi) ad1 = CW * i + 32u * (j1 - lo);
         }
         auto fetch = [&](uint32_t j, f4v (&d)[8]) __attribute__((always_inline)) {
-          const uint32_t ad = j < WAVE ? (uint32_t)__builtin_amdgcn_readlane((int)ad0, (int)j)
-                                       : (uint32_t)__builtin_amdgcn_readlane((int)ad1, (int)(j - WAVE));
+          const uint32_t ad =
+              j < WAVE ? (uint32_t)__builtin_amdgcn_readlane((int)ad0, (int)j)
+                       : (uint32_t)__builtin_amdgcn_readlane((int)ad1, (int)(j - WAVE));
           LDS const f4v* p = (LDS const f4v*)(comp0 + ad);
 #pragma unroll
           for (int t = 0; t < 8; ++t) d[t] = p[t];
@@ -1900,7 +1985,8 @@ __device__ __forceinline__ void radix_sort_keys(GLB uint64_t* src, GLB uint64_t*
         const uint32_t d0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)dg[q]);
         const uint64_t vm = __ballot(valid);
         if (__ballot(valid && dg[q] != d0) == 0) {
-          if (lane == 0 && vm) __atomic_fetch_add(&digit_off[d0 & 255u], (uint32_t)__popcll(vm), __ATOMIC_RELAXED);
+          if (lane == 0 && vm)
+            __atomic_fetch_add(&digit_off[d0 & 255u], (uint32_t)__popcll(vm), __ATOMIC_RELAXED);
         } else if (valid) {
           __atomic_fetch_add(&digit_off[dg[q]], 1u, __ATOMIC_RELAXED);
         }
@@ -2257,8 +2343,9 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
     Lst.c = Chain{0.f, 0.f, 0.f, 0};
     // the exact prefix: every entry with p > p_lim (all V when nothing is left out)
     const uint32_t E = filt ? first_below(Lst, npos, p_lim, false, sh + 12) : V;
-    const bool good = run_semantics(P, u, E, V, p_lim, Lst, sh + 20, (LDS float*)wcnt, tok, len) &&
-                      !(filt && a.out_cap && len > E && a.out_cap > E);
+    const bool good =
+        run_semantics<true>(P, u, E, V, p_lim, Lst, sh + 20, (LDS float*)wcnt, tok, len) &&
+        !(filt && a.out_cap && len > E && a.out_cap > E);
     if (good) break;
     last = SLOW_BINS - 1;
     __syncthreads();
@@ -2794,8 +2881,8 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
   } else {
     List Ls{flat(f.pp), flat(f.pidx), Chain{0.f, 0.f, 0.f, 0}, (float*)f.pp};
     uint32_t tok = 0, len = 0;
-    bool good = run_semantics(P, u, n, a.V, plim_e, Ls, f.fm + F_SCR, (LDS float*)f.keys, tok,
-                              len);
+    bool good = run_semantics<false>(P, u, n, a.V, plim_e, Ls, f.fm + F_SCR,
+                                     (LDS float*)f.keys, tok, len);
     if (good && a.out_cap && len > n && a.out_cap > n) good = false;
     if (good) write_outputs(a, b, tok, len, Ls, m, S);
     res = good ? 0u : 2u;
