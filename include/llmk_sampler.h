@@ -72,8 +72,9 @@ typedef struct llmk_sampler llmk_sampler; /* opaque; owns device workspace */
 typedef enum { LLMK_F32 = 0, LLMK_BF16 = 1, LLMK_F16 = 2 } llmk_dtype;
 
 typedef struct {
-  /* logits[b * row_stride + v], v < vocab; row_stride in elements.  fp32 rows
-   * must be 16-byte aligned, bf16 and f16 rows 8-byte aligned. */
+  /* logits[b * row_stride + v], v < vocab; row_stride in elements.  Rows
+   * must be 16-byte aligned (fp32: row_stride a multiple of 4, bf16 and f16:
+   * of 8), else LLMK_ERR_ALIGNMENT. */
   const void* logits;
   int32_t dtype; /* llmk_dtype */
   uint32_t batch;

@@ -707,7 +707,18 @@ struct Raw {
   uint32_t mw[4];  // allow-mask words of the lane's 4 runs
 };
 
-// Lane `lane` owns tile offsets 256r + 4*lane + q (r, q in 0..3).
+// The vocabulary index of the lane's value j of the tile at tb: an f32 tile
+// is four runs of 256 tokens, the lane holding 4 consecutive tokens of each
+// (one 16-byte load per run); a 16-bit tile two runs of 512, the lane holding
+// 8 consecutive tokens of each (again one 16-byte load per run).
+template <int DT>
+__device__ __forceinline__ uint32_t tile_pos(uint32_t tb, int lane, int j) {
+  if ((DT & 3) == LLMK_F32)
+    return tb + 256u * (uint32_t)(j >> 2) + 4u * (uint32_t)lane + (uint32_t)(j & 3);
+  return tb + 512u * (uint32_t)(j >> 3) + 8u * (uint32_t)lane + (uint32_t)(j & 7);
+}
+
+// Lane `lane` owns the tile positions tile_pos gives.
 template <int DT>
 __device__ __forceinline__ void load_tile(const Args& a, const void* row,
                                           const uint32_t* mrow, const Hist& h,
@@ -726,37 +737,45 @@ __device__ __forceinline__ void load_tile(const Args& a, const void* row,
         raw.d[4 * r + 3] = __float_as_uint(x.w);
       }
     } else {
-      const GLB u2v* p = (const GLB u2v*)G((const uint16_t*)row + tb) + lane;
+      // two 16-byte loads: tokens 512h + 8 lane .. 512h + 8 lane + 7
+      const GLB u4v* p = (const GLB u4v*)G((const uint16_t*)row + tb) + lane;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const u2v x = __builtin_nontemporal_load(p + 64 * r);
-        raw.d[2 * r + 0] = x.x;
-        raw.d[2 * r + 1] = x.y;
+      for (int hh = 0; hh < 2; ++hh) {
+        const u4v x = __builtin_nontemporal_load(p + 64 * hh);
+        raw.d[4 * hh + 0] = x.x;
+        raw.d[4 * hh + 1] = x.y;
+        raw.d[4 * hh + 2] = x.z;
+        raw.d[4 * hh + 3] = x.w;
       }
     }
   } else {
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t e = tb + 256u * r + 4u * lane + q;
-        if ((DT & 3) == LLMK_F32) {
-          raw.d[4 * r + q] = e < a.V ? G((const uint32_t*)row)[e] : 0xff800000u;  // -inf past V
-        } else {
-          // the raw 16-bit value, -inf past V
-          const uint32_t hv = e < a.V ? (uint32_t)G((const uint16_t*)row)[e]
-                                      : ((DT & 3) == LLMK_BF16 ? 0xff80u : 0xfc00u);
-          const int w = 2 * r + (q >> 1);
-          if ((q & 1) == 0) raw.d[w] = hv;
-          else raw.d[w] |= hv << 16;
-        }
+    for (int j = 0; j < 16; ++j) {
+      const uint32_t e = tile_pos<DT>(tb, lane, j);
+      if ((DT & 3) == LLMK_F32) {
+        raw.d[j] = e < a.V ? G((const uint32_t*)row)[e] : 0xff800000u;  // -inf past V
+      } else {
+        // the raw 16-bit value, -inf past V
+        const uint32_t hv = e < a.V ? (uint32_t)G((const uint16_t*)row)[e]
+                                    : ((DT & 3) == LLMK_BF16 ? 0xff80u : 0xfc00u);
+        if ((j & 1) == 0) raw.d[j >> 1] = hv;
+        else raw.d[j >> 1] |= hv << 16;
       }
+    }
   }
   if (mrow) {
+    if ((DT & 3) == LLMK_F32) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const uint32_t wi = (tb >> 5) + 8u * r + ((uint32_t)lane >> 3);
-      raw.mw[r] = (wi < a.mask_words) ? G(mrow)[wi] : 0u;
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t wi = (tb >> 5) + 8u * r + ((uint32_t)lane >> 3);
+        raw.mw[r] = (wi < a.mask_words) ? G(mrow)[wi] : 0u;
+      }
+    } else {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const uint32_t wi = (tb >> 5) + 16u * hh + ((uint32_t)lane >> 2);
+        raw.mw[hh] = (wi < a.mask_words) ? G(mrow)[wi] : 0u;
+      }
     }
   }
 }
@@ -3681,7 +3700,6 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   }
   uint32_t since = EMPTY;
 
-  const uint32_t sh4 = (4u * (uint32_t)lane) & 31u;
   auto process = [&](const Raw& raw, uint32_t t) __attribute__((always_inline)) {
     float v[16];
     unpack<DT>(raw, v);
@@ -3690,29 +3708,32 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
       // positions past V hold -inf, which the cap would have made -cap
 #pragma unroll
       for (int j = 0; j < 16; ++j)
-        if (tb + 256u * (j >> 2) + 4u * (uint32_t)lane + (j & 3) >= a.V) v[j] = NEG_INF;
+        if (tile_pos<DT>(tb, lane, j) >= a.V) v[j] = NEG_INF;
     }
     // history tokens and disallowed tokens become -inf (a uniform branch per
-    // case, so a row without a mask spends nothing on one)
+    // case, so a row without a mask spends nothing on one): a run's tokens
+    // lie in one 32-bit word of the mask and of the bitmap
+    constexpr int RUNS = (DT & 3) == LLMK_F32 ? 4 : 2, RL = 16 / RUNS;
+    const uint32_t shr = (RL * (uint32_t)lane) & 31u;
+    const uint32_t wl = (uint32_t)lane / (32u / RL);
     if (mrow) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
+      for (int r = 0; r < RUNS; ++r) {
         uint32_t x = ~raw.mw[r];
-        if (have) x |= h.bitmap[((tb - lo) >> 5) + 8u * r + ((uint32_t)lane >> 3)];
+        if (have) x |= h.bitmap[((tb - lo) >> 5) + (uint32_t)(8 * RL) * r / 4u + wl];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[4 * r + q] = exclude(v[4 * r + q], x, sh4 + q);
+        for (int q = 0; q < RL; ++q) v[RL * r + q] = exclude(v[RL * r + q], x, shr + q);
       }
     } else if (have) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const uint32_t x = h.bitmap[((tb - lo) >> 5) + 8u * r + ((uint32_t)lane >> 3)];
+      for (int r = 0; r < RUNS; ++r) {
+        const uint32_t x = h.bitmap[((tb - lo) >> 5) + (uint32_t)(8 * RL) * r / 4u + wl];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[4 * r + q] = exclude(v[4 * r + q], x, sh4 + q);
+        for (int q = 0; q < RL; ++q) v[RL * r + q] = exclude(v[RL * r + q], x, shr + q);
       }
     }
-    tile_reduce(E, v, t, [&](int j) -> uint32_t {
-      return tb + 256u * (j >> 2) + 4u * (uint32_t)lane + (j & 3);
-    }, since, lane);
+    tile_reduce(E, v, t, [&](int j) -> uint32_t { return tile_pos<DT>(tb, lane, j); }, since,
+                lane);
   };
   // Later tiles are claimed dynamically, so the waves finish together.
   auto grab = [&]() -> uint32_t {
@@ -4593,9 +4614,9 @@ static int sample_batch_run(const Ws& ws, uint32_t max_batch, uint32_t max_vocab
   if (!(in->softcap >= 0.0f) || !(in->softcap < __builtin_huge_valf()))
     return fail(LLMK_ERR_INVALID_ARGUMENT, "softcap must be finite and >= 0 (0 = off)");
   const size_t esz = in->dtype == LLMK_F32 ? 4 : 2;
-  const size_t align = in->dtype == LLMK_F32 ? 16 : 8;
+  const size_t align = 16;  // the tiles' 16-byte loads
   if (((uintptr_t)in->logits % align) != 0 || ((in->row_stride * esz) % align) != 0)
-    return fail(LLMK_ERR_ALIGNMENT, "logit rows must be 16-byte (fp32) / 8-byte (bf16) aligned");
+    return fail(LLMK_ERR_ALIGNMENT, "logit rows must be 16-byte aligned");
 
   Args a;
   a.logits = in->logits;

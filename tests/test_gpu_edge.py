@@ -210,6 +210,12 @@ def test_host_errors(sampler):
     with pytest.raises(llmk.SamplerError) as e:
         sampler.sample_batch(db)
     assert e.value.code == _lib.LLMK_ERR_ALIGNMENT
+    # 16-bit rows too: a stride of 108 bf16 elements (216 bytes) is 8-byte
+    # but not 16-byte aligned
+    db.logits = torch.zeros(2, 108, dtype=torch.bfloat16, device="cuda:0")
+    with pytest.raises(llmk.SamplerError) as e:
+        sampler.sample_batch(db)
+    assert e.value.code == _lib.LLMK_ERR_ALIGNMENT
     # the reference's per-row call and sample() wrapper
     lg = torch.tensor([0.1, 0.5, 3.0, 0.2], device="cuda:0")
     assert llmk.sample(sampler, lg, 0.0, 0.5) == 2
