@@ -1757,11 +1757,13 @@ __device__ __attribute__((noinline)) u2v window_scan(f4v x0, f4v x1, f4v x2, f4v
 // the window's start (the sum only grows, so such an e adds 0 wherever it
 // falls).  A cheap bound on l finds them (the product with 1/T is within a
 // few ulps of l, far inside the margin), and a wave whose window part keeps
-// at most 256 entries packs them in order into LDS, four per lane, so that
-// the exact division and exp run on those alone.  A window whose entries
-// are all packed and number at most SERIAL_MAX is then summed by one lane,
-// entry after entry (a few cycles each, against microseconds for a round of
-// the workgroup scan); any other window goes through block_seq_sum.
+// at most 256 entries packs them in order into LDS, so that the exact
+// division and exp run on those alone (one per lane per 64 entries).  A
+// window whose entries are all packed and number at most SERIAL_MAX is then
+// summed in order by wave 0, every lane alike, entry after entry (a few
+// cycles each, against microseconds for a round of the workgroup scan); any
+// other window goes through block_seq_sum (window_scan).  The next window's
+// logits and mask word are requested before a window is summed.
 // sc: 96 + NW*256 words of scratch.
 // A function of its own (not inlined, scalars only across the call): its
 // registers are then allocated apart from the stream loop's, which an
