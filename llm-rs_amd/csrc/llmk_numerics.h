@@ -47,6 +47,12 @@ __device__ __forceinline__ void exp_tab_init() {
   if (threadIdx.x < 32) g_exptab[threadIdx.x] = kExpTab[threadIdx.x];
 }
 
+// REMAT: the polynomial's constant term is written into a register pair at
+// each call (two moves the compiler cannot hoist), so that a loop calling
+// exp_ref does not hold it in registers across its whole body: under
+// register pressure the compiler spilled it, and every reload from scratch
+// waited for all the loads in flight.
+template <bool REMAT = false>
 __device__ __forceinline__ float exp_ref(float x) {
   const bool live = x >= -0x1.9fe368p6f;  // false for -inf
   const double xd = live ? (double)x : 0.0;
@@ -57,7 +63,14 @@ __device__ __forceinline__ float exp_ref(float x) {
   // (ki << 47) mod 2^64 touches only the high word: (ki << 15) << 32
   const uint64_t t = g_exptab[ki & 31u] + ((uint64_t)(ki << 15) << 32);
   const double s = __longlong_as_double((long long)t);
-  const double z = __builtin_fma(0x1.c6af84b912394p-20, r, 0x1.ebfce50fac4f3p-13);
+  double c0 = 0x1.ebfce50fac4f3p-13;
+  if (REMAT) {
+    uint32_t lo, hi;
+    asm volatile("v_mov_b32 %0, 0x50fac4f3" : "=v"(lo));
+    asm volatile("v_mov_b32 %0, 0x3f2ebfce" : "=v"(hi));
+    c0 = __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+  }
+  const double z = __builtin_fma(0x1.c6af84b912394p-20, r, c0);
   const double r2 = r * r;
   double y = __builtin_fma(0x1.62e42ff0c52d6p-6, r, 1.0);
   y = __builtin_fma(z, r2, y);

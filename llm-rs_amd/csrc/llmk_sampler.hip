@@ -1524,13 +1524,13 @@ __device__ __forceinline__ Par wave_par_incl(Par x) {
 template <bool STOPS>
 __device__ __forceinline__ float block_seq_scan(const float (&e)[16], uint32_t nq, float c,
                                                 uint32_t& it, LDS uint32_t* sc, float thr,
-                                                uint32_t& stop_at) {
+                                                uint32_t& stop_at, uint32_t s_start = 0) {
   constexpr uint32_t Q = 16, TOP = 1u << 24;
   stop_at = EMPTY;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
   LDS uint64_t* ev = (LDS uint64_t*)sc;  // [3]: first event (index << 32 | new sum bits)
   LDS uint32_t* wt = sc + 6;             // [NW][2]: wave totals
-  uint32_t s = 0;                        // entries before s are summed
+  uint32_t s = s_start;                  // entries before s are summed (into c)
   for (;; ++it) {
     LDS uint64_t* slot = ev + it % 3u;
     if (tid == 0) ev[(it + 1) % 3u] = ~0ull;
@@ -1743,7 +1743,46 @@ __device__ __attribute__((noinline)) u2v window_scan(f4v x0, f4v x1, f4v x2, f4v
       e[q] = ((live >> q) & 1u) && l != NEG_INF ? exp_ref(l - m) : 0.0f;
     }
   }
-  const float r = block_seq_sum(e, nq, c, it, sc);
+  uint32_t s0 = 0;
+  if (c == 0.0f) {
+    // A sum from zero crosses a binade at every doubling, at first every few
+    // entries, and each crossing costs a round of the workgroup scan (a
+    // first window took ~80 us against ~16 for the others): wave 0 first
+    // adds its own entries, the window's first NT*16/16, one after another,
+    // and the scan starts past them.  They are staged in comp0, free once
+    // every wave holds its terms.
+    const uint32_t wv = threadIdx.x >> 6;
+    LDS float* stage = (LDS float*)(comp - CW * wv);
+    LDS float* bc = (LDS float*)sc + 40;  // past the scan's 6 + NW*2 words
+    __syncthreads();
+    if (wv == 0) {
+#pragma unroll
+      for (uint32_t q = 0; q < Q; q += 4)
+        *(LDS f4v*)(stage + Q * lane + q) = f4v{e[q], e[q + 1], e[q + 2], e[q + 3]};
+      WaveSync::sync();
+      // in every lane alike (broadcast reads), eight 16-byte reads, then
+      // their 32 additions in order
+      float cc = 0.0f;
+      for (uint32_t k = 0; k < Q * WAVE; k += 32u) {
+        f4v y[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) y[j] = *(LDS const f4v*)(stage + k + 4 * j);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          cc = cc + y[j].x;
+          cc = cc + y[j].y;
+          cc = cc + y[j].z;
+          cc = cc + y[j].w;
+        }
+      }
+      if (lane == 0) *bc = cc;
+    }
+    __syncthreads();
+    c = *bc;
+    s0 = Q * WAVE;
+  }
+  uint32_t st;
+  const float r = block_seq_scan<false>(e, nq, c, it, sc, 0.0f, st, s0);
   return u2v{__float_as_uint(r), it};
 }
 
@@ -1805,7 +1844,7 @@ __device__ __attribute__((noinline)) float exact_normaliser(
   const float rT = 1.0f / P.T;
   auto exact_e = [&](float x) __attribute__((always_inline)) {
     const float l = (P.T != 1.0f) ? x / P.T : x;
-    return (l == NEG_INF) ? 0.0f : exp_ref(l - m);
+    return (l == NEG_INF) ? 0.0f : exp_ref<true>(l - m);
   };
   if (tid < 3) ((LDS uint64_t*)sc)[tid] = ~0ull;
   __syncthreads();
