@@ -69,3 +69,32 @@ def test_full_size_matches_reference(sampler, name):
     assert_bit_exact(w, gpu, O.sample_workload(O.MIRROR, w, out_cap=CAP, nthreads=16), CAP, name)
     assert_matches_ref(w, gpu, O.sample_workload(O.REF, w, out_cap=CAP, nthreads=16), CAP, name)
     assert sampler.status() == 0
+
+
+def test_normaliser_windows_that_start_at_zero(sampler):
+    """Rows without top-k whose exact normaliser meets a window with its sum
+    still at zero in different ways: a flat row (wave 0's 1024 entries added
+    in order before the workgroup scan), a row whose first 1024 or 1500
+    logits are -inf (that prefix adds nothing and the scan finds the first
+    term itself), a huge logit among the first entries, a first window that
+    is all -inf (the prefix applies to the second), and a sparse first
+    window (packed, summed by wave 0) before dense ones.  Tokens, kept ids
+    and probability bits against the reference oracle and the mirror."""
+    rng = np.random.default_rng(23)
+    B, V = 6, 40000
+    lg = rng.normal(0, 2.0, (B, V)).astype(np.float32)
+    lg[1, :1024] = -np.inf
+    lg[2, :1500] = -np.inf
+    lg[3, 3] = 30.0
+    lg[4, :16384] = -np.inf
+    lg[5, :16384][np.arange(16384) % 8 != 0] = -np.inf
+    u = rng.random(B).astype(np.float32)
+    from gpu_util import workload
+    w = workload(lg, T=[1.0, 0.8, 1.2, 1.0, 1.0, 0.9], K=0, P=[0.9, 0.95, 0.8, 0.99, 0.9, 0.95],
+                 u=u, name="zero-start windows")
+    print("[case] normaliser windows starting at zero", flush=True)
+    gpu = run_gpu(sampler, w, CAP)
+    assert_bit_exact(w, gpu, O.sample_workload(O.MIRROR, w, out_cap=CAP, nthreads=16), CAP,
+                     "zero-start windows")
+    assert_matches_ref(w, gpu, O.sample_workload(O.REF, w, out_cap=CAP, nthreads=16), CAP,
+                       "zero-start windows")
