@@ -1709,6 +1709,46 @@ __device__ __forceinline__ LDS T* sgpr_lds(LDS T* p) {
   return (LDS T*)(uintptr_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)a);
 }
 
+// A window whose sum starts at zero: wave 0's entries (the window's first
+// 1024, sixteen a lane in order) added one after another, returned to every
+// thread.  A sum from zero crosses a binade at every doubling, at first every
+// few entries, and each crossing costs a round of the workgroup scan (a first
+// window took ~80 us against ~16 for the others).  The entries are staged in
+// stage (comp0, free once every wave holds its terms), the sum passed through
+// bc.  A call of its own, so that the window scan's registers stay as they
+// were.  Every thread calls it.
+__device__ __attribute__((noinline)) float zero_start_sum(f4v a0, f4v a1, f4v a2, f4v a3,
+                                                          LDS float* stage, LDS float* bc) {
+  const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
+  __syncthreads();
+  if (wv == 0) {
+    LDS f4v* st = (LDS f4v*)(stage + 16u * lane);
+    st[0] = a0;
+    st[1] = a1;
+    st[2] = a2;
+    st[3] = a3;
+    WaveSync::sync();
+    // in every lane alike (broadcast reads), eight 16-byte reads, then their
+    // 32 additions in order
+    float cc = 0.0f;
+    for (uint32_t k = 0; k < 16u * WAVE; k += 32u) {
+      f4v y[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) y[j] = *(LDS const f4v*)(stage + k + 4 * j);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        cc = cc + y[j].x;
+        cc = cc + y[j].y;
+        cc = cc + y[j].z;
+        cc = cc + y[j].w;
+      }
+    }
+    if (lane == 0) *bc = cc;
+  }
+  __syncthreads();
+  return *bc;
+}
+
 // A window that the serial sum cannot take, as a call of its own: the exact
 // terms of an unpacked wave (x, the processed logits, where `live`) or the
 // packed terms of a packed wave (comp, its nw entries), then block_seq_sum.
@@ -1745,40 +1785,9 @@ __device__ __attribute__((noinline)) u2v window_scan(f4v x0, f4v x1, f4v x2, f4v
   }
   uint32_t s0 = 0;
   if (c == 0.0f) {
-    // A sum from zero crosses a binade at every doubling, at first every few
-    // entries, and each crossing costs a round of the workgroup scan (a
-    // first window took ~80 us against ~16 for the others): wave 0 first
-    // adds its own entries, the window's first NT*16/16, one after another,
-    // and the scan starts past them.  They are staged in comp0, free once
-    // every wave holds its terms.
-    const uint32_t wv = threadIdx.x >> 6;
-    LDS float* stage = (LDS float*)(comp - CW * wv);
-    LDS float* bc = (LDS float*)sc + 40;  // past the scan's 6 + NW*2 words
-    __syncthreads();
-    if (wv == 0) {
-#pragma unroll
-      for (uint32_t q = 0; q < Q; q += 4)
-        *(LDS f4v*)(stage + Q * lane + q) = f4v{e[q], e[q + 1], e[q + 2], e[q + 3]};
-      WaveSync::sync();
-      // in every lane alike (broadcast reads), eight 16-byte reads, then
-      // their 32 additions in order
-      float cc = 0.0f;
-      for (uint32_t k = 0; k < Q * WAVE; k += 32u) {
-        f4v y[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) y[j] = *(LDS const f4v*)(stage + k + 4 * j);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          cc = cc + y[j].x;
-          cc = cc + y[j].y;
-          cc = cc + y[j].z;
-          cc = cc + y[j].w;
-        }
-      }
-      if (lane == 0) *bc = cc;
-    }
-    __syncthreads();
-    c = *bc;
+    c = zero_start_sum(f4v{e[0], e[1], e[2], e[3]}, f4v{e[4], e[5], e[6], e[7]},
+                       f4v{e[8], e[9], e[10], e[11]}, f4v{e[12], e[13], e[14], e[15]},
+                       (LDS float*)(comp - CW * (threadIdx.x >> 6)), (LDS float*)sc + 40);
     s0 = Q * WAVE;
   }
   uint32_t st;
