@@ -332,3 +332,64 @@ def test_mask_forms_random(sampler, seed):
                              rng.uniform(0.99, 0.99999)])) for _ in range(B)]
     check(sampler, "k", rows, ks, pad=int(rng.integers(0, 9)))
     check(sampler, "p", rows, tps, pad=(-V) % 4 + 4 * int(rng.integers(0, 3)))
+
+
+def test_mask_forms_properties_at_full_batch():
+    """The whole C3 batch (256 rows of 151936, more than the oracle covers in
+    seconds), checked row by row through properties that fix the mask forms
+    whatever the row.  apply_top_k (sampler.rs:160-173): values only ever
+    replaced by -inf; every masked value below every kept one; at least k
+    values at or above the smallest kept value and fewer than k strictly
+    above it, so the threshold is the k-th largest value and its ties stay;
+    a second application changes nothing.  apply_top_p (sampler.rs:176-216):
+    values only ever replaced by -inf; the kept values a top segment of the
+    row's order (ties at the cut may split); the row's maximum kept; the kept
+    softmax mass, in float64, at least top_p less the error bound of the
+    reference's float32 arithmetic: its normaliser is a sequential float32
+    sum of V terms and its cumulative sum one of the kept terms, each
+    addition off by at most half an ulp of the running sum, so the relative
+    error is below (V + kept) * 2^-24.  The bound is not slack: at this
+    shape terms below half an ulp of the running sum (about 12) are dropped
+    whole, so the float32 normaliser reads low and the kept mass falls short
+    of top_p by about 2e-4."""
+    B, V = 256, 151936
+    rows = c3_rows(B, V, 31)
+    rows[::4] = np.round(rows[::4] * 2.0) / 2.0  # heavy ties on every fourth row
+    rows[1::8, : V // 3] = -np.inf                # -inf prefixes
+    ks = np.array([[1, 50, 1000, 1024, 1025, 5000, 75968, V][i % 8] for i in range(B)])
+    tps = np.array([[0.5, 0.9, 0.95, 0.999, 0.1, 0.8][i % 6] for i in range(B)], np.float32)
+    s = llmk.HipSampler(max_batch=B, max_vocab=V)
+    try:
+        t = torch.from_numpy(rows.copy()).cuda()
+        kt = torch.tensor(ks.astype(np.int32)).cuda()
+        print(f"[case] top_k properties B={B} V={V}", flush=True)
+        s.apply_top_k(t, kt)
+        once = t.cpu().numpy()
+        s.apply_top_k(t, kt)
+        assert np.array_equal(t.cpu().numpy().view(np.uint32), once.view(np.uint32)), \
+            "apply_top_k is not idempotent"
+        t = torch.from_numpy(rows.copy()).cuda()
+        print(f"[case] top_p properties B={B} V={V}", flush=True)
+        s.apply_top_p(t, torch.tensor(tps).cuda())
+        pmask = t.cpu().numpy()
+    finally:
+        s.close()
+    for i in range(B):
+        r, o, k = rows[i], once[i], int(ks[i])
+        kept = o > -np.inf
+        assert np.array_equal(o[kept], r[kept]) and np.all(np.isneginf(o[~kept])), f"row {i}"
+        if k >= V:
+            assert np.array_equal(o, r), f"row {i}: top_k {k} >= V masks nothing"
+            continue
+        lo = r[kept].min()
+        assert np.all(r[~kept] < lo), f"row {i}: a masked value at or above a kept one"
+        assert (r >= lo).sum() >= k > (r > lo).sum(), f"row {i}: threshold is not the {k}-th largest"
+    for i in range(B):
+        r, o, p = rows[i], pmask[i], float(tps[i])
+        kept = o > -np.inf
+        assert np.array_equal(o[kept], r[kept]) and np.all(np.isneginf(o[~kept])), f"row {i}"
+        assert o[np.argmax(r)] == r.max(), f"row {i}: the maximum was masked"
+        assert np.all(r[~kept] <= r[kept].min()), f"row {i}: kept values are not a top segment"
+        e = np.exp(r.astype(np.float64) - r.max())
+        tol = (V + int(kept.sum())) * 2.0**-24
+        assert e[kept].sum() / e.sum() >= p - tol, f"row {i}: kept mass below top_p {p}"
