@@ -195,7 +195,9 @@ __device__ __forceinline__ RowP row_params(const Args& a, const RowIn& in) {
                    !finitef(r.pp) || !finitef(r.fp);
   r.mode = bad ? MODE_INVALID : (r.T <= 1e-5f ? MODE_GREEDY : MODE_SAMPLE);
   const bool topk_on = r.K > 0 && (uint32_t)r.K < a.V;
-  r.Kc = topk_on ? ((uint32_t)r.K <= KMAX ? (uint32_t)r.K : 0u) : KCAND_NOK;
+  // top-k rows gather one candidate past the K-th (the band check compares
+  // the two)
+  r.Kc = topk_on ? ((uint32_t)r.K <= KMAX ? (uint32_t)r.K + 1u : 0u) : KCAND_NOK;
   return r;
 }
 
@@ -1340,6 +1342,236 @@ __device__ __forceinline__ uint32_t cut_id(uint32_t len, uint32_t n, uint32_t i0
   return (len > 0 && len <= n) ? v : 0u;
 }
 
+// ---------------------------------------------------------------------------
+// The rounding band of S = 1 on rows that top-k renormalises
+// ---------------------------------------------------------------------------
+// Such a row is sampled with S = 1 (p = e): the reference divides by its
+// sequential sum S first (sampler.rs:66-71) and by a renormalising sum before
+// any later step reads a probability (min-p's cut, then top-k, :83-88), so S
+// cancels in exact arithmetic.  band_certain_wave proves from the sorted e
+// alone that every decision (min-p cut, top-k set and order, top-p cut at
+// :97, the draw at :118) is the reference's for any S it can hold; a row it
+// cannot prove is sampled again with the reference's own S.  The bound: p
+// known to relative R (2^-24 for fl(e / S)); a sequential sum rounds each
+// partial sum by at most half an ulp of it (u times the value while the
+// scale is S's, the binade's half ulp once normalised); a renormalisation
+// divides by a sum known to relative sigma and rounds once more:
+// R' = (R + sigma + u)(1 + 2^-10), the factor covering second-order terms.
+// A decision is certain when its exact value (sums of the e in double)
+// lies outside its bound; order is certain unless two entries within 2^-20
+// relative have their indices inverted (fl(e_a/S) == fl(e_b/S) ties go by
+// index); entries below 2^-100 (p could be subnormal) are never certain.
+// The doubles are summed in one fixed order, which the CPU oracle follows:
+// a wave's DPP scan within 64 entries (row_shr 1, 2, 4, 8 within rows of 16,
+// then row_bcast 15 and 31), then the chunk's carry.  One wave; acc(j) =
+// (e bits, index) of entry j < E; entries past E are <= ptail.
+constexpr double BAND_U = 0x1p-24;
+constexpr double BAND_F = 1.0 + 0x1p-10;
+constexpr double BAND_SL = 0x1p-36;
+constexpr double BAND_CLOSE = 1.0 + 0x1p-20;
+// half an ulp of a float of magnitude x in (0, 2): 2^(floor(log2 x) - 24)
+__device__ __forceinline__ double band_hu(double x) {
+  if (!(x > 0.0)) return 0.0;
+  const uint64_t ex = ((uint64_t)__double_as_longlong(x) >> 52) & 0x7ffu;
+  return __longlong_as_double((long long)((ex - 24u) << 52));
+}
+template <int CTRL, int RM, bool BC>
+__device__ __forceinline__ double dppd(double x) {
+  const uint64_t b = (uint64_t)__double_as_longlong(x);
+  const uint32_t lo = dppu<CTRL, RM, BC>(0u, (uint32_t)b);
+  const uint32_t hi = dppu<CTRL, RM, BC>(0u, (uint32_t)(b >> 32));
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+// inclusive prefix over the wave (lanes outside a step's reach add +0)
+__device__ __forceinline__ double wave_prefix_d(double x) {
+  x = x + dppd<0x111, 0xf, true>(x);
+  x = x + dppd<0x112, 0xf, true>(x);
+  x = x + dppd<0x114, 0xf, true>(x);
+  x = x + dppd<0x118, 0xf, true>(x);
+  x = x + dppd<0x142, 0xa, false>(x);
+  x = x + dppd<0x143, 0xc, false>(x);
+  return x;
+}
+__device__ __forceinline__ double readlane_d(double x, int l) {
+  const uint64_t b = (uint64_t)__double_as_longlong(x);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+template <class ACC>
+struct BandList {
+  ACC acc;
+  uint32_t E;
+  __device__ __forceinline__ double e(uint32_t j) const {
+    return j < E ? (double)__uint_as_float(acc(j).x) : 0.0;
+  }
+  // P_{n-1} (prefix of e over [0, n)) and sum_{1 <= j < n} P_j
+  __device__ __forceinline__ void sums(uint32_t n, int lane, double& ptot, double& qtot) const {
+    double cp = 0.0, cq = 0.0;
+    for (uint32_t c0 = 0; c0 < n; c0 += WAVE) {
+      const uint32_t j = c0 + (uint32_t)lane;
+      const double Pj = wave_prefix_d(j < n ? e(j) : 0.0) + cp;
+      const double Qj = wave_prefix_d((j < n && j >= 1) ? Pj : 0.0) + cq;
+      if (c0 + WAVE >= n) {
+        ptot = readlane_d(Pj, (int)((n - 1) & 63u));
+        qtot = readlane_d(Qj, (int)((n - 1) & 63u));
+      } else {
+        cp = readlane_d(Pj, 63);
+        cq = readlane_d(Qj, 63);
+      }
+    }
+  }
+  // The first j < n whose cumulative may reach thr (C_j + B_j >= thr), n if
+  // none; certain: the reference's cumulative surely reaches it there and
+  // not before.  C_j = P_j (1 / tot), B_j = R C_j + sum_{1<=i<=j} hu(C_i (1 +
+  // R) F) + SL C_j.  bj, pj: B_j and P_j there (at n - 1 when none).
+  __device__ __forceinline__ uint32_t find(uint32_t n, double tot, double R, double thr,
+                                           int lane, bool& certain, double& bj,
+                                           double& pj) const {
+    const double rt = 1.0 / tot;
+    double cp = 0.0, ch = 0.0;
+    for (uint32_t c0 = 0; c0 < n; c0 += WAVE) {
+      const uint32_t j = c0 + (uint32_t)lane;
+      const double Pj = wave_prefix_d(j < n ? e(j) : 0.0) + cp;
+      const double C = Pj * rt;
+      const double hj = (j < n && j >= 1) ? band_hu(C * (1.0 + R) * BAND_F) : 0.0;
+      const double Hj = wave_prefix_d(hj) + ch;
+      const double b = R * C + Hj + BAND_SL * C;
+      const uint64_t hit = __ballot(j < n && C + b >= thr);
+      if (hit) {
+        const int l = __ffsll((unsigned long long)hit) - 1;
+        certain = __builtin_amdgcn_readlane((int)(C - b >= thr), l) != 0;
+        bj = readlane_d(b, l);
+        pj = readlane_d(Pj, l);
+        return c0 + (uint32_t)l;
+      }
+      if (c0 + WAVE >= n) {
+        bj = readlane_d(b, (int)((n - 1) & 63u));
+        pj = readlane_d(Pj, (int)((n - 1) & 63u));
+      } else {
+        cp = readlane_d(Pj, 63);
+        ch = readlane_d(Hj, 63);
+      }
+    }
+    certain = true;
+    return n;
+  }
+};
+// sorted (p desc, idx asc) keys
+struct KeyAcc {
+  LDS const uint64_t* k;
+  __device__ __forceinline__ u2v operator()(uint32_t j) const {
+    const uint64_t x = k[j];
+    return u2v{~(uint32_t)(x >> 32), (uint32_t)x};
+  }
+};
+// sorted p and index arrays (LDS or global)
+template <class PF, class PI>
+struct ArrAcc {
+  PF p;
+  PI i;
+  __device__ __forceinline__ u2v operator()(uint32_t j) const {
+    return u2v{__float_as_uint(p[j]), i[j]};
+  }
+};
+template <class ACC>
+__device__ __noinline__ bool band_certain_wave(ACC acc, uint32_t E, uint32_t full,
+                                               float ptail, float min_p, int32_t K,
+                                               float top_p, float u) {
+  const int lane = (int)(threadIdx.x & 63u);
+  const BandList<ACC> L{acc, E};
+  uint32_t len = full;
+  double R = BAND_U;
+  bool normalised = false;
+  // entries whose p = e / S could be subnormal
+  const uint32_t lim = (K > 0 && (uint32_t)K + 1u < E) ? (uint32_t)K + 1u : E;
+  for (uint32_t c0 = 0; c0 < lim; c0 += WAVE) {
+    const uint32_t j = c0 + (uint32_t)lane;
+    const float x = j < lim ? __uint_as_float(acc(j).x) : 0.0f;
+    if (__ballot(x > 0.0f && x < 0x1p-100f)) return false;
+  }
+  double ptot = 0.0, qtot = 0.0;
+  auto renormalise = [&](uint32_t n) {
+    L.sums(n, lane, ptot, qtot);
+    const double sg = R + BAND_U * (1.0 + R) * BAND_F * (qtot / ptot);
+    R = (R + sg + BAND_U) * BAND_F;
+    normalised = true;
+  };
+  // min-p: kept iff fl(e/S) >= fl(min_p fl(1/S)) (e_0 = 1, the maximum);
+  // certain outside min_p (1 -+ 2^-21)
+  if (min_p > 0.0f) {
+    if (min_p < 0x1p-100f || E == 0) return false;
+    const double hi = (double)min_p * (1.0 + 0x1p-21);
+    const double lo = (double)min_p * (1.0 - 0x1p-21);
+    const uint32_t n = E < len ? E : len;
+    uint32_t cut = EMPTY;
+    for (uint32_t c0 = 0; c0 < n; c0 += WAVE) {
+      const uint32_t j = c0 + (uint32_t)lane;
+      const uint64_t hit = __ballot(j < n && L.e(j) < hi);
+      if (hit) {
+        cut = c0 + (uint32_t)(__ffsll((unsigned long long)hit) - 1);
+        break;
+      }
+    }
+    if (cut != EMPTY) {
+      if (L.e(cut) >= lo) return false;
+    } else if (E < len) {
+      if ((double)ptail >= lo) return false;
+      cut = E;
+    }
+    if (cut != EMPTY && cut < len) {
+      len = cut;
+      if (len == 0) return false;
+      renormalise(len);
+      if (!(ptot > 0.0)) return false;
+    }
+  }
+  // top-k: the first K in (p desc, idx asc) order; no pair whose order could
+  // change, across the boundary included (an unknown entry K close to the
+  // last kept one could be either side of it)
+  uint32_t np;
+  if (K > 0 && (uint32_t)K < len) {
+    if ((uint32_t)K > E) return false;
+    if ((uint32_t)K == E && L.e(K - 1) < (double)ptail * BAND_CLOSE) return false;
+    np = (uint32_t)K < E ? (uint32_t)K + 1u : (uint32_t)K;
+  } else {
+    np = E < len ? E : len;
+  }
+  for (uint32_t c0 = 0; c0 + 1 < np; c0 += WAVE) {
+    const uint32_t j = c0 + (uint32_t)lane;
+    bool bad = false;
+    if (j + 1 < np) {
+      const u2v x0 = acc(j), x1 = acc(j + 1);
+      bad = (double)__uint_as_float(x0.x) < (double)__uint_as_float(x1.x) * BAND_CLOSE &&
+            x0.y > x1.y;
+    }
+    if (__ballot(bad)) return false;
+  }
+  if (K > 0 && (uint32_t)K < len) {
+    len = (uint32_t)K;
+    renormalise(len);
+    if (!(ptot > 0.0)) return false;
+  }
+  if (!normalised || len > E) return false;
+  // top-p: the first cumulative >= top_p, then the renormalisation by that
+  // same cumulative
+  if (top_p < 1.0f) {
+    bool cert;
+    double b, pc;
+    const uint32_t j = L.find(len, ptot, R, (double)top_p, lane, cert, b, pc);
+    if (!cert) return false;
+    const double sp = b / (pc * (1.0 / ptot));
+    R = (R + sp + BAND_U) * BAND_F;
+    len = j < len ? j + 1 : len;
+    ptot = pc;
+  }
+  // the draw: the first cumulative >= u, else the last
+  bool cert;
+  double b, pc;
+  (void)L.find(len, ptot, R, (double)u, lane, cert, b, pc);
+  return cert;
+}
+
 __device__ __forceinline__ bool semantics_regs(const RowP& P, float u, uint32_t n,
                                                uint32_t full_len, float ptail, float& p0,
                                                float& p1,
@@ -2169,9 +2401,14 @@ __device__ __forceinline__ void radix_sort_keys(GLB uint64_t* src, GLB uint64_t*
 //      p > p_lim.  If the semantics need an entry past it, C and D are done
 //      again with every bin chosen.
 // ---------------------------------------------------------------------------
+// approx: S = 1 stands in for the reference's S (a row that top-k
+// renormalises); its result stands only if the band check proves it, else S
+// is computed (exact_normaliser) and the row sampled again.  need_exact: the
+// candidate path's band check already failed; S is computed first.
 template <int DT>
 __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b, const RowP& P,
-                                         float S, float m, float L, LDS uint32_t* smem) {
+                                         float S, float m, float L, LDS uint32_t* smem,
+                                         bool approx, bool need_exact) {
   const uint32_t tid = threadIdx.x;
   const int lane = (int)(tid & 63), wv = (int)(tid >> 6);
   const uint32_t V = a.V;
@@ -2217,6 +2454,12 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
   build_history<DT>(a, P, b, row, 0, V, nwords, h, red, &sh[10]);
   if (tid == 0 && (sh[10] & FLAG_HIST_OVERFLOW))
     atomicOr(w.status, LLMK_STATUS_HISTORY_OVERFLOW);
+  const uint32_t* mask_row = a.mask ? a.mask + (uint64_t)b * a.mask_words : nullptr;
+  if (need_exact) {
+    // sh, red, digit_off and wcnt are scratch of the normaliser here
+    S = exact_normaliser<DT>(row, mask_row, V, P.T, m, h.bitmap, h.pre, h.pen, true, smem);
+    approx = false;
+  }
   GLB uint64_t* kA = G(w.slow_keys) + (uint64_t)slot * 3 * (uint64_t)w.max_vocab;
   GLB uint64_t* kB = kA + w.max_vocab;
   GLB uint32_t* zl = (GLB uint32_t*)(kB + w.max_vocab);  // zero-probability indices
@@ -2320,7 +2563,9 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
   uint32_t last = sh[11];
   uint32_t tok = 0, len = 0;
   List Lst{flat(plist), flat(ilist), Chain{0.f, 0.f, 0.f, 0}, nullptr};
-  for (int attempt = 0; attempt < 2; ++attempt) {
+  // at most: the chosen bins, every bin, then both again with the
+  // reference's S when the band check fails
+  for (int attempt = 0; attempt < 4; ++attempt) {
     const bool filt = last < SLOW_BINS - 1;
     // ---- C: exact p of the chosen elements, in index order
     uint32_t npos = 0, nzero = 0, lkey = 0;
@@ -2415,6 +2660,26 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
     const bool good =
         run_semantics<true>(P, u, E, V, p_lim, Lst, sh + 20, (LDS float*)wcnt, tok, len) &&
         !(filt && a.out_cap && len > E && a.out_cap > E);
+    if (good && approx) {
+      // plist holds the p (= e) unchanged: the slow path's semantics divide
+      // through the list's chain
+      if (wv == 0) {
+        const bool ok = band_certain_wave(ArrAcc<const GLB float*, const GLB uint32_t*>{
+                                              plist, ilist},
+                                          E, V, p_lim, P.min_p, P.K, P.top_p, u);
+        if (tid == 0) sh[9] = ok ? 1u : 0u;
+      }
+      __syncthreads();
+      const bool ok = sh[9] != 0;
+      __syncthreads();
+      if (!ok) {
+        // the reference's S, then the same bins again (chosen by count on a
+        // top-k row, whatever S)
+        S = exact_normaliser<DT>(row, mask_row, V, P.T, m, h.bitmap, h.pre, h.pen, true, smem);
+        approx = false;
+        continue;
+      }
+    }
     if (good) break;
     last = SLOW_BINS - 1;
     __syncthreads();
@@ -2491,7 +2756,8 @@ __device__ __forceinline__ uint32_t kth_largest_key(LDS const float* cval, uint3
 // ---------------------------------------------------------------------------
 enum : uint32_t {
   F_DONE = 0, F_S = 1, F_M = 2, F_TOTAL = 3, F_LAM = 4, F_PLIM = 5, F_L = 6, F_GREEDY = 7,
-  F_SCR = 8
+  F_SCR = 8,
+  F_BAND = 120  // band_certain_wave's verdict (wave 1 beside wave 0's semantics)
 };
 // LDS layout of the finalize (words): slots, candidate lists, keys, tables
 struct FinLds {
@@ -2608,13 +2874,15 @@ __device__ __forceinline__ void sort_keys(const FinLds& f, uint32_t n) {
 }
 
 // The candidate path under policy SY.  Returns 0 when the row is done, 1
-// when its candidates exceed what SY handles, 2 when it needs the slow path.
+// when its candidates exceed what SY handles, 2 when it needs the slow path,
+// 4 when a row sampled with S = 1 (approx) cannot be proven by the band
+// check (the reference's S is needed).
 template <class SY>
 __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, uint32_t b,
                                                    const RowP& P, float S, float m, float u,
                                                    uint32_t total, uint32_t lam,
                                                    const FinLds& f, uint32_t gather_cap,
-                                                   uint32_t keep_cap) {
+                                                   uint32_t keep_cap, bool approx) {
   LDS const u2v* lcand = (LDS const u2v*)((LDS uint32_t*)f.tl + a.lds_cand);
   const uint32_t id = SY::id();
   if (total > gather_cap) return 1;
@@ -2867,10 +3135,11 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
       });
     }
   } else {
-  // ---- top-k rows: the exact K-th largest candidate logit tightens the
-  // bound (every element below it has p <= plim of that bound)
+  // ---- top-k rows: the exact (K+1)-th largest candidate logit tightens
+  // the bound (every element below it has p <= plim of that bound; the
+  // entry past the K-th stays in the list for the band check)
   if (n0 > 2u * (uint32_t)P.K) {
-    const uint32_t tau = kth_largest_key<SY>(cval, n0, (uint32_t)P.K,
+    const uint32_t tau = kth_largest_key<SY>(cval, n0, (uint32_t)P.K + 1u,
                                              (LDS uint32_t*)f.keys, f.fm + F_SCR);
     lam_e = tau;
     plim_e = tau > 0x007fffffu ? prob_of(funkey(tau - 1), P.T, m, S) : 0.0f;
@@ -2896,9 +3165,9 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
       if (keep) f.keys[pos] = key;
       n += tot;
     }
-    // a tightened bound that keeps fewer than K (ties in p across it) falls
-    // back to the gather bound
-    if (!(topk && n < (uint32_t)P.K && lam_e != lam)) break;
+    // a tightened bound that keeps fewer than K + 1 (ties in p across it)
+    // falls back to the gather bound
+    if (!(topk && n < (uint32_t)P.K + 1u && lam_e != lam)) break;
     lam_e = lam;
     plim_e = plim;
   }
@@ -2913,20 +3182,38 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
     f.pidx[i] = (uint32_t)k;
   }
   SY::sync();
-  // ---- min-p / top-k / top-p / draw in wave 0
+  // ---- min-p / top-k / top-p / draw in wave 0 (and the band check of a
+  // row sampled with S = 1 in wave 1 beside it, or after a workgroup's
+  // semantics); outputs only once the result stands
   uint32_t res = 2;
   if (n <= 128) {
+    float p0 = 0.0f, p1 = 0.0f;
+    uint32_t i0 = 0, i1 = 0, tok = 0, len = 0;
+    bool good = false;
     if (threadIdx.x < WAVE) {
       const int lane = (int)threadIdx.x;
-      float p0 = (uint32_t)lane < n ? f.pp[lane] : 0.0f;
-      float p1 = (uint32_t)lane + 64 < n ? f.pp[64 + lane] : 0.0f;
-      const uint32_t i0 = (uint32_t)lane < n ? f.pidx[lane] : 0u;
-      const uint32_t i1 = (uint32_t)lane + 64 < n ? f.pidx[64 + lane] : 0u;
-      uint32_t tok = 0, len = 0;
+      p0 = (uint32_t)lane < n ? f.pp[lane] : 0.0f;
+      p1 = (uint32_t)lane + 64 < n ? f.pp[64 + lane] : 0.0f;
+      i0 = (uint32_t)lane < n ? f.pidx[lane] : 0u;
+      i1 = (uint32_t)lane + 64 < n ? f.pidx[64 + lane] : 0u;
       // f.keys is free once sorted into skeys and copied out
-      bool good = semantics_regs(P, u, n, a.V, plim_e, p0, p1, i0, i1, lane,
-                                 (LDS float*)f.keys, tok, len);
+      good = semantics_regs(P, u, n, a.V, plim_e, p0, p1, i0, i1, lane,
+                            (LDS float*)f.keys, tok, len);
       if (good && a.out_cap && len > n && a.out_cap > n) good = false;
+    } else if (approx && threadIdx.x < 2 * WAVE) {
+      const bool ok = band_certain_wave(KeyAcc{f.skeys}, n, a.V, plim_e, P.min_p, P.K,
+                                        P.top_p, u);
+      if (threadIdx.x == WAVE) f.fm[F_BAND] = ok ? 1u : 0u;
+    }
+    if (approx) SY::sync();
+    if (threadIdx.x < WAVE) {
+      const int lane = (int)threadIdx.x;
+      if (good && approx && f.fm[F_BAND] == 0) {
+        good = false;
+        res = 4;
+      } else {
+        res = good ? 0u : 2u;
+      }
       if (good) {
         const uint32_t ic = a.cut ? cut_id(len, n, i0, i1) : 0u;
         if (lane == 0) {
@@ -2945,7 +3232,6 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
           if (a.out_probs) G(a.out_probs)[ob + 64 + lane] = p1;
         }
       }
-      res = good ? 0u : 2u;
     }
   } else {
     List Ls{flat(f.pp), flat(f.pidx), Chain{0.f, 0.f, 0.f, 0}, (float*)f.pp};
@@ -2953,8 +3239,21 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
     bool good = run_semantics<false>(P, u, n, a.V, plim_e, Ls, f.fm + F_SCR,
                                      (LDS float*)f.keys, tok, len);
     if (good && a.out_cap && len > n && a.out_cap > n) good = false;
-    if (good) write_outputs(a, b, tok, len, Ls, m, S);
     res = good ? 0u : 2u;
+    if (good && approx) {
+      // the sorted keys are intact (the semantics divided pp in place)
+      if (threadIdx.x < WAVE) {
+        const bool ok = band_certain_wave(KeyAcc{f.skeys}, n, a.V, plim_e, P.min_p, P.K,
+                                          P.top_p, u);
+        if (threadIdx.x == 0) f.fm[F_BAND] = ok ? 1u : 0u;
+      }
+      SY::sync();
+      if (f.fm[F_BAND] == 0) {
+        good = false;
+        res = 4;
+      }
+    }
+    if (good) write_outputs(a, b, tok, len, Ls, m, S);
   }
   if (SY::N > WAVE) {
     if (threadIdx.x == 0) f.fm[F_DONE] = res;
@@ -2968,11 +3267,13 @@ __device__ __forceinline__ uint32_t candidate_path(const Args& a, const Ws& w, u
 // LDS (total <= LCAP), with the whole workgroup: one candidate per thread
 // for the gather and the filter, the rank sort split eight ways (each
 // thread compares one key with sixteen others), the semantics in wave 0
-// from registers.  Returns 0 when the row is done, 1 when it needs the
-// general path (more than 128 kept), 2 for the slow path.
+// from registers, and on a row sampled with S = 1 (approx) the band check
+// in wave 1 beside them.  Returns 0 when the row is done, 1 when it needs
+// the general path (more than 128 kept), 2 for the slow path, 4 when S = 1
+// cannot be proven (the reference's S is needed).
 __device__ __forceinline__ uint32_t candidate_fast(const Args& a, uint32_t b, const RowP& P,
                                                    float S, float m, float u, uint32_t total,
-                                                   uint32_t lam, const FinLds& f) {
+                                                   uint32_t lam, const FinLds& f, bool approx) {
   using SY = BlockSync;
   const uint32_t tid = threadIdx.x;
   LDS const u2v* lcand = (LDS const u2v*)((LDS uint32_t*)f.tl + a.lds_cand);
@@ -2993,16 +3294,19 @@ __device__ __forceinline__ uint32_t candidate_fast(const Args& a, uint32_t b, co
   const uint32_t n0 = both & 0xffffu;
   uint32_t n = both >> 16;
   float ptail = plim;  // every element not kept has p <= ptail
+  // the kept list reaches one entry past the K-th, which the band check
+  // compares with the K-th
+  const uint32_t K1 = topk ? umin((uint32_t)P.K + 1u, n0) : 0u;
   if (n <= 128 || !topk) {
     if (k0) f.keys[pos >> 16] = pkey(pv0, e.y);
   } else {
-    // more than 128 kept: the exact K-th largest tightens the bound
+    // more than 128 kept: the exact (K+1)-th largest tightens the bound
     if (g0) {
       cval[pos & 0xffffu] = v0;
       cidx[pos & 0xffffu] = e.y;
     }
     SY::sync();
-    const uint32_t tau = kth_largest_key<SY>(cval, n0, (uint32_t)P.K, (LDS uint32_t*)f.keys,
+    const uint32_t tau = kth_largest_key<SY>(cval, n0, K1, (LDS uint32_t*)f.keys,
                                              f.fm + F_SCR);
     uint32_t lam_e = tau;
     float plim_e = tau > 0x007fffffu ? prob_of(funkey(tau - 1), P.T, m, S) : 0.0f;
@@ -3021,9 +3325,9 @@ __device__ __forceinline__ uint32_t candidate_fast(const Args& a, uint32_t b, co
       }
       const uint32_t p2 = SY::excl_scan(keep, f.red, n);
       if (keep) f.keys[p2] = key;
-      // a tightened bound that keeps fewer than K (ties in p across it)
+      // a tightened bound that keeps fewer than K + 1 (ties in p across it)
       // falls back to the gather bound
-      if (!(n < (uint32_t)P.K && lam_e != lam)) break;
+      if (!(n < K1 && lam_e != lam)) break;
       lam_e = lam;
       plim_e = plim;
     }
@@ -3069,9 +3373,13 @@ __device__ __forceinline__ uint32_t candidate_fast(const Args& a, uint32_t b, co
                           len);
     if (good && a.out_cap && len > n && a.out_cap > n) good = false;
     if (lane == 0) f.fm[F_DONE] = good ? 0u : 2u;
+  } else if (approx && tid < 2 * WAVE) {
+    const bool ok = band_certain_wave(KeyAcc{f.skeys}, n, a.V, ptail, P.min_p, P.K, P.top_p, u);
+    if (tid == WAVE) f.fm[F_BAND] = ok ? 1u : 0u;
   }
   SY::sync();
-  const uint32_t res = f.fm[F_DONE];
+  uint32_t res = f.fm[F_DONE];
+  if (res == 0 && approx && f.fm[F_BAND] == 0) res = 4;
   if (tid < WAVE && res == 0) {
     const int lane = (int)tid;
     const uint32_t ic = a.cut ? cut_id(len, n, i0, i1) : 0u;
@@ -3219,18 +3527,23 @@ __device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_
   }
   __syncthreads();
   path = f.fm[F_DONE];
+  // S = 1 stands in for the reference's S on a row that top-k renormalises
+  const bool approx = topk && L != NEG_INF;
   if (path == 3) {
-    path = candidate_fast(a, b, P, S, m, u, f.fm[F_TOTAL], f.fm[F_LAM], f);
+    path = candidate_fast(a, b, P, S, m, u, f.fm[F_TOTAL], f.fm[F_LAM], f, approx);
     if (path == 0) return;
   }
   if (path == 1) {
     const uint32_t total = f.fm[F_TOTAL], lam = f.fm[F_LAM];
     __syncthreads();
-    path = candidate_path<BlockSync>(a, w, b, P, S, m, u, total, lam, f, EMPTY, SORT_CAP);
+    path = candidate_path<BlockSync>(a, w, b, P, S, m, u, total, lam, f, EMPTY, SORT_CAP,
+                                     approx);
     if (path == 0) return;
   }
   __syncthreads();
-  slow_row<DT>(a, w, b, P, S, m, L, smem);
+  // path 4: the band check could not prove S = 1; the slow path computes
+  // the reference's S first
+  slow_row<DT>(a, w, b, P, S, m, L, smem, approx && path != 4, approx && path == 4);
 }
 
 // ---------------------------------------------------------------------------

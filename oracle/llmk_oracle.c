@@ -312,6 +312,235 @@ static void semantics(plist* Lp, const llmk_oracle_params* prm, float u,
   *Lp = L;
 }
 
+/* ------------------------------------------------------------------------ */
+/* The rounding band of S = 1 on rows that top-k renormalises                 */
+/* ------------------------------------------------------------------------ */
+
+/* On a row that top-k renormalises the reference computes p_i = fl(e_i / S)
+ * with S its sequential sum over the whole row (sampler.rs:66-71), then
+ * renormalises the kept entries (:83-88, and min-p's cut, which comes
+ * first).  S cancels in exact arithmetic, so S = 1 gives the same decisions
+ * (min-p cut, top-k set and order, top-p cut, drawn token) unless one of
+ * them lies within the rounding of the f32 arithmetic.  band_certain proves,
+ * from the e_i of the sorted list alone, that every decision is the same
+ * for every S the reference can hold: with p_i known only to relative R
+ * (R = 2^-24 for fl(e_i / S)), each sequential sum rounds by at most half an
+ * ulp of its running value (bounded by u times the value where the scale is
+ * S's, by the binade's half ulp once the values are normalised), each
+ * renormalisation divides by a sum known to relative sigma and rounds again
+ * (R' = (R + sigma + u)(1 + 2^-10), the factor covering second-order
+ * terms), and a decision is certain when its exact value (a sum of the e_i
+ * in double) lies outside the band of its bound.  Entries whose order could
+ * differ (fl(e_a / S) == fl(e_b / S) ties ordered by index: e_a and e_b
+ * within 2^-20 relative with their indices inverted; equal e keep their
+ * index order under any S) and entries below 2^-100 (p could be
+ * subnormal) are uncertain too.
+ *
+ * The doubles are summed in the order a 64-lane wave computes them on the
+ * device (wave_prefix64: a DPP scan within 64 entries, then the chunk's
+ * carry), so both sides see the same bits.
+ *
+ * e: the list's values (p with S = 1) in (p desc, idx asc) order, E of them
+ * exact; every entry past E is <= ptail; full: the row's length. */
+#define BAND_U 0x1p-24
+#define BAND_F (1.0 + 0x1p-10)
+#define BAND_SL 0x1p-36
+#define BAND_CLOSE (1.0 + 0x1p-20)
+
+/* half an ulp of a float of magnitude x in (0, 2): 2^(floor(log2 x) - 24) */
+static double band_hu(double x) {
+  if (!(x > 0.0)) return 0.0;
+  int ex;
+  (void)frexp(x, &ex);
+  return ldexp(1.0, ex - 25);
+}
+
+/* inclusive prefix of 64 values as the device's wave computes it: steps of
+ * row_shr 1, 2, 4, 8 within rows of 16 lanes, then row 0's total added to
+ * row 1 and row 2's to row 3 (row_bcast 15), then row 1's new total to rows
+ * 2 and 3 (row_bcast 31) */
+static void dpp_scan64(double* y) {
+  for (int d = 1; d < 16; d <<= 1) {
+    double z[64];
+    for (int j = 0; j < 64; ++j) z[j] = (j & 15) >= d ? y[j] + y[j - d] : y[j];
+    memcpy(y, z, sizeof z);
+  }
+  const double t15 = y[15], t47 = y[47];
+  for (int j = 16; j < 32; ++j) y[j] = y[j] + t15;
+  for (int j = 48; j < 64; ++j) y[j] = y[j] + t47;
+  const double t31 = y[31];
+  for (int j = 32; j < 64; ++j) y[j] = y[j] + t31;
+}
+
+/* inclusive prefix of x[0..n) in place: chunks of 64, each scanned as a
+ * wave does, plus the carry of the chunks before it */
+static void wave_prefix64(double* x, uint32_t n) {
+  double carry = 0.0;
+  for (uint32_t c0 = 0; c0 < n; c0 += 64) {
+    double y[64];
+    for (uint32_t j = 0; j < 64; ++j) y[j] = c0 + j < n ? x[c0 + j] : 0.0;
+    dpp_scan64(y);
+    for (uint32_t j = 0; j < 64; ++j) y[j] = y[j] + carry;
+    carry = y[63];
+    for (uint32_t j = 0; j < 64 && c0 + j < n; ++j) x[c0 + j] = y[j];
+  }
+}
+
+/* sigma of a renormalisation over [0, n): the reference's sequential sum of
+ * p_i known to relative R, against the exact sum P[n-1] (P: prefix of e) */
+static double band_sigma(const double* P, uint32_t n, double R, double* work) {
+  for (uint32_t j = 0; j < n; ++j) work[j] = j >= 1 ? P[j] : 0.0;
+  wave_prefix64(work, n);
+  return R + BAND_U * (1.0 + R) * BAND_F * (work[n - 1] / P[n - 1]);
+}
+
+/* the first j < n whose cumulative may reach thr (C + B >= thr); sets
+ * *certain when the reference's cumulative surely reaches it there and
+ * surely not before; returns n when none may.  C_j = P[j] (1 / P[n-1]),
+ * B_j = R C_j + sum_{1 <= i <= j} hu(C_i (1 + R) F) + SL C_j. */
+static uint32_t band_find(const double* P, uint32_t n, double R, double thr,
+                          double* B, int* certain) {
+  const double rt = 1.0 / P[n - 1];
+  for (uint32_t j = 0; j < n; ++j)
+    B[j] = j >= 1 ? band_hu((P[j] * rt) * (1.0 + R) * BAND_F) : 0.0;
+  wave_prefix64(B, n);
+  *certain = 1;
+  for (uint32_t j = 0; j < n; ++j) {
+    const double C = P[j] * rt;
+    const double b = R * C + B[j] + BAND_SL * C;
+    B[j] = b;
+    if (C + b >= thr) {
+      *certain = (C - b >= thr);
+      return j;
+    }
+  }
+  return n;
+}
+
+static int band_certain(const float* e, const uint32_t* idx, uint32_t E,
+                        uint32_t full, float ptail,
+                        const llmk_oracle_params* prm, float u) {
+  const int32_t K = prm->top_k;
+  uint32_t len = full;
+  double R = BAND_U;
+  int normalised = 0;
+  /* entries whose p = e / S could be subnormal */
+  const uint32_t lim = (K > 0 && (uint32_t)K + 1u < E) ? (uint32_t)K + 1u : E;
+  for (uint32_t j = 0; j < lim; ++j)
+    if (e[j] > 0.0f && e[j] < 0x1p-100f) return 0;
+  double* P = (double*)malloc(sizeof(double) * (E ? E : 1));
+  double* W = (double*)malloc(sizeof(double) * (E ? E : 1));
+  int ok = 0;
+  /* min-p: kept iff fl(e/S) >= fl(min_p * fl(1/S)) (e_0 = 1, the maximum);
+   * certain outside min_p (1 -+ 2^-21) */
+  if (prm->min_p > 0.0f) {
+    if (prm->min_p < 0x1p-100f || E == 0) goto out;
+    const double hi = (double)prm->min_p * (1.0 + 0x1p-21);
+    const double lo = (double)prm->min_p * (1.0 - 0x1p-21);
+    uint32_t cut = 0xffffffffu;
+    const uint32_t n = E < len ? E : len;
+    for (uint32_t j = 0; j < n; ++j)
+      if ((double)e[j] < hi) {
+        cut = j;
+        break;
+      }
+    if (cut != 0xffffffffu) {
+      if ((double)e[cut] >= lo) goto out;
+    } else if (E < len) {
+      if ((double)ptail >= lo) goto out;
+      cut = E;
+    }
+    if (cut != 0xffffffffu && cut < len) {
+      len = cut;
+      if (len == 0) goto out;
+      for (uint32_t j = 0; j < len; ++j) P[j] = (double)e[j];
+      wave_prefix64(P, len);
+      if (!(P[len - 1] > 0.0)) goto out;
+      const double sg = band_sigma(P, len, R, W);
+      R = (R + sg + BAND_U) * BAND_F;
+      normalised = 1;
+    }
+  }
+  /* top-k: the first K in (p desc, idx asc) order; no pair whose order could
+   * change, across the boundary included (an unknown entry K close to the
+   * last kept one could be either side of it) */
+  if (K > 0 && (uint32_t)K < len) {
+    if ((uint32_t)K > E) goto out;
+    if ((uint32_t)K == E && (double)e[K - 1] < (double)ptail * BAND_CLOSE) goto out;
+    const uint32_t np = (uint32_t)K < E ? (uint32_t)K + 1u : (uint32_t)K;
+    for (uint32_t j = 0; j + 1 < np; ++j)
+      if ((double)e[j] < (double)e[j + 1] * BAND_CLOSE && idx[j] > idx[j + 1]) goto out;
+    len = (uint32_t)K;
+    for (uint32_t j = 0; j < len; ++j) P[j] = (double)e[j];
+    wave_prefix64(P, len);
+    if (!(P[len - 1] > 0.0)) goto out;
+    const double sg = band_sigma(P, len, R, W);
+    R = (R + sg + BAND_U) * BAND_F;
+    normalised = 1;
+  } else {
+    const uint32_t n = E < len ? E : len;
+    for (uint32_t j = 0; j + 1 < n; ++j)
+      if ((double)e[j] < (double)e[j + 1] * BAND_CLOSE && idx[j] > idx[j + 1]) goto out;
+  }
+  if (!normalised || len > E) goto out;
+  /* top-p: the first cumulative >= top_p, then the renormalisation by that
+   * same cumulative */
+  if (prm->top_p < 1.0f) {
+    int cert;
+    const uint32_t j = band_find(P, len, R, (double)prm->top_p, W, &cert);
+    if (!cert) goto out;
+    const uint32_t cut = j < len ? j + 1 : len;
+    const double sp = W[cut - 1] / (P[cut - 1] * (1.0 / P[len - 1]));
+    R = (R + sp + BAND_U) * BAND_F;
+    len = cut;
+  }
+  /* the draw: the first cumulative >= u, else the last */
+  {
+    int cert;
+    (void)band_find(P, len, R, (double)u, W, &cert);
+    if (!cert) goto out;
+  }
+  ok = 1;
+out:
+  free(P);
+  free(W);
+  return ok;
+}
+
+/* The first n entries of a row's sorted list with S = 1: e = exp_ref(l - m)
+ * of the processed logits (mirror), in (e desc, idx asc) order. */
+int llmk_oracle_sorted_e(const float* logits, uint32_t V, const llmk_oracle_params* prm,
+                         const uint32_t* hist, uint32_t H, const uint32_t* mask,
+                         uint32_t n, float* e_out, uint32_t* idx_out) {
+  if (V == 0) return -1;
+  float* l = (float*)malloc(sizeof(float) * V);
+  int rc = llmk_oracle_process_logits(LLMK_ORACLE_MIRROR, logits, V, prm, hist, H, mask, l);
+  if (rc != 0) {
+    free(l);
+    return rc;
+  }
+  apply_temperature(l, V, prm->temperature);
+  float m = -INFINITY;
+  for (uint32_t i = 0; i < V; ++i) m = fmaxf(m, l[i]);
+  uint64_t* keys = (uint64_t*)malloc(sizeof(uint64_t) * V);
+  for (uint32_t i = 0; i < V; ++i)
+    keys[i] = pkey(l[i] == -INFINITY ? 0.0f : llmk_oracle_exp_ref(l[i] - m), i);
+  sort_u64(keys, V);
+  for (uint32_t j = 0; j < n && j < V; ++j) {
+    idx_out[j] = (uint32_t)(keys[j] & 0xffffffffu);
+    e_out[j] = u2f(~(uint32_t)(keys[j] >> 32));
+  }
+  free(keys);
+  free(l);
+  return 0;
+}
+
+int llmk_oracle_band_certain(const float* e_sorted, const uint32_t* idx, uint32_t E,
+                             uint32_t full, float ptail,
+                             const llmk_oracle_params* prm, float u) {
+  return band_certain(e_sorted, idx, E, full, ptail, prm, u);
+}
+
 /* The penalised, masked logits before the greedy check (sampler.rs:34-37
  * plus the extensions in their order); NaN becomes -inf in mirror mode. */
 int llmk_oracle_process_logits(int mode, const float* logits, uint32_t V,
@@ -377,9 +606,13 @@ int llmk_oracle_sample_row(int mode, const float* logits, uint32_t V,
   /* Softmax, :56-71.  The exp is glibc's expf in both modes (exp_ref
    * restates it bit for bit).  S is the sequential f32 sum in index order
    * (:66), except in mirror mode on rows where top-k renormalises
-   * (0 < top_k < V, :80-89): there every probability is divided by the
-   * top-k sum before any step reads it, S cancels in exact arithmetic, and
-   * mirror takes S = 1 (the engine computes no normaliser for such rows). */
+   * (0 < top_k < V, :80-89): there every probability is divided by a
+   * renormalising sum before any step reads it and S cancels in exact
+   * arithmetic, so mirror first takes S = 1 (e itself), as the engine does,
+   * and keeps that result when band_certain proves that every decision is
+   * the reference's for any S; otherwise it computes S and the reference's
+   * arithmetic, as the engine then does too.  Tokens, kept counts and kept
+   * ids are the reference's on every row either way. */
   float m = -INFINITY;
   for (uint32_t i = 0; i < V; ++i) m = fmaxf(m, l[i]);
   float* e = (float*)malloc(sizeof(float) * V);
@@ -390,30 +623,29 @@ int llmk_oracle_sample_row(int mode, const float* logits, uint32_t V,
                                           : expf(l[i] - m);
   }
   const int topk_on = prm->top_k > 0 && (uint32_t)prm->top_k < V;
-  float S;
-  if (mode == LLMK_ORACLE_MIRROR && topk_on) S = 1.0f;
-  else {
-    S = 0.0f;
-    for (uint32_t i = 0; i < V; ++i) S += e[i];
-  }
-  if (S > 0.0f)
-    for (uint32_t i = 0; i < V; ++i) e[i] = e[i] / S;
-
-  /* Sort (p desc, idx asc), :77 */
   uint64_t* keys = (uint64_t*)malloc(sizeof(uint64_t) * V);
-  for (uint32_t i = 0; i < V; ++i) keys[i] = pkey(e[i], i);
-  sort_u64(keys, V);
   plist L;
-  L.n = V;
   L.p = (float*)malloc(sizeof(float) * V);
   L.idx = (uint32_t*)malloc(sizeof(uint32_t) * V);
-  for (uint32_t j = 0; j < V; ++j) {
-    L.idx[j] = (uint32_t)(keys[j] & 0xffffffffu);
-    L.p[j] = u2f(~(uint32_t)(keys[j] >> 32));
+  for (int pass = (mode == LLMK_ORACLE_MIRROR && topk_on) ? 0 : 1; pass < 2; ++pass) {
+    float S = 1.0f;
+    if (pass == 1) {
+      S = 0.0f;
+      for (uint32_t i = 0; i < V; ++i) S += e[i];
+    }
+    /* Sort (p desc, idx asc), :77 */
+    for (uint32_t i = 0; i < V; ++i) keys[i] = pkey(S > 0.0f ? e[i] / S : e[i], i);
+    sort_u64(keys, V);
+    L.n = V;
+    for (uint32_t j = 0; j < V; ++j) {
+      L.idx[j] = (uint32_t)(keys[j] & 0xffffffffu);
+      L.p[j] = u2f(~(uint32_t)(keys[j] >> 32));
+    }
+    if (pass == 0 && !band_certain(L.p, L.idx, V, V, 0.0f, prm, u)) continue;
+    semantics(&L, prm, u, out_token, out_ids, out_probs, out_cap, out_count);
+    break;
   }
   free(keys);
-
-  semantics(&L, prm, u, out_token, out_ids, out_probs, out_cap, out_count);
   free(L.p);
   free(L.idx);
   free(e);

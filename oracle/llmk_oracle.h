@@ -19,10 +19,14 @@
  *                        differs from REF in one place: on rows where top-k
  *                        renormalises (0 < top_k < V, sampler.rs:80-89) the
  *                        softmax normaliser S, which cancels there in exact
- *                        arithmetic, is taken as 1 instead of the sequential
- *                        sum (sampler.rs:66).  Every other row is computed
- *                        exactly as REF (NaN logits aside: mirror reads them
- *                        as -inf).
+ *                        arithmetic, is first taken as 1, and that result is
+ *                        kept when llmk_oracle_band_certain proves each of
+ *                        its decisions to be REF's; otherwise the row is
+ *                        computed as REF.  Tokens, kept counts and kept ids
+ *                        are therefore REF's on every row; probabilities
+ *                        differ only in their last bits on rows kept at
+ *                        S = 1.  Every other row is computed exactly as REF
+ *                        (NaN logits aside: mirror reads them as -inf).
  *
  * Both modes: ties in probability are ordered by index ascending (the
  * reference's sort_unstable_by leaves tie order unspecified, sampler.rs:77),
@@ -80,6 +84,20 @@ int llmk_oracle_process_logits(int mode, const float* logits, uint32_t V,
                                const uint32_t* hist, uint32_t H,
                                const uint32_t* mask, float* out);
 
+/* 1 when the decisions of llmk_oracle_semantics on a list of e = p with
+ * S = 1 (min-p cut, top-k set and order, top-p cut, drawn token) are the
+ * reference's for every normaliser S it can hold (p = fl(e / S), then its
+ * renormalisations), 0 when one lies in the rounding band.  e_sorted[0..E)
+ * in (p desc, idx asc) order, exact; entries past E (of full) are <= ptail. */
+int llmk_oracle_band_certain(const float* e_sorted, const uint32_t* idx, uint32_t E,
+                             uint32_t full, float ptail,
+                             const llmk_oracle_params* prm, float u);
+/* The first n entries (n <= V) of a row's list with S = 1 (e = exp_ref of
+ * the processed logits over T, less their maximum) in (e desc, idx asc)
+ * order.  Returns 0, -1, -2 as llmk_oracle_sample_row. */
+int llmk_oracle_sorted_e(const float* logits, uint32_t V, const llmk_oracle_params* prm,
+                         const uint32_t* hist, uint32_t H, const uint32_t* mask,
+                         uint32_t n, float* e_out, uint32_t* idx_out);
 /* The steps after the sort — min-p, top-k, top-p, draw — on a list already
  * in (p desc, idx asc) order (p_sorted[n], idx[n]).  Outputs as above. */
 int llmk_oracle_semantics(const float* p_sorted, const uint32_t* idx, uint32_t n,

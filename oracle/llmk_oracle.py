@@ -38,6 +38,10 @@ def load():
     lib.llmk_oracle_sample_row.restype = ctypes.c_int
     lib.llmk_oracle_process_logits.argtypes = [ctypes.c_int, P, u32, P, P, u32, P, P]
     lib.llmk_oracle_process_logits.restype = ctypes.c_int
+    lib.llmk_oracle_sorted_e.argtypes = [P, u32, P, P, u32, P, u32, P, P]
+    lib.llmk_oracle_sorted_e.restype = ctypes.c_int
+    lib.llmk_oracle_band_certain.argtypes = [P, P, u32, u32, f32, P, f32]
+    lib.llmk_oracle_band_certain.restype = ctypes.c_int
     lib.llmk_oracle_semantics.argtypes = [P, P, u32, P, f32, P, P, P, u32, P]
     lib.llmk_oracle_semantics.restype = ctypes.c_int
     lib.llmk_oracle_exp_ref.argtypes = [f32]
@@ -159,6 +163,33 @@ def semantics(p_sorted, idx, prm, u=0.0, out_cap=None):
                                    _p(ids), _p(probs), cap, ctypes.byref(cnt))
     k = min(cnt.value, cap)
     return rc, tok.value, ids[:k], probs[:k], cnt.value
+
+
+def sorted_e(logits, prm, hist=(), mask=None, n=None):
+    """The row's first n entries with S = 1, (e, idx) in (e desc, idx asc)
+    order (llmk_oracle_sorted_e)."""
+    l = _f32p(logits)
+    n = l.size if n is None else min(n, l.size)
+    h = np.ascontiguousarray(hist, dtype=np.uint32)
+    m = None if mask is None else np.ascontiguousarray(mask, dtype=np.uint32)
+    e = np.zeros(n, np.float32)
+    ix = np.zeros(n, np.uint32)
+    rc = load().llmk_oracle_sorted_e(_p(l), l.size, ctypes.byref(prm), _p(h) if h.size else None,
+                                     h.size, _p(m), n, _p(e), _p(ix))
+    if rc != 0:
+        raise ValueError(f"oracle rc {rc}")
+    return e, ix
+
+
+def band_certain(e_sorted, idx, prm, u, E=None, full=None, ptail=0.0):
+    """llmk_oracle_band_certain: True when S = 1's decisions on the sorted
+    list are the reference's for every normaliser S."""
+    e = _f32p(e_sorted)
+    ix = np.ascontiguousarray(idx, dtype=np.uint32)
+    E = e.size if E is None else E
+    full = e.size if full is None else full
+    return bool(load().llmk_oracle_band_certain(_p(e), _p(ix), E, full, float(ptail),
+                                                ctypes.byref(prm), float(u)))
 
 
 def process_logits(mode, logits, prm, hist=(), mask=None):

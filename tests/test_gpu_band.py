@@ -1,0 +1,85 @@
+"""GPU: rows that top-k renormalises are sampled as the reference samples
+them for every uniform and top_p, through the C ABI.
+
+The engine samples such a row with S = 1 (p = e) and keeps that result only
+when its band check proves each decision to be the reference's; otherwise it
+computes the reference's own normaliser S (llm-core/src/sampler.rs:66) and
+samples the row again in the reference's arithmetic.  The uniforms and top_p
+values here are chosen on the CPU between the reference's cumulative and
+that of S = 1 for one entry (tests/band_util.py), where S = 1 alone draws
+another token or keeps another count.  Tokens, kept counts and kept ids
+must be the reference oracle's, and every output the mirror oracle's bit
+for bit.  Marked gpu."""
+import numpy as np
+import pytest
+
+import llmk
+from llmk import synth
+from oracle import llmk_oracle as O
+
+import band_util as BU
+from gpu_util import assert_bit_exact, run_gpu
+from test_gpu_parity import assert_matches_ref
+
+pytestmark = pytest.mark.gpu
+
+CAP = 256
+
+
+@pytest.fixture(scope="module")
+def sampler():
+    s = llmk.HipSampler(max_batch=64, max_vocab=256000)
+    yield s
+    s.close()
+
+
+def _check(sampler, w, label):
+    gpu = run_gpu(sampler, w, CAP)
+    assert_bit_exact(w, gpu, O.sample_workload(O.MIRROR, w, out_cap=CAP, nthreads=16), CAP, label)
+    assert_matches_ref(w, gpu, O.sample_workload(O.REF, w, out_cap=CAP, nthreads=16), CAP, label)
+    assert sampler.status() == 0
+
+
+@pytest.mark.parametrize("name,B", [("C3", 24), ("C5", 12)])
+def test_uniforms_where_s1_draws_another_token(sampler, name, B):
+    w = synth.make(name, B=B)
+    hit = 0
+    for r in range(w.B):
+        u = BU.divergent_uniform(w, r, cap=CAP)
+        if u is not None:
+            w.uniforms[r] = np.float32(u)
+            hit += 1
+    print(f"[case] {name} B={w.B}: {hit} rows with a divergent uniform", flush=True)
+    assert hit >= (6 if name == "C3" else 2)
+    _check(sampler, w, f"{name} divergent uniforms")
+
+
+def test_top_p_where_s1_cuts_elsewhere(sampler):
+    w = synth.make("C3", B=24)
+    hit = 0
+    for r in range(w.B):
+        t = BU.divergent_top_p(w, r, cap=CAP)
+        if t is not None:
+            w.top_p[r] = np.float32(t)
+            hit += 1
+    print(f"[case] C3 B={w.B}: {hit} rows with a divergent top_p", flush=True)
+    assert hit >= 4
+    _check(sampler, w, "C3 divergent top_p")
+
+
+def test_k_above_the_fast_path(sampler):
+    """top-k above the candidate path's reach (K > 1024) goes through the
+    slow path, whose band check reads the sorted list in global memory."""
+    w = synth.make("C3", B=8)
+    w.top_k[:] = np.array([1500, 3000, 1100, 2000, 1500, 5000, 1025, 4096], np.int32)
+    w.top_p[:] = np.float32(0.999)
+    for r in range(0, w.B, 2):
+        u = BU.divergent_uniform(w, r, cap=8192)
+        if u is not None:
+            w.uniforms[r] = np.float32(u)
+    print("[case] C3 B=8, top-k 1025..5000", flush=True)
+    gpu = run_gpu(sampler, w, 64)
+    assert_bit_exact(w, gpu, O.sample_workload(O.MIRROR, w, out_cap=64, nthreads=16), 64,
+                     "large K")
+    assert_matches_ref(w, gpu, O.sample_workload(O.REF, w, out_cap=64, nthreads=16), 64,
+                       "large K")
