@@ -3402,21 +3402,168 @@ __device__ __forceinline__ uint32_t candidate_fast(const Args& a, uint32_t b, co
   return res;
 }
 
+// ---------------------------------------------------------------------------
+// The kernel's arguments for a call of its own
+// ---------------------------------------------------------------------------
+// A rare path made a call of its own, so that its registers are allocated
+// apart from the stream path's (inlined together, they spilled), reads the
+// kernel's arguments from the copy in g_kctx, which the kernel writes
+// before the call (passed by reference, they would be copied to scratch).
+struct KCtx {
+  Args a;
+  Ws w;
+};
+__shared__ KCtx g_kctx;
+// stream_kernel's parameters lie in the kernel-argument segment in order,
+// each at its natural alignment: a at 0, w next, as in KCtx.
+constexpr size_t kWsOffset = (sizeof(Args) + alignof(Ws) - 1) / alignof(Ws) * alignof(Ws);
+static_assert(offsetof(KCtx, w) == kWsOffset, "KCtx mirrors the kernel's parameters");
+// Copies the kernel's parameters into g_kctx, a word a thread from the
+// kernel-argument segment (copying the by-value parameters instead would
+// keep every field of them in registers from the kernel's start).  In a
+// kernel only; every thread, a barrier after it.
+__device__ __forceinline__ void kctx_fill() {
+  typedef const __attribute__((address_space(4))) uint32_t KWord;
+  KWord* k = (KWord*)__builtin_amdgcn_kernarg_segment_ptr();
+  LDS uint32_t* d = (LDS uint32_t*)&g_kctx;
+  for (uint32_t i = threadIdx.x; i < (uint32_t)(sizeof(KCtx) / 4); i += NT) d[i] = k[i];
+}
+// The arguments back from g_kctx into scalar registers: every word is
+// the same in all lanes, which a read of the first lane tells the compiler
+// (loaded as they are, each would take a vector register).
+__device__ __forceinline__ KCtx kctx_load() {
+  constexpr uint32_t N = (uint32_t)(sizeof(KCtx) / 4);
+  uint32_t wd[N];
+#pragma unroll
+  for (uint32_t i = 0; i < N; ++i)
+    wd[i] = (uint32_t)__builtin_amdgcn_readfirstlane((int)((LDS const uint32_t*)&g_kctx)[i]);
+  KCtx c;
+  __builtin_memcpy(&c, wd, sizeof(KCtx));
+  return c;
+}
+
+// The segment table (counts, thresholds, flags of the row's segments), the
+// bound plim, then the candidate path: 0 when the row is done, 2 for the
+// slow path, 4 when approx (S = 1) could not be proven.  Every thread.
+template <int DT>
+__device__ __forceinline__ uint32_t candidate_paths(const Args& a, const Ws& w, uint32_t b,
+                                                    const RowP& P, float S, float m, float L,
+                                                    float u, u4v seg_own, bool approx,
+                                                    LDS uint32_t* smem) {
+  const uint32_t tid = threadIdx.x;
+  const int lane = (int)(tid & 63), wv = (int)(tid >> 6);
+  const FinLds f = fin_carve(smem);
+  uint32_t path = 2;  // 0 done, 1 workgroup candidate path, 2 slow path, 3 fast path
+  if (wv == 0) {
+    // ---- segment table: counts, thresholds, flags
+    uint32_t cnt = 0, beta = 0, flg = 0;
+    if (a.G == 1) {
+      if (lane == 0) {
+        cnt = seg_own.x < CAND_CAP ? seg_own.x : CAND_CAP;
+        beta = seg_own.y;
+        flg = seg_own.z;
+      }
+    } else if ((uint32_t)lane < a.G) {
+      const u4v sm = G(w.seg_meta)[row_seg_to_wg(a, b, (uint32_t)lane)];
+      cnt = sm.x < CAND_CAP ? sm.x : CAND_CAP;
+      beta = sm.y;
+      flg = sm.z;
+    }
+    const uint32_t lam = wave_max_u32(beta << BIN_SHIFT);
+    const bool ovf = __ballot((flg & FLAG_OVERFLOW) != 0) != 0;
+    const uint32_t off_incl = wave_incl_scan(cnt);
+    const uint32_t total = bcast63u(off_incl);
+    if ((uint32_t)lane <= a.G) f.soff[lane] = off_incl - cnt;  // lane G: the total
+    WaveSync::sync();
+    // the bound on p of every element outside the candidate buffers, once
+    // (wave 0) rather than in every thread of the candidate path
+    const float plim = lam > 0x007fffffu ? prob_of(funkey(lam - 1), P.T, m, S) : 0.0f;
+    if (lane == 0) {
+      f.fm[F_S] = __float_as_uint(S);
+      f.fm[F_M] = __float_as_uint(m);
+      f.fm[F_L] = __float_as_uint(L);
+      f.fm[F_PLIM] = __float_as_uint(plim);
+      f.fm[F_TOTAL] = total;
+      f.fm[F_LAM] = lam;
+    }
+    if (!(L == NEG_INF || P.Kc == 0 || ovf))
+      path = (a.G == 1 && total <= LCAP) ? 3u : 1u;
+    if (lane == 0) f.fm[F_DONE] = path;
+  }
+  __syncthreads();
+  path = f.fm[F_DONE];
+  if (path == 3) {
+    path = candidate_fast(a, b, P, S, m, u, f.fm[F_TOTAL], f.fm[F_LAM], f, approx);
+    if (path == 0) return 0;
+  }
+  if (path == 1) {
+    const uint32_t total = f.fm[F_TOTAL], lam = f.fm[F_LAM];
+    __syncthreads();
+    path = candidate_path<BlockSync>(a, w, b, P, S, m, u, total, lam, f, EMPTY, SORT_CAP,
+                                     approx);
+    if (path == 0) return 0;
+  }
+  __syncthreads();
+  return path;
+}
+
+// The rows the candidate path did not finish (path: 2, the slow path; 4, a
+// row that top-k renormalises whose band check failed).  For path 4 the
+// reference's S (exact_normaliser, over the row's history tables, built
+// again: the candidate path has overwritten a single-segment row's own),
+// then the candidate path again in the reference's arithmetic, else the
+// slow path.  A call of its own (rare), its registers allocated apart from
+// the stream path's; it reads the kernel's arguments from g_kctx, which the
+// caller writes first.
+template <int DT>
+__device__ __noinline__ void finalize_rare(uint32_t b, RowP P, float S, float m, float L,
+                                           float u, u4v seg_own, bool approx, uint32_t path) {
+  extern __shared__ __align__(16) uint32_t smem[];
+  const KCtx c = kctx_load();
+  const Args& a = c.a;
+  const Ws& w = c.w;
+  const uint32_t tid = threadIdx.x;
+  LDS uint32_t* sm = (LDS uint32_t*)smem;
+  if (path != 4) {
+    slow_row<DT>(a, w, b, P, S, m, L, sm, approx, false);
+    return;
+  }
+  LDS uint32_t* sc = sm;  // below the tables in both layouts
+  const void* row = (const char*)a.logits +
+                    (uint64_t)b * a.stride * ((DT & 3) == LLMK_F32 ? 4u : 2u);
+  // a single-segment row's tables where its stream phase had them (below
+  // its kept partials and candidates, which the candidate path reads again);
+  // a row of several segments in the slow path's layout
+  Hist h;
+  const uint32_t nwords = a.G == 1 ? a.ntiles * 32 : (a.V + 31) / 32;
+  hist_carve(h, a.G == 1 ? sm + 64 + M_NMISC + NBINS + 64 : sm + 128 + 256 + NW * 256 + SLOW_BINS,
+             nwords);
+  h.lo = 0;
+  if (tid == 0) sc[64] = 0;
+  build_history<DT>(a, P, b, row, 0, a.V, nwords, h, sc + 128, &sc[64]);
+  S = exact_normaliser<DT>(row, a.mask ? a.mask + (uint64_t)b * a.mask_words : nullptr, a.V,
+                           P.T, m, h.bitmap, h.pre, h.pen, true, sc);
+  __syncthreads();
+  path = candidate_paths<DT>(a, w, b, P, S, m, L, u, seg_own, false, sm);
+  if (path != 0) slow_row<DT>(a, w, b, P, S, m, L, sm, false, false);
+}
+
 // seg_own: for a single-segment row, this workgroup's (count, beta, flags);
 // u: the row's uniform (loaded with the parameters, so that no global load
 // is outstanding at the finalize's barriers).
 //
 // The normaliser S: 1 on a row that top-k renormalises (0 < top_k < V,
 // sampler.rs:80-89: every probability is divided by the top-k sum before
-// any step reads it, so S cancels and none is computed), 0 for a row whose
-// logits are all -inf, else the reference's own sequential f32 sum in index
-// order (exact_normaliser; sampler.rs:66).  A single-segment row still holds
-// the whole row's history tables from its stream phase; a row of several
+// any step reads it, so S cancels in exact arithmetic) until its band check
+// fails, then the reference's own; 0 for a row whose logits are
+// all -inf; else the reference's own sequential f32 sum in index order
+// (exact_normaliser; sampler.rs:66).  A single-segment row still holds the
+// whole row's history tables from its stream phase; a row of several
 // segments rebuilds them first.
 template <int DT>
 __device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_t b,
-                                             const RowP& P, bool have_vt, u4v seg_own,
-                                             float u, LDS uint32_t* smem) {
+                                             const RowP& P, bool have_vt, u4v seg_own, float u,
+                                             LDS uint32_t* smem) {
   const uint32_t tid = threadIdx.x;
   const int lane = (int)(tid & 63), wv = (int)(tid >> 6);
   const FinLds f = fin_carve(smem);
@@ -3488,62 +3635,15 @@ __device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_
     S = exact_normaliser<DT>(row, a.mask ? a.mask + (uint64_t)b * a.mask_words : nullptr, a.V,
                              P.T, m, h.bitmap, h.pre, h.pen, have_hist, sc);
   }
-  uint32_t path = 2;  // 0 done, 1 workgroup candidate path, 2 slow path, 3 fast path
-  if (wv == 0) {
-    // ---- segment table: counts, thresholds, flags
-    uint32_t cnt = 0, beta = 0, flg = 0;
-    if (a.G == 1) {
-      if (lane == 0) {
-        cnt = seg_own.x < CAND_CAP ? seg_own.x : CAND_CAP;
-        beta = seg_own.y;
-        flg = seg_own.z;
-      }
-    } else if ((uint32_t)lane < a.G) {
-      const u4v sm = G(w.seg_meta)[row_seg_to_wg(a, b, (uint32_t)lane)];
-      cnt = sm.x < CAND_CAP ? sm.x : CAND_CAP;
-      beta = sm.y;
-      flg = sm.z;
-    }
-    const uint32_t lam = wave_max_u32(beta << BIN_SHIFT);
-    const bool ovf = __ballot((flg & FLAG_OVERFLOW) != 0) != 0;
-    const uint32_t off_incl = wave_incl_scan(cnt);
-    const uint32_t total = bcast63u(off_incl);
-    if ((uint32_t)lane <= a.G) f.soff[lane] = off_incl - cnt;  // lane G: the total
-    WaveSync::sync();
-    // the bound on p of every element outside the candidate buffers, once
-    // (wave 0) rather than in every thread of the candidate path
-    const float plim = lam > 0x007fffffu ? prob_of(funkey(lam - 1), P.T, m, S) : 0.0f;
-    if (lane == 0) {
-      f.fm[F_S] = __float_as_uint(S);
-      f.fm[F_M] = __float_as_uint(m);
-      f.fm[F_L] = __float_as_uint(L);
-      f.fm[F_PLIM] = __float_as_uint(plim);
-      f.fm[F_TOTAL] = total;
-      f.fm[F_LAM] = lam;
-    }
-    if (!(L == NEG_INF || P.Kc == 0 || ovf))
-      path = (a.G == 1 && total <= LCAP) ? 3u : 1u;
-    if (lane == 0) f.fm[F_DONE] = path;
-  }
-  __syncthreads();
-  path = f.fm[F_DONE];
   // S = 1 stands in for the reference's S on a row that top-k renormalises
   const bool approx = topk && L != NEG_INF;
-  if (path == 3) {
-    path = candidate_fast(a, b, P, S, m, u, f.fm[F_TOTAL], f.fm[F_LAM], f, approx);
-    if (path == 0) return;
-  }
-  if (path == 1) {
-    const uint32_t total = f.fm[F_TOTAL], lam = f.fm[F_LAM];
-    __syncthreads();
-    path = candidate_path<BlockSync>(a, w, b, P, S, m, u, total, lam, f, EMPTY, SORT_CAP,
-                                     approx);
-    if (path == 0) return;
-  }
+  const uint32_t path = candidate_paths<DT>(a, w, b, P, S, m, L, u, seg_own, approx, smem);
+  if (path == 0) return;
+  // the slow path, or (4) the band check could not prove S = 1: the
+  // reference's S, then the candidate path again
+  kctx_fill();
   __syncthreads();
-  // path 4: the band check could not prove S = 1; the slow path computes
-  // the reference's S first
-  slow_row<DT>(a, w, b, P, S, m, L, smem, approx && path != 4, approx && path == 4);
+  finalize_rare<DT>(b, P, S, m, L, u, seg_own, approx, path);
 }
 
 // ---------------------------------------------------------------------------
@@ -4135,8 +4235,7 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   const uint32_t last = misc[M_LAST];
   const u4v seg_own = u4v{misc[M_CCOUNT], misc[M_BETA], misc[M_FLAGS], 0u};
   __syncthreads();  // finalize reuses this shared memory
-  if (!last) return;
-  finalize_row<DT>(a, w, b, P, have, seg_own, u_row, sm);
+  if (last) finalize_row<DT>(a, w, b, P, have, seg_own, u_row, sm);
 }
 
 
@@ -4811,8 +4910,10 @@ extern "C" const char* llmk_last_error(void) { return g_last_error.c_str(); }
 static constexpr size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
 // Dynamic LDS of one workgroup: the CU's 160 KiB less the kernels' static
-// tables (the expf table and the phase words, under 512 bytes).
-static constexpr size_t LDS_DYN_MAX = 160 * 1024 - 512;
+// LDS (the expf table, the phase words and the copy of the arguments for the
+// finalize's rare paths, under 1 KiB).
+static_assert(sizeof(KCtx) + 32 * 8 + 4 * 4 + 2 * 4 < 1024, "static LDS above 1 KiB");
+static constexpr size_t LDS_DYN_MAX = 160 * 1024 - 1024;
 
 // The workspace of the sampling kernel for batches up to mb rows of up to mv
 // logits, pool workgroup entries and `slots` slow-path slots: byte offsets
