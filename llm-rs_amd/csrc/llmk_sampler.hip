@@ -1929,6 +1929,98 @@ __device__ __attribute__((noinline)) u2v block_list_scan(List list, uint32_t n, 
   return u2v{stop, __float_as_uint(c)};
 }
 
+// ---------------------------------------------------------------------------
+// Sequential f32 sums in binades
+// ---------------------------------------------------------------------------
+// While a running sum c >= 0 stays in the binade [2^eb, 2^(eb+1)) (below
+// 2^-125 the quantum is 2^-149 throughout) it is an integer C of quanta
+// q = 2^(eb-23), C < 2^24, and adding a term p adds round(p / q) quanta, a
+// tie going to the even sum: the increment of a run of terms depends on C
+// only through its parity, so a run is a pair of increments (from an even,
+// from an odd C), and runs compose in order.  An increment that would take C
+// to 2^24 or beyond leaves the binade; it saturates at XS_SAT, and the run is
+// then taken apart.
+constexpr uint32_t XS_SAT = 1u << 24;
+__device__ __forceinline__ Par sat_then(Par f, Par g) {
+  const uint32_t a0 = f.a0 + ((f.a0 & 1u) ? g.a1 : g.a0);
+  const uint32_t a1 = f.a1 + ((f.a1 & 1u) ? g.a0 : g.a1);
+  return Par{umin(a0, XS_SAT), umin(a1, XS_SAT)};
+}
+__device__ __forceinline__ Par wave_par_incl_sat(Par x) {
+  x = sat_then(dpp_par<0x111, 0xf, true>(x), x);
+  x = sat_then(dpp_par<0x112, 0xf, true>(x), x);
+  x = sat_then(dpp_par<0x114, 0xf, true>(x), x);
+  x = sat_then(dpp_par<0x118, 0xf, true>(x), x);
+  x = sat_then(dpp_par<0x142, 0xa, false>(x), x);
+  x = sat_then(dpp_par<0x143, 0xc, false>(x), x);
+  return x;
+}
+// binade exponent of a positive normal or subnormal float (subnormals: -126)
+__device__ __forceinline__ int binade_of(float c) {
+  return (int)umax((__float_as_uint(c) >> 23) & 255u, 1u) - 127;
+}
+// floor(log2 x) of a positive normal double
+__device__ __forceinline__ int binade_d(double x) {
+  return (int)(((uint64_t)__double_as_longlong(x) >> 52) & 0x7ffu) - 1023;
+}
+// The pair of a lane's Q consecutive terms (>= 0) in the binade of exponent eb.
+template <int Q>
+__device__ __forceinline__ Par lane_pair(const float (&e)[Q], int eb) {
+  uint32_t s0 = 0, s1 = 1;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const float x = __builtin_fminf(__builtin_ldexpf(e[q], 23 - eb), 0x1p25f);
+    const float k = __builtin_floorf(x);
+    const float fr = x - k;
+    const uint32_t ki = (uint32_t)k;
+    const uint32_t r = fr > 0.5f ? ki + 1u : ki;
+    const uint32_t t = fr == 0.5f ? 1u : 0u;
+    s0 += r + (t & ((s0 ^ r) & 1u));
+    s1 += r + (t & ((s1 ^ r) & 1u));
+  }
+  return Par{umin(s0, XS_SAT), umin(s1 - 1u, XS_SAT)};
+}
+
+// c + the first n of a wave's terms in order, exactly (lane l holding terms
+// Q l .. Q l + Q - 1, zeros past n): a lane at a time while c is 0 (from 0
+// the sum leaves its binade at almost every term); then the lanes' pairs in
+// c's binade, a wave scan; the lanes before the first one where c leaves the
+// binade are added by their pairs, that lane's terms one f32 addition each,
+// and the scan resumes after it.  Every lane returns the sum.
+template <int Q>
+__device__ __forceinline__ float wave_sum_q(float c, const float (&p)[Q], uint32_t n) {
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t nl = (n + Q - 1) / Q;  // lanes holding terms
+  uint32_t pos = 0;                     // lanes before pos are in c
+  while (pos < nl) {
+    if (c == 0.0f) {
+#pragma unroll
+      for (int q = 0; q < Q; ++q) c = c + rl(p[q], pos);  // zeros past n add nothing
+      ++pos;
+      continue;
+    }
+    const int eb = binade_of(c);
+    const uint32_t C = (uint32_t)__builtin_ldexpf(c, 23 - eb);
+    Par x = Par{0u, 0u};
+    if (lane >= pos) x = lane_pair<Q>(p, eb);
+    const Par in = wave_par_incl_sat(x);
+    const uint32_t inc = (C & 1u) ? in.a1 : in.a0;
+    const uint64_t cross = __ballot(lane >= pos && lane < nl && C + inc >= XS_SAT);
+    if (cross == 0ull) {
+      c = __builtin_ldexpf((float)(C + (uint32_t)__builtin_amdgcn_readlane((int)inc, 63)), eb - 23);
+      break;
+    }
+    const uint32_t l = (uint32_t)__builtin_ctzll(cross);
+    const uint32_t Cb = l > pos ? C + (uint32_t)__builtin_amdgcn_readlane((int)inc, (int)l - 1) : C;
+    float cb = __builtin_ldexpf((float)Cb, eb - 23);
+#pragma unroll
+    for (int q = 0; q < Q; ++q) cb = cb + rl(p[q], l);
+    c = cb;
+    pos = l + 1;
+  }
+  return c;
+}
+
 // A wave-uniform 64-bit value, or LDS pointer, in scalar registers.
 __device__ __forceinline__ uint64_t sgpr_u64(uint64_t x) {
   const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)x);
@@ -1941,114 +2033,38 @@ __device__ __forceinline__ LDS T* sgpr_lds(LDS T* p) {
   return (LDS T*)(uintptr_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)a);
 }
 
-// A window whose sum starts at zero: wave 0's entries (the window's first
-// 1024, sixteen a lane in order) added one after another, returned to every
-// thread.  A sum from zero crosses a binade at every doubling, at first every
-// few entries, and each crossing costs a round of the workgroup scan (a first
-// window took ~80 us against ~16 for the others).  The entries are staged in
-// stage (comp0, free once every wave holds its terms), the sum passed through
-// bc.  A call of its own, so that the window scan's registers stay as they
-// were.  Every thread calls it.
-__device__ __attribute__((noinline)) float zero_start_sum(f4v a0, f4v a1, f4v a2, f4v a3,
-                                                          LDS float* stage, LDS float* bc) {
-  const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6;
-  __syncthreads();
-  if (wv == 0) {
-    LDS f4v* st = (LDS f4v*)(stage + 16u * lane);
-    st[0] = a0;
-    st[1] = a1;
-    st[2] = a2;
-    st[3] = a3;
-    WaveSync::sync();
-    // in every lane alike (broadcast reads), eight 16-byte reads, then their
-    // 32 additions in order
-    float cc = 0.0f;
-    for (uint32_t k = 0; k < 16u * WAVE; k += 32u) {
-      f4v y[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) y[j] = *(LDS const f4v*)(stage + k + 4 * j);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        cc = cc + y[j].x;
-        cc = cc + y[j].y;
-        cc = cc + y[j].z;
-        cc = cc + y[j].w;
-      }
-    }
-    if (lane == 0) *bc = cc;
-  }
-  __syncthreads();
-  return *bc;
-}
-
-// A window that the serial sum cannot take, as a call of its own: the exact
-// terms of an unpacked wave (x, the processed logits, where `live`) or the
-// packed terms of a packed wave (comp, its nw entries), then block_seq_sum.
-// Its registers (sixteen exps in flight, the scan's pairs) are allocated
-// apart from the window loop of exact_normaliser, which with them inlined
-// spilled the row's pointers, and every reload waited for the next window's
-// logits in flight.  Returns (sum bits, slot rotation).
-__device__ __attribute__((noinline)) u2v window_scan(f4v x0, f4v x1, f4v x2, f4v x3,
-                                                     uint32_t live, uint32_t nw, float T,
-                                                     float m, float c, uint32_t it,
-                                                     LDS uint32_t* sc, LDS const float* comp) {
-  constexpr uint32_t Q = 16, CW = 256;
-  const uint32_t lane = threadIdx.x & 63u;
-  float e[Q];
-  uint32_t nq = Q;
-  if (nw <= CW) {
-    // thread entries 4 lane .. 4 lane + 3, in order
-#pragma unroll
-    for (uint32_t q = 0; q < 4; ++q) {
-      const uint32_t k = 4u * lane + q;
-      e[q] = k < nw ? comp[k] : 0.0f;
-    }
-#pragma unroll
-    for (uint32_t q = 4; q < Q; ++q) e[q] = 0.0f;
-    nq = 4;
-  } else {
-    const float x[Q] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w,
-                        x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
-#pragma unroll
-    for (uint32_t q = 0; q < Q; ++q) {
-      const float l = (T != 1.0f) ? x[q] / T : x[q];
-      e[q] = ((live >> q) & 1u) && l != NEG_INF ? exp_ref(l - m) : 0.0f;
-    }
-  }
-  uint32_t s0 = 0;
-  if (c == 0.0f) {
-    c = zero_start_sum(f4v{e[0], e[1], e[2], e[3]}, f4v{e[4], e[5], e[6], e[7]},
-                       f4v{e[8], e[9], e[10], e[11]}, f4v{e[12], e[13], e[14], e[15]},
-                       (LDS float*)(comp - CW * (threadIdx.x >> 6)), (LDS float*)sc + 40);
-    s0 = Q * WAVE;
-  }
-  uint32_t st;
-  const float r = block_seq_scan<false>(e, nq, c, it, sc, 0.0f, st, s0);
-  return u2v{__float_as_uint(r), it};
-}
-
 // S = the sequential f32 sum in index order of e_i = exp_ref(fl(l_i - m))
 // (0 for l_i = -inf), l_i = fl(v_i / T) the processed logit (penalties from
 // the history tables h if have_hist, the allow-mask, NaN read as -inf)
-// divided by T (sampler.rs:53, :57-66).  The whole workgroup, windows of
-// NT*16 consecutive elements, the next window's logits requested before the
-// current one is summed.  Most entries cannot change the sum: zeros (-inf
-// logits), and, once the sum is positive, every e below half its quantum at
-// the window's start (the sum only grows, so such an e adds 0 wherever it
-// falls).  A cheap bound on l finds them (the product with 1/T is within a
-// few ulps of l, far inside the margin), and a wave whose window part keeps
-// at most 256 entries packs them in order into LDS, so that the exact
-// division and exp run on those alone (one per lane per 64 entries).  A
-// window whose entries are all packed and number at most SERIAL_MAX is then
-// summed in order by wave 0, every lane alike, entry after entry (a few
-// cycles each, against microseconds for a round of the workgroup scan); any
-// other window goes through block_seq_sum (window_scan).  The next window's
-// logits and mask word are requested before a window is summed.
-// sc: 96 + NW*256 words of scratch.
+// divided by T (sampler.rs:53, :57-66).  The whole workgroup, in windows of
+// NT*16 consecutive elements, thread t holding elements 16t .. 16t+15 of a
+// window (wave w: its 1024-element segment w); the next window's logits are
+// requested before the current one is summed.
+//
+// Most elements cannot change the sum: zeros (-inf logits), and, once the sum
+// is positive, every e below half its quantum at the window's start (the sum
+// only grows, so such an e adds 0 wherever it falls).  A cheap bound on l
+// finds them (the product with 1/T is within a few ulps of l, far inside the
+// margin).  A wave whose segment keeps at most 256 (its live terms) packs
+// them in order into LDS, so that the exact division and exp run on those
+// alone, and goes on with them four a lane; any other keeps its sixteen a
+// lane (dead ones 0).
+//
+// Then each wave predicts the binades its segment's running sum occupies,
+// from the window's exact starting sum and the segments' sums (within the
+// drift n u of an f32 sum of n terms), and sums its terms in pairs in each
+// (at most three); wave 0 walks the sixteen segments with the exact running
+// sum: a run of segments whose pair covers the sum's binade and keeps it
+// there is added at once; a segment where the sum leaves its binade, or that
+// no pair covers, is summed by the wave that holds it (wave_sum_q), at wave
+// 0's request through LDS.  The sum is exact whatever the predictions; they
+// only decide how much is summed lane by lane.  sc: XS_SC words of scratch.
 // A function of its own (not inlined, scalars only across the call): its
 // registers are then allocated apart from the stream loop's, which an
 // inlined copy crowds into spilling.
-constexpr uint32_t SERIAL_MAX = 2048;
+constexpr uint32_t XS_NB = 3;                    // binades summarised per segment
+constexpr uint32_t XS_CW = 256;                  // live terms a wave packs
+constexpr uint32_t XS_SC = 136 + NW * XS_CW;     // scratch words
 template <int DT>
 __device__ __attribute__((noinline)) float exact_normaliser(
     const void* row, const uint32_t* mask_row, uint32_t V, float T, float m,
@@ -2075,21 +2091,18 @@ __device__ __attribute__((noinline)) float exact_normaliser(
   h.pen = pen;
   h.tokr = nullptr;
   h.lo = 0;
-  RowP P;
-  P.T = T;
-  constexpr uint32_t Q = 16, W = NT * Q, CW = 256;
-  LDS uint32_t* nwv = sc + 64;                         // [NW]: packed entries per wave (~0: not packed)
-  LDS float* cbc = (LDS float*)(sc + 80);              // the serial sum's result
-  LDS float* comp0 = (LDS float*)(sc + 96);            // [NW][CW]
-  LDS float* comp = comp0 + CW * wv;                   // this wave's packed entries
-  const float rT = 1.0f / P.T;
+  constexpr uint32_t Q = 16, W = NT * Q, CW = XS_CW;
+  enum : uint32_t { REQ = 0, CV = 1, ACK = 2, CEND = 3 };
+  constexpr uint32_t FINISHED = 0xfffffffeu;
+  LDS uint32_t* segp = sc;                         // [NW][7]: binades, three pairs
+  LDS float* wsum = (LDS float*)(sc + 112);        // [NW]: the segments' sums
+  LDS uint32_t* ctl = sc + 128;                    // the walk's requests
+  LDS float* comp = (LDS float*)(sc + 136) + CW * wv;  // this wave's packed terms
+  const float rT = 1.0f / T;
   auto exact_e = [&](float x) __attribute__((always_inline)) {
-    const float l = (P.T != 1.0f) ? x / P.T : x;
+    const float l = (T != 1.0f) ? x / T : x;
     return (l == NEG_INF) ? 0.0f : exp_ref<true>(l - m);
   };
-  if (tid < 3) ((LDS uint64_t*)sc)[tid] = ~0ull;
-  __syncthreads();
-  uint32_t it = 0;
   float c = 0.0f;
   float xn[Q];
   load16<DT>(row, Q * tid, V, xn);
@@ -2105,10 +2118,7 @@ __device__ __attribute__((noinline)) float exact_normaliser(
     const uint32_t hw = (have_hist && e0 < V) ? h.bitmap[(e0 - h.lo) >> 5] >> (e0 & 16u) : 0u;
     // entries below lim (on l - m) add nothing to a sum of binade eb or above
     float lim = NEG_INF;
-    if (c > 0.0f) {
-      const int eb = (int)umax((__float_as_uint(c) >> 23) & 255u, 1u) - 127;
-      lim = (float)(eb - 24) * 0.693147f - (0.01f + 1e-6f * fabsf(m));
-    }
+    if (c > 0.0f) lim = (float)(binade_of(c) - 24) * 0.693147f - (0.01f + 1e-6f * fabsf(m));
     uint32_t live = 0;
 #pragma unroll
     for (uint32_t q = 0; q < Q; ++q) {
@@ -2123,94 +2133,159 @@ __device__ __attribute__((noinline)) float exact_normaliser(
       load16<DT>(row, e0 + W, V, xn);
       if (mrow && e0 + W < V) mwn = mrow[(e0 + W) >> 5];
     }
+    // ---- the exact terms: packed (four a lane, in order) or sixteen a lane
     const uint32_t n = (uint32_t)__popc(live);
     const uint32_t incl = wave_incl_scan(n);
     const uint32_t nw = bcast63u(incl);
-    if (nw <= CW) {
-      // pack this wave's entries in order; their exact terms one per lane
-      // per 64 entries (a wave with 40 entries computes one exp, not four)
+    const bool packed = nw <= CW;  // wave-uniform
+    float e[Q];
+    float pk[4];
+    if (packed) {
       uint32_t at = incl - n;
 #pragma unroll
       for (uint32_t q = 0; q < Q; ++q)
         if ((live >> q) & 1u) comp[at++] = x[q];
       WaveSync::sync();
-      float e[4];
 #pragma unroll
-      for (uint32_t q = 0; q < 4; ++q) {
-        const uint32_t k = (uint32_t)lane + WAVE * q;
-        e[q] = 0.0f;
-        if (WAVE * q < nw && k < nw) e[q] = exact_e(comp[k]);
+      for (uint32_t k = 0; k < CW / WAVE; ++k) {
+        const uint32_t i = lane + WAVE * k;
+        if (WAVE * k < nw && i < nw) comp[i] = exact_e(comp[i]);
       }
       WaveSync::sync();
-      // the exact terms, in the same order, then zeros up to a multiple of
-      // 32 (the serial sum adds whole chunks of 32; +0 leaves a sum >= 0
-      // unchanged)
+      const f4v v4 = ((LDS const f4v*)comp)[lane];
+      pk[0] = 4 * lane + 0 < nw ? v4.x : 0.0f;
+      pk[1] = 4 * lane + 1 < nw ? v4.y : 0.0f;
+      pk[2] = 4 * lane + 2 < nw ? v4.z : 0.0f;
+      pk[3] = 4 * lane + 3 < nw ? v4.w : 0.0f;
+    } else {
 #pragma unroll
-      for (uint32_t q = 0; q < 4; ++q) {
-        const uint32_t k = (uint32_t)lane + WAVE * q;
-        if (k < nw) comp[k] = e[q];
-      }
-      if (nw + (uint32_t)lane < ((nw + 31u) & ~31u)) comp[nw + lane] = 0.0f;
+      for (uint32_t q = 0; q < Q; ++q) e[q] = ((live >> q) & 1u) ? exact_e(x[q]) : 0.0f;
     }
-    if (lane == 0) nwv[wv] = nw <= CW ? nw : EMPTY;
+    // the terms a segment holds: nw packed, else the elements in V
+    const uint32_t sbase = w0 + TILE * wv;
+    const uint32_t nseg = packed ? nw : (sbase < V ? umin(TILE, V - sbase) : 0u);
+    // ---- the segment's sum, then the binades its running sum occupies
+    float ls = 0.0f;
+    if (packed) {
+      ls = (pk[0] + pk[1]) + (pk[2] + pk[3]);
+    } else {
+#pragma unroll
+      for (uint32_t q = 0; q < Q; ++q) ls += e[q];
+    }
+    ls = wave_tree_sum(ls);
+    if (lane == 0) wsum[wv] = ls;
+    if (tid == 0) {
+      ctl[REQ] = EMPTY;
+      ctl[ACK] = EMPTY;
+    }
     __syncthreads();
-    uint32_t tot = 0;
+    double before = (double)c;
+    for (uint32_t i = 0; i < wv; ++i) before += (double)wsum[i];
+    // the drift of an f32 sum of n terms (n: the window's elements up to
+    // this segment's end) and of the segments' f32 sums
+    const double drift = (double)(TILE * (wv + 1)) * 0x1p-24 * 1.01 + 0x1p-19;
+    const double plo = before * (1.0 - drift), phi = (before + (double)wsum[wv]) * (1.0 + drift);
+    uint32_t hdr = 0;  // eb_lo + 256 in bits 0..15, binades in 16..23 (0: no pairs)
+    Par pr[XS_NB];
 #pragma unroll
-    for (uint32_t i = 0; i < NW; ++i) tot += umin(nwv[i], SERIAL_MAX + 1u);
-    if (tot <= SERIAL_MAX) {
-      // every wave packed, few entries: wave 0 sums them in order, in every
-      // lane alike (the reads are broadcasts), in chunks of 32: eight 16-byte
-      // reads, then their 32 additions (a read per four additions, or per
-      // wave's short list, would wait on the LDS each time)
-      if (wv == 0) {
-        // chunk j (j = lane, lane + 64) of the waves' lists in order: its
-        // offset in comp0
-        const uint32_t nl = (uint32_t)lane < NW ? (nwv[lane] + 31u) >> 5 : 0u;
-        const uint32_t ci = wave_incl_scan(nl);
-        const uint32_t nchk = bcast63u(ci);
-        uint32_t ad0 = 0, ad1 = 0;
+    for (uint32_t k = 0; k < XS_NB; ++k) pr[k] = Par{0u, 0u};
+    if (plo >= 0x1p-126 && phi < 0x1p120) {
+      const int elo = binade_d(plo), ehi = binade_d(phi);
+      const int nb = ehi - elo + 1;
+      if (nb <= (int)XS_NB) {
 #pragma unroll
-        for (uint32_t i = 0; i < NW; ++i) {
-          const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)ci, (int)i);
-          const uint32_t lo = hi - (uint32_t)__builtin_amdgcn_readlane((int)nl, (int)i);
-          const uint32_t j0 = (uint32_t)lane, j1 = (uint32_t)lane + WAVE;
-          if (j0 >= lo && j0 < hi) ad0 = CW * i + 32u * (j0 - lo);
-          if (j1 >= lo && j1 < hi) ad1 = CW * i + 32u * (j1 - lo);
-        }
-        auto fetch = [&](uint32_t j, f4v (&d)[8]) __attribute__((always_inline)) {
-          const uint32_t ad =
-              j < WAVE ? (uint32_t)__builtin_amdgcn_readlane((int)ad0, (int)j)
-                       : (uint32_t)__builtin_amdgcn_readlane((int)ad1, (int)(j - WAVE));
-          LDS const f4v* p = (LDS const f4v*)(comp0 + ad);
-#pragma unroll
-          for (int t = 0; t < 8; ++t) d[t] = p[t];
-        };
-        float cc = c;
-        for (uint32_t j = 0; j < nchk; ++j) {
-          f4v y[8];
-          fetch(j, y);
-#pragma unroll
-          for (int t = 0; t < 8; ++t) {
-            cc = cc + y[t].x;
-            cc = cc + y[t].y;
-            cc = cc + y[t].z;
-            cc = cc + y[t].w;
+        for (int k = 0; k < (int)XS_NB; ++k) {
+          if (k < nb) {
+            const Par y = packed ? wave_par_incl_sat(lane_pair<4>(pk, elo + k))
+                                 : wave_par_incl_sat(lane_pair<Q>(e, elo + k));
+            pr[k] = Par{(uint32_t)__builtin_amdgcn_readlane((int)y.a0, 63),
+                        (uint32_t)__builtin_amdgcn_readlane((int)y.a1, 63)};
           }
         }
-        if (lane == 0) *cbc = cc;
+        hdr = (uint32_t)(elo + 256) | ((uint32_t)nb << 16);
       }
-      __syncthreads();
-      c = *cbc;
-      __syncthreads();  // nwv, comp and cbc are rewritten next window
-    } else {
-      const u2v r = window_scan(f4v{x[0], x[1], x[2], x[3]}, f4v{x[4], x[5], x[6], x[7]},
-                                f4v{x[8], x[9], x[10], x[11]}, f4v{x[12], x[13], x[14], x[15]},
-                                live, nw, P.T, m, c, it, sc, comp);
-      c = __uint_as_float(r.x);
-      it = r.y;
     }
+    if (lane == 0) {
+      segp[7 * wv] = hdr;
+#pragma unroll
+      for (uint32_t k = 0; k < XS_NB; ++k) {
+        segp[7 * wv + 1 + 2 * k] = pr[k].a0;
+        segp[7 * wv + 2 + 2 * k] = pr[k].a1;
+      }
+    }
+    __syncthreads();
+    // ---- the walk
+    if (wv == 0) {
+      float cc = c;
+      uint32_t s = 0;
+      while (s < (uint32_t)NW) {
+        if (__float_as_uint(cc) >= 0x00800000u) {
+          // segments s .. s + g - 1 keep the sum in its binade (a prefix of the lanes)
+          const int eb = binade_of(cc);
+          const uint32_t C = (uint32_t)__builtin_ldexpf(cc, 23 - eb);
+          const uint32_t j = s + lane;
+          Par px = Par{XS_SAT, XS_SAT};
+          if (j < (uint32_t)NW) {
+            const uint32_t hj = segp[7 * j];
+            const int k = eb - ((int)(hj & 0xffffu) - 256);
+            if ((hj >> 16) != 0u && k >= 0 && k < (int)(hj >> 16))
+              px = Par{segp[7 * j + 1 + 2 * k], segp[7 * j + 2 + 2 * k]};
+          }
+          const Par in = wave_par_incl_sat(px);
+          const uint32_t inc = (C & 1u) ? in.a1 : in.a0;
+          const uint64_t good = __ballot(j < (uint32_t)NW && C + inc < XS_SAT);
+          const uint32_t g = ~good == 0ull ? 64u : (uint32_t)__builtin_ctzll(~good);
+          if (g > 0) {
+            const uint32_t ig = (uint32_t)__builtin_amdgcn_readlane((int)inc, (int)g - 1);
+            cc = __builtin_ldexpf((float)(C + ig), eb - 23);
+            s += g;
+            continue;
+          }
+        }
+        // segment s, lane by lane, by the wave that holds it
+        if (s == 0) {
+          cc = packed ? wave_sum_q<4>(cc, pk, nseg) : wave_sum_q<Q>(cc, e, nseg);
+        } else {
+          if (lane == 0) {
+            __hip_atomic_store(&ctl[CV], __float_as_uint(cc), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_WORKGROUP);
+            __hip_atomic_store(&ctl[REQ], s, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+          }
+          while (__hip_atomic_load(&ctl[ACK], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != s)
+            __builtin_amdgcn_s_sleep(1);
+          cc = __uint_as_float(
+              __hip_atomic_load(&ctl[CV], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+        }
+        ++s;
+      }
+      if (lane == 0) {
+        ctl[CEND] = __float_as_uint(cc);
+        __hip_atomic_store(&ctl[REQ], FINISHED, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+    } else {
+      // until wave 0 asks for this segment or has walked the window
+      for (;;) {
+        const uint32_t r =
+            __hip_atomic_load(&ctl[REQ], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (r == wv) {
+          const float cin = __uint_as_float(
+              __hip_atomic_load(&ctl[CV], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+          const float cout = packed ? wave_sum_q<4>(cin, pk, nseg) : wave_sum_q<Q>(cin, e, nseg);
+          if (lane == 0) {
+            __hip_atomic_store(&ctl[CV], __float_as_uint(cout), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_WORKGROUP);
+            __hip_atomic_store(&ctl[ACK], wv, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+          }
+          break;
+        }
+        if (r == FINISHED) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+    }
+    __syncthreads();
+    c = __uint_as_float(ctl[CEND]);
+    __syncthreads();  // ctl, segp, wsum and comp are rewritten next window
   }
-  __syncthreads();  // the caller may reuse sc
   return c;
 }
 
