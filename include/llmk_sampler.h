@@ -50,8 +50,9 @@ extern "C" {
 /* Bits of the device status word (llmk_sampler_status). */
 #define LLMK_STATUS_INVALID_PARAMS 0x1u
 /* More than 8192 distinct history tokens fell in one vocabulary segment of a
- * row: the tokens past the first 8192 (by id) of that segment were sampled
- * without penalties. */
+ * row (the fast path's LDS tables): the row was sampled by the slow path over
+ * its materialised logits, every history token penalised by its count.  The
+ * result is exact; the bit reports only that the row took the slower path. */
 #define LLMK_STATUS_HISTORY_OVERFLOW 0x2u
 #define LLMK_STATUS_SLOT_TIMEOUT 0x4u /* slow-path scratch slot not acquired */
 /* llmk_history_append found a row's history buffer full (its token was not

@@ -2478,10 +2478,20 @@ __device__ __forceinline__ void radix_sort_keys(GLB uint64_t* src, GLB uint64_t*
 // ---------------------------------------------------------------------------
 // approx: S = 1 stands in for the reference's S (a row that top-k
 // renormalises); its result stands only if the band check proves it, else S
-// is computed (exact_normaliser) and the row sampled again.  need_exact: the
-// candidate path's band check already failed; S is computed first.
-template <int DT>
-__device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b, const RowP& P,
+// is computed (exact_normaliser) and the row sampled again.  need_exact: S is
+// computed first (the candidate path's band check already failed, or the row
+// has no top-k).
+//
+// MAT: the row's history holds more distinct tokens than the LDS tables
+// (U_MAX ranks), so the row is first materialised: its processed logits
+// (softcap, penalties by each token's count, the allow-mask, NaN as -inf)
+// into the slot's scratch, the counts gathered there with global atomics;
+// every pass then reads them from there (sampler.rs:132-146 has no limit on
+// the history), and the row's maximum is taken again from them.  Without
+// MAT, a row whose tables overflow returns true at once (nothing written):
+// the caller runs it again with MAT.
+template <int DT, bool MAT>
+__device__ __forceinline__ bool slow_row(const Args& a, const Ws& w, uint32_t b, const RowP& P,
                                          float S, float m, float L, LDS uint32_t* smem,
                                          bool approx, bool need_exact) {
   const uint32_t tid = threadIdx.x;
@@ -2521,31 +2531,118 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
       if (a.out_cnt) a.out_cnt[b] = 0;
       atomicOr(w.status, LLMK_STATUS_SLOT_TIMEOUT);
     }
-    return;
+    return false;
   }
   const void* row = (const char*)a.logits +
                     (uint64_t)b * a.stride * ((DT & 3) == LLMK_F32 ? 4u : 2u);
   if (tid == 0) sh[10] = 0;
   build_history<DT>(a, P, b, row, 0, V, nwords, h, red, &sh[10]);
-  if (tid == 0 && (sh[10] & FLAG_HIST_OVERFLOW))
-    atomicOr(w.status, LLMK_STATUS_HISTORY_OVERFLOW);
   const uint32_t* mask_row = a.mask ? a.mask + (uint64_t)b * a.mask_words : nullptr;
-  if (need_exact) {
-    // sh, red, digit_off and wcnt are scratch of the normaliser here
-    S = exact_normaliser<DT>(row, mask_row, V, P.T, m, h.bitmap, h.pre, h.pen, true, smem);
-    approx = false;
-  }
   GLB uint64_t* kA = G(w.slow_keys) + (uint64_t)slot * 3 * (uint64_t)w.max_vocab;
   GLB uint64_t* kB = kA + w.max_vocab;
   GLB uint32_t* zl = (GLB uint32_t*)(kB + w.max_vocab);  // zero-probability indices
+  GLB float* proc = (GLB float*)(zl + w.max_vocab);      // materialised logits (past zl)
   GLB float* plist = G(w.slow_p) + (uint64_t)slot * w.max_vocab;
   GLB uint32_t* ilist = G(w.slow_idx) + (uint64_t)slot * w.max_vocab;
   const GLB uint32_t* mrow = a.mask ? G(a.mask) + (uint64_t)b * a.mask_words : nullptr;
+  if (!MAT && (sh[10] & FLAG_HIST_OVERFLOW) != 0) {  // uniform (after the tables' barrier)
+    __syncthreads();
+    if (tid == 0) {
+      __threadfence();
+      atomicExch(&w.slow_lock[slot], 0u);
+    }
+    return true;
+  }
+  if constexpr (MAT) {
+    if (tid == 0) atomicOr(w.status, LLMK_STATUS_HISTORY_OVERFLOW);
+    // the counts of the row's history tokens, then the processed logits
+    GLB uint32_t* cnt = (GLB uint32_t*)proc;
+    for (uint32_t i = tid; i < V; i += NT) cnt[i] = 0;
+    __syncthreads();
+    const uint32_t h0 = G(a.hoff)[b];
+    const uint32_t h1 = a.hlen ? h0 + G(a.hlen)[b] : G(a.hoff)[b + 1];
+    for (uint32_t i = h0 + tid; i < h1; i += NT) {
+      const uint32_t t = G(a.htok)[i];
+      if (t < V)
+        __hip_atomic_fetch_add(&cnt[t], hist_weight(a, i), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    __threadfence_block();
+    __syncthreads();
+    const bool need_cnt = P.fp != 0.0f;
+    for (uint32_t e0 = 8 * tid; e0 < V; e0 += 8 * NT) {
+      float v[8];
+      load8<DT>(row, e0, V, v);
+      const uint32_t mw = (mrow && e0 < V) ? mrow[e0 >> 5] : 0xffffffffu;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const uint32_t e = e0 + q;
+        if (e >= V) break;
+        float x = v[q];
+        const uint32_t k = cnt[e];
+        if (k) x = penalize(x, P, need_cnt ? k : 1u);
+        if (!((mw >> (e & 31)) & 1u) || !(x > NEG_INF)) x = NEG_INF;
+        proc[e] = x;
+      }
+    }
+    __threadfence_block();
+    __syncthreads();
+    // the row's maximum (and first index of it) over the processed logits:
+    // the stream phase's, taken with the history cut short, may differ
+    float mx = NEG_INF;
+    uint32_t mi = EMPTY;
+    for (uint32_t e = tid; e < V; e += NT) {
+      const float x = proc[e];
+      if (x > mx) {
+        mx = x;
+        mi = e;
+      }
+    }
+    mx = block_max(mx, (LDS float*)red);
+    if (!(mi != EMPTY && proc[mi] == mx)) mi = EMPTY;
+    mi = block_min_u32(mi, red);
+    L = mx;
+    m = (P.T != 1.0f) ? L / P.T : L;
+    if (L == NEG_INF) S = 0.0f;
+    if (P.mode == MODE_GREEDY) {
+      // sampler.rs:40-50: the first index holding the maximum
+      if (tid == 0) {
+        const uint32_t bi = mi == EMPTY ? 0u : mi;
+        a.out_tok[b] = bi;
+        if (a.out_cnt) a.out_cnt[b] = 1;
+        if (a.out_cap) {
+          if (a.out_ids) a.out_ids[(uint64_t)b * a.out_cap] = bi;
+          if (a.out_probs) a.out_probs[(uint64_t)b * a.out_cap] = 1.0f;
+        }
+        __threadfence();
+        atomicExch(&w.slow_lock[slot], 0u);
+      }
+      return false;
+    }
+    if (L == NEG_INF) {
+      need_exact = false;
+      approx = false;
+    }
+  }
+  if (need_exact) {
+    // sh, red, digit_off and wcnt are scratch of the normaliser here
+    if constexpr (MAT)
+      S = exact_normaliser<LLMK_F32>((const float*)proc, nullptr, V, P.T, m, h.bitmap, h.pre,
+                                     h.pen, false, smem);
+    else
+      S = exact_normaliser<DT>(row, mask_row, V, P.T, m, h.bitmap, h.pre, h.pen, true, smem);
+    approx = false;
+  }
   const float u = G(a.u)[b];
   const float c2 = LOG2E_F / P.T;
   const float nbL = -(L * c2);
   // processed logits (penalties, mask, NaN as -inf) of e0 .. e0+7 and their bins
   auto processed = [&](uint32_t e0, float v[8]) __attribute__((always_inline)) {
+    if constexpr (MAT) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[q] = e0 + q < V ? proc[e0 + q] : NEG_INF;
+      return;
+    }
     load8<DT>(row, e0, V, v);
     const uint32_t mw = (mrow && e0 < V) ? mrow[e0 >> 5] : 0xffffffffu;
 #pragma unroll
@@ -2750,7 +2847,11 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
       if (!ok) {
         // the reference's S, then the same bins again (chosen by count on a
         // top-k row, whatever S)
-        S = exact_normaliser<DT>(row, mask_row, V, P.T, m, h.bitmap, h.pre, h.pen, true, smem);
+        if constexpr (MAT)
+          S = exact_normaliser<LLMK_F32>((const float*)proc, nullptr, V, P.T, m, h.bitmap, h.pre,
+                                         h.pen, false, smem);
+        else
+          S = exact_normaliser<DT>(row, mask_row, V, P.T, m, h.bitmap, h.pre, h.pen, true, smem);
         approx = false;
         continue;
       }
@@ -2768,6 +2869,7 @@ __device__ __forceinline__ void slow_row(const Args& a, const Ws& w, uint32_t b,
     __threadfence();
     atomicExch(&w.slow_lock[slot], 0u);
   }
+  return false;
 }
 
 // Key (fkey) of the K-th largest of cval[0..n) (K <= n), by a four-round
@@ -3519,12 +3621,14 @@ __device__ __forceinline__ KCtx kctx_load() {
 
 // The segment table (counts, thresholds, flags of the row's segments), the
 // bound plim, then the candidate path: 0 when the row is done, 2 for the
-// slow path, 4 when approx (S = 1) could not be proven.  Every thread.
+// slow path, 4 when approx (S = 1) could not be proven, 5 when a segment's
+// history (or, hist_ovf, the whole row's) outgrew the LDS tables.  Every
+// thread.
 template <int DT>
 __device__ __forceinline__ uint32_t candidate_paths(const Args& a, const Ws& w, uint32_t b,
                                                     const RowP& P, float S, float m, float L,
                                                     float u, u4v seg_own, bool approx,
-                                                    LDS uint32_t* smem) {
+                                                    LDS uint32_t* smem, bool hist_ovf = false) {
   const uint32_t tid = threadIdx.x;
   const int lane = (int)(tid & 63), wv = (int)(tid >> 6);
   const FinLds f = fin_carve(smem);
@@ -3563,6 +3667,7 @@ __device__ __forceinline__ uint32_t candidate_paths(const Args& a, const Ws& w, 
     }
     if (!(L == NEG_INF || P.Kc == 0 || ovf))
       path = (a.G == 1 && total <= LCAP) ? 3u : 1u;
+    if (hist_ovf || __ballot((flg & FLAG_HIST_OVERFLOW) != 0) != 0ull) path = 5;
     if (lane == 0) f.fm[F_DONE] = path;
   }
   __syncthreads();
@@ -3582,27 +3687,25 @@ __device__ __forceinline__ uint32_t candidate_paths(const Args& a, const Ws& w, 
   return path;
 }
 
-// The rows the candidate path did not finish (path: 2, the slow path; 4, a
-// row that top-k renormalises whose band check failed).  For path 4 the
-// reference's S (exact_normaliser, over the row's history tables, built
-// again: the candidate path has overwritten a single-segment row's own),
-// then the candidate path again in the reference's arithmetic, else the
-// slow path.  A call of its own (rare), its registers allocated apart from
-// the stream path's; it reads the kernel's arguments from g_kctx, which the
-// caller writes first.
+// The slow path over the materialised row (slow_row<DT, true>): a call of
+// its own, so that the other rare paths keep their registers; the kernel's
+// arguments from g_kctx.
 template <int DT>
-__device__ __noinline__ void finalize_rare(uint32_t b, RowP P, float S, float m, float L,
-                                           float u, u4v seg_own, bool approx, uint32_t path) {
+__device__ __noinline__ void slow_row_mat(uint32_t b, RowP P, bool approx, bool need_exact) {
   extern __shared__ __align__(16) uint32_t smem[];
   const KCtx c = kctx_load();
-  const Args& a = c.a;
-  const Ws& w = c.w;
+  (void)slow_row<DT, true>(c.a, c.w, b, P, approx ? 1.0f : 0.0f, 0.0f, 0.0f,
+                           (LDS uint32_t*)smem, approx, need_exact);
+}
+
+// Path 4 of finalize_rare: the reference's S, then the candidate path again
+// (or the slow path).  Returns true when the row's history outgrows the
+// tables (the materialised slow path then takes it).
+template <int DT>
+__device__ __forceinline__ bool exact_rerun(const Args& a, const Ws& w, uint32_t b,
+                                            const RowP& P, float m, float L, float u,
+                                            u4v seg_own, LDS uint32_t* sm) {
   const uint32_t tid = threadIdx.x;
-  LDS uint32_t* sm = (LDS uint32_t*)smem;
-  if (path != 4) {
-    slow_row<DT>(a, w, b, P, S, m, L, sm, approx, false);
-    return;
-  }
   LDS uint32_t* sc = sm;  // below the tables in both layouts
   const void* row = (const char*)a.logits +
                     (uint64_t)b * a.stride * ((DT & 3) == LLMK_F32 ? 4u : 2u);
@@ -3616,11 +3719,43 @@ __device__ __noinline__ void finalize_rare(uint32_t b, RowP P, float S, float m,
   h.lo = 0;
   if (tid == 0) sc[64] = 0;
   build_history<DT>(a, P, b, row, 0, a.V, nwords, h, sc + 128, &sc[64]);
-  S = exact_normaliser<DT>(row, a.mask ? a.mask + (uint64_t)b * a.mask_words : nullptr, a.V,
+  if (sc[64] & FLAG_HIST_OVERFLOW) return true;  // the whole row's history outgrows the tables
+  const float S =
+      exact_normaliser<DT>(row, a.mask ? a.mask + (uint64_t)b * a.mask_words : nullptr, a.V,
                            P.T, m, h.bitmap, h.pre, h.pen, true, sc);
   __syncthreads();
-  path = candidate_paths<DT>(a, w, b, P, S, m, L, u, seg_own, false, sm);
-  if (path != 0) slow_row<DT>(a, w, b, P, S, m, L, sm, false, false);
+  const uint32_t path = candidate_paths<DT>(a, w, b, P, S, m, L, u, seg_own, false, sm);
+  return path != 0 && slow_row<DT, false>(a, w, b, P, S, m, L, sm, false, false);
+}
+
+// The rows the candidate path did not finish (path: 2, the slow path; 4, a
+// row that top-k renormalises whose band check failed; 5, a row whose
+// history outgrows the LDS tables, which the slow path materialises, with
+// approx for a row that top-k renormalises).  For path 4 the reference's S
+// (exact_normaliser, over the row's history tables, built again: the
+// candidate path has overwritten a single-segment row's own), then the
+// candidate path again in the reference's arithmetic, else the slow path.
+// A call of its own (rare), its registers allocated apart from the stream
+// path's; it reads the kernel's arguments from g_kctx, which the caller
+// writes first.  The materialised slow path is one call at its end (a call
+// in each branch cost the others registers: apply_top_p 470 -> 525 us).
+template <int DT>
+__device__ __noinline__ void finalize_rare(uint32_t b, RowP P, float S, float m, float L,
+                                           float u, u4v seg_own, bool approx, uint32_t path) {
+  extern __shared__ __align__(16) uint32_t smem[];
+  const KCtx c = kctx_load();
+  const Args& a = c.a;
+  const Ws& w = c.w;
+  LDS uint32_t* sm = (LDS uint32_t*)smem;
+  // mat: the row goes to the materialised slow path (one call, at the end)
+  bool mat = path == 5;
+  if (!mat && path != 4) {
+    mat = slow_row<DT, false>(a, w, b, P, S, m, L, sm, approx, false);
+  } else if (!mat) {
+    mat = exact_rerun<DT>(a, w, b, P, m, L, u, seg_own, sm);
+    approx = false;
+  }
+  if (mat) slow_row_mat<DT>(b, P, approx, !approx);
 }
 
 // seg_own: for a single-segment row, this workgroup's (count, beta, flags);
@@ -3643,12 +3778,21 @@ __device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_
   const int lane = (int)(tid & 63), wv = (int)(tid >> 6);
   const FinLds f = fin_carve(smem);
   const uint32_t nslots = a.ntiles + (have_vt ? a.nchunks : 0u);
-  // ---- wave 0: the row maximum L (and the greedy token)
+  // ---- wave 0: the row maximum L (and the greedy token, unless a segment's
+  // history outgrew its tables: the slow path then materialises the row)
   if (wv == 0) {
     const GLB f2v* part = G(w.tile_part) + (uint64_t)b * MAX_SLOTS;
     LDS const f2v* lpart = (LDS const f2v*)(smem + a.lds_part);
     float L = NEG_INF;
+    uint32_t hov = 0;
     if (P.mode == MODE_GREEDY) {
+      uint32_t flg = 0;
+      if (a.G == 1) flg = seg_own.z;
+      else if ((uint32_t)lane < a.G) flg = G(w.seg_meta)[row_seg_to_wg(a, b, (uint32_t)lane)].z;
+      hov = __ballot((flg & FLAG_HIST_OVERFLOW) != 0) != 0ull ? 1u : 0u;
+    }
+    if (hov) {
+    } else if (P.mode == MODE_GREEDY) {
       for (uint32_t c = (uint32_t)lane; c < nslots; c += WAVE) {
         const f2v q = a.G == 1 ? lpart[c] : part[c];
         f.tl[c] = q.x;
@@ -3676,14 +3820,18 @@ __device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_
         L = fmaxf(L, a.G == 1 ? lpart[c].x : part[c].x);
       L = wave_max(L);
     }
-    if (lane == 0) g_bcast[0] = __float_as_uint(L);
+    if (lane == 0) {
+      g_bcast[0] = __float_as_uint(L);
+      g_bcast[1] = hov;
+    }
   }
   __syncthreads();
-  if (P.mode == MODE_GREEDY) return;
+  if (P.mode == MODE_GREEDY && g_bcast[1] == 0) return;
   const float L = __uint_as_float(g_bcast[0]);
   const float m = (P.T != 1.0f) ? L / P.T : L;
   const bool topk = P.K > 0 && (uint32_t)P.K < a.V;
   float S = 1.0f;
+  bool rebuilt_ovf = false;
   if (L == NEG_INF) {
     S = 0.0f;
   } else if (!topk) {
@@ -3704,18 +3852,23 @@ __device__ __forceinline__ void finalize_row(const Args& a, const Ws& w, uint32_
                         (uint64_t)b * a.stride * ((DT & 3) == LLMK_F32 ? 4u : 2u);
       build_history<DT>(a, P, b, row, 0, a.V, nwords, h, sc + 128, &sc[64]);
       have_hist = true;  // built (empty when the row has no penalised history)
+      // the whole row's history outgrows the tables (the segments' did not)
+      rebuilt_ovf = (sc[64] & FLAG_HIST_OVERFLOW) != 0;
     }
     const void* row = (const char*)a.logits +
                       (uint64_t)b * a.stride * ((DT & 3) == LLMK_F32 ? 4u : 2u);
-    S = exact_normaliser<DT>(row, a.mask ? a.mask + (uint64_t)b * a.mask_words : nullptr, a.V,
-                             P.T, m, h.bitmap, h.pre, h.pen, have_hist, sc);
+    if (!rebuilt_ovf)
+      S = exact_normaliser<DT>(row, a.mask ? a.mask + (uint64_t)b * a.mask_words : nullptr,
+                               a.V, P.T, m, h.bitmap, h.pre, h.pen, have_hist, sc);
   }
   // S = 1 stands in for the reference's S on a row that top-k renormalises
   const bool approx = topk && L != NEG_INF;
-  const uint32_t path = candidate_paths<DT>(a, w, b, P, S, m, L, u, seg_own, approx, smem);
+  const uint32_t path =
+      candidate_paths<DT>(a, w, b, P, S, m, L, u, seg_own, approx, smem, rebuilt_ovf);
   if (path == 0) return;
-  // the slow path, or (4) the band check could not prove S = 1: the
-  // reference's S, then the candidate path again
+  // the slow path, (4) the band check could not prove S = 1: the reference's
+  // S, then the candidate path again, or (5) the row's history outgrew the
+  // tables: the slow path materialises the row
   kctx_fill();
   __syncthreads();
   finalize_rare<DT>(b, P, S, m, L, u, seg_own, approx, path);
@@ -4291,7 +4444,6 @@ __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   __syncthreads();
   if (tid == 0) {
     const uint32_t fl = misc[M_FLAGS];
-    if (fl & FLAG_HIST_OVERFLOW) atomicOr(w.status, LLMK_STATUS_HISTORY_OVERFLOW);
     if (fl & FLAG_NAN) atomicOr(w.status, LLMK_STATUS_NAN_LOGITS);
     uint32_t last = 1;
     if (a.G > 1) {  // a single-segment row passes its table in registers

@@ -172,24 +172,29 @@ def test_invalid_parameters_and_status(sampler):
     assert sampler.status() == 0  # reading clears it
 
 
-def test_history_overflow_keeps_the_first_ranks(sampler):
+def test_history_overflow_penalises_every_token(sampler):
     """Past 8192 distinct history tokens in one vocabulary segment (16384
-    tokens for a one-row batch of this vocabulary), the segment's later
-    tokens by id are sampled as ordinary tokens, and the status word says
-    so.  The result equals the oracle's on the history without them."""
+    tokens a segment for rows of this vocabulary in a small batch) the row is
+    materialised by the slow path: every one of the 20,000 distinct tokens
+    is penalised, as the reference does (sampler.rs:132-146, no limit), and
+    the status word says the row took that path.  A top-k row, a top-k-off
+    row and a greedy row, each checked bit-exact against the oracle on the
+    full history."""
     V = 151936
-    lg = np.random.default_rng(8).normal(0, 3, (1, V)).astype(np.float32)
+    lg = np.random.default_rng(8).normal(0, 3, (3, V)).astype(np.float32)
     hist = np.concatenate([np.arange(20000), [5, 5, 9000, 17000, 17000]])
-    kept = hist[(hist < 8192) | (hist >= 16384)]  # segment 1 holds 3616 < 8192
-    args = dict(T=0.8, K=40, P=0.95, R=1.1, PR=0.3, FR=0.2, u=0.3)
-    w = workload(lg, hists=[hist], **args)
+    T = np.array([0.8, 0.8, 0.0], np.float32)
+    K = np.array([40, 0, 0], np.int32)
+    P = np.array([0.95, 0.9, 1.0], np.float32)
+    w = workload(lg, hists=[hist] * 3, T=T, K=K, P=P, R=1.1, PR=0.3, FR=0.2, u=0.3)
     sampler.status()
-    print("[case] history overflow", flush=True)
+    print("[case] history overflow: 20000 distinct tokens, top-k / top-p / greedy", flush=True)
     gpu = run_gpu(sampler, w, CAP)
     assert sampler.status() & _lib.LLMK_STATUS_HISTORY_OVERFLOW
-    w2 = workload(lg, hists=[kept], **args)
-    orc = O.sample_workload(O.MIRROR, w2, out_cap=CAP, nthreads=16)
-    assert_bit_exact(w2, gpu, orc, CAP, "history overflow")
+    orc = O.sample_workload(O.MIRROR, w, out_cap=CAP, nthreads=16)
+    assert_bit_exact(w, gpu, orc, CAP, "history overflow")
+    ref = O.sample_workload(O.REF, w, out_cap=CAP, nthreads=16)
+    assert np.array_equal(gpu[0], ref[1]), (gpu[0], ref[1])
 
 
 def test_host_errors(sampler):
