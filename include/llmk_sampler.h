@@ -73,9 +73,13 @@ typedef struct llmk_sampler llmk_sampler; /* opaque; owns device workspace */
 typedef enum { LLMK_F32 = 0, LLMK_BF16 = 1, LLMK_F16 = 2 } llmk_dtype;
 
 typedef struct {
-  /* logits[b * row_stride + v], v < vocab; row_stride in elements.  Rows
-   * must be 16-byte aligned (fp32: row_stride a multiple of 4, bf16 and f16:
-   * of 8), else LLMK_ERR_ALIGNMENT. */
+  /* logits[b * row_stride + v], v < vocab; row_stride in elements, rows at
+   * any element offset.  Rows that do not start 16-byte aligned (fp32:
+   * row_stride not a multiple of 4, bf16 and f16: not of 8, or a base
+   * address off 16 bytes) are first copied to aligned rows in the handle's
+   * staging buffer, which llmk_sample_batch allocates (once, and again when
+   * a call needs more); llmk_sample_batch_static, which allocates nothing,
+   * returns LLMK_ERR_ALIGNMENT for them. */
   const void* logits;
   int32_t dtype; /* llmk_dtype */
   uint32_t batch;

@@ -4967,7 +4967,8 @@ __global__ __launch_bounds__(HCA_T) void history_count_append_kernel(
     eq = umin(eq, red[HCA_T / WAVE + i]);
   }
   if (eq != EMPTY) {
-    if (tid == 0) C[eq] = C[eq] + 1u;
+    // a listed count of 0 reads as 1 occurrence (hist_weight): one more is 2
+    if (tid == 0) C[eq] = umax(C[eq], 1u) + 1u;
     return;
   }
   if (n >= cap) {
@@ -5115,6 +5116,8 @@ struct llmk_sampler {
   Ws ws;
   void* mem;
   size_t mem_bytes;
+  void* stage;         // aligned copies of rows passed at any offset (allocated on demand)
+  size_t stage_bytes;
 };
 
 static thread_local std::string g_last_error;
@@ -5239,6 +5242,7 @@ extern "C" void llmk_sampler_destroy(llmk_sampler* s) {
   (void)hipSetDevice(s->device);
   (void)hipDeviceSynchronize();
   (void)hipFree(s->mem);
+  if (s->stage) (void)hipFree(s->stage);
   delete s;
 }
 
@@ -5385,11 +5389,59 @@ static int sample_batch_run(const Ws& ws, uint32_t max_batch, uint32_t max_vocab
   return LLMK_OK;
 }
 
+// Rows at any element offset (sampler.rs:25-29 samples any &[f32], which
+// candle.rs:2007-2009 narrows from the lm_head output at any offset): copied
+// element by element, each read at its own alignment, into rows of stride
+// round_up(V, 8) that start 16-byte aligned, which the sampling kernel reads.
+__global__ __launch_bounds__(256) void realign_kernel(const void* src, uint64_t src_stride,
+                                                      void* dst, uint64_t dst_stride, uint32_t V,
+                                                      uint32_t esz) {
+  const uint32_t b = blockIdx.y;
+  for (uint32_t k = 0; k < 4; ++k) {
+    const uint32_t e = blockIdx.x * 1024u + 256u * k + threadIdx.x;
+    if (e >= V) break;
+    if (esz == 4)
+      G((float*)dst)[(uint64_t)b * dst_stride + e] =
+          G((const float*)src)[(uint64_t)b * src_stride + e];
+    else
+      G((uint16_t*)dst)[(uint64_t)b * dst_stride + e] =
+          G((const uint16_t*)src)[(uint64_t)b * src_stride + e];
+  }
+}
+
 static int sample_batch_impl(llmk_sampler* s, const llmk_sample_batch_args* in,
                              void* stream, u4v* cut, uint32_t tp_clamp) {
   if (!s) return fail(LLMK_ERR_INVALID_ARGUMENT, "sampler is NULL");
   HIPCHK(hipSetDevice(s->device));
   const uint32_t pool = s->max_batch > MAX_WGS ? s->max_batch : MAX_WGS;
+  const size_t esz = in && in->dtype == LLMK_F32 ? 4 : 2;
+  const bool valid = in && in->logits && in->batch > 0 && in->vocab > 0 &&
+                     in->batch <= s->max_batch && in->vocab <= s->max_vocab &&
+                     in->row_stride >= in->vocab &&
+                     (in->dtype == LLMK_F32 || in->dtype == LLMK_BF16 || in->dtype == LLMK_F16);
+  if (valid &&
+      (((uintptr_t)in->logits % 16) != 0 || ((in->row_stride * esz) % 16) != 0)) {
+    // rows at any offset: their aligned copies (the staging rows grow on
+    // demand; the call then allocates, once)
+    const uint64_t dstride = ((uint64_t)in->vocab + 7) / 8 * 8;
+    const size_t need = (size_t)in->batch * dstride * esz;
+    if (need > s->stage_bytes) {
+      HIPCHK(hipDeviceSynchronize());  // an earlier call may still read the old rows
+      if (s->stage) HIPCHK(hipFree(s->stage));
+      s->stage = nullptr;
+      s->stage_bytes = 0;
+      HIPCHK(hipMalloc(&s->stage, need));
+      s->stage_bytes = need;
+    }
+    hipLaunchKernelGGL(realign_kernel, dim3((in->vocab + 1023) / 1024, in->batch), dim3(256), 0,
+                       (hipStream_t)stream, in->logits, in->row_stride, s->stage, dstride,
+                       in->vocab, (uint32_t)esz);
+    HIPCHK(hipGetLastError());
+    llmk_sample_batch_args al = *in;
+    al.logits = s->stage;
+    al.row_stride = dstride;
+    return sample_batch_run(s->ws, s->max_batch, s->max_vocab, pool, &al, stream, cut, tp_clamp);
+  }
   return sample_batch_run(s->ws, s->max_batch, s->max_vocab, pool, in, stream, cut, tp_clamp);
 }
 

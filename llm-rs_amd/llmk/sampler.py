@@ -405,6 +405,10 @@ class HipSampler:
                                "draft_probs must be a row-major float32 [batch, >= vocab] tensor")
         if probs.shape != ids.shape or draft_probs.shape[0] != B or counts.numel() != B:
             raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT, "inconsistent shapes")
+        if V > draft_probs.shape[1]:
+            # the kernel reads q[id] for every id < vocab of the last row too
+            raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT,
+                               f"vocab {V} above draft_probs' {draft_probs.shape[1]} columns")
         tok = torch.empty(B, dtype=torch.int32, device=ids.device)
         acc = torch.empty(B, dtype=torch.int32, device=ids.device)
         st = self._stream(ids, stream)

@@ -83,3 +83,33 @@ def run_gpu_strided(sampler, w, out_cap=64, extra=4):
     ids = r.ids.cpu().numpy().view(np.uint32) if out_cap else None
     probs = r.probs.cpu().numpy() if out_cap else None
     return tok, ids, probs, cnt
+
+
+def run_gpu_offset(sampler, w, out_cap=64, offset=1, extra=3):
+    """Like run_gpu, with row b at element offset + b * (V + extra) of one
+    buffer (rows at any alignment), the rest of the buffer +inf, which must
+    never be read."""
+    import torch
+    db = w.to_device()
+    stride = w.V + extra
+    n = w.B * stride + offset + 8
+    if w.dtype in ("bf16", "f16"):
+        buf = np.full(n, 0x7F80 if w.dtype == "bf16" else 0x7C00, np.uint16)
+        for b in range(w.B):
+            buf[offset + b * stride:offset + b * stride + w.V] = w.bf16_bits[b]
+        t = torch.from_numpy(buf.view(np.int16)).to("cuda:0").view(
+            torch.bfloat16 if w.dtype == "bf16" else torch.float16)
+    else:
+        buf = np.full(n, np.inf, np.float32)
+        for b in range(w.B):
+            buf[offset + b * stride:offset + b * stride + w.V] = w.logits[b]
+        t = torch.from_numpy(buf).to("cuda:0")
+    db.logits = t.as_strided((w.B, w.V), (stride, 1), offset)
+    db.vocab = w.V
+    r = sampler.sample_batch(db, out_cap=out_cap)
+    torch.cuda.synchronize()
+    tok = r.tokens.cpu().numpy().view(np.uint32)
+    cnt = r.count.cpu().numpy().view(np.uint32)
+    ids = r.ids.cpu().numpy().view(np.uint32) if out_cap else None
+    probs = r.probs.cpu().numpy() if out_cap else None
+    return tok, ids, probs, cnt

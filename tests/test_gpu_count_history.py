@@ -225,3 +225,26 @@ def test_count_append_long_tables(sampler):
         assert ln[b] == len(u)
         assert np.array_equal(tb[b * cap:b * cap + len(u)], u), f"row {b}"
         assert np.array_equal(cb[b * cap:b * cap + len(u)], c), f"row {b}"
+
+
+def test_count_append_to_a_zero_count_entry(sampler):
+    """A listed token with count 0 is read as one occurrence (the sampler
+    weighs a listed entry at least 1); appending it once more makes 2, and
+    the next step's frequency penalty sees 2 occurrences."""
+    cap = 8
+    base = np.array([3, 7, 11], np.uint32)
+    cnt = np.array([0, 2, 0], np.uint32)
+    buf_t = np.zeros(cap, np.uint32)
+    buf_c = np.zeros(cap, np.uint32)
+    buf_t[:3], buf_c[:3] = base, cnt
+    d_off = torch.zeros(1, dtype=torch.int32, device="cuda:0")
+    d_len = torch.full((1,), 3, dtype=torch.int32, device="cuda:0")
+    d_tok = torch.from_numpy(buf_t.view(np.int32)).cuda()
+    d_cnt = torch.from_numpy(buf_c.view(np.int32)).cuda()
+    print("[case] append to a zero-count entry", flush=True)
+    sampler.history_count_append(d_off, d_len, d_tok, d_cnt, cap,
+                                 torch.tensor([3], dtype=torch.int32, device="cuda:0"))
+    torch.cuda.synchronize()
+    cb = d_cnt.cpu().numpy().view(np.uint32)
+    assert list(cb[:3]) == [2, 2, 0], cb[:3]
+    assert int(d_len.cpu()[0]) == 3

@@ -99,3 +99,11 @@ def test_static_limits():
     a.batch, a.vocab, a.row_stride = 4, (1 << 18) + 1, (1 << 18) + 8
     assert lib.llmk_sample_batch_static(a, None, None) == _lib.LLMK_ERR_CAPACITY
     assert lib.llmk_sample_batch_static(None, None, None) == _lib.LLMK_ERR_INVALID_ARGUMENT
+    # rows off 16 bytes: the handle copies them to aligned rows, the static
+    # call (which allocates nothing) refuses them before sampling
+    import ctypes
+    a.batch, a.vocab, a.row_stride, a.dtype = 2, 101, 101, _lib.LLMK_F32
+    a.logits = ctypes.c_void_p(0x1004)
+    a.uniforms = ctypes.c_void_p(0x2000)
+    a.out_tokens = ctypes.c_void_p(0x3000)
+    assert lib.llmk_sample_batch_static(a, None, None) == _lib.LLMK_ERR_ALIGNMENT
