@@ -6,6 +6,7 @@ built here, so its tests are not run; their literal vectors are the fixture.
   python tests/golden/make_reference_kats.py
 """
 import json
+import math
 import os
 
 import numpy as np
@@ -97,6 +98,12 @@ KATS = [
          logits=[6.0], history=[0], penalty=3.0, expect=[2.0], tol=1e-5),
     dict(name="order_temp_then_rep", src=f"{T}:801-811", op="temp_then_rep",
          logits=[6.0], history=[0], penalty=3.0, t=3.0, expect=[0.667], tol=1e-3),
+    # final_logit_softcapping, cap * tanh(x / cap) (candle.rs:1803-1807): the
+    # test's expected values are that closed form in f64, cast to f32
+    dict(name="softcap_thirty", src=f"{T}:251-263", op="softcap",
+         logits=[10.0, -20.0, 0.0], cap=30.0,
+         expect=[float(f32(30.0 * math.tanh(10.0 / 30.0))), float(f32(30.0 * math.tanh(-20.0 / 30.0))), 0.0],
+         tol=1e-4),
 ]
 
 

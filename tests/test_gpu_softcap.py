@@ -84,6 +84,33 @@ def test_last_position_of_bsv_logits(sampler, cap):
     assert sampler.status() == 0
 
 
+def test_reference_softcap_kat(sampler):
+    """mlc_test.rs:251-263 ([10, -20, 0], cap 30, expected cap * tanh(x / cap)
+    to 1e-4) through llmk_sample_batch with softcap = 30: the kept
+    probabilities are the softmax of the test's expected values, and the row
+    is bit-equal to the oracle sampling its own capped logits."""
+    import json
+    import os
+    from gpu_util import workload
+    with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "reference_kats.json")) as f:
+        kat = next(k for k in json.load(f)["kats"] if k["op"] == "softcap")
+    lg = np.asarray(kat["logits"], np.float32)
+    expect = np.asarray(kat["expect"], np.float64)
+    e = np.exp(expect - expect.max())
+    for u in (0.0, 0.5, 0.999):
+        w = workload(lg, T=1.0, u=u, name="softcap_kat")
+        print(f"[case] softcap KAT u={u}", flush=True)
+        gpu = run(sampler, w, kat["cap"])
+        orc = O.sample_workload(O.MIRROR, capped(w, kat["cap"]), out_cap=CAP, nthreads=1)
+        assert_bit_exact(w, gpu, orc, CAP, "softcap-kat")
+        n = int(gpu[3][0])
+        assert n == 3
+        d = np.zeros(3)
+        d[gpu[1][0, :n]] = gpu[2][0, :n]
+        np.testing.assert_allclose(d, e / e.sum(), atol=kat["tol"], rtol=0)
+    assert sampler.status() == 0
+
+
 def test_softcap_rejects_bad_values(sampler):
     w = make("C3", 2, "f32")
     db = w.to_device()

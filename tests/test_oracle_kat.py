@@ -1,6 +1,8 @@
 """The CPU oracle against the reference's own known-answer vectors
 (tests/golden/reference_kats.json, transcribed from llm-tests/tests/mlc_test.rs
-and mlc_parity.rs with file:line per vector), in both oracle modes."""
+and mlc_parity.rs with file:line per vector), in both oracle modes.  The
+softcap vector (mlc_test.rs:251-263) pins the capped values to the test's
+1e-4; the bit-level composition below that stays unpinned."""
 import json
 import math
 import os
@@ -103,6 +105,14 @@ def test_reference_kat(kat, mode):
     elif op == "logit_bias":
         out = O.apply_logit_bias(lg, kat["bias_tokens"], kat["bias_values"])
         assert np.array_equal(out, np.asarray(kat["expect"], np.float32))
+    elif op == "softcap":
+        # the oracle's softcap in f32 logits (candle's CPU ops, llmk_oracle_softcap)
+        out = O.softcap("f32", lg, kat["cap"])
+        np.testing.assert_array_less(np.abs(out - np.asarray(kat["expect"], np.float32)), kat["tol"])
+        # and the capped distribution the sampler then draws from
+        d, ids, probs = _dist(mode, out)
+        e = np.exp(np.asarray(kat["expect"], np.float64) - max(kat["expect"]))
+        np.testing.assert_allclose(d, e / e.sum(), atol=kat["tol"], rtol=0)
     else:
         raise AssertionError(f"unknown op {op}")
 
