@@ -184,10 +184,12 @@ int llmk_apply_top_k(llmk_sampler* s, float* logits, uint32_t batch, uint32_t vo
  * -inf.  Rows with top_p[b] >= 1 or NaN, or whose probabilities sum to 0
  * (every logit -inf), are left as they are.  The probabilities are those of
  * llmk_sample_batch at temperature 1 (the same exp and normaliser), and the
- * kept set is what llmk_sample_batch keeps with that top_p alone.  Rows as
- * for llmk_sample_batch (f32, 16-byte aligned); batch and vocab within the handle's
+ * kept set is what llmk_sample_batch keeps with that top_p alone.  f32 rows
+ * at any element offset and stride; batch and vocab within the handle's
  * maxima; uses the handle's workspace (stream order, like
- * llmk_sample_batch); allocates nothing. */
+ * llmk_sample_batch).  Allocates nothing, except that rows not starting
+ * 16-byte aligned are read through the handle's staging buffer, allocated
+ * as llmk_sample_batch does. */
 int llmk_apply_top_p(llmk_sampler* s, float* logits, uint32_t batch, uint32_t vocab,
                      uint64_t row_stride, const float* top_p, void* hip_stream);
 

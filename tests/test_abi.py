@@ -61,7 +61,8 @@ def test_constants_match_header():
     for name in ("LLMK_OK", "LLMK_ERR_INVALID_ARGUMENT", "LLMK_ERR_EMPTY_LOGITS", "LLMK_ERR_CAPACITY",
                  "LLMK_ERR_HIP", "LLMK_ERR_ALIGNMENT", "LLMK_ERR_UNSUPPORTED",
                  "LLMK_STATUS_INVALID_PARAMS", "LLMK_STATUS_HISTORY_OVERFLOW",
-                 "LLMK_STATUS_SLOT_TIMEOUT", "LLMK_STATUS_HISTORY_FULL", "LLMK_INVALID_TOKEN"):
+                 "LLMK_STATUS_SLOT_TIMEOUT", "LLMK_STATUS_HISTORY_FULL", "LLMK_STATUS_NAN_LOGITS",
+                 "LLMK_INVALID_TOKEN"):
         m = re.search(rf"#define {name} \(?(-?(?:0x)?[0-9a-f]+)u?\)?", src)
         assert m, name
         assert int(m.group(1), 0) == getattr(_lib, name), name
