@@ -4,6 +4,21 @@
 // rint, ldexp, conversions), so a CPU restatement of the same steps gives the
 // same bits.  The file is compiled with -ffp-contract=off: an FMA appears
 // only where it is written.
+//
+// Provenance of the numerical methods restated here (exp, expm1, tanh):
+//  - expf: the method and the exp2f_data constants (the 2^(i/32) table, the
+//    cubic's coefficients) of Szabolcs Nagy's expf in Arm's
+//    optimized-routines, which glibc 2.28 and later ship as
+//    sysdeps/ieee754/flt-32/e_expf.c:
+//      Copyright (c) 2017-2018, Arm Limited.
+//      SPDX-License-Identifier: MIT
+//  - expm1f, tanhf: fdlibm's method and coefficients, as glibc's
+//    s_expm1f.c and s_tanhf.c carry them:
+//      Copyright (C) 1993 by Sun Microsystems, Inc. All rights reserved.
+//      Developed at SunPro, a Sun Microsystems, Inc. business.
+//      Permission to use, copy, modify, and distribute this
+//      software is freely granted, provided that this notice
+//      is preserved.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>

@@ -9,9 +9,10 @@
 //              LDS bitmap + popcount prefix (rank of a token among the
 //              history's distinct tokens) and a table of the penalised logits
 //              of those tokens (repetition, presence, frequency).
-//   * stream   the segment's logits are read once from HBM with 128-bit (fp32)
-//              / 64-bit (bf16) non-temporal loads, 1024-token tiles, each lane
-//              owning 4 runs of 4 consecutive tokens.  Per tile: history
+//   * stream   the segment's logits are read once from HBM with 128-bit
+//              non-temporal loads in 1024-token tiles: an fp32 lane owns 4
+//              runs of 4 consecutive tokens, a bf16/f16 lane 2 runs of 8
+//              (one 16-byte load per run).  Per tile: history
 //              tokens take their penalised value, the allow-mask applies, and
 //              the wave computes the tile max and the tile's share of the
 //              softmax normaliser sum 2^((l - max) log2(e)/T) with a DPP
@@ -23,12 +24,21 @@
 //              normaliser S, computes exact probabilities of the candidates,
 //              ranks them by (p desc, idx asc), proves no other token can
 //              precede the ones used, and runs min-p / top-k / top-p / the
-//              draw exactly as sampler.rs:77-124.
+//              draw exactly as sampler.rs:77-124.  Rows without top-k use the
+//              reference's sequential f32 S (the exact normaliser); top-k
+//              rows take S = 1 only where a rounding-band check proves every
+//              decision (min-p cut, top-k set, top-p cut, draw) to be the
+//              reference's whatever S is, else the exact S and a rerun.
 //   * slow     rows the candidate path cannot prove exact (top-k = 0 with a
 //              large nucleus, candidate overflow, fully masked rows) are done
 //              by the same workgroup: exact probabilities of the whole row,
 //              a stable LSD radix sort in a global scratch slot, and the same
-//              sequential semantics.
+//              sequential semantics.  Rows whose history outgrows the LDS
+//              rank tables take it over logits penalised and materialised in
+//              the slot.
+//
+// Rows that do not start 16-byte aligned are first copied to aligned rows of
+// a staging buffer (realign_kernel).
 //
 // Numerics are fixed (llmk_numerics.h); the CPU mirror oracle restates them.
 #include <hip/hip_runtime.h>

@@ -92,6 +92,19 @@ def _on_device(dev: torch.device, **tensors) -> None:
                                f"{name} is on {t.device}, the logits on {dev}")
 
 
+def _rows(t: torch.Tensor) -> bool:
+    """A [rows, columns] tensor with unit stride along the columns.  torch
+    gives a dimension of size 1 any stride (a one-row view of a 1-D tensor
+    has stride 0 across rows), so such a dimension is not checked."""
+    return t.dim() == 2 and (t.stride(1) == 1 or t.shape[1] <= 1)
+
+
+def _row_stride(t: torch.Tensor) -> int:
+    """Elements from one row's start to the next; a single row is read as
+    packed whatever stride torch gives its size-1 dimension."""
+    return t.stride(0) if t.shape[0] > 1 else max(t.stride(0), t.shape[1])
+
+
 def _flat(name: str, t: Optional[torch.Tensor], dtypes) -> None:
     """Per-row arrays are read as dense vectors of one element type."""
     if t is not None and (t.dtype not in dtypes or not t.is_contiguous()):
@@ -119,7 +132,7 @@ def _batch_args(db: DeviceBatch, out_tokens: torch.Tensor,
     else:
         raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT,
                            "logits must be float32, bfloat16 or float16")
-    if lg.dim() != 2 or lg.stride(1) != 1:
+    if not _rows(lg):
         raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT,
                            "logits must be [batch, >= vocab] with unit stride along the vocabulary")
     fields = dict(uniforms=db.uniforms, temperature=db.temperature, top_k=db.top_k,
@@ -146,7 +159,7 @@ def _batch_args(db: DeviceBatch, out_tokens: torch.Tensor,
     a.dtype = dt
     a.batch = B
     a.vocab = V
-    a.row_stride = lg.stride(0)
+    a.row_stride = _row_stride(lg)
     a.temperature = _ptr(db.temperature)
     a.top_k = _ptr(db.top_k)
     a.top_p = _ptr(db.top_p)
@@ -281,7 +294,7 @@ class HipSampler:
 
     def _mask(self, fn: str, logits: torch.Tensor, param: torch.Tensor, dtype: torch.dtype,
               stream: Optional[torch.cuda.Stream]) -> None:
-        if logits.dtype != torch.float32 or logits.dim() != 2 or logits.stride(1) != 1:
+        if logits.dtype != torch.float32 or not _rows(logits):
             raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT,
                                "logits must be a row-major float32 [batch, vocab] tensor")
         _on_device(logits.device, param=param)
@@ -290,7 +303,7 @@ class HipSampler:
         st = self._stream(logits, stream)
         p = param.to(dtype).contiguous()
         rc = getattr(self._lib, fn)(self._h, logits.data_ptr(), logits.shape[0], logits.shape[1],
-                                    logits.stride(0), p.data_ptr(),
+                                    _row_stride(logits), p.data_ptr(),
                                     ctypes.c_void_p(st.cuda_stream))
         if rc != 0:
             raise SamplerError(rc, _lib.last_error())
@@ -311,7 +324,7 @@ class HipSampler:
                          stream: Optional[torch.cuda.Stream] = None) -> None:
         """logits[b, tokens[j]] += values[j] for j in offsets[b]..offsets[b+1]
         (the formula of mlc_parity.rs:1060-1072), in place on [B, V] float32."""
-        if logits.dtype != torch.float32 or logits.dim() != 2 or logits.stride(1) != 1:
+        if logits.dtype != torch.float32 or not _rows(logits):
             raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT,
                                "logits must be a row-major float32 [batch, vocab] tensor")
         _on_device(logits.device, offsets=offsets, tokens=tokens, values=values)
@@ -323,7 +336,7 @@ class HipSampler:
         val = values.to(torch.float32).contiguous()
         st = self._stream(logits, stream)
         rc = self._lib.llmk_apply_logit_bias(self._h, logits.data_ptr(), logits.shape[0],
-                                             logits.shape[1], logits.stride(0), off.data_ptr(),
+                                             logits.shape[1], _row_stride(logits), off.data_ptr(),
                                              tok.data_ptr(), val.data_ptr(),
                                              ctypes.c_void_p(st.cuda_stream))
         if rc != 0:
@@ -399,8 +412,7 @@ class HipSampler:
                              ("draft_tokens", draft_tokens, _I32), ("u_accept", u_accept, _F32),
                              ("u_resample", u_resample, _F32)):
             _flat(name, t, dts)
-        if (draft_probs.dtype != torch.float32 or draft_probs.dim() != 2
-                or draft_probs.stride(1) != 1):
+        if draft_probs.dtype != torch.float32 or not _rows(draft_probs):
             raise SamplerError(_lib.LLMK_ERR_INVALID_ARGUMENT,
                                "draft_probs must be a row-major float32 [batch, >= vocab] tensor")
         if probs.shape != ids.shape or draft_probs.shape[0] != B or counts.numel() != B:
@@ -414,7 +426,7 @@ class HipSampler:
         st = self._stream(ids, stream)
         rc = self._lib.llmk_verify_batch(self._h, B, V, ids.data_ptr(), probs.data_ptr(), cap,
                                          counts.data_ptr(), draft_tokens.data_ptr(),
-                                         draft_probs.data_ptr(), draft_probs.stride(0),
+                                         draft_probs.data_ptr(), _row_stride(draft_probs),
                                          u_accept.data_ptr(), u_resample.data_ptr(),
                                          tok.data_ptr(), acc.data_ptr(),
                                          ctypes.c_void_p(st.cuda_stream))

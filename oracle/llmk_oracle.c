@@ -14,6 +14,21 @@
  *   sample                   :219-228  -> llmk_oracle_sample_simple()
  * Speculative verification (docs/mlc-contracts.md:83-84) -> llmk_oracle_verify_row().
  * Presence/frequency formula: llm-tests/tests/mlc_parity.rs:1074-1089.
+ *
+ * Provenance of the numerical methods restated here (exp, expm1, tanh):
+ *  - expf: the method and the exp2f_data constants (the 2^(i/32) table, the
+ *    cubic's coefficients) of Szabolcs Nagy's expf in Arm's
+ *    optimized-routines, which glibc 2.28 and later ship as
+ *    sysdeps/ieee754/flt-32/e_expf.c:
+ *      Copyright (c) 2017-2018, Arm Limited.
+ *      SPDX-License-Identifier: MIT
+ *  - expm1f, tanhf: fdlibm's method and coefficients, as glibc's
+ *    s_expm1f.c and s_tanhf.c carry them:
+ *      Copyright (C) 1993 by Sun Microsystems, Inc. All rights reserved.
+ *      Developed at SunPro, a Sun Microsystems, Inc. business.
+ *      Permission to use, copy, modify, and distribute this
+ *      software is freely granted, provided that this notice
+ *      is preserved.
  */
 #define _GNU_SOURCE
 #include "llmk_oracle.h"

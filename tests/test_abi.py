@@ -107,3 +107,20 @@ def test_sample_params_defaults_follow_types_rs():
     p = llmk.SampleParams()
     assert (p.temperature, p.top_p, p.top_k, p.repetition_penalty, p.max_new_tokens) == (1.0, 1.0, 0, 1.0, 512)
     assert (p.presence_penalty, p.frequency_penalty, p.min_p) == (0.0, 0.0, 0.0)
+
+
+def test_single_row_strides_are_read_as_packed():
+    """torch gives a size-1 dimension any stride (np.atleast_2d of a 1-D
+    array has stride 0 across rows): one row is read as packed, and a
+    one-column tensor needs no unit column stride."""
+    import numpy as np
+    import torch
+    from llmk import sampler as S
+    one = torch.from_numpy(np.atleast_2d(np.zeros(3, np.float32)))
+    assert one.stride(0) == 0
+    assert S._rows(one) and S._row_stride(one) == 3
+    assert S._row_stride(torch.zeros(4, 10)) == 10
+    assert S._row_stride(torch.zeros(8, 20)[:, 5:15]) == 20
+    col = torch.zeros(3, 5)[:, 2:3]
+    assert S._rows(col)
+    assert not S._rows(torch.zeros(5, 3).t())

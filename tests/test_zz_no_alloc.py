@@ -70,6 +70,36 @@ def test_static_matches_handle_on_two_calls(sampler):
             assert free1 == free0, f"device memory moved by {free0 - free1} bytes"
 
 
+def test_static_every_row_on_the_slow_path(sampler):
+    """256 rows that all take the slow path (top-k off, a nucleus of most of
+    the vocabulary) queue 32 deep on each of the static workspace's 8
+    slow-path slots, where the handle has a slot per row: the same results,
+    and no slot wait runs out (LLMK_STATUS_SLOT_TIMEOUT)."""
+    from gpu_util import workload
+    rng = np.random.default_rng(256)
+    B, V = 256, 151936
+    lg = rng.normal(0.0, 2.0, (B, V)).astype(np.float32)
+    hists = [rng.integers(0, V, 64) for _ in range(B)]
+    w = workload(lg, T=1.0, K=0, P=0.999, R=1.1, hists=hists,
+                 u=rng.random(B).astype(np.float32), name="slow256")
+    print(f"[case] static vs handle, every row slow, B={B} V={V}", flush=True)
+    db = w.to_device()
+    ref = outputs(B)
+    sampler.launch(db, *ref)
+    torch.cuda.synchronize()
+    assert sampler.status() == 0
+    got = outputs(B)
+    status = torch.zeros(1, dtype=torch.int32, device="cuda:0")
+    llmk.sample_batch_static(db, *got, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) & _lib.LLMK_STATUS_SLOT_TIMEOUT == 0
+    assert int(status.item()) == 0
+    h, r = host(got), host(ref)
+    assert_same(w, h, r, "slow256")
+    # the nuclei are wide: every kept list overflows the 64 entries returned
+    assert np.all(h[3] > 1000), "a row did not keep a wide nucleus"
+
+
 def test_static_status_word():
     """A NaN logit raises LLMK_STATUS_NAN_LOGITS in the caller's status word;
     the call without a status pointer drops the bits."""
