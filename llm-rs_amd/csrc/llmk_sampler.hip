@@ -95,6 +95,11 @@ constexpr uint32_t SLOW_BINS = 2048; // slow path: bins of the processed logits
 constexpr uint32_t EMPTY = 0xffffffffu;
 constexpr float NEG_INF = -__builtin_huge_valf();
 constexpr float LOG2E_F = 0x1.715476p+0f;  // the slow path's bins of (l - L)/T, in octaves
+// The exact S of rows that fail the band check, on many workgroups (phase 1)
+constexpr uint32_t XS_JOBS = 8;                        // rows per call
+constexpr uint32_t XS_W = 16 * TILE;                   // a window: 16 segments of a tile
+constexpr uint32_t XS_SAVE = 2 * MAX_SLOTS + 2 * LCAP;  // LDS partials + candidates
+constexpr uint32_t XS_JOB_WORDS = 32;
 
 // Words a workgroup passes from one phase to the next past the dynamic
 // shared memory, which each phase lays out afresh (static LDS).
@@ -129,6 +134,15 @@ struct Args {
   // (the mask form's no-op, not an invalid row)
   u4v* cut;
   uint32_t tp_clamp;
+  // 0: the sampling launch; 1: the launch after it that sums the reference's
+  // S, window by window on many workgroups, for the rows whose band check
+  // failed (up to xs_cap rows per call; the sampling launch does the rest
+  // itself)
+  uint32_t phase, xs_cap;
+  uint32_t xs_lds;  // phase 1's dynamic LDS in words
+  // the call's parity: its jobs are counted in xs_ctl[epoch & 1], and its
+  // sampling launch clears the other count for the next call
+  uint32_t epoch;
 };
 
 struct Ws {
@@ -144,6 +158,18 @@ struct Ws {
   u4v* cut;              // [max_batch]: apply_top_p's cut per row
   uint32_t* mtok;        // [max_batch]: apply_top_p's (unused) draws
   float* zu;             // [max_batch]: zeros, its uniforms
+  // the exact S of deferred rows (phase 1): jobs posted, workgroups done and
+  // per job its arrival count; the jobs; per job and window its sum and that
+  // sum's flag; per job and segment its pairs and terms; per job the
+  // single-segment row's LDS partials and candidates
+  uint32_t* xs_ctl;      // [2 + XS_JOBS]: job counts of even / odd calls, arrivals
+  uint32_t* xs_job;      // [XS_JOBS][XS_JOB_WORDS]
+  float* xs_wsum;        // [XS_JOBS][xs_maxw]
+  uint32_t* xs_wflag;    // [XS_JOBS][xs_maxw]
+  uint32_t* xs_meta;     // [XS_JOBS][xs_maxw * 16][8]
+  float* xs_terms;       // [XS_JOBS][xs_maxw * 16][TILE]
+  uint32_t* xs_save;     // [XS_JOBS][XS_SAVE]
+  uint32_t xs_maxw;
   uint32_t max_vocab;
   uint32_t slow_slots;   // min(max_batch, SLOW_SLOTS): rows b, b + slow_slots, ... share one
 };
@@ -3708,13 +3734,14 @@ __device__ __noinline__ void slow_row_mat(uint32_t b, RowP P, bool approx, bool 
                            (LDS uint32_t*)smem, approx, need_exact);
 }
 
-// Path 4 of finalize_rare: the reference's S, then the candidate path again
-// (or the slow path).  Returns true when the row's history outgrows the
-// tables (the materialised slow path then takes it).
+// Path 4 of finalize_rare: the reference's S (S_in when it is given, not
+// NaN, as the many-workgroup sum of phase 1 hands it over), then the
+// candidate path again (or the slow path).  Returns true when the row's
+// history outgrows the tables (the materialised slow path then takes it).
 template <int DT>
 __device__ __forceinline__ bool exact_rerun(const Args& a, const Ws& w, uint32_t b,
                                             const RowP& P, float m, float L, float u,
-                                            u4v seg_own, LDS uint32_t* sm) {
+                                            u4v seg_own, LDS uint32_t* sm, float S_in) {
   const uint32_t tid = threadIdx.x;
   LDS uint32_t* sc = sm;  // below the tables in both layouts
   const void* row = (const char*)a.logits +
@@ -3727,21 +3754,72 @@ __device__ __forceinline__ bool exact_rerun(const Args& a, const Ws& w, uint32_t
   hist_carve(h, a.G == 1 ? sm + 64 + M_NMISC + NBINS + 64 : sm + 128 + 256 + NW * 256 + SLOW_BINS,
              nwords);
   h.lo = 0;
-  if (tid == 0) sc[64] = 0;
-  build_history<DT>(a, P, b, row, 0, a.V, nwords, h, sc + 128, &sc[64]);
-  if (sc[64] & FLAG_HIST_OVERFLOW) return true;  // the whole row's history outgrows the tables
+  // The tables serve the normaliser and tell whether the whole row's history
+  // outgrows them.  With S given, a single-segment row needs neither: its
+  // one segment's tables held the whole row's history without overflow.
+  if (!(S_in == S_in && a.G == 1)) {
+    if (tid == 0) sc[64] = 0;
+    build_history<DT>(a, P, b, row, 0, a.V, nwords, h, sc + 128, &sc[64]);
+    if (sc[64] & FLAG_HIST_OVERFLOW) return true;  // the whole row's history outgrows them
+  }
   const float S =
-      exact_normaliser<DT>(row, a.mask ? a.mask + (uint64_t)b * a.mask_words : nullptr, a.V,
-                           P.T, m, h.bitmap, h.pre, h.pen, true, sc);
+      S_in == S_in
+          ? S_in
+          : exact_normaliser<DT>(row, a.mask ? a.mask + (uint64_t)b * a.mask_words : nullptr,
+                                 a.V, P.T, m, h.bitmap, h.pre, h.pen, true, sc);
   __syncthreads();
   const uint32_t path = candidate_paths<DT>(a, w, b, P, S, m, L, u, seg_own, false, sm);
   return path != 0 && slow_row<DT, false>(a, w, b, P, S, m, L, sm, false, false);
 }
 
+// Posts a row whose band check failed as a job of phase 1 (the launch after
+// this one sums its S on many workgroups and finishes the row): its
+// parameters, m, L, u, seg_own and, for a single-segment row, the LDS
+// partials and candidates the candidate path reads again.  False when the
+// call's xs_cap jobs are taken (the row is then finished here).
+__device__ __forceinline__ bool xs_post(const Args& a, const Ws& w, uint32_t b, const RowP& P,
+                                        float m, float L, float u, u4v seg_own,
+                                        LDS uint32_t* sm) {
+  const uint32_t tid = threadIdx.x;
+  if (a.xs_cap == 0) return false;  // no phase 1 in this call
+  if (tid == 0)
+    g_bcast[2] = __hip_atomic_fetch_add(&w.xs_ctl[a.epoch & 1u], 1u, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  const uint32_t j = g_bcast[2];
+  if (j >= a.xs_cap) return false;
+  GLB uint32_t* rec = G(w.xs_job) + (uint64_t)j * XS_JOB_WORDS;
+  if (tid == 0) {
+    rec[0] = b;
+    rec[1] = __float_as_uint(P.T);
+    rec[2] = __float_as_uint(P.top_p);
+    rec[3] = __float_as_uint(P.min_p);
+    rec[4] = __float_as_uint(P.rp);
+    rec[5] = __float_as_uint(P.pp);
+    rec[6] = __float_as_uint(P.fp);
+    rec[7] = (uint32_t)P.K;
+    rec[8] = P.mode;
+    rec[9] = P.Kc;
+    rec[10] = __float_as_uint(m);
+    rec[11] = __float_as_uint(L);
+    rec[12] = __float_as_uint(u);
+    rec[13] = seg_own.x;
+    rec[14] = seg_own.y;
+    rec[15] = seg_own.z;
+    rec[16] = seg_own.w;
+  }
+  if (a.G == 1) {
+    GLB uint32_t* sv = G(w.xs_save) + (uint64_t)j * XS_SAVE;
+    for (uint32_t i = tid; i < XS_SAVE; i += NT) sv[i] = sm[a.lds_part + i];
+  }
+  return true;  // the kernel's end orders these stores before phase 1
+}
+
 // The rows the candidate path did not finish (path: 2, the slow path; 4, a
 // row that top-k renormalises whose band check failed; 5, a row whose
 // history outgrows the LDS tables, which the slow path materialises, with
-// approx for a row that top-k renormalises).  For path 4 the reference's S
+// approx for a row that top-k renormalises; 6, a row of path 4 back from
+// phase 1 with the reference's S).  For path 4 the reference's S
 // (exact_normaliser, over the row's history tables, built again: the
 // candidate path has overwritten a single-segment row's own), then the
 // candidate path again in the reference's arithmetic, else the slow path.
@@ -3759,13 +3837,401 @@ __device__ __noinline__ void finalize_rare(uint32_t b, RowP P, float S, float m,
   LDS uint32_t* sm = (LDS uint32_t*)smem;
   // mat: the row goes to the materialised slow path (one call, at the end)
   bool mat = path == 5;
-  if (!mat && path != 4) {
+  if (!mat && path != 4 && path != 6) {
     mat = slow_row<DT, false>(a, w, b, P, S, m, L, sm, approx, false);
   } else if (!mat) {
-    mat = exact_rerun<DT>(a, w, b, P, m, L, u, seg_own, sm);
+    if (path == 4 && a.phase == 0 && xs_post(a, w, b, P, m, L, u, seg_own, sm)) return;
+    mat = exact_rerun<DT>(a, w, b, P, m, L, u, seg_own, sm, path == 6 ? S : __builtin_nanf(""));
     approx = false;
   }
   if (mat) slow_row_mat<DT>(b, P, approx, !approx);
+}
+
+// ---------------------------------------------------------------------------
+// Phase 1: the reference's S of the rows whose band check failed, on many
+// workgroups
+// ---------------------------------------------------------------------------
+// The launch after the sampling launch, grid xs_cap x nwin: workgroup (j, k)
+// takes window k (XS_W elements) of job j's row; the last window of a job
+// to finish walks the windows and finishes the row.  A window:
+//   * its processed logits (history tables of its own range, the mask) and
+//     the exact terms e = exp_ref(fl(l / T) - m) of all its elements, whose
+//     f32 sum A_k it publishes (release) for the windows after it;
+//   * the sums of the windows before it (acquire; they run beside it: the
+//     grid fits the GPU, one workgroup a CU, and a wait that runs out drops
+//     only the estimate) give the exact sequential sum at its start c_k to
+//     within a relative (window end) n u: recursive f32 summation of
+//     positive terms is off by at most u per addition of the sum so far,
+//     and each A_i by n_i u of its own;
+//   * from that lower bound the terms that cannot change the sum (below
+//     half its quantum) are dropped, each segment packs or keeps its live
+//     terms and forms its pairs in the binades its running sum can occupy,
+//     exactly as exact_normaliser does within one workgroup, and publishes
+//     them with its terms.
+// The walker, wave 0 of the job's last workgroup, then sums the segments in
+// order with the exact running sum: runs covered by pairs at once, the
+// others lane by lane from their published terms (wave_sum_q).  The sum is
+// exact whatever the estimates.  Then the row's candidate path runs again
+// with that S (finalize_rare, path 6), its LDS partials and candidates
+// restored first.
+constexpr uint32_t XS_SPIN = 1u << 16;
+template <int DT>
+__device__ __noinline__ void xs_phase() {
+  extern __shared__ __align__(16) uint32_t smem[];
+  const KCtx kc = kctx_load();
+  const Args& a = kc.a;
+  const Ws& w = kc.w;
+  LDS uint32_t* sm = (LDS uint32_t*)smem;
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  const uint32_t wv = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));
+  const uint32_t nwin = (a.V + XS_W - 1) / XS_W;
+  const uint32_t j = blockIdx.x / nwin, k = blockIdx.x % nwin;
+  {
+    const GLB uint32_t* rec = G(w.xs_job) + (uint64_t)j * XS_JOB_WORDS;
+    if (tid < 17) sm[tid] = rec[tid];
+    __syncthreads();
+    auto sw = [&](uint32_t i) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)sm[i]); };
+    const uint32_t b = sw(0);
+    RowP P;
+    P.T = __uint_as_float(sw(1));
+    P.top_p = __uint_as_float(sw(2));
+    P.min_p = __uint_as_float(sw(3));
+    P.rp = __uint_as_float(sw(4));
+    P.pp = __uint_as_float(sw(5));
+    P.fp = __uint_as_float(sw(6));
+    P.K = (int32_t)sw(7);
+    P.mode = sw(8);
+    P.Kc = sw(9);
+    const float m = __uint_as_float(sw(10)), L = __uint_as_float(sw(11));
+    const float u = __uint_as_float(sw(12));
+    const u4v seg_own = u4v{sw(13), sw(14), sw(15), sw(16)};
+    __syncthreads();
+    const uint32_t maxw = w.xs_maxw;
+    GLB float* wsum = G(w.xs_wsum) + (uint64_t)j * maxw;
+    GLB uint32_t* wflag = G(w.xs_wflag) + (uint64_t)j * maxw;
+    GLB uint32_t* meta = G(w.xs_meta) + (uint64_t)j * maxw * 16 * 8;
+    GLB float* terms = G(w.xs_terms) + (uint64_t)j * maxw * 16 * TILE;
+    const void* row = (const char*)a.logits +
+                      (uint64_t)b * a.stride * ((DT & 3) == LLMK_F32 ? 4u : 2u);
+    const GLB uint32_t* mrow = a.mask ? G(a.mask) + (uint64_t)b * a.mask_words : nullptr;
+    // ---- the window
+    // LDS: [0, 64) reductions, 64 flags, [128, 192) the history build's
+    // scan, [256, ...) the window's history tables, then the packed terms
+    constexpr uint32_t HW = XS_W / 32;
+    LDS float* segw = (LDS float*)(sm + 200);   // [NW] all terms
+    LDS float* segl = (LDS float*)(sm + 216);   // [NW] live terms
+    LDS uint32_t* hb = sm + 256;
+    LDS float* comp = (LDS float*)(hb + hist_lds_words(HW)) + XS_CW * wv;
+    const uint32_t lo = k * XS_W, hi = umin(lo + XS_W, a.V);
+    Hist h;
+    hist_carve(h, hb, HW);
+    h.lo = lo;
+    // the window's logits requested first, the history tables built meanwhile
+    const uint32_t e0 = lo + 16 * tid;
+    float x[16];
+    load16<DT>(row, e0, a.V, x);
+    const uint32_t mw = (mrow && e0 < a.V) ? mrow[e0 >> 5] >> (e0 & 16u) : 0xffffffffu;
+    if (tid == 0) sm[64] = 0;
+    build_history<DT>(a, P, b, row, lo, hi, HW, h, sm + 128, &sm[64]);
+    const uint32_t hw = e0 < a.V ? h.bitmap[(e0 - lo) >> 5] >> (e0 & 16u) : 0u;
+    float e[16];
+    float ls = 0.0f;
+#pragma unroll
+    for (uint32_t q = 0; q < 16; ++q) {
+      float v = x[q];
+      if ((hw >> q) & 1u) v = h.pen[h.rank(e0 + q)];
+      if (!((mw >> q) & 1u) || !(v > NEG_INF)) v = NEG_INF;
+      const float l = (P.T != 1.0f) ? v / P.T : v;
+      e[q] = (l == NEG_INF) ? 0.0f : exp_ref<true>(l - m);
+      ls += e[q];
+    }
+    ls = wave_tree_sum(ls);
+    if (lane == 0) segw[wv] = ls;
+    __syncthreads();
+    if (tid == 0) {
+      float A = 0.0f;
+      for (uint32_t i = 0; i < (uint32_t)NW; ++i) A += segw[i];
+      wsum[k] = A;
+      __hip_atomic_store(&wflag[k], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // ---- the sums before this window (wave 0), then the bounds on c_k
+    if (wv == 0) {
+      double pre = 0.0;
+      uint32_t ok = 1;
+      for (uint32_t i0 = 0; i0 < k && ok; i0 += WAVE) {
+        const uint32_t i = i0 + lane;
+        bool have = i >= k;
+        for (uint32_t n = 0; __ballot(!have) != 0ull; ++n) {
+          if (n == XS_SPIN) {
+            ok = 0;
+            break;
+          }
+          if (!have)
+            have = __hip_atomic_load(&wflag[i], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+          if (__ballot(!have) != 0ull) __builtin_amdgcn_s_sleep(2);
+        }
+        if (!ok) break;
+        double v = i < k ? (double)wsum[i] : 0.0;
+        v = v + dppd<0x111, 0xf, true>(v);
+        v = v + dppd<0x112, 0xf, true>(v);
+        v = v + dppd<0x114, 0xf, true>(v);
+        v = v + dppd<0x118, 0xf, true>(v);
+        v = v + dppd<0x142, 0xa, false>(v);
+        v = v + dppd<0x143, 0xc, false>(v);
+        pre += readlane_d(v, 63);
+      }
+      if (lane == 0) {
+        sm[66] = ok;
+        sm[68] = (uint32_t)__double_as_longlong(pre);
+        sm[69] = (uint32_t)((uint64_t)__double_as_longlong(pre) >> 32);
+      }
+    }
+    __syncthreads();
+    const double pre = __longlong_as_double((long long)(((uint64_t)sm[69] << 32) | sm[68]));
+    double clo = 0.0, chi = 0.0;  // window 0 starts at 0 exactly
+    if (k > 0) {
+      if (sm[66]) {
+        const double d = (double)(lo + XS_W) * 0x1p-24 * 2.02 + 0x1p-30;
+        clo = pre * (1.0 - d);
+        chi = pre * (1.0 + d);
+      } else {
+        chi = __builtin_huge_val();  // no estimate: nothing dropped, no pairs
+      }
+    }
+    // ---- the live terms: an e below half the quantum of c_k's lowest
+    // possible binade adds nothing (c only grows)
+    const float lim = clo >= 0x1p-126 ? (float)__builtin_ldexp(1.0, binade_d(clo) - 24) : 0.0f;
+    uint32_t live = 0;
+#pragma unroll
+    for (uint32_t q = 0; q < 16; ++q)
+      if (e[q] > 0.0f && !(e[q] < lim)) live |= 1u << q;
+    const uint32_t n = (uint32_t)__popc(live);
+    const uint32_t incl = wave_incl_scan(n);
+    const uint32_t nw = bcast63u(incl);
+    const bool packed = nw <= XS_CW;
+    float pk[4];
+    if (packed) {
+      uint32_t at = incl - n;
+#pragma unroll
+      for (uint32_t q = 0; q < 16; ++q)
+        if ((live >> q) & 1u) comp[at++] = e[q];
+      WaveSync::sync();
+      const f4v v4 = ((LDS const f4v*)comp)[lane];
+      pk[0] = 4 * lane + 0 < nw ? v4.x : 0.0f;
+      pk[1] = 4 * lane + 1 < nw ? v4.y : 0.0f;
+      pk[2] = 4 * lane + 2 < nw ? v4.z : 0.0f;
+      pk[3] = 4 * lane + 3 < nw ? v4.w : 0.0f;
+    } else {
+#pragma unroll
+      for (uint32_t q = 0; q < 16; ++q)
+        if (!((live >> q) & 1u)) e[q] = 0.0f;
+    }
+    const uint32_t sbase = lo + TILE * wv;
+    const uint32_t nseg = packed ? nw : (sbase < a.V ? umin(TILE, a.V - sbase) : 0u);
+    float ll = 0.0f;
+    if (packed) {
+      ll = (pk[0] + pk[1]) + (pk[2] + pk[3]);
+    } else {
+#pragma unroll
+      for (uint32_t q = 0; q < 16; ++q) ll += e[q];
+    }
+    ll = wave_tree_sum(ll);
+    if (lane == 0) segl[wv] = ll;
+    __syncthreads();
+    double blo = clo, bhi = chi;
+    for (uint32_t i = 0; i < wv; ++i) {
+      blo += (double)segl[i];
+      bhi += (double)segl[i];
+    }
+    const double drift = (double)(TILE * (wv + 1)) * 0x1p-24 * 1.01 + 0x1p-19;
+    const double plo = blo * (1.0 - drift), phi = (bhi + (double)segl[wv]) * (1.0 + drift);
+    uint32_t hdr = 0;
+    Par pr[XS_NB];
+#pragma unroll
+    for (uint32_t q = 0; q < XS_NB; ++q) pr[q] = Par{0u, 0u};
+    if (plo >= 0x1p-126 && phi < 0x1p120) {
+      const int elo = binade_d(plo), ehi = binade_d(phi);
+      const int nb = ehi - elo + 1;
+      if (nb <= (int)XS_NB) {
+#pragma unroll
+        for (int q = 0; q < (int)XS_NB; ++q) {
+          if (q < nb) {
+            const Par y = packed ? wave_par_incl_sat(lane_pair<4>(pk, elo + q))
+                                 : wave_par_incl_sat(lane_pair<16>(e, elo + q));
+            pr[q] = Par{(uint32_t)__builtin_amdgcn_readlane((int)y.a0, 63),
+                        (uint32_t)__builtin_amdgcn_readlane((int)y.a1, 63)};
+          }
+        }
+        hdr = (uint32_t)(elo + 256) | ((uint32_t)nb << 16);
+      }
+    }
+    // ---- publish the segment: header, pairs, count, terms
+    const uint32_t sg = 16 * k + wv;
+    GLB uint32_t* mt = meta + (uint64_t)sg * 8;
+    GLB float* tt = terms + (uint64_t)sg * TILE;
+    if (lane == 0) {
+      mt[0] = hdr;
+#pragma unroll
+      for (uint32_t q = 0; q < XS_NB; ++q) {
+        mt[1 + 2 * q] = pr[q].a0;
+        mt[2 + 2 * q] = pr[q].a1;
+      }
+      mt[7] = nseg | (packed ? 0x80000000u : 0u);
+    }
+    if (packed) {
+      *(GLB f4v*)(tt + 4 * lane) = f4v{pk[0], pk[1], pk[2], pk[3]};
+    } else {
+#pragma unroll
+      for (uint32_t q = 0; q < 16; q += 4)
+        *(GLB f4v*)(tt + 16 * lane + q) = f4v{e[q], e[q + 1], e[q + 2], e[q + 3]};
+    }
+    // the barrier gathers every wave's stores in this CU's caches; thread 0's
+    // arrival then releases them (a write-back of the cache) and, for the
+    // last window, acquires the others' (an invalidation the whole
+    // workgroup's loads see); one fence per workgroup, not one per wave
+    __syncthreads();
+    if (tid == 0)
+      sm[70] = __hip_atomic_fetch_add(&w.xs_ctl[2 + j], 1u, __ATOMIC_ACQ_REL,
+                                      __HIP_MEMORY_SCOPE_AGENT) == nwin - 1
+                   ? 1u
+                   : 0u;
+    __syncthreads();
+    if (sm[70]) {
+      // ---- the walker: every window's segments, in order
+      const uint32_t ns = 16 * nwin;
+      LDS uint32_t* segp = sm + 256;         // [ns][8]
+      LDS uint32_t* pfs = segp + ns * 8;     // [ns]: LDS copy of a segment's terms, or EMPTY
+      LDS uint32_t* pfl = pfs + ns;          // [ns]: the segment of each copy
+      LDS float* pf = (LDS float*)(pfl + ns);  // [npf][TILE]
+      const uint32_t npf = (a.xs_lds - (256 + 10 * ns)) / TILE;
+      // the segments' headers and the terms of window 0's segments, in one
+      // round of loads: from a sum that starts at zero, window 0 crosses a
+      // binade at each doubling, so the walk sums most of its segments lane
+      // by lane
+      const uint32_t n0 = umin(16u, npf);
+      {
+        uint32_t mv[8];
+        float tv[16];
+#pragma unroll
+        for (uint32_t q = 0; q < 8; ++q) {
+          const uint32_t i = tid + q * NT;
+          mv[q] = i < ns * 8 ? meta[i] : 0u;
+        }
+#pragma unroll
+        for (uint32_t q = 0; q < 16; ++q) tv[q] = q < n0 ? terms[q * TILE + tid] : 0.0f;
+#pragma unroll
+        for (uint32_t q = 0; q < 8; ++q) {
+          const uint32_t i = tid + q * NT;
+          if (i < ns * 8) segp[i] = mv[q];
+        }
+#pragma unroll
+        for (uint32_t q = 0; q < 16; ++q)
+          if (q < n0) pf[q * TILE + tid] = tv[q];
+      }
+      __syncthreads();
+      // then the other segments without pairs, as many as fit (the rest
+      // are read when the walk reaches them)
+      if (wv == 0) {
+        uint32_t used = n0;
+        for (uint32_t s0 = 0; s0 < ns; s0 += WAVE) {
+          const uint32_t si = s0 + lane;
+          const bool want = si >= n0 && si < ns && (segp[8 * si] >> 16) == 0u;
+          const uint32_t r = used + (uint32_t)__popcll(__ballot(want) & ((1ull << lane) - 1ull));
+          if (si < n0) pfs[si] = si;
+          else if (si < ns) pfs[si] = (want && r < npf) ? r : EMPTY;
+          if (want && r < npf) pfl[r] = si;
+          used += (uint32_t)__popcll(__ballot(want));
+        }
+        if (lane == 0) sm[72] = umin(used, npf);
+      }
+      __syncthreads();
+      const uint32_t nused = sm[72];
+      // eight segments' loads in flight before their stores (thread t copies
+      // element t of each; past a segment's count the copy is never read)
+      for (uint32_t s0 = n0; s0 < nused; s0 += 8) {
+        float v[8];
+#pragma unroll
+        for (uint32_t q = 0; q < 8; ++q)
+          v[q] = s0 + q < nused ? terms[(uint64_t)pfl[s0 + q] * TILE + tid] : 0.0f;
+#pragma unroll
+        for (uint32_t q = 0; q < 8; ++q)
+          if (s0 + q < nused) pf[(s0 + q) * TILE + tid] = v[q];
+      }
+      __syncthreads();
+      if (wv == 0) {
+        float cc = 0.0f;
+        uint32_t s = 0;
+        while (s < ns) {
+          if (__float_as_uint(cc) >= 0x00800000u) {
+            const int eb = binade_of(cc);
+            const uint32_t C = (uint32_t)__builtin_ldexpf(cc, 23 - eb);
+            const uint32_t js = s + lane;
+            Par px = Par{XS_SAT, XS_SAT};
+            if (js < ns) {
+              const uint32_t hj = segp[8 * js];
+              const int q = eb - ((int)(hj & 0xffffu) - 256);
+              if ((hj >> 16) != 0u && q >= 0 && q < (int)(hj >> 16))
+                px = Par{segp[8 * js + 1 + 2 * q], segp[8 * js + 2 + 2 * q]};
+            }
+            const Par in = wave_par_incl_sat(px);
+            const uint32_t inc = (C & 1u) ? in.a1 : in.a0;
+            const uint64_t good = __ballot(js < ns && C + inc < XS_SAT);
+            const uint32_t g = ~good == 0ull ? 64u : (uint32_t)__builtin_ctzll(~good);
+            if (g > 0) {
+              const uint32_t ig = (uint32_t)__builtin_amdgcn_readlane((int)inc, (int)g - 1);
+              cc = __builtin_ldexpf((float)(C + ig), eb - 23);
+              s += g;
+              continue;
+            }
+          }
+          // segment s lane by lane, from its published terms (their LDS
+          // copy when it has one)
+          const uint32_t mts = segp[8 * s + 7];
+          const uint32_t cnt = mts & 0x7fffffffu;
+          const uint32_t slot = pfs[s];
+          const GLB float* ts = terms + (uint64_t)s * TILE;
+          LDS const float* tl = pf + (uint64_t)(slot == EMPTY ? 0u : slot) * TILE;
+          if (mts >> 31) {
+            float p4[4];
+            const f4v v4 = slot != EMPTY ? *(LDS const f4v*)(tl + 4 * lane)
+                                         : *(const GLB f4v*)(ts + 4 * lane);
+            p4[0] = 4 * lane + 0 < cnt ? v4.x : 0.0f;
+            p4[1] = 4 * lane + 1 < cnt ? v4.y : 0.0f;
+            p4[2] = 4 * lane + 2 < cnt ? v4.z : 0.0f;
+            p4[3] = 4 * lane + 3 < cnt ? v4.w : 0.0f;
+            cc = wave_sum_q<4>(cc, p4, cnt);
+          } else {
+            float p16[16];
+#pragma unroll
+            for (uint32_t q = 0; q < 16; q += 4) {
+              const f4v v4 = slot != EMPTY ? *(LDS const f4v*)(tl + 16 * lane + q)
+                                           : *(const GLB f4v*)(ts + 16 * lane + q);
+              p16[q] = v4.x;
+              p16[q + 1] = v4.y;
+              p16[q + 2] = v4.z;
+              p16[q + 3] = v4.w;
+            }
+            cc = wave_sum_q<16>(cc, p16, cnt);
+          }
+          ++s;
+        }
+        if (lane == 0) sm[71] = __float_as_uint(cc);
+      }
+      __syncthreads();
+      const float S = __uint_as_float(sm[71]);
+      // the job's counters back to zero for the next call
+      if (tid == 0) __hip_atomic_store(&w.xs_ctl[2 + j], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (uint32_t i = tid; i < nwin; i += NT) wflag[i] = 0u;
+      __syncthreads();
+      // the row's LDS partials and candidates, then its candidate path
+      if (a.G == 1) {
+        const GLB uint32_t* sv = G(w.xs_save) + (uint64_t)j * XS_SAVE;
+        for (uint32_t i = tid; i < XS_SAVE; i += NT) sm[a.lds_part + i] = sv[i];
+      }
+      __syncthreads();
+      finalize_rare<DT>(b, P, S, m, L, u, seg_own, false, 6u);
+    }
+  }
 }
 
 // seg_own: for a single-segment row, this workgroup's (count, beta, flags);
@@ -4154,6 +4620,28 @@ __device__ __forceinline__ void vtile_chunk(const Args& a, uint32_t t0, uint32_t
 template <int DT>
 __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   extern __shared__ __align__(16) uint32_t smem[];
+  if (a.phase) {
+    // The launch after the sampling launch: the S of the rows whose band
+    // check failed.  Most calls have none; a workgroup without a job ends
+    // here, before any call (a call saves the callee's registers).
+    const uint32_t nwin = (a.V + XS_W - 1) / XS_W;
+    if (threadIdx.x == 0)
+      g_bcast[2] = __hip_atomic_load(&w.xs_ctl[a.epoch & 1u], __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (blockIdx.x / nwin < umin(g_bcast[2], a.xs_cap)) {
+      exp_tab_init();
+      softcap_init<DT>(a);
+      kctx_fill();
+      __syncthreads();
+      xs_phase<DT>();
+    }
+    return;
+  }
+  // the next call's job count starts at zero (nothing reads it in this call)
+  if (blockIdx.x == 0 && threadIdx.x == 0)
+    __hip_atomic_store(&w.xs_ctl[(a.epoch + 1u) & 1u], 0u, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
   const uint32_t tid = threadIdx.x;
   const int lane = (int)(tid & 63);
   const int wv = __builtin_amdgcn_readfirstlane((int)(tid >> 6));  // wave-uniform
@@ -5128,6 +5616,7 @@ struct llmk_sampler {
   size_t mem_bytes;
   void* stage;         // aligned copies of rows passed at any offset (allocated on demand)
   size_t stage_bytes;
+  uint32_t epoch;      // calls made (their parity picks the job count)
 };
 
 static thread_local std::string g_last_error;
@@ -5159,8 +5648,10 @@ static constexpr size_t LDS_DYN_MAX = 160 * 1024 - 1024;
 // logits, pool workgroup entries and `slots` slow-path slots: byte offsets
 // of its arrays in one 256-byte aligned block.
 struct WsLayout {
-  size_t arrive, part, meta, cand, lock, skeys, sp, si, status, cut, mtok, zu, total;
+  size_t arrive, part, meta, cand, lock, skeys, sp, si, status, cut, mtok, zu;
+  size_t xctl, xjob, xwsum, xwflag, xmeta, xterms, xsave, total;
 };
+static constexpr uint32_t xs_maxw(uint32_t mv) { return (mv + XS_W - 1) / XS_W; }
 static constexpr WsLayout ws_layout(uint32_t mb, uint32_t mv, uint32_t pool, uint32_t slots) {
   WsLayout L{};
   size_t off = 0;
@@ -5176,6 +5667,14 @@ static constexpr WsLayout ws_layout(uint32_t mb, uint32_t mv, uint32_t pool, uin
   L.cut = off; off = align_up(off + 16ull * mb, 256);
   L.mtok = off; off = align_up(off + 4ull * mb, 256);
   L.zu = off; off = align_up(off + 4ull * mb, 256);
+  const uint64_t mw = xs_maxw(mv);
+  L.xctl = off; off = align_up(off + 4ull * (2 + XS_JOBS), 256);
+  L.xjob = off; off = align_up(off + 4ull * XS_JOBS * XS_JOB_WORDS, 256);
+  L.xwsum = off; off = align_up(off + 4ull * XS_JOBS * mw, 256);
+  L.xwflag = off; off = align_up(off + 4ull * XS_JOBS * mw, 256);
+  L.xmeta = off; off = align_up(off + 4ull * XS_JOBS * mw * 16 * 8, 256);
+  L.xterms = off; off = align_up(off + 4ull * XS_JOBS * mw * 16 * TILE, 256);
+  L.xsave = off; off = align_up(off + 4ull * XS_JOBS * XS_SAVE, 256);
   L.total = off;
   return L;
 }
@@ -5193,6 +5692,14 @@ static Ws ws_carve(char* base, const WsLayout& L, uint32_t mv, uint32_t slots) {
   w.cut = (u4v*)(base + L.cut);
   w.mtok = (uint32_t*)(base + L.mtok);
   w.zu = (float*)(base + L.zu);
+  w.xs_ctl = (uint32_t*)(base + L.xctl);
+  w.xs_job = (uint32_t*)(base + L.xjob);
+  w.xs_wsum = (float*)(base + L.xwsum);
+  w.xs_wflag = (uint32_t*)(base + L.xwflag);
+  w.xs_meta = (uint32_t*)(base + L.xmeta);
+  w.xs_terms = (float*)(base + L.xterms);
+  w.xs_save = (uint32_t*)(base + L.xsave);
+  w.xs_maxw = xs_maxw(mv);
   w.max_vocab = mv;
   w.slow_slots = slots;
   return w;
@@ -5292,9 +5799,13 @@ static float dtype_round(double x, int fmt) {
 // One sampling launch on workspace ws, sized for batches up to max_batch rows
 // of up to max_vocab logits with `pool` workgroup entries, on the current
 // device.
+// Phase 1 runs when it can pay for its launch (about 4 us): the call has
+// top-k rows (only they are deferred) and at least XS_MIN_BATCH rows (at a
+// few thousandths of rows failing the band check, fewer rows rarely have one).
+constexpr uint32_t XS_MIN_BATCH = 16;
 static int sample_batch_run(const Ws& ws, uint32_t max_batch, uint32_t max_vocab, uint32_t pool,
                             const llmk_sample_batch_args* in, void* stream, u4v* cut,
-                            uint32_t tp_clamp) {
+                            uint32_t tp_clamp, uint32_t epoch) {
   if (!in) return fail(LLMK_ERR_INVALID_ARGUMENT, "args is NULL");
   if (in->vocab == 0) return fail(LLMK_ERR_EMPTY_LOGITS, "Empty logits passed to sampler");
   if (in->batch == 0) return fail(LLMK_ERR_INVALID_ARGUMENT, "batch is 0");
@@ -5357,6 +5868,14 @@ static int sample_batch_run(const Ws& ws, uint32_t max_batch, uint32_t max_vocab
   a.out_cap = in->out_cap;
   a.cut = cut;
   a.tp_clamp = tp_clamp;
+  a.phase = 0;
+  // phase 1's grid (jobs x windows) fits the GPU at one workgroup a CU, so
+  // a window's wait for the sums before it always ends
+  const uint32_t nwin = xs_maxw(in->vocab);
+  const bool phase1 = in->top_k != nullptr && in->batch >= XS_MIN_BATCH;
+  a.xs_cap = !phase1 ? 0u : (256 / nwin < XS_JOBS ? 256 / nwin : XS_JOBS);
+  a.xs_lds = 0;
+  a.epoch = epoch;
   a.ntiles = (a.V + TILE - 1) / TILE;
   a.nchunks = (a.ntiles + CHUNK_TILES - 1) / CHUNK_TILES;
   // Segments per row: enough workgroups to cover the 256 CUs, whole 16-tile
@@ -5383,19 +5902,32 @@ static int sample_batch_run(const Ws& ws, uint32_t max_batch, uint32_t max_vocab
   const size_t lds = 4 * words;
   if (lds > LDS_DYN_MAX)
     return fail(LLMK_ERR_CAPACITY, "vocabulary too large for one workgroup's LDS tables");
-  const dim3 grid(a.B * a.G), block(NT);
   const bool sc = in->softcap > 0.0f;
-  if (a.dtype == LLMK_F32) {
-    if (sc) hipLaunchKernelGGL(stream_kernel<LLMK_F32 | SOFTCAP>, grid, block, lds, st, a, ws);
-    else hipLaunchKernelGGL(stream_kernel<LLMK_F32>, grid, block, lds, st, a, ws);
-  } else if (a.dtype == LLMK_BF16) {
-    if (sc) hipLaunchKernelGGL(stream_kernel<LLMK_BF16 | SOFTCAP>, grid, block, lds, st, a, ws);
-    else hipLaunchKernelGGL(stream_kernel<LLMK_BF16>, grid, block, lds, st, a, ws);
-  } else {
-    if (sc) hipLaunchKernelGGL(stream_kernel<LLMK_F16 | SOFTCAP>, grid, block, lds, st, a, ws);
-    else hipLaunchKernelGGL(stream_kernel<LLMK_F16>, grid, block, lds, st, a, ws);
-  }
+  auto launch = [&](const Args& x, dim3 grid, size_t bytes) {
+    const dim3 block(NT);
+    if (x.dtype == LLMK_F32) {
+      if (sc) hipLaunchKernelGGL(stream_kernel<LLMK_F32 | SOFTCAP>, grid, block, bytes, st, x, ws);
+      else hipLaunchKernelGGL(stream_kernel<LLMK_F32>, grid, block, bytes, st, x, ws);
+    } else if (x.dtype == LLMK_BF16) {
+      if (sc) hipLaunchKernelGGL(stream_kernel<LLMK_BF16 | SOFTCAP>, grid, block, bytes, st, x, ws);
+      else hipLaunchKernelGGL(stream_kernel<LLMK_BF16>, grid, block, bytes, st, x, ws);
+    } else {
+      if (sc) hipLaunchKernelGGL(stream_kernel<LLMK_F16 | SOFTCAP>, grid, block, bytes, st, x, ws);
+      else hipLaunchKernelGGL(stream_kernel<LLMK_F16>, grid, block, bytes, st, x, ws);
+    }
+  };
+  launch(a, dim3(a.B * a.G), lds);
   HIPCHK(hipGetLastError());
+  // phase 1: the S of the rows whose band check failed (most calls have
+  // none: each workgroup then reads the job count and ends)
+  if (phase1) {
+    Args a1 = a;
+    a1.phase = 1;
+    const size_t lds1 = 4 * (256 + hist_lds_words(XS_W / 32) + NW * XS_CW);
+    a1.xs_lds = (uint32_t)((lds > lds1 ? lds : lds1) / 4);
+    launch(a1, dim3(a.xs_cap * nwin), 4 * (size_t)a1.xs_lds);
+    HIPCHK(hipGetLastError());
+  }
   return LLMK_OK;
 }
 
@@ -5450,9 +5982,15 @@ static int sample_batch_impl(llmk_sampler* s, const llmk_sample_batch_args* in,
     llmk_sample_batch_args al = *in;
     al.logits = s->stage;
     al.row_stride = dstride;
-    return sample_batch_run(s->ws, s->max_batch, s->max_vocab, pool, &al, stream, cut, tp_clamp);
+    const int rc = sample_batch_run(s->ws, s->max_batch, s->max_vocab, pool, &al, stream, cut,
+                                    tp_clamp, s->epoch);
+    if (rc == LLMK_OK) ++s->epoch;  // the parity advances with the launches only
+    return rc;
   }
-  return sample_batch_run(s->ws, s->max_batch, s->max_vocab, pool, in, stream, cut, tp_clamp);
+  const int rc = sample_batch_run(s->ws, s->max_batch, s->max_vocab, pool, in, stream, cut,
+                                  tp_clamp, s->epoch);
+  if (rc == LLMK_OK) ++s->epoch;
+  return rc;
 }
 
 extern "C" int llmk_sample_batch(llmk_sampler* s, const llmk_sample_batch_args* in,
@@ -5487,11 +6025,12 @@ static char* g_static_ptr[STATIC_MAX_DEVICES];  // device address of scratch, pe
 // be captured in a HIP graph).
 __global__ __launch_bounds__(256) void static_clear_kernel(uint32_t* arrive, uint32_t n_arrive,
                                                            uint32_t* lock, uint32_t n_lock,
-                                                           uint32_t* status) {
+                                                           uint32_t* status, uint32_t* xs_ctl) {
   const uint32_t i = blockIdx.x * 256 + threadIdx.x;
   if (i < n_arrive) arrive[i] = 0;
   if (i < n_lock) lock[i] = 0;
   if (i == 0) status[0] = 0;
+  if (i < 2 + XS_JOBS) xs_ctl[i] = 0;
 }
 
 // Device address of this device's scratch array, looked up (and the
@@ -5528,11 +6067,13 @@ extern "C" int llmk_sample_batch_static(const llmk_sample_batch_args* in, uint32
   Ws ws = ws_carve(base, STATIC_LAYOUT, STATIC_MAX_VOCAB, STATIC_SLOTS);
   hipStream_t st = (hipStream_t)stream;
   hipLaunchKernelGGL(static_clear_kernel, dim3((STATIC_MAX_BATCH + 255) / 256), dim3(256), 0, st,
-                     ws.row_arrive, STATIC_MAX_BATCH, ws.slow_lock, STATIC_SLOTS, ws.status);
+                     ws.row_arrive, STATIC_MAX_BATCH, ws.slow_lock, STATIC_SLOTS, ws.status,
+                     ws.xs_ctl);
   HIPCHK(hipGetLastError());
   if (status) ws.status = status;
+  // the clear kernel zeroed both job counts: every call can use parity 0
   return sample_batch_run(ws, STATIC_MAX_BATCH, STATIC_MAX_VOCAB, STATIC_POOL, in, stream,
-                          nullptr, 0u);
+                          nullptr, 0u, 0u);
 }
 
 // Checks shared by the mask forms: in-place f32 rows.
