@@ -14,13 +14,11 @@
 //              runs of 4 consecutive tokens, a bf16/f16 lane 2 runs of 8
 //              (one 16-byte load per run).  Per tile: history
 //              tokens take their penalised value, the allow-mask applies, and
-//              the wave computes the tile max and the tile's share of the
-//              softmax normaliser sum 2^((l - max) log2(e)/T) with a DPP
-//              balanced-tree sum — or the tile argmax for greedy rows — and
-//              appends top candidates above a rising threshold kept in an LDS
-//              histogram of the logits' order-preserving keys.
+//              the wave computes the tile max (or the tile argmax for greedy
+//              rows) and appends top candidates above a rising threshold
+//              kept in an LDS histogram of the logits' order-preserving keys.
 //   * finalize the last workgroup of the row (arrival counter when a row spans
-//              several workgroups) merges the tile partials into the
+//              several workgroups) merges the tile maxima, takes the
 //              normaliser S, computes exact probabilities of the candidates,
 //              ranks them by (p desc, idx asc), proves no other token can
 //              precede the ones used, and runs min-p / top-k / top-p / the
@@ -28,7 +26,10 @@
 //              reference's sequential f32 S (the exact normaliser); top-k
 //              rows take S = 1 only where a rounding-band check proves every
 //              decision (min-p cut, top-k set, top-p cut, draw) to be the
-//              reference's whatever S is, else the exact S and a rerun.
+//              reference's whatever S is, else the exact S and a rerun: the
+//              launch after this one (phase 1, xs_phase) sums that S over
+//              the row's 16384-element windows on many workgroups, and the
+//              last of them runs the row's candidate path again.
 //   * slow     rows the candidate path cannot prove exact (top-k = 0 with a
 //              large nucleus, candidate overflow, fully masked rows) are done
 //              by the same workgroup: exact probabilities of the whole row,
