@@ -4616,29 +4616,30 @@ __device__ __forceinline__ void vtile_chunk(const Args& a, uint32_t t0, uint32_t
 }
 
 // ---------------------------------------------------------------------------
-// The kernel
+// The kernels
 // ---------------------------------------------------------------------------
+// Phase 1, the launch after the sampling launch: the S of the rows whose
+// band check failed.  Most calls have none; a workgroup without a job ends
+// before any call (a call saves the callee's registers).
+template <int DT>
+__global__ __launch_bounds__(NT) void xs_kernel(Args a, Ws w) {
+  const uint32_t nwin = (a.V + XS_W - 1) / XS_W;
+  if (threadIdx.x == 0)
+    g_bcast[2] = __hip_atomic_load(&w.xs_ctl[a.epoch & 1u], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (blockIdx.x / nwin < umin(g_bcast[2], a.xs_cap)) {
+    exp_tab_init();
+    softcap_init<DT>(a);
+    kctx_fill();
+    __syncthreads();
+    xs_phase<DT>();
+  }
+}
+
 template <int DT>
 __global__ __launch_bounds__(NT) void stream_kernel(Args a, Ws w) {
   extern __shared__ __align__(16) uint32_t smem[];
-  if (a.phase) {
-    // The launch after the sampling launch: the S of the rows whose band
-    // check failed.  Most calls have none; a workgroup without a job ends
-    // here, before any call (a call saves the callee's registers).
-    const uint32_t nwin = (a.V + XS_W - 1) / XS_W;
-    if (threadIdx.x == 0)
-      g_bcast[2] = __hip_atomic_load(&w.xs_ctl[a.epoch & 1u], __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    if (blockIdx.x / nwin < umin(g_bcast[2], a.xs_cap)) {
-      exp_tab_init();
-      softcap_init<DT>(a);
-      kctx_fill();
-      __syncthreads();
-      xs_phase<DT>();
-    }
-    return;
-  }
   // the next call's job count starts at zero (nothing reads it in this call)
   if (blockIdx.x == 0 && threadIdx.x == 0)
     __hip_atomic_store(&w.xs_ctl[(a.epoch + 1u) & 1u], 0u, __ATOMIC_RELAXED,
@@ -5711,7 +5712,10 @@ static int set_kernel_attributes() {
   const void* kernels[] = {
       (const void*)stream_kernel<LLMK_F32>,           (const void*)stream_kernel<LLMK_BF16>,
       (const void*)stream_kernel<LLMK_F16>,           (const void*)stream_kernel<LLMK_F32 | SOFTCAP>,
-      (const void*)stream_kernel<LLMK_BF16 | SOFTCAP>, (const void*)stream_kernel<LLMK_F16 | SOFTCAP>};
+      (const void*)stream_kernel<LLMK_BF16 | SOFTCAP>, (const void*)stream_kernel<LLMK_F16 | SOFTCAP>,
+      (const void*)xs_kernel<LLMK_F32>,               (const void*)xs_kernel<LLMK_BF16>,
+      (const void*)xs_kernel<LLMK_F16>,               (const void*)xs_kernel<LLMK_F32 | SOFTCAP>,
+      (const void*)xs_kernel<LLMK_BF16 | SOFTCAP>,     (const void*)xs_kernel<LLMK_F16 | SOFTCAP>};
   for (const void* k : kernels)
     HIPCHK(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_DYN_MAX));
   HIPCHK(hipFuncSetAttribute((const void*)topk_mask_kernel,
@@ -5906,15 +5910,25 @@ static int sample_batch_run(const Ws& ws, uint32_t max_batch, uint32_t max_vocab
   const bool sc = in->softcap > 0.0f;
   auto launch = [&](const Args& x, dim3 grid, size_t bytes) {
     const dim3 block(NT);
-    if (x.dtype == LLMK_F32) {
-      if (sc) hipLaunchKernelGGL(stream_kernel<LLMK_F32 | SOFTCAP>, grid, block, bytes, st, x, ws);
-      else hipLaunchKernelGGL(stream_kernel<LLMK_F32>, grid, block, bytes, st, x, ws);
-    } else if (x.dtype == LLMK_BF16) {
-      if (sc) hipLaunchKernelGGL(stream_kernel<LLMK_BF16 | SOFTCAP>, grid, block, bytes, st, x, ws);
-      else hipLaunchKernelGGL(stream_kernel<LLMK_BF16>, grid, block, bytes, st, x, ws);
+    const int v = (x.dtype == LLMK_F32 ? 0 : x.dtype == LLMK_BF16 ? 2 : 4) + (sc ? 1 : 0);
+    if (x.phase == 0) {
+      switch (v) {
+        case 0: hipLaunchKernelGGL(stream_kernel<LLMK_F32>, grid, block, bytes, st, x, ws); break;
+        case 1: hipLaunchKernelGGL(stream_kernel<LLMK_F32 | SOFTCAP>, grid, block, bytes, st, x, ws); break;
+        case 2: hipLaunchKernelGGL(stream_kernel<LLMK_BF16>, grid, block, bytes, st, x, ws); break;
+        case 3: hipLaunchKernelGGL(stream_kernel<LLMK_BF16 | SOFTCAP>, grid, block, bytes, st, x, ws); break;
+        case 4: hipLaunchKernelGGL(stream_kernel<LLMK_F16>, grid, block, bytes, st, x, ws); break;
+        default: hipLaunchKernelGGL(stream_kernel<LLMK_F16 | SOFTCAP>, grid, block, bytes, st, x, ws);
+      }
     } else {
-      if (sc) hipLaunchKernelGGL(stream_kernel<LLMK_F16 | SOFTCAP>, grid, block, bytes, st, x, ws);
-      else hipLaunchKernelGGL(stream_kernel<LLMK_F16>, grid, block, bytes, st, x, ws);
+      switch (v) {
+        case 0: hipLaunchKernelGGL(xs_kernel<LLMK_F32>, grid, block, bytes, st, x, ws); break;
+        case 1: hipLaunchKernelGGL(xs_kernel<LLMK_F32 | SOFTCAP>, grid, block, bytes, st, x, ws); break;
+        case 2: hipLaunchKernelGGL(xs_kernel<LLMK_BF16>, grid, block, bytes, st, x, ws); break;
+        case 3: hipLaunchKernelGGL(xs_kernel<LLMK_BF16 | SOFTCAP>, grid, block, bytes, st, x, ws); break;
+        case 4: hipLaunchKernelGGL(xs_kernel<LLMK_F16>, grid, block, bytes, st, x, ws); break;
+        default: hipLaunchKernelGGL(xs_kernel<LLMK_F16 | SOFTCAP>, grid, block, bytes, st, x, ws);
+      }
     }
   };
   launch(a, dim3(a.B * a.G), lds);
