@@ -35,9 +35,10 @@ def kernel_source_digest():
 
 
 def measured_traffic(config):
-    """HBM bytes per launch of the stream kernel from the committed counter
-    summary (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy), or None when
-    there is none or it was measured on another version of the kernel."""
+    """HBM bytes per call (the sampling launch and the one after it) from the
+    committed counter summary (FETCH_SIZE + WRITE_SIZE, scaled by a plain
+    copy), or None when there is none or it was measured on another version
+    of the kernels."""
     import re
     path = os.path.join(ROOT, "profiles", f"stream_kernel_{config}_hbm_traffic.md")
     try:
@@ -88,8 +89,10 @@ def rotated_sets(llmk, db0, logit_bytes, sets=0):
 
 
 def back_to_back(torch, s, prepared, K, stream):
-    """K launches of llmk_sample_batch, rotating over the prepared argument
-    sets, between two events on the launch stream: the time per launch."""
+    """K calls of llmk_sample_batch, rotating over the prepared argument
+    sets, between two events on the launch stream: the time per call (its
+    sampling launch, and the launch after it that finishes rows whose band
+    check failed, when the call has top-k and 16 rows or more)."""
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -331,7 +334,7 @@ def main():
     K = args.steps
     # timed steps: K back-to-back launches between two events on the launch
     # stream; the time per step is also the stream kernel's average duration
-    # (one launch per step, nothing between launches)
+    # (one call per step, nothing between calls)
     ms_per_step = back_to_back(torch, s, prepared, K, stream)
     value = B / (ms_per_step * 1e-3)
     achieved = step_bytes / (ms_per_step * 1e-3) / 1e9
@@ -388,7 +391,7 @@ def main():
             "frac": achieved / HBM_PEAK_GBPS,
             "traffic": traffic,
             "traffic_source": traffic_src,
-            "kernel": "llmk::stream_kernel",
+            "kernel": "llmk::stream_kernel + llmk::xs_kernel (one call)",
             "kernel_avg_us": ms_per_step * 1e3,
             "achievable_read_GBps": read_gbps,
             "frac_of_achievable": achieved / read_gbps,
