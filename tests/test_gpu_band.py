@@ -83,3 +83,35 @@ def test_k_above_the_fast_path(sampler):
                      "large K")
     assert_matches_ref(w, gpu, O.sample_workload(O.REF, w, out_cap=64, nthreads=16), 64,
                        "large K")
+
+
+@pytest.mark.parametrize("dtype,cap", [("f32", 0.0), ("bf16", 0.0), ("f16", 0.0), ("f32", 30.0),
+                                       ("bf16", 30.0)])
+def test_deferred_rows_in_every_dtype(sampler, dtype, cap):
+    """Rows whose band check fails in a call of 20 rows (at least 16: their
+    S comes from the second launch, window by window on many workgroups)
+    with f32, bf16 and f16 logits, and with the softcap fused into the
+    reads: the same outputs as the oracles on the (capped) logits."""
+    from test_gpu_softcap import capped, make
+    w = make("C3", 20, dtype)
+    c = capped(w, cap) if cap else w
+    hit = 0
+    for r in range(w.B):
+        u = BU.divergent_uniform(c, r, cap=CAP)
+        if u is not None:
+            w.uniforms[r] = c.uniforms[r] = np.float32(u)
+            hit += 1
+    print(f"[case] deferred rows {dtype} softcap {cap}: {hit} rows", flush=True)
+    assert hit >= 4
+    db = w.to_device()
+    db.softcap = cap
+    r = sampler.sample_batch(db, out_cap=CAP)
+    import torch
+    torch.cuda.synchronize()
+    gpu = (r.tokens.cpu().numpy().view(np.uint32), r.ids.cpu().numpy().view(np.uint32),
+           r.probs.cpu().numpy(), r.count.cpu().numpy().view(np.uint32))
+    assert_bit_exact(w, gpu, O.sample_workload(O.MIRROR, c, out_cap=CAP, nthreads=16), CAP,
+                     f"deferred {dtype} {cap}")
+    assert_matches_ref(w, gpu, O.sample_workload(O.REF, c, out_cap=CAP, nthreads=16), CAP,
+                       f"deferred {dtype} {cap}")
+    assert sampler.status() == 0
