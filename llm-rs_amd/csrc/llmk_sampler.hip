@@ -3877,7 +3877,7 @@ __device__ __noinline__ void finalize_rare(uint32_t b, RowP P, float S, float m,
 // restored first.
 constexpr uint32_t XS_SPIN = 1u << 16;
 template <int DT>
-__device__ __noinline__ void xs_phase() {
+__device__ __forceinline__ void xs_phase() {
   extern __shared__ __align__(16) uint32_t smem[];
   const KCtx kc = kctx_load();
   const Args& a = kc.a;
@@ -4224,13 +4224,19 @@ __device__ __noinline__ void xs_phase() {
       if (tid == 0) __hip_atomic_store(&w.xs_ctl[2 + j], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       for (uint32_t i = tid; i < nwin; i += NT) wflag[i] = 0u;
       __syncthreads();
-      // the row's LDS partials and candidates, then its candidate path
+      // the row's LDS partials and candidates, then its candidate path: for
+      // a single-segment row here (its history never outgrew its tables),
+      // the rest through finalize_rare (a call: its register saves cost
+      // microseconds)
       if (a.G == 1) {
         const GLB uint32_t* sv = G(w.xs_save) + (uint64_t)j * XS_SAVE;
         for (uint32_t i = tid; i < XS_SAVE; i += NT) sm[a.lds_part + i] = sv[i];
+        __syncthreads();
+        const uint32_t path = candidate_paths<DT>(a, w, b, P, S, m, L, u, seg_own, false, sm);
+        if (path != 0) finalize_rare<DT>(b, P, S, m, L, u, seg_own, false, path);
+      } else {
+        finalize_rare<DT>(b, P, S, m, L, u, seg_own, false, 6u);
       }
-      __syncthreads();
-      finalize_rare<DT>(b, P, S, m, L, u, seg_own, false, 6u);
     }
   }
 }
