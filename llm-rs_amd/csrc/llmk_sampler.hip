@@ -5625,6 +5625,7 @@ struct llmk_sampler {
   void* stage;         // aligned copies of rows passed at any offset (allocated on demand)
   size_t stage_bytes;
   uint32_t epoch;      // calls made (their parity picks the job count)
+  uint32_t ncu;        // the device's compute units
 };
 
 static thread_local std::string g_last_error;
@@ -5757,6 +5758,10 @@ extern "C" int llmk_sampler_create(llmk_sampler** out, int device,
   s->device = device;
   s->max_batch = max_batch;
   s->max_vocab = max_vocab;
+  int ncu = 0;
+  if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+    ncu = 0;  // phase 1 then stays off
+  s->ncu = (uint32_t)(ncu > 0 ? ncu : 0);
   s->mem = mem;
   s->mem_bytes = L.total;
   s->ws = ws_carve((char*)mem, L, max_vocab, slots);
@@ -5816,7 +5821,7 @@ static float dtype_round(double x, int fmt) {
 constexpr uint32_t XS_MIN_BATCH = 16;
 static int sample_batch_run(const Ws& ws, uint32_t max_batch, uint32_t max_vocab, uint32_t pool,
                             const llmk_sample_batch_args* in, void* stream, u4v* cut,
-                            uint32_t tp_clamp, uint32_t epoch) {
+                            uint32_t tp_clamp, uint32_t epoch, uint32_t ncu) {
   if (!in) return fail(LLMK_ERR_INVALID_ARGUMENT, "args is NULL");
   if (in->vocab == 0) return fail(LLMK_ERR_EMPTY_LOGITS, "Empty logits passed to sampler");
   if (in->batch == 0) return fail(LLMK_ERR_INVALID_ARGUMENT, "batch is 0");
@@ -5884,7 +5889,8 @@ static int sample_batch_run(const Ws& ws, uint32_t max_batch, uint32_t max_vocab
   // a window's wait for the sums before it always ends
   const uint32_t nwin = xs_maxw(in->vocab);
   const bool phase1 = in->top_k != nullptr && in->batch >= XS_MIN_BATCH;
-  a.xs_cap = !phase1 ? 0u : (256 / nwin < XS_JOBS ? 256 / nwin : XS_JOBS);
+  // (jobs x windows within the device's CUs: every workgroup resident)
+  a.xs_cap = !phase1 ? 0u : (ncu / nwin < XS_JOBS ? ncu / nwin : XS_JOBS);
   a.xs_lds = 0;
   a.epoch = epoch;
   a.ntiles = (a.V + TILE - 1) / TILE;
@@ -5941,7 +5947,7 @@ static int sample_batch_run(const Ws& ws, uint32_t max_batch, uint32_t max_vocab
   HIPCHK(hipGetLastError());
   // phase 1: the S of the rows whose band check failed (most calls have
   // none: each workgroup then reads the job count and ends)
-  if (phase1) {
+  if (a.xs_cap > 0) {
     Args a1 = a;
     a1.phase = 1;
     const size_t lds1 = 4 * (256 + hist_lds_words(XS_W / 32) + NW * XS_CW);
@@ -6004,12 +6010,12 @@ static int sample_batch_impl(llmk_sampler* s, const llmk_sample_batch_args* in,
     al.logits = s->stage;
     al.row_stride = dstride;
     const int rc = sample_batch_run(s->ws, s->max_batch, s->max_vocab, pool, &al, stream, cut,
-                                    tp_clamp, s->epoch);
+                                    tp_clamp, s->epoch, s->ncu);
     if (rc == LLMK_OK) ++s->epoch;  // the parity advances with the launches only
     return rc;
   }
   const int rc = sample_batch_run(s->ws, s->max_batch, s->max_vocab, pool, in, stream, cut,
-                                  tp_clamp, s->epoch);
+                                  tp_clamp, s->epoch, s->ncu);
   if (rc == LLMK_OK) ++s->epoch;
   return rc;
 }
@@ -6040,6 +6046,7 @@ static __device__ __align__(256) uint8_t scratch[STATIC_LAYOUT.total];
 constexpr int STATIC_MAX_DEVICES = 64;
 static std::mutex g_static_mu;
 static char* g_static_ptr[STATIC_MAX_DEVICES];  // device address of scratch, per device
+static uint32_t g_static_ncu[STATIC_MAX_DEVICES];  // compute units, per device
 
 // Clears what every call must find at zero: the rows' arrival counters, the
 // slow-path slot locks and the status word (a fill kernel, so the call can
@@ -6056,7 +6063,7 @@ __global__ __launch_bounds__(256) void static_clear_kernel(uint32_t* arrive, uin
 
 // Device address of this device's scratch array, looked up (and the
 // kernels' LDS limits set) on the first call on each device.
-static int static_scratch(int dev, char** out) {
+static int static_scratch(int dev, char** out, uint32_t* ncu) {
   if (dev < 0 || dev >= STATIC_MAX_DEVICES)
     return fail(LLMK_ERR_UNSUPPORTED, "device ordinal above 63");
   std::lock_guard<std::mutex> g(g_static_mu);
@@ -6066,9 +6073,13 @@ static int static_scratch(int dev, char** out) {
     void* ptr = nullptr;
     HIPCHK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
     if (!ptr) return fail(LLMK_ERR_HIP, "hipGetSymbolAddress(scratch) returned NULL");
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
+    g_static_ncu[dev] = (uint32_t)(n > 0 ? n : 0);
     g_static_ptr[dev] = (char*)ptr;
   }
   *out = g_static_ptr[dev];
+  *ncu = g_static_ncu[dev];
   return LLMK_OK;
 }
 
@@ -6083,7 +6094,8 @@ extern "C" int llmk_sample_batch_static(const llmk_sample_batch_args* in, uint32
   int dev = 0;
   HIPCHK(hipGetDevice(&dev));
   char* base = nullptr;
-  const int rc = static_scratch(dev, &base);
+  uint32_t ncu = 0;
+  const int rc = static_scratch(dev, &base, &ncu);
   if (rc != LLMK_OK) return rc;
   Ws ws = ws_carve(base, STATIC_LAYOUT, STATIC_MAX_VOCAB, STATIC_SLOTS);
   hipStream_t st = (hipStream_t)stream;
@@ -6094,7 +6106,7 @@ extern "C" int llmk_sample_batch_static(const llmk_sample_batch_args* in, uint32
   if (status) ws.status = status;
   // the clear kernel zeroed both job counts: every call can use parity 0
   return sample_batch_run(ws, STATIC_MAX_BATCH, STATIC_MAX_VOCAB, STATIC_POOL, in, stream,
-                          nullptr, 0u, 0u);
+                          nullptr, 0u, 0u, ncu);
 }
 
 // Checks shared by the mask forms: in-place f32 rows.
