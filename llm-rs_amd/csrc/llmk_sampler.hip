@@ -101,6 +101,8 @@ constexpr uint32_t XS_JOBS = 8;                        // rows per call
 constexpr uint32_t XS_W = 16 * TILE;                   // a window: 16 segments of a tile
 constexpr uint32_t XS_SAVE = 2 * MAX_SLOTS + 2 * LCAP;  // LDS partials + candidates
 constexpr uint32_t XS_JOB_WORDS = 32;
+constexpr uint32_t XS_PRE = 2 + XS_JOBS;                // xs_ctl: window 0's (sum, tag) per job
+constexpr uint32_t XS_CTL_WORDS = XS_PRE + 2 * XS_JOBS;
 
 // Words a workgroup passes from one phase to the next past the dynamic
 // shared memory, which each phase lays out afresh (static LDS).
@@ -163,7 +165,8 @@ struct Ws {
   // per job its arrival count; the jobs; per job and window its sum and that
   // sum's flag; per job and segment its pairs and terms; per job the
   // single-segment row's LDS partials and candidates
-  uint32_t* xs_ctl;      // [2 + XS_JOBS]: job counts of even / odd calls, arrivals
+  uint32_t* xs_ctl;      // [XS_CTL_WORDS]: job counts of even / odd calls, arrivals,
+                         // window 0's (sum, tag) per job
   uint32_t* xs_job;      // [XS_JOBS][XS_JOB_WORDS]
   float* xs_wsum;        // [XS_JOBS][xs_maxw]
   uint32_t* xs_wflag;    // [XS_JOBS][xs_maxw]
@@ -2018,17 +2021,17 @@ __device__ __forceinline__ Par lane_pair(const float (&e)[Q], int eb) {
   return Par{umin(s0, XS_SAT), umin(s1 - 1u, XS_SAT)};
 }
 
-// c + the first n of a wave's terms in order, exactly (lane l holding terms
-// Q l .. Q l + Q - 1, zeros past n): a lane at a time while c is 0 (from 0
-// the sum leaves its binade at almost every term); then the lanes' pairs in
-// c's binade, a wave scan; the lanes before the first one where c leaves the
-// binade are added by their pairs, that lane's terms one f32 addition each,
-// and the scan resumes after it.  Every lane returns the sum.
+// c + the terms of lanes pos .. nl - 1 of a wave in order, exactly (lane l
+// holding terms Q l .. Q l + Q - 1, zeros past the count), by rounds: a lane
+// at a time while c is 0 (from 0 the sum leaves its binade at almost every
+// term); then the lanes' pairs in c's binade, a wave scan; the lanes before
+// the first one where c leaves the binade are added by their pairs, that
+// lane's terms one f32 addition each, and the scan resumes after it.  Every
+// lane returns the sum.
 template <int Q>
-__device__ __forceinline__ float wave_sum_q(float c, const float (&p)[Q], uint32_t n) {
+__device__ __forceinline__ float wave_sum_rounds(float c, const float (&p)[Q], uint32_t nl,
+                                                 uint32_t pos) {
   const uint32_t lane = threadIdx.x & 63u;
-  const uint32_t nl = (n + Q - 1) / Q;  // lanes holding terms
-  uint32_t pos = 0;                     // lanes before pos are in c
   while (pos < nl) {
     if (c == 0.0f) {
 #pragma unroll
@@ -2056,6 +2059,77 @@ __device__ __forceinline__ float wave_sum_q(float c, const float (&p)[Q], uint32
     pos = l + 1;
   }
   return c;
+}
+
+// c + the first n of a wave's terms in order, exactly (lane l holding terms
+// Q l .. Q l + Q - 1, zeros past n), in one pass of pairs.  Each lane bounds
+// the running sums over its terms from c and the exact prefix of the lanes'
+// sums: the sequential f32 sum of k positive terms from c is within
+// k u (1.001) of the exact one (u = 2^-24 per addition; plus 2^-150 per
+// addition below 2^-126), and a lane's own f32 sum within Q u of its terms'.
+// A lane whose bounds share one binade forms its pair there; consecutive such
+// lanes of one binade form a run, and a segmented wave scan gives each run's
+// pair.  The walk then adds a run at once (its sum provably stays in the
+// binade) and every other lane (a binade crossing, or c = 0) one f32 addition
+// a term.  Where the sum is not where the bounds say (it cannot be; the check
+// keeps the result exact whatever), the rest goes by rounds
+// (wave_sum_rounds).  Every lane returns the sum.
+template <int Q>
+__device__ __forceinline__ float wave_sum_q(float c, const float (&p)[Q], uint32_t n) {
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t nl = (n + Q - 1) / Q;  // lanes holding terms
+  if (nl == 0) return c;
+  float ls = 0.0f;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) ls += p[q];
+  const double lsd = (double)ls;
+  const double base = (double)c + (wave_prefix_d(lsd) - lsd);
+  const double d = (double)(Q * (lane + 2u) + 4u) * 0x1p-24 * 1.02 + 0x1p-45;
+  const double ab = (double)(Q * (lane + 1u)) * 0x1p-150;
+  const double lo = base * (1.0 - d) - ab, hi = (base + lsd) * (1.0 + d) + ab;
+  const int eb = binade_d(lo);
+  const bool ok = lane < nl && lo >= 0x1p-126 && hi < 0x1p120 && binade_d(hi) == eb;
+  const uint32_t key = ok ? (uint32_t)(eb + 512) : 0u;
+  const uint32_t prev =
+      (uint32_t)__builtin_amdgcn_ds_bpermute((int)(((lane + 63u) & 63u) * 4u), (int)key);
+  const uint64_t heads = __ballot(!ok || lane == 0 || prev != key);
+  const uint64_t bad = __ballot(!ok);
+  // each lane's run start, then the pairs scanned within runs
+  const uint32_t rs = 63u - (uint32_t)__builtin_clzll(heads & ((2ull << lane) - 1ull));
+  Par x = lane_pair<Q>(p, ok ? eb : 0);
+  Par y = sat_then(dpp_par<0x111, 0xf, true>(x), x);
+  x = rs + 1u <= lane ? y : x;
+  y = sat_then(dpp_par<0x112, 0xf, true>(x), x);
+  x = rs + 2u <= lane ? y : x;
+  y = sat_then(dpp_par<0x114, 0xf, true>(x), x);
+  x = rs + 4u <= lane ? y : x;
+  y = sat_then(dpp_par<0x118, 0xf, true>(x), x);
+  x = rs + 8u <= lane ? y : x;
+  y = sat_then(dpp_par<0x142, 0xa, false>(x), x);
+  x = rs + 1u <= (lane & ~15u) ? y : x;
+  y = sat_then(dpp_par<0x143, 0xc, false>(x), x);
+  x = rs <= 31u ? y : x;
+  uint32_t pos = 0;
+  while (pos < nl) {
+    if ((bad >> pos) & 1ull) {
+#pragma unroll
+      for (int q = 0; q < Q; ++q) c = c + rl(p[q], pos);
+      ++pos;
+      continue;
+    }
+    const uint64_t after = heads & ~((2ull << pos) - 1ull);
+    const uint32_t end = after ? (uint32_t)__builtin_ctzll(after) : 64u;
+    const uint32_t last = (end < nl ? end : nl) - 1u;
+    const int ebr = __builtin_amdgcn_readlane(eb, (int)pos);
+    if (!(c >= 0x1p-126f) || binade_of(c) != ebr) break;
+    const uint32_t C = (uint32_t)__builtin_ldexpf(c, 23 - ebr);
+    const uint32_t inc = (C & 1u) ? (uint32_t)__builtin_amdgcn_readlane((int)x.a1, (int)last)
+                                  : (uint32_t)__builtin_amdgcn_readlane((int)x.a0, (int)last);
+    if (C + inc >= XS_SAT) break;
+    c = __builtin_ldexpf((float)(C + inc), ebr - 23);
+    pos = last + 1u;
+  }
+  return pos < nl ? wave_sum_rounds<Q>(c, p, nl, pos) : c;
 }
 
 // A wave-uniform 64-bit value, or LDS pointer, in scalar registers.
@@ -2281,7 +2355,8 @@ __device__ __attribute__((noinline)) float exact_normaliser(
         }
         // segment s, lane by lane, by the wave that holds it
         if (s == 0) {
-          cc = packed ? wave_sum_q<4>(cc, pk, nseg) : wave_sum_q<Q>(cc, e, nseg);
+          cc = packed ? wave_sum_rounds<4>(cc, pk, (nseg + 3u) / 4u, 0u)
+                      : wave_sum_rounds<Q>(cc, e, (nseg + Q - 1u) / Q, 0u);
         } else {
           if (lane == 0) {
             __hip_atomic_store(&ctl[CV], __float_as_uint(cc), __ATOMIC_RELAXED,
@@ -2307,7 +2382,8 @@ __device__ __attribute__((noinline)) float exact_normaliser(
         if (r == wv) {
           const float cin = __uint_as_float(
               __hip_atomic_load(&ctl[CV], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
-          const float cout = packed ? wave_sum_q<4>(cin, pk, nseg) : wave_sum_q<Q>(cin, e, nseg);
+          const float cout = packed ? wave_sum_rounds<4>(cin, pk, (nseg + 3u) / 4u, 0u)
+                                    : wave_sum_rounds<Q>(cin, e, (nseg + Q - 1u) / Q, 0u);
           if (lane == 0) {
             __hip_atomic_store(&ctl[CV], __float_as_uint(cout), __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -3876,6 +3952,104 @@ __device__ __noinline__ void finalize_rare(uint32_t b, RowP P, float S, float m,
 // with that S (finalize_rare, path 6), its LDS partials and candidates
 // restored first.
 constexpr uint32_t XS_SPIN = 1u << 16;
+// The exact running sum from cc over segments s .. se - 1, by one wave (every
+// lane returns it): a run of segments whose pair covers the sum's binade and
+// keeps it there is added at once, any other segment lane by lane
+// (wave_sum_q).  hdr(i, x): word x of segment i's record (0 the header, 1-6
+// its pairs, 7 its count and packed bit); T::get4 / T::get16 read a lane's
+// terms of a packed / dense segment.
+template <class H, class T>
+__device__ __forceinline__ float xs_walk(float cc, uint32_t s, uint32_t se, H hdr, T src) {
+  const uint32_t lane = threadIdx.x & 63u;
+  while (s < se) {
+    if (__float_as_uint(cc) >= 0x00800000u) {
+      const int eb = binade_of(cc);
+      const uint32_t C = (uint32_t)__builtin_ldexpf(cc, 23 - eb);
+      const uint32_t js = s + lane;
+      Par px = Par{XS_SAT, XS_SAT};
+      if (js < se) {
+        const uint32_t hj = hdr(js, 0u);
+        const int q = eb - ((int)(hj & 0xffffu) - 256);
+        if ((hj >> 16) != 0u && q >= 0 && q < (int)(hj >> 16))
+          px = Par{hdr(js, 1u + 2u * (uint32_t)q), hdr(js, 2u + 2u * (uint32_t)q)};
+      }
+      const Par in = wave_par_incl_sat(px);
+      const uint32_t inc = (C & 1u) ? in.a1 : in.a0;
+      const uint64_t good = __ballot(js < se && C + inc < XS_SAT);
+      const uint32_t g = ~good == 0ull ? 64u : (uint32_t)__builtin_ctzll(~good);
+      if (g > 0) {
+        const uint32_t ig = (uint32_t)__builtin_amdgcn_readlane((int)inc, (int)g - 1);
+        cc = __builtin_ldexpf((float)(C + ig), eb - 23);
+        s += g;
+        continue;
+      }
+    }
+    const uint32_t mts = hdr(s, 7u);
+    const uint32_t cnt = mts & 0x7fffffffu;
+    if (mts >> 31) {
+      float p4[4];
+      src.get4(s, lane, p4);
+#pragma unroll
+      for (uint32_t q = 0; q < 4; ++q) p4[q] = 4 * lane + q < cnt ? p4[q] : 0.0f;
+      cc = wave_sum_q<4>(cc, p4, cnt);
+    } else {
+      float p16[16];
+      src.get16(s, lane, p16);
+      cc = wave_sum_q<16>(cc, p16, cnt);
+    }
+    ++s;
+  }
+  return cc;
+}
+// a segment's terms: its LDS copy when it has one, else the published ones
+struct XsTerms {
+  LDS const float* pf;       // [npf][TILE]
+  LDS const uint32_t* pfs;   // segment -> copy, or EMPTY
+  const GLB float* terms;    // [ns][TILE]
+  __device__ __forceinline__ void get4(uint32_t s, uint32_t lane, float (&p)[4]) const {
+    const uint32_t slot = pfs[s];
+    const f4v v = slot != EMPTY ? *(LDS const f4v*)(pf + (uint64_t)slot * TILE + 4 * lane)
+                                : *(const GLB f4v*)(terms + (uint64_t)s * TILE + 4 * lane);
+    p[0] = v.x;
+    p[1] = v.y;
+    p[2] = v.z;
+    p[3] = v.w;
+  }
+  __device__ __forceinline__ void get16(uint32_t s, uint32_t lane, float (&p)[16]) const {
+    const uint32_t slot = pfs[s];
+#pragma unroll
+    for (uint32_t q = 0; q < 16; q += 4) {
+      const f4v v = slot != EMPTY
+                        ? *(LDS const f4v*)(pf + (uint64_t)slot * TILE + 16 * lane + q)
+                        : *(const GLB f4v*)(terms + (uint64_t)s * TILE + 16 * lane + q);
+      p[q] = v.x;
+      p[q + 1] = v.y;
+      p[q + 2] = v.z;
+      p[q + 3] = v.w;
+    }
+  }
+};
+// window 0's own copy of its segments' terms (segment s at s * TILE)
+struct XsOwnTerms {
+  LDS const float* t;
+  __device__ __forceinline__ void get4(uint32_t s, uint32_t lane, float (&p)[4]) const {
+    const f4v v = *(LDS const f4v*)(t + s * TILE + 4 * lane);
+    p[0] = v.x;
+    p[1] = v.y;
+    p[2] = v.z;
+    p[3] = v.w;
+  }
+  __device__ __forceinline__ void get16(uint32_t s, uint32_t lane, float (&p)[16]) const {
+#pragma unroll
+    for (uint32_t q = 0; q < 16; q += 4) {
+      const f4v v = *(LDS const f4v*)(t + s * TILE + 16 * lane + q);
+      p[q] = v.x;
+      p[q + 1] = v.y;
+      p[q + 2] = v.z;
+      p[q + 3] = v.w;
+    }
+  }
+};
 template <int DT>
 __device__ __forceinline__ void xs_phase() {
   extern __shared__ __align__(16) uint32_t smem[];
@@ -4086,6 +4260,32 @@ __device__ __forceinline__ void xs_phase() {
       for (uint32_t q = 0; q < 16; q += 4)
         *(GLB f4v*)(tt + 16 * lane + q) = f4v{e[q], e[q + 1], e[q + 2], e[q + 3]};
     }
+    // window 0 (of several) keeps its records and terms in LDS too, past the
+    // history tables and the packing space, for its own walk below
+    LDS uint32_t* own = hb + hist_lds_words(HW) + NW * XS_CW;  // [16][8], then [16][TILE]
+    if (k == 0 && nwin > 1) {
+      if (lane == 0) {
+        own[8 * wv] = hdr;
+#pragma unroll
+        for (uint32_t q = 0; q < XS_NB; ++q) {
+          own[8 * wv + 1 + 2 * q] = pr[q].a0;
+          own[8 * wv + 2 + 2 * q] = pr[q].a1;
+        }
+        own[8 * wv + 7] = nseg | (packed ? 0x80000000u : 0u);
+      }
+      LDS float* ot = (LDS float*)(own + 128) + TILE * wv;
+      if (packed) {
+        *(LDS f4v*)(ot + 4 * lane) = f4v{pk[0], pk[1], pk[2], pk[3]};
+      } else {
+#pragma unroll
+        for (uint32_t q = 0; q < 16; q += 4)
+          *(LDS f4v*)(ot + 16 * lane + q) = f4v{e[q], e[q + 1], e[q + 2], e[q + 3]};
+      }
+    }
+    // the sum at window 0's end, once window 0 has walked itself: the call's
+    // tag (its count of calls + 1) marks it as this call's
+    const uint32_t tag = a.epoch + 1u;
+    GLB uint32_t* own_sum = G(w.xs_ctl) + XS_PRE + 2 * j;  // (sum, tag)
     // the barrier gathers every wave's stores in this CU's caches; thread 0's
     // arrival then releases them (a write-back of the cache) and, for the
     // last window, acquires the others' (an invalidation the whole
@@ -4105,11 +4305,14 @@ __device__ __forceinline__ void xs_phase() {
       LDS uint32_t* pfl = pfs + ns;          // [ns]: the segment of each copy
       LDS float* pf = (LDS float*)(pfl + ns);  // [npf][TILE]
       const uint32_t npf = (a.xs_lds - (256 + 10 * ns)) / TILE;
-      // the segments' headers and the terms of window 0's segments, in one
-      // round of loads: from a sum that starts at zero, window 0 crosses a
-      // binade at each doubling, so the walk sums most of its segments lane
-      // by lane
-      const uint32_t n0 = umin(16u, npf);
+      // window 0, when it is not this one, walks its own segments and
+      // publishes the sum at its end (below); the walk here starts there
+      const bool from_own = k != 0;
+      // the segments' headers, and the terms of window 0's segments when the
+      // walk starts at zero (from there window 0 crosses a binade at each
+      // doubling, so the walk sums most of its segments lane by lane), in
+      // one round of loads
+      const uint32_t n0 = from_own ? 0u : umin(16u, npf);
       {
         uint32_t mv[8];
         float tv[16];
@@ -4130,13 +4333,14 @@ __device__ __forceinline__ void xs_phase() {
           if (q < n0) pf[q * TILE + tid] = tv[q];
       }
       __syncthreads();
-      // then the other segments without pairs, as many as fit (the rest
-      // are read when the walk reaches them)
+      // then the other segments without pairs past window 0, as many as fit
+      // (the rest are read when the walk reaches them)
+      const uint32_t sfirst = from_own ? 16u : n0;
       if (wv == 0) {
         uint32_t used = n0;
         for (uint32_t s0 = 0; s0 < ns; s0 += WAVE) {
           const uint32_t si = s0 + lane;
-          const bool want = si >= n0 && si < ns && (segp[8 * si] >> 16) == 0u;
+          const bool want = si >= sfirst && si < ns && (segp[8 * si] >> 16) == 0u;
           const uint32_t r = used + (uint32_t)__popcll(__ballot(want) & ((1ull << lane) - 1ull));
           if (si < n0) pfs[si] = si;
           else if (si < ns) pfs[si] = (want && r < npf) ? r : EMPTY;
@@ -4160,62 +4364,26 @@ __device__ __forceinline__ void xs_phase() {
       }
       __syncthreads();
       if (wv == 0) {
-        float cc = 0.0f;
-        uint32_t s = 0;
-        while (s < ns) {
-          if (__float_as_uint(cc) >= 0x00800000u) {
-            const int eb = binade_of(cc);
-            const uint32_t C = (uint32_t)__builtin_ldexpf(cc, 23 - eb);
-            const uint32_t js = s + lane;
-            Par px = Par{XS_SAT, XS_SAT};
-            if (js < ns) {
-              const uint32_t hj = segp[8 * js];
-              const int q = eb - ((int)(hj & 0xffffu) - 256);
-              if ((hj >> 16) != 0u && q >= 0 && q < (int)(hj >> 16))
-                px = Par{segp[8 * js + 1 + 2 * q], segp[8 * js + 2 + 2 * q]};
+        // window 0's sum at its end (a bounded wait; if it runs out, the
+        // walk starts at zero and reads window 0's terms from memory)
+        float c0 = 0.0f;
+        uint32_t s0 = 0;
+        if (from_own) {
+          for (uint32_t n = 0; n < XS_SPIN; ++n) {
+            const uint32_t t = __hip_atomic_load(own_sum + 1, __ATOMIC_ACQUIRE,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+            if ((uint32_t)__builtin_amdgcn_readfirstlane((int)t) == tag) {
+              c0 = __uint_as_float(
+                  (uint32_t)__builtin_amdgcn_readfirstlane((int)own_sum[0]));
+              s0 = 16;
+              break;
             }
-            const Par in = wave_par_incl_sat(px);
-            const uint32_t inc = (C & 1u) ? in.a1 : in.a0;
-            const uint64_t good = __ballot(js < ns && C + inc < XS_SAT);
-            const uint32_t g = ~good == 0ull ? 64u : (uint32_t)__builtin_ctzll(~good);
-            if (g > 0) {
-              const uint32_t ig = (uint32_t)__builtin_amdgcn_readlane((int)inc, (int)g - 1);
-              cc = __builtin_ldexpf((float)(C + ig), eb - 23);
-              s += g;
-              continue;
-            }
+            __builtin_amdgcn_s_sleep(2);
           }
-          // segment s lane by lane, from its published terms (their LDS
-          // copy when it has one)
-          const uint32_t mts = segp[8 * s + 7];
-          const uint32_t cnt = mts & 0x7fffffffu;
-          const uint32_t slot = pfs[s];
-          const GLB float* ts = terms + (uint64_t)s * TILE;
-          LDS const float* tl = pf + (uint64_t)(slot == EMPTY ? 0u : slot) * TILE;
-          if (mts >> 31) {
-            float p4[4];
-            const f4v v4 = slot != EMPTY ? *(LDS const f4v*)(tl + 4 * lane)
-                                         : *(const GLB f4v*)(ts + 4 * lane);
-            p4[0] = 4 * lane + 0 < cnt ? v4.x : 0.0f;
-            p4[1] = 4 * lane + 1 < cnt ? v4.y : 0.0f;
-            p4[2] = 4 * lane + 2 < cnt ? v4.z : 0.0f;
-            p4[3] = 4 * lane + 3 < cnt ? v4.w : 0.0f;
-            cc = wave_sum_q<4>(cc, p4, cnt);
-          } else {
-            float p16[16];
-#pragma unroll
-            for (uint32_t q = 0; q < 16; q += 4) {
-              const f4v v4 = slot != EMPTY ? *(LDS const f4v*)(tl + 16 * lane + q)
-                                           : *(const GLB f4v*)(ts + 16 * lane + q);
-              p16[q] = v4.x;
-              p16[q + 1] = v4.y;
-              p16[q + 2] = v4.z;
-              p16[q + 3] = v4.w;
-            }
-            cc = wave_sum_q<16>(cc, p16, cnt);
-          }
-          ++s;
         }
+        const float cc = xs_walk(c0, s0, ns,
+                                 [&](uint32_t i, uint32_t x) { return segp[8 * i + x]; },
+                                 XsTerms{pf, pfs, terms});
         if (lane == 0) sm[71] = __float_as_uint(cc);
       }
       __syncthreads();
@@ -4236,6 +4404,15 @@ __device__ __forceinline__ void xs_phase() {
         if (path != 0) finalize_rare<DT>(b, P, S, m, L, u, seg_own, false, path);
       } else {
         finalize_rare<DT>(b, P, S, m, L, u, seg_own, false, 6u);
+      }
+    } else if (k == 0 && wv == 0) {
+      // ---- window 0's own walk, from zero, over its LDS copy
+      const float cc = xs_walk(0.0f, 0u, 16u,
+                               [&](uint32_t i, uint32_t x) { return own[8 * i + x]; },
+                               XsOwnTerms{(LDS const float*)(own + 128)});
+      if (lane == 0) {
+        own_sum[0] = __float_as_uint(cc);
+        __hip_atomic_store(own_sum + 1, tag, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }
@@ -5677,7 +5854,7 @@ static constexpr WsLayout ws_layout(uint32_t mb, uint32_t mv, uint32_t pool, uin
   L.mtok = off; off = align_up(off + 4ull * mb, 256);
   L.zu = off; off = align_up(off + 4ull * mb, 256);
   const uint64_t mw = xs_maxw(mv);
-  L.xctl = off; off = align_up(off + 4ull * (2 + XS_JOBS), 256);
+  L.xctl = off; off = align_up(off + 4ull * XS_CTL_WORDS, 256);
   L.xjob = off; off = align_up(off + 4ull * XS_JOBS * XS_JOB_WORDS, 256);
   L.xwsum = off; off = align_up(off + 4ull * XS_JOBS * mw, 256);
   L.xwflag = off; off = align_up(off + 4ull * XS_JOBS * mw, 256);
@@ -5950,7 +6127,9 @@ static int sample_batch_run(const Ws& ws, uint32_t max_batch, uint32_t max_vocab
   if (a.xs_cap > 0) {
     Args a1 = a;
     a1.phase = 1;
-    const size_t lds1 = 4 * (256 + hist_lds_words(XS_W / 32) + NW * XS_CW);
+    // (a window's history tables and packing space, then window 0's copy of
+    // its records and terms)
+    const size_t lds1 = 4 * (256 + hist_lds_words(XS_W / 32) + NW * XS_CW + 128 + NW * TILE);
     a1.xs_lds = (uint32_t)((lds > lds1 ? lds : lds1) / 4);
     launch(a1, dim3(a.xs_cap * nwin), 4 * (size_t)a1.xs_lds);
     HIPCHK(hipGetLastError());
@@ -6058,7 +6237,7 @@ __global__ __launch_bounds__(256) void static_clear_kernel(uint32_t* arrive, uin
   if (i < n_arrive) arrive[i] = 0;
   if (i < n_lock) lock[i] = 0;
   if (i == 0) status[0] = 0;
-  if (i < 2 + XS_JOBS) xs_ctl[i] = 0;
+  if (i < XS_CTL_WORDS) xs_ctl[i] = 0;
 }
 
 // Device address of this device's scratch array, looked up (and the
