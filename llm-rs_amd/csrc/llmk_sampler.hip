@@ -172,6 +172,7 @@ struct Ws {
   uint32_t* xs_wflag;    // [XS_JOBS][xs_maxw]
   uint32_t* xs_meta;     // [XS_JOBS][xs_maxw * 16][8]
   float* xs_terms;       // [XS_JOBS][xs_maxw * 16][TILE]
+  uint32_t* xs_runs;     // [XS_JOBS][xs_maxw * 16][XS_RUNW]
   uint32_t* xs_save;     // [XS_JOBS][XS_SAVE]
   uint32_t xs_maxw;
   uint32_t max_vocab;
@@ -2061,39 +2062,39 @@ __device__ __forceinline__ float wave_sum_rounds(float c, const float (&p)[Q], u
   return c;
 }
 
-// c + the first n of a wave's terms in order, exactly (lane l holding terms
-// Q l .. Q l + Q - 1, zeros past n), in one pass of pairs.  Each lane bounds
-// the running sums over its terms from c and the exact prefix of the lanes'
-// sums: the sequential f32 sum of k positive terms from c is within
-// k u (1.001) of the exact one (u = 2^-24 per addition; plus 2^-150 per
-// addition below 2^-126), and a lane's own f32 sum within Q u of its terms'.
-// A lane whose bounds share one binade forms its pair there; consecutive such
-// lanes of one binade form a run, and a segmented wave scan gives each run's
-// pair.  The walk then adds a run at once (its sum provably stays in the
-// binade) and every other lane (a binade crossing, or c = 0) one f32 addition
-// a term.  Where the sum is not where the bounds say (it cannot be; the check
-// keeps the result exact whatever), the rest goes by rounds
-// (wave_sum_rounds).  Every lane returns the sum.
+// The runs of a wave's terms (lane l holding terms Q l .. Q l + Q - 1, zeros
+// from lane nl on) for a running sum that enters them anywhere in [clo, chi].
+// Each lane bounds the running sums over its terms from those bounds and the
+// exact prefix of the lanes' sums: the sequential f32 sum of k positive terms
+// from c is within k u (1.001) of the exact one (u = 2^-24 per addition; plus
+// 2^-150 per addition below 2^-126), and a lane's own f32 sum within Q u of
+// its terms'.  A lane whose bounds share one binade forms its pair there;
+// consecutive such lanes of one binade form a run, and a segmented wave scan
+// gives each lane its run's pair so far.  RunLane.k: the lane's binade + 512
+// (0: no run, the lane is summed one addition a term), bit 16 set where a
+// run (or such a lane) starts.
+struct RunLane {
+  uint32_t a0, a1, k;
+};
 template <int Q>
-__device__ __forceinline__ float wave_sum_q(float c, const float (&p)[Q], uint32_t n) {
+__device__ __forceinline__ RunLane seg_runs(const float (&p)[Q], uint32_t nl, double clo,
+                                            double chi) {
   const uint32_t lane = threadIdx.x & 63u;
-  const uint32_t nl = (n + Q - 1) / Q;  // lanes holding terms
-  if (nl == 0) return c;
   float ls = 0.0f;
 #pragma unroll
   for (int q = 0; q < Q; ++q) ls += p[q];
   const double lsd = (double)ls;
-  const double base = (double)c + (wave_prefix_d(lsd) - lsd);
+  const double pre = wave_prefix_d(lsd) - lsd;
   const double d = (double)(Q * (lane + 2u) + 4u) * 0x1p-24 * 1.02 + 0x1p-45;
   const double ab = (double)(Q * (lane + 1u)) * 0x1p-150;
-  const double lo = base * (1.0 - d) - ab, hi = (base + lsd) * (1.0 + d) + ab;
+  const double lo = (clo + pre) * (1.0 - d) - ab, hi = (chi + pre + lsd) * (1.0 + d) + ab;
   const int eb = binade_d(lo);
   const bool ok = lane < nl && lo >= 0x1p-126 && hi < 0x1p120 && binade_d(hi) == eb;
   const uint32_t key = ok ? (uint32_t)(eb + 512) : 0u;
   const uint32_t prev =
       (uint32_t)__builtin_amdgcn_ds_bpermute((int)(((lane + 63u) & 63u) * 4u), (int)key);
-  const uint64_t heads = __ballot(!ok || lane == 0 || prev != key);
-  const uint64_t bad = __ballot(!ok);
+  const bool head = !ok || lane == 0 || prev != key;
+  const uint64_t heads = __ballot(head);
   // each lane's run start, then the pairs scanned within runs
   const uint32_t rs = 63u - (uint32_t)__builtin_clzll(heads & ((2ull << lane) - 1ull));
   Par x = lane_pair<Q>(p, ok ? eb : 0);
@@ -2109,6 +2110,18 @@ __device__ __forceinline__ float wave_sum_q(float c, const float (&p)[Q], uint32
   x = rs + 1u <= (lane & ~15u) ? y : x;
   y = sat_then(dpp_par<0x143, 0xc, false>(x), x);
   x = rs <= 31u ? y : x;
+  return RunLane{x.a0, x.a1, key | (head ? 0x10000u : 0u)};
+}
+// c + the terms of lanes 0 .. nl - 1 in order, exactly, c inside the bounds
+// r was formed for: a run at once (its sum provably stays in its binade),
+// every other lane (a binade crossing, or c = 0) one f32 addition a term.
+// Where the sum is not where the bounds say (it cannot be; the check keeps
+// the result exact whatever), the rest goes by rounds (wave_sum_rounds).
+// Every lane returns the sum.
+template <int Q>
+__device__ __forceinline__ float runs_walk(float c, const float (&p)[Q], uint32_t nl, RunLane r) {
+  const uint64_t heads = __ballot((r.k >> 16) & 1u);
+  const uint64_t bad = __ballot((r.k & 0xffffu) == 0u);
   uint32_t pos = 0;
   while (pos < nl) {
     if ((bad >> pos) & 1ull) {
@@ -2120,16 +2133,23 @@ __device__ __forceinline__ float wave_sum_q(float c, const float (&p)[Q], uint32
     const uint64_t after = heads & ~((2ull << pos) - 1ull);
     const uint32_t end = after ? (uint32_t)__builtin_ctzll(after) : 64u;
     const uint32_t last = (end < nl ? end : nl) - 1u;
-    const int ebr = __builtin_amdgcn_readlane(eb, (int)pos);
+    const int ebr = (int)((uint32_t)__builtin_amdgcn_readlane((int)r.k, (int)pos) & 0xffffu) - 512;
     if (!(c >= 0x1p-126f) || binade_of(c) != ebr) break;
     const uint32_t C = (uint32_t)__builtin_ldexpf(c, 23 - ebr);
-    const uint32_t inc = (C & 1u) ? (uint32_t)__builtin_amdgcn_readlane((int)x.a1, (int)last)
-                                  : (uint32_t)__builtin_amdgcn_readlane((int)x.a0, (int)last);
+    const uint32_t inc = (C & 1u) ? (uint32_t)__builtin_amdgcn_readlane((int)r.a1, (int)last)
+                                  : (uint32_t)__builtin_amdgcn_readlane((int)r.a0, (int)last);
     if (C + inc >= XS_SAT) break;
     c = __builtin_ldexpf((float)(C + inc), ebr - 23);
     pos = last + 1u;
   }
   return pos < nl ? wave_sum_rounds<Q>(c, p, nl, pos) : c;
+}
+// c + the first n of a wave's terms in order, exactly, by their runs from c.
+template <int Q>
+__device__ __forceinline__ float wave_sum_q(float c, const float (&p)[Q], uint32_t n) {
+  const uint32_t nl = (n + Q - 1) / Q;  // lanes holding terms
+  if (nl == 0) return c;
+  return runs_walk<Q>(c, p, nl, seg_runs<Q>(p, nl, (double)c, (double)c));
 }
 
 // A wave-uniform 64-bit value, or LDS pointer, in scalar registers.
@@ -3952,6 +3972,11 @@ __device__ __noinline__ void finalize_rare(uint32_t b, RowP P, float S, float m,
 // with that S (finalize_rare, path 6), its LDS partials and candidates
 // restored first.
 constexpr uint32_t XS_SPIN = 1u << 16;
+constexpr uint32_t XS_RUNW = 256;              // a segment's runs: a lane's (a0, a1, k, 0)
+constexpr uint32_t XS_SLOT = TILE + XS_RUNW;   // an LDS copy: terms, then runs
+constexpr uint32_t XS_PACKED = 0x80000000u;    // record word 7: packed terms
+constexpr uint32_t XS_RUNS = 0x40000000u;      //   runs formed with the terms
+constexpr uint32_t XS_CNT = 0x3fffffffu;       //   the terms' count
 // The exact running sum from cc over segments s .. se - 1, by one wave (every
 // lane returns it): a run of segments whose pair covers the sum's binade and
 // keeps it there is added at once, any other segment lane by lane
@@ -3985,30 +4010,47 @@ __device__ __forceinline__ float xs_walk(float cc, uint32_t s, uint32_t se, H hd
       }
     }
     const uint32_t mts = hdr(s, 7u);
-    const uint32_t cnt = mts & 0x7fffffffu;
-    if (mts >> 31) {
+    const uint32_t cnt = mts & XS_CNT;
+    // the segment's runs, formed with its terms for the bounds on its start,
+    // or formed here from the exact sum
+    const bool have = (mts & XS_RUNS) != 0u;
+    RunLane r = RunLane{0u, 0u, 0u};
+    if (have) r = src.runs(s, lane);
+    if (mts & XS_PACKED) {
       float p4[4];
       src.get4(s, lane, p4);
 #pragma unroll
       for (uint32_t q = 0; q < 4; ++q) p4[q] = 4 * lane + q < cnt ? p4[q] : 0.0f;
-      cc = wave_sum_q<4>(cc, p4, cnt);
+      const uint32_t nl = (cnt + 3u) / 4u;
+      if (nl > 0) cc = runs_walk<4>(cc, p4, nl, have ? r : seg_runs<4>(p4, nl, cc, cc));
     } else {
       float p16[16];
       src.get16(s, lane, p16);
-      cc = wave_sum_q<16>(cc, p16, cnt);
+      const uint32_t nl = (cnt + 15u) / 16u;
+      if (nl > 0) cc = runs_walk<16>(cc, p16, nl, have ? r : seg_runs<16>(p16, nl, cc, cc));
     }
     ++s;
   }
   return cc;
 }
-// a segment's terms: its LDS copy when it has one, else the published ones
+// a segment's terms and runs: their LDS copy when it has one, else the
+// published ones
 struct XsTerms {
-  LDS const float* pf;       // [npf][TILE]
+  LDS const float* pf;       // [npf][XS_SLOT]: terms, then runs
   LDS const uint32_t* pfs;   // segment -> copy, or EMPTY
   const GLB float* terms;    // [ns][TILE]
+  const GLB uint32_t* rw;    // [ns][XS_RUNW]
+  __device__ __forceinline__ RunLane runs(uint32_t s, uint32_t lane) const {
+    const uint32_t slot = pfs[s];
+    const u4v v = slot != EMPTY
+                      ? *(LDS const u4v*)((LDS const uint32_t*)pf + (uint64_t)slot * XS_SLOT +
+                                          TILE + 4 * lane)
+                      : *(const GLB u4v*)(rw + (uint64_t)s * XS_RUNW + 4 * lane);
+    return RunLane{v.x, v.y, v.z};
+  }
   __device__ __forceinline__ void get4(uint32_t s, uint32_t lane, float (&p)[4]) const {
     const uint32_t slot = pfs[s];
-    const f4v v = slot != EMPTY ? *(LDS const f4v*)(pf + (uint64_t)slot * TILE + 4 * lane)
+    const f4v v = slot != EMPTY ? *(LDS const f4v*)(pf + (uint64_t)slot * XS_SLOT + 4 * lane)
                                 : *(const GLB f4v*)(terms + (uint64_t)s * TILE + 4 * lane);
     p[0] = v.x;
     p[1] = v.y;
@@ -4020,7 +4062,7 @@ struct XsTerms {
 #pragma unroll
     for (uint32_t q = 0; q < 16; q += 4) {
       const f4v v = slot != EMPTY
-                        ? *(LDS const f4v*)(pf + (uint64_t)slot * TILE + 16 * lane + q)
+                        ? *(LDS const f4v*)(pf + (uint64_t)slot * XS_SLOT + 16 * lane + q)
                         : *(const GLB f4v*)(terms + (uint64_t)s * TILE + 16 * lane + q);
       p[q] = v.x;
       p[q + 1] = v.y;
@@ -4029,9 +4071,14 @@ struct XsTerms {
     }
   }
 };
-// window 0's own copy of its segments' terms (segment s at s * TILE)
+// window 0's own copy of its segments' terms (segment s at s * TILE) and
+// runs (at 16 * TILE + s * XS_RUNW)
 struct XsOwnTerms {
   LDS const float* t;
+  __device__ __forceinline__ RunLane runs(uint32_t s, uint32_t lane) const {
+    const u4v v = *(LDS const u4v*)((LDS const uint32_t*)t + 16 * TILE + s * XS_RUNW + 4 * lane);
+    return RunLane{v.x, v.y, v.z};
+  }
   __device__ __forceinline__ void get4(uint32_t s, uint32_t lane, float (&p)[4]) const {
     const f4v v = *(LDS const f4v*)(t + s * TILE + 4 * lane);
     p[0] = v.x;
@@ -4086,6 +4133,7 @@ __device__ __forceinline__ void xs_phase() {
     GLB uint32_t* wflag = G(w.xs_wflag) + (uint64_t)j * maxw;
     GLB uint32_t* meta = G(w.xs_meta) + (uint64_t)j * maxw * 16 * 8;
     GLB float* terms = G(w.xs_terms) + (uint64_t)j * maxw * 16 * TILE;
+    GLB uint32_t* runs = G(w.xs_runs) + (uint64_t)j * maxw * 16 * XS_RUNW;
     const void* row = (const char*)a.logits +
                       (uint64_t)b * a.stride * ((DT & 3) == LLMK_F32 ? 4u : 2u);
     const GLB uint32_t* mrow = a.mask ? G(a.mask) + (uint64_t)b * a.mask_words : nullptr;
@@ -4240,7 +4288,18 @@ __device__ __forceinline__ void xs_phase() {
         hdr = (uint32_t)(elo + 256) | ((uint32_t)nb << 16);
       }
     }
-    // ---- publish the segment: header, pairs, count, terms
+    // ---- the runs of a segment the walk may sum lane by lane (no pairs, or
+    // pairs in more than one binade), for a start anywhere in [blo, bhi]
+    // widened by the drift
+    const bool want_runs = (hdr >> 16) != 1u && bhi < 0x1p120 && nseg > 0;
+    RunLane rn = RunLane{0u, 0u, 0u};
+    if (want_runs) {
+      const double slo = blo * (1.0 - drift), shi = bhi * (1.0 + drift);
+      rn = packed ? seg_runs<4>(pk, (nseg + 3u) / 4u, slo, shi)
+                  : seg_runs<16>(e, (nseg + 15u) / 16u, slo, shi);
+    }
+    const uint32_t word7 = nseg | (packed ? XS_PACKED : 0u) | (want_runs ? XS_RUNS : 0u);
+    // ---- publish the segment: header, pairs, count, terms, runs
     const uint32_t sg = 16 * k + wv;
     GLB uint32_t* mt = meta + (uint64_t)sg * 8;
     GLB float* tt = terms + (uint64_t)sg * TILE;
@@ -4251,8 +4310,10 @@ __device__ __forceinline__ void xs_phase() {
         mt[1 + 2 * q] = pr[q].a0;
         mt[2 + 2 * q] = pr[q].a1;
       }
-      mt[7] = nseg | (packed ? 0x80000000u : 0u);
+      mt[7] = word7;
     }
+    if (want_runs)
+      *(GLB u4v*)(runs + (uint64_t)sg * XS_RUNW + 4 * lane) = u4v{rn.a0, rn.a1, rn.k, 0u};
     if (packed) {
       *(GLB f4v*)(tt + 4 * lane) = f4v{pk[0], pk[1], pk[2], pk[3]};
     } else {
@@ -4260,9 +4321,10 @@ __device__ __forceinline__ void xs_phase() {
       for (uint32_t q = 0; q < 16; q += 4)
         *(GLB f4v*)(tt + 16 * lane + q) = f4v{e[q], e[q + 1], e[q + 2], e[q + 3]};
     }
-    // window 0 (of several) keeps its records and terms in LDS too, past the
-    // history tables and the packing space, for its own walk below
-    LDS uint32_t* own = hb + hist_lds_words(HW) + NW * XS_CW;  // [16][8], then [16][TILE]
+    // window 0 (of several) keeps its records, terms and runs in LDS too, in
+    // the history tables' place (no wave reads them past the barrier before
+    // the pairs), for its own walk below
+    LDS uint32_t* own = hb;  // [16][8], then [16][TILE] terms, then [16][XS_RUNW] runs
     if (k == 0 && nwin > 1) {
       if (lane == 0) {
         own[8 * wv] = hdr;
@@ -4271,8 +4333,10 @@ __device__ __forceinline__ void xs_phase() {
           own[8 * wv + 1 + 2 * q] = pr[q].a0;
           own[8 * wv + 2 + 2 * q] = pr[q].a1;
         }
-        own[8 * wv + 7] = nseg | (packed ? 0x80000000u : 0u);
+        own[8 * wv + 7] = word7;
       }
+      if (want_runs)
+        *(LDS u4v*)(own + 128 + 16 * TILE + XS_RUNW * wv + 4 * lane) = u4v{rn.a0, rn.a1, rn.k, 0u};
       LDS float* ot = (LDS float*)(own + 128) + TILE * wv;
       if (packed) {
         *(LDS f4v*)(ot + 4 * lane) = f4v{pk[0], pk[1], pk[2], pk[3]};
@@ -4303,8 +4367,8 @@ __device__ __forceinline__ void xs_phase() {
       LDS uint32_t* segp = sm + 256;         // [ns][8]
       LDS uint32_t* pfs = segp + ns * 8;     // [ns]: LDS copy of a segment's terms, or EMPTY
       LDS uint32_t* pfl = pfs + ns;          // [ns]: the segment of each copy
-      LDS float* pf = (LDS float*)(pfl + ns);  // [npf][TILE]
-      const uint32_t npf = (a.xs_lds - (256 + 10 * ns)) / TILE;
+      LDS float* pf = (LDS float*)(pfl + ns);  // [npf][XS_SLOT]: terms, then runs
+      const uint32_t npf = (a.xs_lds - (256 + 10 * ns)) / XS_SLOT;
       // window 0, when it is not this one, walks its own segments and
       // publishes the sum at its end (below); the walk here starts there
       const bool from_own = k != 0;
@@ -4316,6 +4380,7 @@ __device__ __forceinline__ void xs_phase() {
       {
         uint32_t mv[8];
         float tv[16];
+        uint32_t rv[4];
 #pragma unroll
         for (uint32_t q = 0; q < 8; ++q) {
           const uint32_t i = tid + q * NT;
@@ -4324,23 +4389,32 @@ __device__ __forceinline__ void xs_phase() {
 #pragma unroll
         for (uint32_t q = 0; q < 16; ++q) tv[q] = q < n0 ? terms[q * TILE + tid] : 0.0f;
 #pragma unroll
+        for (uint32_t q = 0; q < 4; ++q) rv[q] = 4 * q < n0 ? runs[q * NT + tid] : 0u;
+#pragma unroll
         for (uint32_t q = 0; q < 8; ++q) {
           const uint32_t i = tid + q * NT;
           if (i < ns * 8) segp[i] = mv[q];
         }
 #pragma unroll
         for (uint32_t q = 0; q < 16; ++q)
-          if (q < n0) pf[q * TILE + tid] = tv[q];
+          if (q < n0) pf[q * XS_SLOT + tid] = tv[q];
+        // runs of segments 4q .. 4q + 3: thread t holds word t of them
+#pragma unroll
+        for (uint32_t q = 0; q < 4; ++q) {
+          const uint32_t sq = 4 * q + tid / XS_RUNW;
+          if (sq < n0) ((LDS uint32_t*)pf)[sq * XS_SLOT + TILE + tid % XS_RUNW] = rv[q];
+        }
       }
       __syncthreads();
-      // then the other segments without pairs past window 0, as many as fit
-      // (the rest are read when the walk reaches them)
+      // then the other segments past window 0 that the walk may sum lane by
+      // lane (no pairs, or pairs in more than one binade), as many as fit (the
+      // rest are read when the walk reaches them)
       const uint32_t sfirst = from_own ? 16u : n0;
       if (wv == 0) {
         uint32_t used = n0;
         for (uint32_t s0 = 0; s0 < ns; s0 += WAVE) {
           const uint32_t si = s0 + lane;
-          const bool want = si >= sfirst && si < ns && (segp[8 * si] >> 16) == 0u;
+          const bool want = si >= sfirst && si < ns && (segp[8 * si] >> 16) != 1u;
           const uint32_t r = used + (uint32_t)__popcll(__ballot(want) & ((1ull << lane) - 1ull));
           if (si < n0) pfs[si] = si;
           else if (si < ns) pfs[si] = (want && r < npf) ? r : EMPTY;
@@ -4355,12 +4429,23 @@ __device__ __forceinline__ void xs_phase() {
       // element t of each; past a segment's count the copy is never read)
       for (uint32_t s0 = n0; s0 < nused; s0 += 8) {
         float v[8];
+        uint32_t rv[2];
 #pragma unroll
         for (uint32_t q = 0; q < 8; ++q)
           v[q] = s0 + q < nused ? terms[(uint64_t)pfl[s0 + q] * TILE + tid] : 0.0f;
 #pragma unroll
+        for (uint32_t q = 0; q < 2; ++q) {
+          const uint32_t sq = s0 + 4 * q + tid / XS_RUNW;
+          rv[q] = sq < nused ? runs[(uint64_t)pfl[sq] * XS_RUNW + tid % XS_RUNW] : 0u;
+        }
+#pragma unroll
         for (uint32_t q = 0; q < 8; ++q)
-          if (s0 + q < nused) pf[(s0 + q) * TILE + tid] = v[q];
+          if (s0 + q < nused) pf[(s0 + q) * XS_SLOT + tid] = v[q];
+#pragma unroll
+        for (uint32_t q = 0; q < 2; ++q) {
+          const uint32_t sq = s0 + 4 * q + tid / XS_RUNW;
+          if (sq < nused) ((LDS uint32_t*)pf)[sq * XS_SLOT + TILE + tid % XS_RUNW] = rv[q];
+        }
       }
       __syncthreads();
       if (wv == 0) {
@@ -4383,7 +4468,7 @@ __device__ __forceinline__ void xs_phase() {
         }
         const float cc = xs_walk(c0, s0, ns,
                                  [&](uint32_t i, uint32_t x) { return segp[8 * i + x]; },
-                                 XsTerms{pf, pfs, terms});
+                                 XsTerms{pf, pfs, terms, runs});
         if (lane == 0) sm[71] = __float_as_uint(cc);
       }
       __syncthreads();
@@ -5835,7 +5920,7 @@ static constexpr size_t LDS_DYN_MAX = 160 * 1024 - 1024;
 // of its arrays in one 256-byte aligned block.
 struct WsLayout {
   size_t arrive, part, meta, cand, lock, skeys, sp, si, status, cut, mtok, zu;
-  size_t xctl, xjob, xwsum, xwflag, xmeta, xterms, xsave, total;
+  size_t xctl, xjob, xwsum, xwflag, xmeta, xterms, xruns, xsave, total;
 };
 static constexpr uint32_t xs_maxw(uint32_t mv) { return (mv + XS_W - 1) / XS_W; }
 static constexpr WsLayout ws_layout(uint32_t mb, uint32_t mv, uint32_t pool, uint32_t slots) {
@@ -5860,6 +5945,7 @@ static constexpr WsLayout ws_layout(uint32_t mb, uint32_t mv, uint32_t pool, uin
   L.xwflag = off; off = align_up(off + 4ull * XS_JOBS * mw, 256);
   L.xmeta = off; off = align_up(off + 4ull * XS_JOBS * mw * 16 * 8, 256);
   L.xterms = off; off = align_up(off + 4ull * XS_JOBS * mw * 16 * TILE, 256);
+  L.xruns = off; off = align_up(off + 4ull * XS_JOBS * mw * 16 * XS_RUNW, 256);
   L.xsave = off; off = align_up(off + 4ull * XS_JOBS * XS_SAVE, 256);
   L.total = off;
   return L;
@@ -5884,6 +5970,7 @@ static Ws ws_carve(char* base, const WsLayout& L, uint32_t mv, uint32_t slots) {
   w.xs_wflag = (uint32_t*)(base + L.xwflag);
   w.xs_meta = (uint32_t*)(base + L.xmeta);
   w.xs_terms = (float*)(base + L.xterms);
+  w.xs_runs = (uint32_t*)(base + L.xruns);
   w.xs_save = (uint32_t*)(base + L.xsave);
   w.xs_maxw = xs_maxw(mv);
   w.max_vocab = mv;
@@ -6127,9 +6214,11 @@ static int sample_batch_run(const Ws& ws, uint32_t max_batch, uint32_t max_vocab
   if (a.xs_cap > 0) {
     Args a1 = a;
     a1.phase = 1;
-    // (a window's history tables and packing space, then window 0's copy of
-    // its records and terms)
-    const size_t lds1 = 4 * (256 + hist_lds_words(XS_W / 32) + NW * XS_CW + 128 + NW * TILE);
+    // (a window's history tables and packing space; window 0's copy of its
+    // records, terms and runs takes the tables' place afterwards)
+    const size_t own = 128 + (size_t)NW * (TILE + XS_RUNW);
+    const size_t hist = hist_lds_words(XS_W / 32) + NW * XS_CW;
+    const size_t lds1 = 4 * (256 + (hist > own ? hist : own));
     a1.xs_lds = (uint32_t)((lds > lds1 ? lds : lds1) / 4);
     launch(a1, dim3(a.xs_cap * nwin), 4 * (size_t)a1.xs_lds);
     HIPCHK(hipGetLastError());
