@@ -2029,14 +2029,26 @@ __device__ __forceinline__ Par lane_pair(const float (&e)[Q], int eb) {
 // the first one where c leaves the binade are added by their pairs, that
 // lane's terms one f32 addition each, and the scan resumes after it.  Every
 // lane returns the sum.
+// c + lane j's Q terms in order, one f32 addition each, added by lane j
+// itself (a chain of register additions; read lane by lane into scalar
+// registers the same chain is several times slower); j wave-uniform, every
+// lane returns the sum.
+template <int Q>
+__device__ __forceinline__ float lane_chain(float c, const float (&p)[Q], uint32_t j) {
+  float x = c;
+  if ((threadIdx.x & 63u) == j) {
+#pragma unroll
+    for (int q = 0; q < Q; ++q) x = x + p[q];
+  }
+  return rl(x, j);
+}
 template <int Q>
 __device__ __forceinline__ float wave_sum_rounds(float c, const float (&p)[Q], uint32_t nl,
                                                  uint32_t pos) {
   const uint32_t lane = threadIdx.x & 63u;
   while (pos < nl) {
     if (c == 0.0f) {
-#pragma unroll
-      for (int q = 0; q < Q; ++q) c = c + rl(p[q], pos);  // zeros past n add nothing
+      c = lane_chain<Q>(c, p, pos);  // zeros past n add nothing
       ++pos;
       continue;
     }
@@ -2053,10 +2065,7 @@ __device__ __forceinline__ float wave_sum_rounds(float c, const float (&p)[Q], u
     }
     const uint32_t l = (uint32_t)__builtin_ctzll(cross);
     const uint32_t Cb = l > pos ? C + (uint32_t)__builtin_amdgcn_readlane((int)inc, (int)l - 1) : C;
-    float cb = __builtin_ldexpf((float)Cb, eb - 23);
-#pragma unroll
-    for (int q = 0; q < Q; ++q) cb = cb + rl(p[q], l);
-    c = cb;
+    c = lane_chain<Q>(__builtin_ldexpf((float)Cb, eb - 23), p, l);
     pos = l + 1;
   }
   return c;
@@ -2125,8 +2134,7 @@ __device__ __forceinline__ float runs_walk(float c, const float (&p)[Q], uint32_
   uint32_t pos = 0;
   while (pos < nl) {
     if ((bad >> pos) & 1ull) {
-#pragma unroll
-      for (int q = 0; q < Q; ++q) c = c + rl(p[q], pos);
+      c = lane_chain<Q>(c, p, pos);
       ++pos;
       continue;
     }
