@@ -4376,7 +4376,10 @@ __device__ __forceinline__ void xs_phase() {
       LDS uint32_t* pfs = segp + ns * 8;     // [ns]: LDS copy of a segment's terms, or EMPTY
       LDS uint32_t* pfl = pfs + ns;          // [ns]: the segment of each copy
       LDS float* pf = (LDS float*)(pfl + ns);  // [npf][XS_SLOT]: terms, then runs
-      const uint32_t npf = (a.xs_lds - (256 + 10 * ns)) / XS_SLOT;
+      // (below a single-segment row's partials and candidates, which go back
+      // in place during the walk)
+      const uint32_t lds_top = a.G == 1 ? a.lds_part : a.xs_lds;
+      const uint32_t npf = (lds_top - (256 + 10 * ns)) / XS_SLOT;
       // window 0, when it is not this one, walks its own segments and
       // publishes the sum at its end (below); the walk here starts there
       const bool from_own = k != 0;
@@ -4456,6 +4459,12 @@ __device__ __forceinline__ void xs_phase() {
         }
       }
       __syncthreads();
+      // a single-segment row's LDS partials and candidates back in place
+      // (waves 1-15, while wave 0 walks)
+      if (a.G == 1 && wv != 0) {
+        const GLB uint32_t* sv = G(w.xs_save) + (uint64_t)j * XS_SAVE;
+        for (uint32_t i = tid - WAVE; i < XS_SAVE; i += NT - WAVE) sm[a.lds_part + i] = sv[i];
+      }
       if (wv == 0) {
         // window 0's sum at its end (a bounded wait; if it runs out, the
         // walk starts at zero and reads window 0's terms from memory)
@@ -4485,14 +4494,11 @@ __device__ __forceinline__ void xs_phase() {
       if (tid == 0) __hip_atomic_store(&w.xs_ctl[2 + j], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       for (uint32_t i = tid; i < nwin; i += NT) wflag[i] = 0u;
       __syncthreads();
-      // the row's LDS partials and candidates, then its candidate path: for
-      // a single-segment row here (its history never outgrew its tables),
-      // the rest through finalize_rare (a call: its register saves cost
+      // the row's candidate path: for a single-segment row here (its history
+      // never outgrew its tables; its partials and candidates are back), the
+      // rest through finalize_rare (a call: its register saves cost
       // microseconds)
       if (a.G == 1) {
-        const GLB uint32_t* sv = G(w.xs_save) + (uint64_t)j * XS_SAVE;
-        for (uint32_t i = tid; i < XS_SAVE; i += NT) sm[a.lds_part + i] = sv[i];
-        __syncthreads();
         const uint32_t path = candidate_paths<DT>(a, w, b, P, S, m, L, u, seg_own, false, sm);
         if (path != 0) finalize_rare<DT>(b, P, S, m, L, u, seg_own, false, path);
       } else {
