@@ -4307,6 +4307,20 @@ __device__ __forceinline__ void xs_phase() {
                   : seg_runs<16>(e, (nseg + 15u) / 16u, slo, shi);
     }
     const uint32_t word7 = nseg | (packed ? XS_PACKED : 0u) | (want_runs ? XS_RUNS : 0u);
+    // window 0 (of several) starts its own walk here: its first segment's
+    // runs were formed for a start at exactly 0, so wave 0 sums them while
+    // the other waves form their pairs (sm[73]: the sum, sm[74]: segments
+    // done)
+    if (k == 0 && wv == 0 && nwin > 1) {
+      float c0 = 0.0f;
+      if (want_runs)
+        c0 = packed ? runs_walk<4>(0.0f, pk, (nseg + 3u) / 4u, rn)
+                    : runs_walk<16>(0.0f, e, (nseg + 15u) / 16u, rn);
+      if (lane == 0) {
+        sm[73] = __float_as_uint(c0);
+        sm[74] = want_runs ? 1u : 0u;
+      }
+    }
     // ---- publish the segment: header, pairs, count, terms, runs
     const uint32_t sg = 16 * k + wv;
     GLB uint32_t* mt = meta + (uint64_t)sg * 8;
@@ -4380,9 +4394,18 @@ __device__ __forceinline__ void xs_phase() {
       // in place during the walk)
       const uint32_t lds_top = a.G == 1 ? a.lds_part : a.xs_lds;
       const uint32_t npf = (lds_top - (256 + 10 * ns)) / XS_SLOT;
-      // window 0, when it is not this one, walks its own segments and
-      // publishes the sum at its end (below); the walk here starts there
-      const bool from_own = k != 0;
+      // window 0 walks its own segments (below, or first here when it is the
+      // last to arrive) and the walk here starts at their end
+      const bool from_own = nwin > 1;
+      if (k == 0 && from_own) {
+        if (wv == 0) {
+          const float c = xs_walk(__uint_as_float(sm[73]), sm[74], 16u,
+                                  [&](uint32_t i, uint32_t x) { return own[8 * i + x]; },
+                                  XsOwnTerms{(LDS const float*)(own + 128)});
+          if (lane == 0) sm[75] = __float_as_uint(c);
+        }
+        __syncthreads();
+      }
       // the segments' headers, and the terms of window 0's segments when the
       // walk starts at zero (from there window 0 crosses a binade at each
       // doubling, so the walk sums most of its segments lane by lane), in
@@ -4470,7 +4493,10 @@ __device__ __forceinline__ void xs_phase() {
         // walk starts at zero and reads window 0's terms from memory)
         float c0 = 0.0f;
         uint32_t s0 = 0;
-        if (from_own) {
+        if (k == 0 && from_own) {
+          c0 = __uint_as_float(sm[75]);
+          s0 = 16;
+        } else if (from_own) {
           for (uint32_t n = 0; n < XS_SPIN; ++n) {
             const uint32_t t = __hip_atomic_load(own_sum + 1, __ATOMIC_ACQUIRE,
                                                  __HIP_MEMORY_SCOPE_AGENT);
@@ -4505,8 +4531,8 @@ __device__ __forceinline__ void xs_phase() {
         finalize_rare<DT>(b, P, S, m, L, u, seg_own, false, 6u);
       }
     } else if (k == 0 && wv == 0) {
-      // ---- window 0's own walk, from zero, over its LDS copy
-      const float cc = xs_walk(0.0f, 0u, 16u,
+      // ---- window 0's own walk over its LDS copy, on from its first segment
+      const float cc = xs_walk(__uint_as_float(sm[73]), sm[74], 16u,
                                [&](uint32_t i, uint32_t x) { return own[8 * i + x]; },
                                XsOwnTerms{(LDS const float*)(own + 128)});
       if (lane == 0) {
