@@ -156,7 +156,7 @@ int llmk_sample_batch(llmk_sampler* s, const llmk_sample_batch_args* args,
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  Same arguments, semantics and results as
  * llmk_sample_batch, on the current device; its workspace is a static
- * device array of 98 MiB that each GPU the library runs on holds
+ * device array of 108 MiB that each GPU the library runs on holds
  * until the process ends, sized for batch <= 256 and vocab <= 262144 (larger
  * calls fail with LLMK_ERR_CAPACITY).  `status`: optional device u32 into
  * which the call ORs its LLMK_STATUS_* bits (the caller clears it); NULL =

@@ -3972,13 +3972,19 @@ __device__ __noinline__ void finalize_rare(uint32_t b, RowP P, float S, float m,
 //     half its quantum) are dropped, each segment packs or keeps its live
 //     terms and forms its pairs in the binades its running sum can occupy,
 //     exactly as exact_normaliser does within one workgroup, and publishes
-//     them with its terms.
-// The walker, wave 0 of the job's last workgroup, then sums the segments in
-// order with the exact running sum: runs covered by pairs at once, the
-// others lane by lane from their published terms (wave_sum_q).  The sum is
-// exact whatever the estimates.  Then the row's candidate path runs again
-// with that S (finalize_rare, path 6), its LDS partials and candidates
-// restored first.
+//     them with its terms;
+//   * a segment whose sum may leave a binade also publishes its runs
+//     (seg_runs, for a start anywhere in its bounds).
+// Window 0 (of several) walks its own 16 segments from its LDS copy (its
+// first one while its other waves form their pairs) and publishes the exact
+// sum at its end with the call's tag.  The walker, wave 0 of the job's last
+// workgroup, waits for that sum (bounded; if the wait ran out it would walk
+// from zero) and sums the other segments in order with the exact running
+// sum: runs of segments covered by pairs at once, any other segment by its
+// runs (runs_walk).  The sum is exact whatever the estimates.  Then the
+// row's candidate path runs again with that S, its LDS partials and
+// candidates put back by the walker's other waves during the walk (a row of
+// several segments: finalize_rare, path 6).
 constexpr uint32_t XS_SPIN = 1u << 16;
 constexpr uint32_t XS_RUNW = 256;              // a segment's runs: a lane's (a0, a1, k, 0)
 constexpr uint32_t XS_SLOT = TILE + XS_RUNW;   // an LDS copy: terms, then runs
