@@ -146,6 +146,10 @@ struct Args {
   // the call's parity: its jobs are counted in xs_ctl[epoch & 1], and its
   // sampling launch clears the other count for the next call
   uint32_t epoch;
+  // phase 1's bounded waits (for the sums of earlier windows, for window
+  // 0's own walk): at most this many polls (XS_SPIN; a test sets 0 to take
+  // the paths where a wait runs out)
+  uint32_t xs_spin;
 };
 
 struct Ws {
@@ -4199,7 +4203,7 @@ __device__ __forceinline__ void xs_phase() {
         const uint32_t i = i0 + lane;
         bool have = i >= k;
         for (uint32_t n = 0; __ballot(!have) != 0ull; ++n) {
-          if (n == XS_SPIN) {
+          if (n == a.xs_spin) {
             ok = 0;
             break;
           }
@@ -4503,7 +4507,7 @@ __device__ __forceinline__ void xs_phase() {
           c0 = __uint_as_float(sm[75]);
           s0 = 16;
         } else if (from_own) {
-          for (uint32_t n = 0; n < XS_SPIN; ++n) {
+          for (uint32_t n = 0; n < a.xs_spin; ++n) {
             const uint32_t t = __hip_atomic_load(own_sum + 1, __ATOMIC_ACQUIRE,
                                                  __HIP_MEMORY_SCOPE_AGENT);
             if ((uint32_t)__builtin_amdgcn_readfirstlane((int)t) == tag) {
@@ -5934,6 +5938,7 @@ struct llmk_sampler {
   size_t stage_bytes;
   uint32_t epoch;      // calls made (their parity picks the job count)
   uint32_t ncu;        // the device's compute units
+  uint32_t xs_spin;    // phase 1's wait limit (LLMK_TEST_XS_SPIN at create, for tests)
 };
 
 static thread_local std::string g_last_error;
@@ -6072,6 +6077,9 @@ extern "C" int llmk_sampler_create(llmk_sampler** out, int device,
   if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
     ncu = 0;  // phase 1 then stays off
   s->ncu = (uint32_t)(ncu > 0 ? ncu : 0);
+  // a test hook: phase 1's waits run out at once with LLMK_TEST_XS_SPIN=0
+  const char* spin = getenv("LLMK_TEST_XS_SPIN");
+  s->xs_spin = spin ? (uint32_t)strtoul(spin, nullptr, 10) : XS_SPIN;
   s->mem = mem;
   s->mem_bytes = L.total;
   s->ws = ws_carve((char*)mem, L, max_vocab, slots);
@@ -6131,7 +6139,8 @@ static float dtype_round(double x, int fmt) {
 constexpr uint32_t XS_MIN_BATCH = 16;
 static int sample_batch_run(const Ws& ws, uint32_t max_batch, uint32_t max_vocab, uint32_t pool,
                             const llmk_sample_batch_args* in, void* stream, u4v* cut,
-                            uint32_t tp_clamp, uint32_t epoch, uint32_t ncu) {
+                            uint32_t tp_clamp, uint32_t epoch, uint32_t ncu,
+                            uint32_t xs_spin = XS_SPIN) {
   if (!in) return fail(LLMK_ERR_INVALID_ARGUMENT, "args is NULL");
   if (in->vocab == 0) return fail(LLMK_ERR_EMPTY_LOGITS, "Empty logits passed to sampler");
   if (in->batch == 0) return fail(LLMK_ERR_INVALID_ARGUMENT, "batch is 0");
@@ -6203,6 +6212,7 @@ static int sample_batch_run(const Ws& ws, uint32_t max_batch, uint32_t max_vocab
   a.xs_cap = !phase1 ? 0u : (ncu / nwin < XS_JOBS ? ncu / nwin : XS_JOBS);
   a.xs_lds = 0;
   a.epoch = epoch;
+  a.xs_spin = xs_spin;
   a.ntiles = (a.V + TILE - 1) / TILE;
   a.nchunks = (a.ntiles + CHUNK_TILES - 1) / CHUNK_TILES;
   // Segments per row: enough workgroups to cover the 256 CUs, whole 16-tile
@@ -6324,12 +6334,12 @@ static int sample_batch_impl(llmk_sampler* s, const llmk_sample_batch_args* in,
     al.logits = s->stage;
     al.row_stride = dstride;
     const int rc = sample_batch_run(s->ws, s->max_batch, s->max_vocab, pool, &al, stream, cut,
-                                    tp_clamp, s->epoch, s->ncu);
+                                    tp_clamp, s->epoch, s->ncu, s->xs_spin);
     if (rc == LLMK_OK) ++s->epoch;  // the parity advances with the launches only
     return rc;
   }
   const int rc = sample_batch_run(s->ws, s->max_batch, s->max_vocab, pool, in, stream, cut,
-                                  tp_clamp, s->epoch, s->ncu);
+                                  tp_clamp, s->epoch, s->ncu, s->xs_spin);
   if (rc == LLMK_OK) ++s->epoch;
   return rc;
 }

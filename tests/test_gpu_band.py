@@ -115,3 +115,41 @@ def test_deferred_rows_in_every_dtype(sampler, dtype, cap):
     assert_matches_ref(w, gpu, O.sample_workload(O.REF, c, out_cap=CAP, nthreads=16), CAP,
                        f"deferred {dtype} {cap}")
     assert sampler.status() == 0
+
+
+def test_phase1_waits_that_run_out(monkeypatch):
+    """Phase 1's bounded waits forced to run out at once (LLMK_TEST_XS_SPIN=0,
+    read when the handle is created): no window waits for the sums before it,
+    so no window past the first bounds its start and none of its segments
+    has pairs or runs from its window (the walk forms them from the exact
+    sum), and a walker that is not window 0 does not wait for window 0's own
+    walk but walks from zero over window 0's published terms and runs.  On
+    rows whose band check fails (C3's parameters, 20 rows, f32), two calls in
+    a row (both job-count parities): the same outputs as the oracles."""
+    import torch
+    from test_gpu_softcap import make
+    monkeypatch.setenv("LLMK_TEST_XS_SPIN", "0")
+    s = llmk.HipSampler(max_batch=64, max_vocab=256000)
+    try:
+        w = make("C3", 20, "f32")
+        hit = 0
+        for r in range(w.B):
+            u = BU.divergent_uniform(w, r, cap=CAP)
+            if u is not None:
+                w.uniforms[r] = np.float32(u)
+                hit += 1
+        assert hit >= 4
+        mirror = O.sample_workload(O.MIRROR, w, out_cap=CAP, nthreads=16)
+        ref = O.sample_workload(O.REF, w, out_cap=CAP, nthreads=16)
+        db = w.to_device()
+        for call in range(2):
+            print(f"[case] phase-1 waits run out, {hit} deferred rows, call {call}", flush=True)
+            r = s.sample_batch(db, out_cap=CAP)
+            torch.cuda.synchronize()
+            gpu = (r.tokens.cpu().numpy().view(np.uint32), r.ids.cpu().numpy().view(np.uint32),
+                   r.probs.cpu().numpy(), r.count.cpu().numpy().view(np.uint32))
+            assert_bit_exact(w, gpu, mirror, CAP, f"waits run out, call {call}")
+            assert_matches_ref(w, gpu, ref, CAP, f"waits run out, call {call}")
+            assert s.status() == 0
+    finally:
+        s.close()
