@@ -15,9 +15,9 @@ S; otherwise the row is sampled with the reference's own S.  Pinned here:
   an entry are uncertain; a spread-out list far from every boundary is
   certain;
 * the mirror oracle against the reference on C3 rows, at uniforms and top_p
-  values that the VERDICT's method finds between the two cumulatives (where
-  S = 1 alone draws another token or keeps another count): the same token,
-  count and ids.
+  values found on rand's 2^-24 grid between the two cumulatives of one entry
+  (where S = 1 alone draws another token or keeps another count): the same
+  token, count and ids.
 """
 import numpy as np
 import pytest
@@ -157,7 +157,7 @@ def c3():
 
 
 def test_mirror_is_reference_where_s1_draws_another_token(c3):
-    """The VERDICT's method on C3 rows: a uniform between REF's and S = 1's
+    """On C3 rows, a uniform on the 2^-24 grid between REF's and S = 1's
     cumulative of one entry draws different tokens from the two; there the
     mirror (the engine's arithmetic) draws REF's token, keeps REF's count
     and ids."""
