@@ -153,3 +153,32 @@ def test_phase1_waits_that_run_out(monkeypatch):
             assert s.status() == 0
     finally:
         s.close()
+
+
+@pytest.mark.parametrize("V", [12000, 20000, 40000])
+def test_deferred_rows_at_small_vocabularies(sampler, V):
+    """Rows whose band check fails at vocabularies of one phase-1 window
+    (12000: window 0 is the walker and sums from zero), two windows (20000:
+    window 0 walks its own segments, the walker goes on from there) and
+    three (40000), C3's parameters, 20 rows: the same outputs as the
+    oracles."""
+    import torch
+    w = synth.make("C3", B=20, V=V)
+    hit = 0
+    for r in range(w.B):
+        u = BU.divergent_uniform(w, r, cap=CAP)
+        if u is not None:
+            w.uniforms[r] = np.float32(u)
+            hit += 1
+    print(f"[case] deferred rows at V={V}: {hit} rows", flush=True)
+    assert hit >= 4
+    db = w.to_device()
+    r = sampler.sample_batch(db, out_cap=CAP)
+    torch.cuda.synchronize()
+    gpu = (r.tokens.cpu().numpy().view(np.uint32), r.ids.cpu().numpy().view(np.uint32),
+           r.probs.cpu().numpy(), r.count.cpu().numpy().view(np.uint32))
+    assert_bit_exact(w, gpu, O.sample_workload(O.MIRROR, w, out_cap=CAP, nthreads=16), CAP,
+                     f"deferred V={V}")
+    assert_matches_ref(w, gpu, O.sample_workload(O.REF, w, out_cap=CAP, nthreads=16), CAP,
+                       f"deferred V={V}")
+    assert sampler.status() == 0
